@@ -1,0 +1,305 @@
+/*
+ * mirai_moe.h -- C-ABI of the MI355X (gfx950) sparse-MoE expert-layer library
+ * (libmirai_moe.so).
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t passed
+ * as void*, and returns an int status (MX_OK on success). On failure a message
+ * is available from mx_last_error() (thread-local). No entry point allocates
+ * device memory: scratch space is passed in by the caller, sized by the
+ * matching *_workspace_size() query. All work is enqueued on `stream`; nothing
+ * synchronises with the host.
+ *
+ * Data formats (row-major, contiguous unless a leading dimension is given):
+ *   tokens          [T, d]          bf16
+ *   logits          [T, E]          fp32
+ *   top_idx         [T, k]          int64   expert id per route slot
+ *   top_scores      [T, k]          fp32 or bf16 (score_dtype)
+ *   NF4 weight      codes [E, out, in/2] uint8 (element 2i in the low nibble,
+ *                   2i+1 in the high nibble), absmax [E, out, in/64] bf16
+ *   INT8 weight     q [E, out, in] int8, scale [E, out] bf16
+ *   BF16 weight     w [E, out, in] bf16
+ *   LoRA factors    A [E, r, in], B [E, out, r] bf16 (rank r <= 32)
+ *
+ * Each declaration cites the reference interface (seruva19/mirai, path:line)
+ * whose semantics it implements.
+ */
+#ifndef MIRAI_MOE_H
+#define MIRAI_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MX_OK 0
+#define MX_ERR_INVALID 1 /* bad argument (shape, dtype, null pointer) */
+#define MX_ERR_HIP 2     /* a HIP runtime call failed */
+
+#define MX_DTYPE_F32 0
+#define MX_DTYPE_BF16 1
+
+#define MX_FMT_BF16 0
+#define MX_FMT_NF4 1
+#define MX_FMT_INT8 2
+
+/* Router normalisation modes. */
+#define MX_RENORM_NONE 0      /* scores = softmax probabilities of the picks   */
+#define MX_RENORM_CLAMP 1     /* p / clamp_min(sum p, 1e-20)                   */
+#define MX_RENORM_EPS 2       /* p / (sum p + 1e-20)                           */
+
+/* Last error message of the calling thread ("" when none). */
+const char *mx_last_error(void);
+/* ABI version; bumped on any signature change. */
+int mx_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Routing                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Top-k token-choice routing over fp32 router logits.
+ * Replaces the softmax -> topk -> gather -> renormalise -> *route_scale
+ * sequence of TokenChoiceRouter.forward
+ * (mirai/core/moe/routing/routers.py:234-249, renorm MX_RENORM_CLAMP) and of
+ * LingBotVideoRouter.forward with score_func="softmax" and a zero correction
+ * bias (mirai/vendors/lingbot_video/transformer_lingbot_video.py:1002-1033,
+ * renorm MX_RENORM_EPS when norm_topk_prob, else MX_RENORM_NONE).
+ * Selection is by logit (softmax is monotone); ties go to the lower expert id;
+ * slots are written in descending-score order. E <= 1024, 1 <= k <= 16.
+ */
+int mx_route_topk(const float *logits, int64_t num_tokens, int num_experts, int top_k,
+                  int renorm, float route_scale, int64_t *top_idx, void *top_scores,
+                  int score_dtype, void *stream);
+
+/*
+ * Backward of mx_route_topk: d(logits) from d(top_scores) for the selected
+ * experts (softmax Jacobian through the renormalisation), i.e. the router-gate
+ * gradient of LingBotVideoRouter.forward
+ * (transformer_lingbot_video.py:1002-1033) under autograd.
+ */
+int mx_route_topk_backward(const float *logits, int64_t num_tokens, int num_experts,
+                           int top_k, int renorm, float route_scale,
+                           const int64_t *top_idx, const float *grad_scores,
+                           float *grad_logits, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Dispatch plan (stable counting sort of routes by expert)                  */
+/* ------------------------------------------------------------------------ */
+
+/* Bytes of scratch needed by mx_build_plan / mx_plan_from_counts. */
+size_t mx_plan_workspace_size(int64_t num_tokens, int top_k, int num_experts);
+
+/*
+ * Device-resident dispatch plan; replaces build_dispatch_plan(backend="device")
+ * (mirai/core/models/compressed_weights/execution/dispatch_preprocess.py:128-179)
+ * and the argsort/bincount/cumsum block of
+ * CompressedGroupedExperts._run_direct_routed_batched_vectorized
+ * (mirai/core/models/compressed_weights/execution/experts.py:2369-2381).
+ * Outputs (all device, any may be NULL except where noted):
+ *   counts[E] int64, starts[E] int64 (exclusive), offsets[E] int32 (inclusive),
+ *   sort_positions[R], sorted_token_indices[R], inverse_order[R] int64,
+ *   sorted_scores[R] (score_dtype, needs top_scores).
+ * R = num_tokens * top_k. Route slots whose expert id is outside [0, E) are
+ * dropped (inverse_order = -1) and counted in the workspace error flag.
+ * The plan stays in `workspace` for the grouped GEMMs of mx_moe_forward.
+ */
+int mx_build_plan(const int64_t *top_idx, const void *top_scores, int score_dtype,
+                  int64_t num_tokens, int top_k, int num_experts, int64_t *counts,
+                  int64_t *starts, int32_t *offsets, int64_t *sort_positions,
+                  int64_t *sorted_token_indices, void *sorted_scores,
+                  int64_t *inverse_order, void *workspace, void *stream);
+
+/*
+ * Plan for rows that are already expert-sorted (counts given on device);
+ * the layout consumed by CompressedGroupedExperts.run_for_loop
+ * (experts.py:1656-1747): segment e holds rows [starts[e], starts[e]+counts[e]).
+ */
+int mx_plan_from_counts(const int64_t *counts, int64_t num_rows, int num_experts,
+                        void *workspace, void *stream);
+
+/* Number of invalid expert ids seen by the last plan built in `workspace`
+ * (device int32 pointer inside the workspace, for an optional host check). */
+const int32_t *mx_plan_error_counter(const void *workspace);
+
+/* ------------------------------------------------------------------------ */
+/* Permute / combine                                                          */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * out[i] = tokens[index[i]] for i < rows (rows whose index is outside
+ * [0, src_rows) are zero); width `cols` elements of `dtype`.
+ * Replaces _PermuteRoutedTokens.forward
+ * (mirai/core/models/compressed_weights/execution/dispatch_ops.py:8-13).
+ */
+int mx_gather_rows(const void *tokens, int64_t src_rows, const int64_t *index, int64_t rows,
+                   int64_t cols, int dtype, void *out, void *stream);
+
+/*
+ * out[index[i]] += row_scale[i] * rows_in[i] in fp32 (row_scale may be NULL
+ * for 1; `out` is zeroed first; indices outside [0, out_rows) are skipped).
+ * Replaces _PermuteRoutedTokens.backward (dispatch_ops.py:15-20) and the
+ * index_add_ of _CombineRoutedTokens.forward (dispatch_ops.py:23-33) for
+ * arbitrary (duplicate-carrying) index lists.
+ */
+int mx_scatter_add_rows(const void *rows_in, const float *row_scale, const int64_t *index,
+                        int64_t rows, int64_t cols, int dtype, int64_t out_rows, float *out,
+                        void *stream);
+
+/*
+ * out[t] = sum over the k slots of token t, in ascending expert order, of
+ * score[t,j] * y[t*k+j] accumulated in fp32, then cast to out_dtype.
+ * Replaces the fp32 output.index_add_ of run_direct_routed
+ * (experts.py:1786-1790, 2430-2438) and _CombineRoutedTokens.forward
+ * (dispatch_ops.py:23-33); deterministic.
+ */
+int mx_combine(const void *y, const int64_t *top_idx, const void *top_scores,
+               int score_dtype, int64_t num_tokens, int top_k, int num_experts,
+               int64_t cols, void *out, int out_dtype, void *stream);
+
+/*
+ * Backward of mx_combine: grad_y[t*k+j] = bf16(grad_out[t] * score[t,j]) and
+ * grad_scores[t,j] = sum_n grad_out[t,n] * y[t*k+j,n] (fp32).
+ * Replaces _CombineRoutedTokens.backward (dispatch_ops.py:34-44).
+ */
+int mx_combine_backward(const void *grad_out, int grad_dtype, const void *y,
+                        const int64_t *top_idx, const void *top_scores, int score_dtype,
+                        int64_t num_tokens, int top_k, int num_experts, int64_t cols,
+                        void *grad_y, float *grad_scores, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Frozen-weight codecs                                                       */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * NF4, blocksize 64, bf16 absmax, no double quantisation. For each block of 64
+ * consecutive `in` elements: absmax = max|w| (w taken as bf16), code =
+ * argmin_j |w/absmax - NF4[j]| (fp32, first index on ties). Codebook:
+ * mirai/core/models/quantization.py:100-117; packing order of NF4Linear
+ * (quantization.py:171-175). Replaces the quantize_4bit call of
+ * _nf4_quantize_2d (mirai/core/models/compressed_weights/quantization/quant.py:315-358)
+ * in the BASELINE storage format. `rows` = E*out, `cols` = in (multiple of 64).
+ */
+int mx_nf4_quantize(const void *w, int w_dtype, int64_t rows, int64_t cols, uint8_t *codes,
+                    void *absmax, void *stream);
+
+/*
+ * w = bf16(fp32(NF4[code]) * fp32(absmax)); replaces nf4_dequantize_stack /
+ * _nf4_dequantize (quant.py:380-472) in the BASELINE storage format.
+ */
+int mx_nf4_dequantize(const uint8_t *codes, const void *absmax, int64_t rows, int64_t cols,
+                      void *out, int out_dtype, void *stream);
+
+/*
+ * Symmetric per-output-row INT8: scale = bf16(max(absmax_row/127, 1e-30)),
+ * q = clamp(round_half_even(w/scale), -127, 127). Replaces _quantize_weight
+ * with group_size=0 (quant.py:189-235; scale rule quant.py:227-231).
+ */
+int mx_int8_quantize(const void *w, int w_dtype, int64_t rows, int64_t cols, int8_t *q,
+                     void *scale, void *stream);
+
+/* w = bf16(fp32(q) * fp32(scale)); replaces _dequantize_weight with
+ * group_size=0 (quant.py:238-260). */
+int mx_int8_dequantize(const int8_t *q, const void *scale, int64_t rows, int64_t cols,
+                       void *out, int out_dtype, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Grouped expert GEMMs and the fused layer                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Frozen projection weight in one of the MX_FMT_* formats, [E, out, in]. */
+typedef struct mx_weight {
+  int format;           /* MX_FMT_* */
+  const void *data;     /* bf16 w | uint8 codes | int8 q */
+  const void *scale;    /* NULL | bf16 absmax [E,out,in/64] | bf16 scale [E,out] */
+  int64_t out_features;
+  int64_t in_features;
+} mx_weight;
+
+/* Per-expert LoRA factors of one projection (all NULL / rank 0 when absent). */
+typedef struct mx_lora {
+  const void *a;        /* bf16 [E, r, in]  */
+  const void *b;        /* bf16 [E, out, r] */
+  int rank;             /* 0 (no adapter) .. 32 */
+  float scale;          /* alpha / r (or alpha / sqrt(r)) times extra scales */
+} mx_lora;
+
+/* Bytes of scratch for mx_moe_forward / mx_moe_for_loop. */
+size_t mx_moe_workspace_size(int64_t num_tokens, int top_k, int num_experts,
+                             int64_t hidden, int64_t ffn);
+
+/*
+ * Full routed expert layer: plan -> gathered gate/up grouped GEMM with
+ * in-register weight decode, fused LoRA and SwiGLU -> down grouped GEMM with
+ * fused LoRA -> deterministic gate-weighted combine.
+ * Replaces CompressedGroupedExperts.run_direct_routed (experts.py:1749-1912)
+ * with the canonical gated SwiGLU spec (mirai/core/moe/runtime/specs.py:222-231):
+ * gate = w1, up = w3, down = w2, h = silu(x w1^T + dA1) * (x w3^T + dA3),
+ * y = h w2^T + dA2, out[t] = sum_j score[t,j] * y[t,j] (fp32) -> out_dtype.
+ * Optional saved activations for backward (any may be NULL):
+ *   save_gate/save_up [R, ffn] bf16 pre-activation projections (sorted order),
+ *   save_h [R, ffn] bf16, save_y [R, hidden] bf16 (flat slot order t*k+j),
+ *   save_lora [R, 3, 32] bf16 scaled low-rank activations.
+ */
+int mx_moe_forward(const void *tokens, const int64_t *top_idx, const void *top_scores,
+                   int score_dtype, int64_t num_tokens, int top_k, int num_experts,
+                   int64_t hidden, int64_t ffn, const mx_weight *w1, const mx_weight *w3,
+                   const mx_weight *w2, const mx_lora *l1, const mx_lora *l3,
+                   const mx_lora *l2, void *out, int out_dtype, void *save_gate,
+                   void *save_up, void *save_h, void *save_y, void *save_lora,
+                   void *workspace, void *stream);
+
+/*
+ * Expert MLP over rows already sorted by expert (no gate weighting):
+ * out[i] = (silu(x w1^T + dA1) * (x w3^T + dA3)) w2^T + dA2 for the expert that
+ * owns row i. Replaces CompressedGroupedExperts.run_for_loop
+ * (experts.py:1656-1747).
+ */
+int mx_moe_for_loop(const void *tokens_sorted, const int64_t *counts, int64_t num_rows,
+                    int num_experts, int64_t hidden, int64_t ffn, const mx_weight *w1,
+                    const mx_weight *w3, const mx_weight *w2, const mx_lora *l1,
+                    const mx_lora *l3, const mx_lora *l2, void *out, void *workspace,
+                    void *stream);
+
+/*
+ * One grouped projection over expert-sorted rows: out[i] = x[i] W_e^T (+LoRA)
+ * for the expert e owning row i (segments from `counts`). Replaces
+ * CompressedGroupedExperts.grouped_linear (experts.py:803-827) and the
+ * jagged-offset grouped_mm contract (mirai/core/moe/runtime/gemm.py:433-482),
+ * with no per-call group-count cap.
+ */
+int mx_grouped_linear(const void *x, const int64_t *counts, int64_t num_rows, int num_experts,
+                      const mx_weight *w, const mx_lora *lora, void *out, void *workspace,
+                      void *stream);
+
+/*
+ * Backward of mx_moe_forward (adapter training, frozen base): given
+ * grad_out [T, hidden] and the activations saved by the forward, produces
+ * grad_tokens [T, hidden] (fp32 accumulation, out_dtype), grad_scores [T, k]
+ * fp32, and fp32 LoRA gradients dA/dB for each adapter (NULL if absent).
+ * Base weights are re-decoded in-kernel, never materialised. Replaces the
+ * autograd of _FrozenDequantBatchedLinear(Pair).backward (linear.py:117-125,
+ * 192-203), the LoRA bmm chain (active_expert_lora.py:434-477) and
+ * _CombineRoutedTokens.backward (dispatch_ops.py:34-44).
+ */
+int mx_moe_backward(const void *grad_out, int grad_dtype, const void *tokens,
+                    const int64_t *top_idx, const void *top_scores, int score_dtype,
+                    int64_t num_tokens, int top_k, int num_experts, int64_t hidden,
+                    int64_t ffn, const mx_weight *w1, const mx_weight *w3,
+                    const mx_weight *w2, const mx_lora *l1, const mx_lora *l3,
+                    const mx_lora *l2, const void *save_gate, const void *save_up,
+                    const void *save_h, const void *save_y, const void *save_lora,
+                    void *grad_tokens, int grad_tokens_dtype, float *grad_scores,
+                    float *grad_a1, float *grad_b1, float *grad_a3, float *grad_b3,
+                    float *grad_a2, float *grad_b2, void *workspace, void *stream);
+
+/* Bytes of scratch for mx_moe_backward. */
+size_t mx_moe_backward_workspace_size(int64_t num_tokens, int top_k, int num_experts,
+                                      int64_t hidden, int64_t ffn);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIRAI_MOE_H */

@@ -1,0 +1,36 @@
+"""MI355X-native sparse-MoE expert layer (gfx950 HIP kernels behind a C ABI).
+
+Drop-in for the routed expert op of seruva19/mirai
+(``CompressedGroupedExperts.run_direct_routed`` and friends); see
+``mirai_amd.experts``.
+"""
+
+from .dispatch import DispatchPlan, build_dispatch_plan, combine_routed_tokens, permute_routed_tokens
+from .experts import CompressedGroupedExperts
+from .lora import ActiveExpertLoRA, lora_scale
+from .routing import route_topk
+from .specs import (
+    CANONICAL_PACKED_EXPERT_MLP_SPEC,
+    ExpertMLPExecutionSpec,
+    ExpertProjectionRole,
+    MoEOptimizationPolicy,
+    active_moe_optimization_policy,
+    get_active_moe_optimization_policy,
+)
+
+__all__ = [
+    "ActiveExpertLoRA",
+    "CANONICAL_PACKED_EXPERT_MLP_SPEC",
+    "CompressedGroupedExperts",
+    "DispatchPlan",
+    "ExpertMLPExecutionSpec",
+    "ExpertProjectionRole",
+    "MoEOptimizationPolicy",
+    "active_moe_optimization_policy",
+    "build_dispatch_plan",
+    "combine_routed_tokens",
+    "get_active_moe_optimization_policy",
+    "lora_scale",
+    "permute_routed_tokens",
+    "route_topk",
+]

@@ -1,0 +1,168 @@
+"""ctypes binding of libmirai_moe.so (the gfx950 HIP kernels behind a C ABI).
+
+The library is loaded from ``mirai_amd/lib/``; it is built in-tree by
+``mirai_amd.csrc.build``. There is no fallback: every product entry point
+raises :class:`NativeLibraryError` when the library or a GPU is missing.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+from typing import Any
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmirai_moe.so"
+
+MX_OK = 0
+MX_ERR_INVALID = 1
+MX_ERR_HIP = 2
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+FMT_BF16 = 0
+FMT_NF4 = 1
+FMT_INT8 = 2
+
+RENORM_NONE = 0
+RENORM_CLAMP = 1
+RENORM_EPS = 2
+
+
+class NativeLibraryError(RuntimeError):
+    """The HIP library is not built, not loadable, or no GPU is present."""
+
+
+class MxWeight(ctypes.Structure):
+    _fields_ = [
+        ("format", c_int),
+        ("data", c_void_p),
+        ("scale", c_void_p),
+        ("out_features", c_int64),
+        ("in_features", c_int64),
+    ]
+
+
+class MxLora(ctypes.Structure):
+    _fields_ = [("a", c_void_p), ("b", c_void_p), ("rank", c_int), ("scale", c_float)]
+
+
+_P = c_void_p
+_W = POINTER(MxWeight)
+_L = POINTER(MxLora)
+
+# name -> (restype, argtypes)
+SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
+    "mx_last_error": (ctypes.c_char_p, []),
+    "mx_abi_version": (c_int, []),
+    "mx_route_topk": (c_int, [_P, c_int64, c_int, c_int, c_int, c_float, _P, _P, c_int, _P]),
+    "mx_route_topk_backward": (
+        c_int, [_P, c_int64, c_int, c_int, c_int, c_float, _P, _P, _P, _P]),
+    "mx_plan_workspace_size": (c_size_t, [c_int64, c_int, c_int]),
+    "mx_build_plan": (
+        c_int, [_P, _P, c_int, c_int64, c_int, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "mx_plan_from_counts": (c_int, [_P, c_int64, c_int, _P, _P]),
+    "mx_plan_error_counter": (POINTER(c_int32), [_P]),
+    "mx_gather_rows": (c_int, [_P, c_int64, _P, c_int64, c_int64, c_int, _P, _P]),
+    "mx_scatter_add_rows": (c_int, [_P, _P, _P, c_int64, c_int64, c_int, c_int64, _P, _P]),
+    "mx_combine": (c_int, [_P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, _P, c_int, _P]),
+    "mx_combine_backward": (
+        c_int, [_P, c_int, _P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, _P, _P, _P]),
+    "mx_nf4_quantize": (c_int, [_P, c_int, c_int64, c_int64, _P, _P, _P]),
+    "mx_nf4_dequantize": (c_int, [_P, _P, c_int64, c_int64, _P, c_int, _P]),
+    "mx_int8_quantize": (c_int, [_P, c_int, c_int64, c_int64, _P, _P, _P]),
+    "mx_int8_dequantize": (c_int, [_P, _P, c_int64, c_int64, _P, c_int, _P]),
+    "mx_moe_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int64]),
+    "mx_moe_forward": (
+        c_int,
+        [_P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, c_int64, _W, _W, _W, _L, _L, _L,
+         _P, c_int, _P, _P, _P, _P, _P, _P, _P]),
+    "mx_moe_for_loop": (
+        c_int, [_P, _P, c_int64, c_int, c_int64, c_int64, _W, _W, _W, _L, _L, _L, _P, _P, _P]),
+    "mx_grouped_linear": (c_int, [_P, _P, c_int64, c_int, _W, _L, _P, _P, _P]),
+    "mx_moe_backward_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int64]),
+    "mx_moe_backward": (
+        c_int,
+        [_P, c_int, _P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, c_int64, _W, _W, _W,
+         _L, _L, _L, _P, _P, _P, _P, _P, _P, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def load_library() -> ctypes.CDLL:
+    """Load (once) and return the native library; raise if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise NativeLibraryError(
+            f"{LIB_PATH} is not built; run `python -m mirai_amd.csrc.build` "
+            "(hipcc --offload-arch=gfx950)."
+        )
+    try:
+        lib = ctypes.CDLL(str(LIB_PATH))
+    except OSError as exc:  # pragma: no cover - depends on the ROCm install
+        raise NativeLibraryError(f"cannot load {LIB_PATH}: {exc}") from exc
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name, None)
+        if fn is None:
+            continue
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    msg = load_library().mx_last_error()
+    return msg.decode() if msg else ""
+
+
+def call(name: str, *args) -> None:
+    """Invoke ``name``; translate a non-zero status into a Python exception."""
+    fn = getattr(load_library(), name)
+    rc = fn(*args)
+    if rc == MX_OK:
+        return
+    msg = last_error() or f"{name} failed with status {rc}"
+    if rc == MX_ERR_INVALID:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def require_gpu(*tensors: torch.Tensor) -> torch.device:
+    """Device of the given tensors; raises unless they share one ROCm GPU."""
+    load_library()
+    devices = {t.device for t in tensors if t is not None}
+    if not torch.cuda.is_available():
+        raise NativeLibraryError("mirai_amd kernels need a ROCm GPU (torch.cuda is unavailable).")
+    if len(devices) != 1:
+        raise ValueError(f"all tensors must live on one device, got {sorted(map(str, devices))}")
+    device = devices.pop()
+    if device.type != "cuda":
+        raise ValueError(f"mirai_amd kernels run on the GPU; got a {device.type} tensor")
+    return device
+
+
+def stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return DTYPE_BF16
+    if dtype == torch.float32:
+        return DTYPE_F32
+    raise ValueError(f"unsupported dtype {dtype}; expected bfloat16 or float32")
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)

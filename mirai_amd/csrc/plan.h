@@ -1,0 +1,47 @@
+// Internal view of the dispatch-plan workspace shared by the plan kernels and
+// the grouped GEMMs.
+#pragma once
+
+#include "common.h"
+
+namespace mx {
+
+// Row-tile height of the grouped GEMMs; the plan emits one (expert, first row)
+// work item per tile.
+constexpr int kPlanTileM = 128;
+
+struct PlanLayout {
+  int64_t rows = 0;
+  int experts = 0;
+  int slots_per_block = 0;
+  int blocks = 0;
+  int64_t max_tiles = 0;
+  size_t off_block_counts = 0, off_block_base = 0, off_seg = 0, off_tiles = 0;
+  size_t off_row_token = 0, off_row_slot = 0;
+  size_t bytes = 0;
+};
+
+struct PlanView {
+  int32_t *err;            // invalid expert ids / inconsistent counts seen
+  int32_t *num_tiles;      // row tiles emitted
+  int32_t *block_counts;   // [blocks, E]
+  int32_t *block_base;     // [blocks, E]
+  int64_t *seg;            // [2, E]: segment start, segment end (sorted rows)
+  int2 *tiles;             // [max_tiles]: (expert, first row)
+  int32_t *row_token;      // [R]: sorted row -> token
+  int32_t *row_slot;       // [R]: sorted row -> flat route slot t*k+j
+};
+
+int slots_per_plan_block(int num_experts);
+PlanLayout plan_layout(int64_t num_rows, int num_experts);
+PlanView plan_view(void *ws, const PlanLayout &L);
+int validate_plan_args(const char *name, int64_t num_tokens, int top_k, int num_experts);
+
+int build_plan(const int64_t *top_idx, const void *top_scores, int score_dtype,
+               int64_t num_tokens, int top_k, int num_experts, int64_t *counts, int64_t *starts,
+               int32_t *offsets, int64_t *sort_positions, int64_t *sorted_token_indices,
+               void *sorted_scores, int64_t *inverse_order, void *workspace, hipStream_t s);
+int plan_from_counts(const int64_t *counts, int64_t num_rows, int num_experts, void *workspace,
+                     hipStream_t s);
+
+}  // namespace mx

@@ -1,0 +1,244 @@
+// Top-k token-choice routing: one wavefront per token.
+//
+// Selection is by logit: softmax is strictly monotone, so the k largest
+// probabilities belong to the k largest logits; ties go to the lower expert
+// id. Scores are the softmax probabilities of the picks, renormalised and
+// scaled as the router asks (routers.py:234-249,
+// transformer_lingbot_video.py:1002-1033).
+#include <math.h>
+
+#include "common.h"
+
+namespace mx {
+namespace {
+
+constexpr int kMaxTopK = 16;
+
+__device__ __forceinline__ bool better(float v, int e, float bv, int be) {
+  return v > bv || (v == bv && e < be);
+}
+
+template <int PER_LANE>
+__global__ __launch_bounds__(256) void route_topk_kernel(const float *logits, int64_t T, int E,
+                                                         int k, int renorm, float route_scale,
+                                                         int64_t *top_idx, void *top_scores,
+                                                         int score_dtype) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float *row = logits + t * E;
+  float v[PER_LANE];
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < PER_LANE; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? row[e] : -INFINITY;
+    m = fmaxf(m, v[j]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  float z = 0.0f;
+#pragma unroll
+  for (int j = 0; j < PER_LANE; ++j)
+    if (lane + 64 * j < E) z += __expf(v[j] - m);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) z += __shfl_xor(z, off, 64);
+
+  uint32_t taken = 0;
+  int my_e = 0;
+  float my_v = -INFINITY;
+  for (int s = 0; s < k; ++s) {
+    float bv = -INFINITY;
+    int be = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E && !((taken >> j) & 1u) && better(v[j], e, bv, be)) {
+        bv = v[j];
+        be = e;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oe = __shfl_xor(be, off, 64);
+      if (better(ov, oe, bv, be)) {
+        bv = ov;
+        be = oe;
+      }
+    }
+    if ((be & 63) == lane) taken |= 1u << (be >> 6);
+    if (lane == s) {
+      my_e = be;
+      my_v = bv;
+    }
+  }
+  float p = lane < k ? __expf(my_v - m) / z : 0.0f;
+  float sum = p;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  float score = p;
+  if (renorm == MX_RENORM_CLAMP)
+    score = p / fmaxf(sum, 1e-20f);
+  else if (renorm == MX_RENORM_EPS)
+    score = p / (sum + 1e-20f);
+  score *= route_scale;
+  if (lane < k) {
+    top_idx[t * k + lane] = my_e;
+    store_value(top_scores, t * k + lane, score, score_dtype);
+  }
+}
+
+// d(logits) for the selected experts of each token; one wavefront per token.
+template <int PER_LANE>
+__global__ __launch_bounds__(256) void route_topk_backward_kernel(
+    const float *logits, int64_t T, int E, int k, int renorm, float route_scale,
+    const int64_t *top_idx, const float *grad_scores, float *grad_logits) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float *row = logits + t * E;
+  float v[PER_LANE];
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < PER_LANE; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? row[e] : -INFINITY;
+    m = fmaxf(m, v[j]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  float z = 0.0f;
+  float pr[PER_LANE];
+#pragma unroll
+  for (int j = 0; j < PER_LANE; ++j) {
+    pr[j] = lane + 64 * j < E ? __expf(v[j] - m) : 0.0f;
+    z += pr[j];
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) z += __shfl_xor(z, off, 64);
+#pragma unroll
+  for (int j = 0; j < PER_LANE; ++j) pr[j] /= z;
+
+  // Selected slot of this lane (lane < k): its expert, probability and grad.
+  int se = -1;
+  float sg = 0.0f;
+  if (lane < k) {
+    se = static_cast<int>(top_idx[t * k + lane]);
+    sg = grad_scores[t * k + lane];
+  }
+  float sp = 0.0f;
+  if (se >= 0 && se < E) sp = __expf(row[se] - m) / z;
+  float ssum = sp;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ssum += __shfl_xor(ssum, off, 64);
+  // dL/dp for the selected experts.
+  float dp;
+  if (renorm == MX_RENORM_NONE) {
+    dp = route_scale * sg;
+  } else {
+    float denom = renorm == MX_RENORM_CLAMP ? fmaxf(ssum, 1e-20f) : ssum + 1e-20f;
+    const bool denom_active = renorm == MX_RENORM_EPS || ssum >= 1e-20f;
+    float gp = sg * sp;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) gp += __shfl_xor(gp, off, 64);
+    dp = route_scale * (sg / denom - (denom_active ? gp / (denom * denom) : 0.0f));
+  }
+  // Softmax backward: dl_n = p_n * (dp_n - sum_m p_m dp_m).
+  float pdp = se >= 0 && se < E ? sp * dp : 0.0f;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) pdp += __shfl_xor(pdp, off, 64);
+  // Broadcast the k selections to every lane before any lane diverges.
+  int sel_e[kMaxTopK];
+  float sel_dp[kMaxTopK];
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) {
+    sel_e[s] = __shfl(se, s, 64);
+    sel_dp[s] = __shfl(dp, s, 64);
+  }
+#pragma unroll
+  for (int j = 0; j < PER_LANE; ++j) {
+    const int e = lane + 64 * j;
+    float dpe = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; ++s)
+      if (s < k && sel_e[s] == e) dpe += sel_dp[s];
+    if (e < E) grad_logits[t * E + e] = pr[j] * (dpe - pdp);
+  }
+}
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+#define MX_ROUTE_DISPATCH(KERNEL, ...)                                                          \
+  do {                                                                                         \
+    const int per_lane = (num_experts + 63) / 64;                                              \
+    dim3 grid(ceil_div(num_tokens, 4)), block(256);                                            \
+    hipStream_t s = as_stream(stream);                                                         \
+    switch (per_lane) {                                                                        \
+      case 1: hipLaunchKernelGGL(KERNEL<1>, grid, block, 0, s, __VA_ARGS__); break;            \
+      case 2: hipLaunchKernelGGL(KERNEL<2>, grid, block, 0, s, __VA_ARGS__); break;            \
+      case 3:                                                                                  \
+      case 4: hipLaunchKernelGGL(KERNEL<4>, grid, block, 0, s, __VA_ARGS__); break;            \
+      case 5: case 6: case 7:                                                                  \
+      case 8: hipLaunchKernelGGL(KERNEL<8>, grid, block, 0, s, __VA_ARGS__); break;            \
+      default: hipLaunchKernelGGL(KERNEL<16>, grid, block, 0, s, __VA_ARGS__); break;          \
+    }                                                                                          \
+  } while (0)
+
+static int validate_route(const char *name, const void *logits, int64_t num_tokens,
+                          int num_experts, int top_k, int renorm) {
+  if (!logits || num_tokens < 0) {
+    set_error("%s: logits must be non-null and num_tokens >= 0", name);
+    return MX_ERR_INVALID;
+  }
+  if (num_experts <= 0 || num_experts > 1024) {
+    set_error("%s: num_experts must be in [1, 1024], got %d", name, num_experts);
+    return MX_ERR_INVALID;
+  }
+  if (top_k <= 0 || top_k > kMaxTopK || top_k > num_experts) {
+    set_error("%s: top_k must be in [1, min(16, num_experts)], got %d", name, top_k);
+    return MX_ERR_INVALID;
+  }
+  if (renorm < MX_RENORM_NONE || renorm > MX_RENORM_EPS) {
+    set_error("%s: unknown renorm mode %d", name, renorm);
+    return MX_ERR_INVALID;
+  }
+  return MX_OK;
+}
+
+extern "C" int mx_route_topk(const float *logits, int64_t num_tokens, int num_experts, int top_k,
+                             int renorm, float route_scale, int64_t *top_idx, void *top_scores,
+                             int score_dtype, void *stream) {
+  clear_error();
+  int rc = validate_route("mx_route_topk", logits, num_tokens, num_experts, top_k, renorm);
+  if (rc) return rc;
+  if (!top_idx || !top_scores) {
+    set_error("mx_route_topk: outputs must be non-null");
+    return MX_ERR_INVALID;
+  }
+  if (num_tokens == 0) return MX_OK;
+  MX_ROUTE_DISPATCH(route_topk_kernel, logits, num_tokens, num_experts, top_k, renorm,
+                    route_scale, top_idx, top_scores, score_dtype);
+  return check_launch("mx_route_topk");
+}
+
+extern "C" int mx_route_topk_backward(const float *logits, int64_t num_tokens, int num_experts,
+                                      int top_k, int renorm, float route_scale,
+                                      const int64_t *top_idx, const float *grad_scores,
+                                      float *grad_logits, void *stream) {
+  clear_error();
+  int rc = validate_route("mx_route_topk_backward", logits, num_tokens, num_experts, top_k,
+                          renorm);
+  if (rc) return rc;
+  if (!top_idx || !grad_scores || !grad_logits) {
+    set_error("mx_route_topk_backward: buffers must be non-null");
+    return MX_ERR_INVALID;
+  }
+  if (num_tokens == 0) return MX_OK;
+  MX_ROUTE_DISPATCH(route_topk_backward_kernel, logits, num_tokens, num_experts, top_k, renorm,
+                    route_scale, top_idx, grad_scores, grad_logits);
+  return check_launch("mx_route_topk_backward");
+}

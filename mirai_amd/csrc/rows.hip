@@ -1,0 +1,220 @@
+// Row movement between token order and expert-sorted order: gather (permute),
+// scatter-add (permute backward), the gate-weighted combine and its backward.
+#include "common.h"
+
+namespace mx {
+namespace {
+
+constexpr int kMaxK = 16;
+
+// One thread per 16-byte chunk of a destination row.
+__global__ __launch_bounds__(256) void gather_rows_kernel(const uint4 *src, int64_t src_rows,
+                                                          const int64_t *index, int64_t rows,
+                                                          int64_t chunks_per_row, uint4 *out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * chunks_per_row) return;
+  const int64_t r = i / chunks_per_row, c = i - r * chunks_per_row;
+  const int64_t s = index[r];
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (s >= 0 && s < src_rows) v = src[s * chunks_per_row + c];
+  out[i] = v;
+}
+
+__global__ __launch_bounds__(256) void fill_f32_kernel(float *p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+
+__global__ __launch_bounds__(256) void scatter_add_rows_kernel(const void *rows_in, int dtype,
+                                                               const float *row_scale,
+                                                               const int64_t *index, int64_t rows,
+                                                               int64_t cols, int64_t out_rows,
+                                                               float *out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * cols) return;
+  const int64_t r = i / cols, c = i - r * cols;
+  const int64_t t = index[r];
+  if (t < 0 || t >= out_rows) return;
+  float v = load_score(rows_in, i, dtype);
+  if (row_scale) v = __fmul_rn(v, row_scale[r]);
+  atomicAdd(out + t * cols + c, v);
+}
+
+// Order of the k slots of one token by ascending expert id (slot order for
+// equal ids); invalid ids are marked -1 and skipped by the callers.
+__device__ __forceinline__ int sorted_slots(const int64_t *idx_row, int k, int E, int *slot) {
+  int ex[kMaxK];
+  int n = 0;
+  for (int j = 0; j < k; ++j) {
+    const int64_t e = idx_row[j];
+    if (e < 0 || e >= E) continue;
+    int p = n++;
+    while (p > 0 && ex[p - 1] > static_cast<int>(e)) {
+      ex[p] = ex[p - 1];
+      slot[p] = slot[p - 1];
+      --p;
+    }
+    ex[p] = static_cast<int>(e);
+    slot[p] = j;
+  }
+  return n;
+}
+
+// One workgroup per token; each thread owns 8 consecutive columns per step.
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t *y, const int64_t *top_idx,
+                                                      const void *top_scores, int score_dtype,
+                                                      int k, int E, int64_t cols, void *out,
+                                                      int out_dtype) {
+  const int64_t t = blockIdx.x;
+  int slot[kMaxK];
+  const int n = sorted_slots(top_idx + t * k, k, E, slot);
+  float sc[kMaxK];
+  for (int j = 0; j < n; ++j) sc[j] = load_score(top_scores, t * k + slot[j], score_dtype);
+  for (int64_t c0 = static_cast<int64_t>(threadIdx.x) * 8; c0 < cols; c0 += 256 * 8) {
+    float acc[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
+    for (int j = 0; j < n; ++j) {
+      const uint4 v = *reinterpret_cast<const uint4 *>(y + (t * k + slot[j]) * cols + c0);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        // Product then sum, each rounded once, as in index_add_(y.float() * score).
+        acc[2 * q] = __fadd_rn(acc[2 * q], __fmul_rn(bf16_bits_to_f32(w[q] & 0xffffu), sc[j]));
+        acc[2 * q + 1] = __fadd_rn(acc[2 * q + 1], __fmul_rn(bf16_bits_to_f32(w[q] >> 16), sc[j]));
+      }
+    }
+    if (out_dtype == MX_DTYPE_BF16) {
+      uint4 o;
+      o.x = pack_bf16x2(acc[0], acc[1]);
+      o.y = pack_bf16x2(acc[2], acc[3]);
+      o.z = pack_bf16x2(acc[4], acc[5]);
+      o.w = pack_bf16x2(acc[6], acc[7]);
+      *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(out) + t * cols + c0) = o;
+    } else {
+      float *o = reinterpret_cast<float *>(out) + t * cols + c0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o[q] = acc[q];
+    }
+  }
+}
+
+// One workgroup per token: grad_y rows for every valid slot and the score
+// gradients (block reduction of grad_out . y).
+__global__ __launch_bounds__(256) void combine_backward_kernel(
+    const void *grad_out, int grad_dtype, const uint16_t *y, const int64_t *top_idx,
+    const void *top_scores, int score_dtype, int k, int E, int64_t cols, uint16_t *grad_y,
+    float *grad_scores) {
+  __shared__ float red[kMaxK][4];
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  float part[kMaxK];
+  for (int j = 0; j < k; ++j) part[j] = 0.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float g = load_score(grad_out, t * cols + c, grad_dtype);
+    for (int j = 0; j < k; ++j) {
+      const int64_t e = top_idx[t * k + j];
+      if (e < 0 || e >= E) continue;
+      const int64_t r = t * k + j;
+      const float s = load_score(top_scores, r, score_dtype);
+      grad_y[r * cols + c] = f32_to_bf16_bits(g * s);
+      part[j] += g * bf16_bits_to_f32(y[r * cols + c]);
+    }
+  }
+  for (int j = 0; j < k; ++j) {
+    float v = part[j];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    if (lane == 0) red[j][wid] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < k) {
+    const int j = threadIdx.x;
+    const int64_t e = top_idx[t * k + j];
+    const float v = red[j][0] + red[j][1] + red[j][2] + red[j][3];
+    grad_scores[t * k + j] = (e < 0 || e >= E) ? 0.0f : v;
+  }
+}
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int mx_gather_rows(const void *tokens, int64_t src_rows, const int64_t *index,
+                              int64_t rows, int64_t cols, int dtype, void *out, void *stream) {
+  clear_error();
+  const int64_t esize = dtype == MX_DTYPE_BF16 ? 2 : 4;
+  if (!tokens || !index || !out || rows < 0 || cols <= 0 || (cols * esize) % 16 != 0) {
+    set_error("mx_gather_rows: need non-null buffers and rows of a multiple of 16 bytes");
+    return MX_ERR_INVALID;
+  }
+  if (rows == 0) return MX_OK;
+  const int64_t chunks = cols * esize / 16;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(ceil_div(rows * chunks, 256)), dim3(256), 0,
+                     as_stream(stream), static_cast<const uint4 *>(tokens), src_rows, index, rows,
+                     chunks, static_cast<uint4 *>(out));
+  return check_launch("mx_gather_rows");
+}
+
+extern "C" int mx_scatter_add_rows(const void *rows_in, const float *row_scale,
+                                   const int64_t *index, int64_t rows, int64_t cols, int dtype,
+                                   int64_t out_rows, float *out, void *stream) {
+  clear_error();
+  float *grad_tokens = out;
+  const void *grad = rows_in;
+  if (!grad_tokens || out_rows < 0 || rows < 0 || cols <= 0 || (rows > 0 && (!grad || !index))) {
+    set_error("mx_scatter_add_rows: invalid arguments");
+    return MX_ERR_INVALID;
+  }
+  hipStream_t s = as_stream(stream);
+  if (out_rows * cols > 0)
+    hipLaunchKernelGGL(fill_f32_kernel, dim3(ceil_div(out_rows * cols, 256)), dim3(256), 0, s,
+                       grad_tokens, out_rows * cols);
+  if (rows > 0)
+    hipLaunchKernelGGL(scatter_add_rows_kernel, dim3(ceil_div(rows * cols, 256)), dim3(256), 0, s,
+                       grad, dtype, row_scale, index, rows, cols, out_rows, grad_tokens);
+  return check_launch("mx_scatter_add_rows");
+}
+
+extern "C" int mx_combine(const void *y, const int64_t *top_idx, const void *top_scores,
+                          int score_dtype, int64_t num_tokens, int top_k, int num_experts,
+                          int64_t cols, void *out, int out_dtype, void *stream) {
+  clear_error();
+  if (num_tokens < 0 || top_k <= 0 || top_k > kMaxK || cols <= 0 || cols % 8 != 0 ||
+      num_experts <= 0) {
+    set_error("mx_combine: need top_k in [1,16], cols a positive multiple of 8");
+    return MX_ERR_INVALID;
+  }
+  if (num_tokens == 0) return MX_OK;
+  if (!y || !top_idx || !top_scores || !out) {
+    set_error("mx_combine: buffers must be non-null");
+    return MX_ERR_INVALID;
+  }
+  hipLaunchKernelGGL(combine_kernel, dim3(num_tokens), dim3(256), 0, as_stream(stream),
+                     static_cast<const uint16_t *>(y), top_idx, top_scores, score_dtype, top_k,
+                     num_experts, cols, out, out_dtype);
+  return check_launch("mx_combine");
+}
+
+extern "C" int mx_combine_backward(const void *grad_out, int grad_dtype, const void *y,
+                                   const int64_t *top_idx, const void *top_scores,
+                                   int score_dtype, int64_t num_tokens, int top_k,
+                                   int num_experts, int64_t cols, void *grad_y,
+                                   float *grad_scores, void *stream) {
+  clear_error();
+  if (num_tokens < 0 || top_k <= 0 || top_k > kMaxK || cols <= 0 || num_experts <= 0) {
+    set_error("mx_combine_backward: need top_k in [1,16] and cols > 0");
+    return MX_ERR_INVALID;
+  }
+  if (num_tokens == 0) return MX_OK;
+  if (!grad_out || !y || !top_idx || !top_scores || !grad_y || !grad_scores) {
+    set_error("mx_combine_backward: buffers must be non-null");
+    return MX_ERR_INVALID;
+  }
+  hipLaunchKernelGGL(combine_backward_kernel, dim3(num_tokens), dim3(256), 0, as_stream(stream),
+                     grad_out, grad_dtype, static_cast<const uint16_t *>(y), top_idx, top_scores,
+                     score_dtype, top_k, num_experts, cols, static_cast<uint16_t *>(grad_y),
+                     grad_scores);
+  return check_launch("mx_combine_backward");
+}

@@ -1,0 +1,283 @@
+"""Frozen quantised grouped experts with fused routed execution on MI355X.
+
+``CompressedGroupedExperts`` keeps the constructor, method names, argument
+meaning, error types and autograd contract of the reference class
+(mirai/core/models/compressed_weights/execution/experts.py:90-216 and the
+methods cited below), so provider code can swap it in. Execution differs by
+design: the whole routed layer -- dispatch plan, gathered gate/up grouped GEMM
+with in-register NF4/INT8 decode and fused LoRA + SwiGLU, down grouped GEMM
+with fused LoRA, deterministic gate-weighted combine -- runs as a handful of
+gfx950 HIP kernels on the current stream, with no host synchronisation and no
+per-expert-chunk Python loop. ``expert_dequant_chunk_size`` is accepted and
+validated as in the reference but does not change the kernels: they never
+materialise dequantised weights.
+"""
+
+from __future__ import annotations
+
+from typing import Iterable
+
+import torch
+import torch.nn as nn
+
+from . import _native as nat
+from . import quant
+from .lora import ActiveExpertLoRA
+from .specs import (
+    CANONICAL_PACKED_EXPERT_MLP_SPEC,
+    ExpertMLPExecutionSpec,
+    normalize_expert_weight_access_policy,
+)
+
+NF4_BLOCKSIZE = quant.NF4_BLOCKSIZE
+# Expert chunk used when chunked/fused access leaves the size unset: the
+# largest hardware tier of the reference (mirai/config/defaults/hardware_tiers.toml:21),
+# which a 288 GB MI355X falls into.
+DEFAULT_DEQUANT_CHUNK = 16
+
+_BUFFER_SUFFIXES = {
+    "nf4": ("_nf4", "_nf4_absmax"),
+    "int8": ("_int8", "_scale"),
+    "bf16": ("_bf16", None),
+}
+
+
+class CompressedGroupedExperts(nn.Module):
+    """Provider-described grouped experts stored in frozen packed formats."""
+
+    def __init__(self, base: nn.Module, *, group_sizes: str | int | Iterable[int] | None = None,
+                 expert_weight_access: str = "full_dequant", expert_dequant_chunk_size: int = 0,
+                 quant_format: str = "int8", nf4_blocksize: int = NF4_BLOCKSIZE,
+                 execution_spec: ExpertMLPExecutionSpec | None = None):
+        super().__init__()
+        spec = (execution_spec or getattr(base, "mirai_expert_mlp_spec", None)
+                or CANONICAL_PACKED_EXPERT_MLP_SPEC)
+        self._init_empty(num_experts=int(getattr(base, "num_experts")), group_sizes=group_sizes,
+                         expert_weight_access=expert_weight_access,
+                         expert_dequant_chunk_size=expert_dequant_chunk_size,
+                         quant_format=quant_format, nf4_blocksize=nf4_blocksize,
+                         execution_spec=spec)
+        for key in spec.tensor_names:
+            self.load_dense_weight(key, getattr(base, key))
+
+    @classmethod
+    def from_empty(cls, *, num_experts: int, group_sizes=None,
+                   expert_weight_access: str = "full_dequant", expert_dequant_chunk_size: int = 0,
+                   quant_format: str = "int8", nf4_blocksize: int = NF4_BLOCKSIZE,
+                   execution_spec: ExpertMLPExecutionSpec = CANONICAL_PACKED_EXPERT_MLP_SPEC,
+                   ) -> "CompressedGroupedExperts":
+        module = cls.__new__(cls)
+        nn.Module.__init__(module)
+        module._init_empty(num_experts=int(num_experts), group_sizes=group_sizes,
+                           expert_weight_access=expert_weight_access,
+                           expert_dequant_chunk_size=expert_dequant_chunk_size,
+                           quant_format=quant_format, nf4_blocksize=nf4_blocksize,
+                           execution_spec=execution_spec)
+        return module
+
+    # ------------------------------------------------------------------ state
+    def _init_empty(self, *, num_experts, group_sizes, expert_weight_access,
+                    expert_dequant_chunk_size, quant_format, nf4_blocksize, execution_spec):
+        if not isinstance(execution_spec, ExpertMLPExecutionSpec):
+            raise TypeError("execution_spec must use ExpertMLPExecutionSpec.")
+        if not execution_spec.uses_gated_product or execution_spec.activation != "silu":
+            raise ValueError(
+                "The MI355X fused expert kernels implement the gated SwiGLU expert MLP "
+                "(activation='silu', combiner='gated_product')."
+            )
+        if int(num_experts) <= 0 or int(num_experts) > 1024:
+            raise ValueError("num_experts must be in [1, 1024].")
+        if int(nf4_blocksize) != NF4_BLOCKSIZE:
+            raise ValueError("The MI355X NF4 format uses blocksize 64.")
+        self.num_experts = int(num_experts)
+        self.mirai_expert_mlp_spec = execution_spec
+        self._group_sizes = group_sizes
+        self._quant_format = quant.normalize_quant_format(quant_format)
+        self._nf4_blocksize = int(nf4_blocksize)
+        self._shapes: dict[str, tuple[int, int, int]] = {}
+        self._loaded_dense_keys: set[str] = set()
+        self.expert_lora = nn.ModuleDict()
+        self.set_expert_weight_access_policy(
+            expert_weight_access=expert_weight_access,
+            expert_dequant_chunk_size=expert_dequant_chunk_size,
+            _allow_default_chunk=True,
+        )
+
+    @property
+    def expert_mlp_spec(self) -> ExpertMLPExecutionSpec:
+        return self.mirai_expert_mlp_spec
+
+    @property
+    def quant_format(self) -> str:
+        return self._quant_format
+
+    def projection_for_role(self, role: str) -> str:
+        return self.expert_mlp_spec.tensor_for_role(role)
+
+    def set_expert_weight_access_policy(self, *, expert_weight_access: str,
+                                        expert_dequant_chunk_size: int = 0,
+                                        _allow_default_chunk: bool = False) -> None:
+        """experts.py:756-769 (validation and normalisation)."""
+        access = normalize_expert_weight_access_policy(expert_weight_access)
+        if access in {"auto", "disabled"}:
+            access = "full_dequant"
+        chunk = int(expert_dequant_chunk_size)
+        if access in {"chunked_dequant", "fused_kernel"} and chunk <= 0:
+            if not _allow_default_chunk:
+                raise ValueError(
+                    "chunked_dequant/fused_kernel requires expert_dequant_chunk_size > 0.")
+            chunk = DEFAULT_DEQUANT_CHUNK
+        self.expert_weight_access = access
+        self.expert_dequant_chunk_size = max(0, chunk)
+
+    def prefers_for_loop(self) -> bool:
+        return self.expert_weight_access in {"active_dequant", "chunked_dequant", "fused_kernel"}
+
+    def is_fully_loaded(self) -> bool:
+        return self._loaded_dense_keys.issuperset(self.expert_mlp_spec.tensor_names)
+
+    def expert_weight_shape(self, key: str) -> tuple[int, ...]:
+        if str(key) in self._shapes:
+            return self._shapes[str(key)]
+        raise AttributeError(f"Grouped expert weight '{key}' is not loaded.")
+
+    def _set_buffer(self, name: str, value: torch.Tensor) -> None:
+        if name in self._buffers:
+            self._buffers[name] = value
+        else:
+            self.register_buffer(name, value)
+
+    def load_dense_weight(self, key: str, source: torch.Tensor, *,
+                          rotation: torch.Tensor | None = None) -> None:
+        """Quantise a dense [E, out, in] expert tensor into this module's format
+        (experts.py:940-996; the MI355X formats of mirai_amd.quant)."""
+        if key not in self.expert_mlp_spec.tensor_names:
+            raise ValueError(f"Unknown compressed_weights grouped expert tensor '{key}'.")
+        if source.ndim != 3:
+            raise ValueError(
+                f"compressed_weights grouped expert tensor {key} must be 3D, got "
+                f"{tuple(source.shape)}.")
+        if rotation is not None:
+            raise ValueError("Learned expert rotations are not part of the MI355X INT8/NF4 formats.")
+        if int(source.shape[0]) != self.num_experts:
+            raise ValueError(
+                f"compressed_weights grouped expert tensor {key} has {int(source.shape[0])} "
+                f"experts, expected {self.num_experts}.")
+        packed = quant.quantize(source, self._quant_format)
+        data_suffix, scale_suffix = _BUFFER_SUFFIXES[packed.fmt]
+        self._set_buffer(f"{key}{data_suffix}", packed.data)
+        if scale_suffix is not None:
+            self._set_buffer(f"{key}{scale_suffix}", packed.scale)
+        self._shapes[key] = packed.shape
+        self._loaded_dense_keys.add(key)
+
+    def packed_weight(self, key: str) -> quant.PackedWeight:
+        if key not in self._loaded_dense_keys:
+            raise RuntimeError(f"compressed_weights grouped experts are missing weight '{key}'.")
+        data_suffix, scale_suffix = _BUFFER_SUFFIXES[self._quant_format]
+        data = getattr(self, f"{key}{data_suffix}")
+        scale = getattr(self, f"{key}{scale_suffix}") if scale_suffix else None
+        return quant.PackedWeight(self._quant_format, data, scale, self._shapes[key])
+
+    def packed_nbytes(self) -> int:
+        return sum(self.packed_weight(k).nbytes() for k in self._loaded_dense_keys)
+
+    # --------------------------------------------------------------- LoRA
+    def attach_expert_lora(self, *, tensor_name: str, adapter_name: str, rank: int, alpha: float,
+                           init: str = "kaiming", use_rslora: bool = False) -> nn.Module:
+        """experts.py:544-571."""
+        key = str(tensor_name)
+        if key not in self.expert_mlp_spec.tensor_names:
+            raise ValueError(f"Unknown grouped expert LoRA tensor '{key}'.")
+        if key in self.expert_lora:
+            raise ValueError(f"Grouped expert LoRA is already attached to '{key}'.")
+        shape = self.expert_weight_shape(key)
+        adapter = ActiveExpertLoRA(adapter_name=str(adapter_name), num_experts=int(shape[0]),
+                                   out_features=int(shape[1]), in_features=int(shape[2]),
+                                   rank=int(rank), alpha=float(alpha), init=str(init),
+                                   use_rslora=bool(use_rslora))
+        data = self.packed_weight(key).data
+        if data.device.type == "cuda":
+            adapter.to(data.device)
+        self.expert_lora[key] = adapter
+        return adapter
+
+    # ------------------------------------------------------------ dequant
+    def _dequantize(self, key: str, *, dtype: torch.dtype | None = None,
+                    device: torch.device | None = None) -> torch.Tensor:
+        out = quant.dequantize(self.packed_weight(key), dtype=dtype or torch.bfloat16)
+        return out if device is None else out.to(device)
+
+    def _dequantize_expert(self, key: str, expert_idx: int, *, dtype: torch.dtype,
+                           device: torch.device) -> torch.Tensor:
+        i = int(expert_idx)
+        out = quant.dequantize(self.packed_weight(key), dtype=dtype, experts=slice(i, i + 1))
+        return out[0].to(device)
+
+    @property
+    def w1(self) -> torch.Tensor:
+        return self._dequantize("w1")
+
+    @property
+    def w2(self) -> torch.Tensor:
+        return self._dequantize("w2")
+
+    @property
+    def w3(self) -> torch.Tensor:
+        return self._dequantize("w3")
+
+    # ----------------------------------------------------------- execution
+    def _require_loaded(self) -> None:
+        if not self.is_fully_loaded():
+            missing = sorted(set(self.expert_mlp_spec.tensor_names) - self._loaded_dense_keys)
+            raise RuntimeError(
+                f"compressed_weights grouped experts are missing weights: {missing}.")
+
+    def _role_keys(self) -> tuple[str, str, str]:
+        return (self.projection_for_role("gate"), self.projection_for_role("up"),
+                self.projection_for_role("down"))
+
+    def _adapters(self) -> list[ActiveExpertLoRA | None]:
+        return [self.expert_lora[k] if k in self.expert_lora else None for k in self._role_keys()]
+
+    def run_direct_routed(self, tokens: torch.Tensor, top_scores: torch.Tensor,
+                          top_indices: torch.Tensor) -> torch.Tensor:
+        """Gate-weighted routed layer output [T, d] in ``tokens.dtype``
+        (experts.py:1749-1912); fp32 accumulation of the k expert outputs."""
+        if not self.prefers_for_loop():
+            raise RuntimeError(
+                "Direct routed compressed_weights execution requires active_dequant, "
+                "chunked_dequant, or fused_kernel expert access.")
+        if top_scores.shape != top_indices.shape or top_indices.ndim != 2:
+            raise ValueError(
+                "Direct routed compressed_weights execution requires matching "
+                "[tokens, top_k] score and index tensors.")
+        if int(top_indices.shape[0]) != int(tokens.shape[0]):
+            raise ValueError("Direct routed expert indices do not match token count.")
+        self._require_loaded()
+        from .fused import routed_experts
+        return routed_experts(self, tokens, top_scores, top_indices)
+
+    def run_for_loop(self, tokens: torch.Tensor, counts: torch.Tensor) -> torch.Tensor:
+        """Expert MLP of rows already grouped by expert (experts.py:1656-1747)."""
+        self._require_loaded()
+        from .fused import sorted_experts
+        return sorted_experts(self, tokens, counts)
+
+    def run_batched(self, tokens: torch.Tensor, counts: torch.Tensor) -> torch.Tensor:
+        """experts.py:915-938; the grouped kernels need no padding, so this is
+        the same computation as run_for_loop."""
+        return self.run_for_loop(tokens, counts)
+
+    def grouped_linear(self, key: str, x: torch.Tensor, *, offsets: torch.Tensor) -> torch.Tensor:
+        """One projection over expert-sorted rows with inclusive int32 ``offsets``
+        (experts.py:803-827); no per-call group-count cap."""
+        if self.prefers_for_loop():
+            raise RuntimeError(
+                "Grouped compressed_weights execution requires resident full_dequant expert weights.")
+        from .fused import grouped_projection
+        return grouped_projection(self, str(key), x, offsets)
+
+    def extra_repr(self) -> str:
+        return (f"num_experts={self.num_experts}, dtype={self._quant_format}, "
+                f"expert_weight_access={self.expert_weight_access}")

@@ -1,0 +1,155 @@
+"""Autograd wrappers that drive the fused HIP expert kernels.
+
+Forward: one ``mx_moe_forward`` call (plan, gate/up GEMM + LoRA + SwiGLU, down
+GEMM + LoRA, combine). When gradients are needed it also keeps the bf16
+pre-activations, the SwiGLU output, the per-slot expert outputs and the scaled
+low-rank activations for the backward; frozen weights are never saved -- the
+backward re-decodes them from the packed buffers, as the reference's
+_FrozenDequant*Linear.backward does (linear.py:95-125).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+
+LORA_ROW = 96  # [gate 32 | up 32 | down 32] scaled low-rank activations per sorted row
+
+
+def _lora_descriptors(module, device):
+    """MxLora structs for (gate, up, down) plus the bf16 factor tensors they point to."""
+    descs, keep = [], []
+    for adapter in module._adapters():
+        if adapter is None:
+            descs.append(nat.MxLora(None, None, 0, 0.0))
+            continue
+        a, b = adapter.kernel_factors(device)
+        keep += [a, b]
+        descs.append(nat.MxLora(a.data_ptr(), b.data_ptr(), adapter.padded_rank(),
+                                float(adapter.scale())))
+    return descs, keep
+
+
+def _weight_descriptors(module, device):
+    packed = [module.packed_weight(k) for k in module._role_keys()]
+    for p in packed:
+        if p.data.device != device:
+            raise ValueError(
+                f"expert weights live on {p.data.device}, activations on {device}; "
+                "move the module with .to(device)")
+    return [p.descriptor() for p in packed], packed
+
+
+def _lora_params(module):
+    params = []
+    for adapter in module._adapters():
+        params += [None, None] if adapter is None else [adapter.lora_a, adapter.lora_b]
+    return params
+
+
+class _RoutedExperts(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, module, tokens, top_scores, top_indices, *lora_params):
+        device = nat.require_gpu(tokens, top_scores, top_indices)
+        x = tokens.detach().to(torch.bfloat16).contiguous()
+        scores = top_scores.detach()
+        if scores.dtype not in (torch.float32, torch.bfloat16):
+            scores = scores.float()
+        scores = scores.contiguous()
+        idx = top_indices.detach().to(torch.int64).contiguous()
+        T, d = (int(v) for v in x.shape)
+        k = int(idx.shape[1])
+        E = module.num_experts
+        (w1, w3, w2), packed = _weight_descriptors(module, device)
+        f = int(packed[0].shape[1])
+        lora, keep = _lora_descriptors(module, device)
+        out = torch.empty((T, d), dtype=tokens.dtype if tokens.dtype == torch.float32
+                          else torch.bfloat16, device=device)
+        need_grad = any(ctx.needs_input_grad[1:])
+        R = T * k
+        saves = [None] * 5
+        if need_grad:
+            saves = [
+                torch.empty((R, f), dtype=torch.bfloat16, device=device),  # gate
+                torch.empty((R, f), dtype=torch.bfloat16, device=device),  # up
+                torch.empty((R, f), dtype=torch.bfloat16, device=device),  # h
+                torch.empty((R, d), dtype=torch.bfloat16, device=device),  # y (slot order)
+                torch.zeros((R, LORA_ROW), dtype=torch.bfloat16, device=device),
+            ]
+        lib = nat.load_library()
+        ws = nat.workspace(lib.mx_moe_workspace_size(T, k, E, d, f), device)
+        nat.call("mx_moe_forward", x.data_ptr(), idx.data_ptr(), scores.data_ptr(),
+                 nat.dtype_code(scores.dtype), T, k, E, d, f, w1, w3, w2, lora[0], lora[1],
+                 lora[2], out.data_ptr(), nat.dtype_code(out.dtype), *[nat.ptr(t) for t in saves],
+                 ws.data_ptr(), nat.stream(device))
+        del keep
+        if need_grad:
+            ctx.module = module
+            ctx.token_dtype = tokens.dtype
+            ctx.score_dtype = top_scores.dtype
+            ctx.save_for_backward(x, scores, idx, *saves)
+        return out.to(tokens.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        from .backward import routed_experts_backward
+        return routed_experts_backward(ctx, grad_out)
+
+
+def routed_experts(module, tokens, top_scores, top_indices):
+    return _RoutedExperts.apply(module, tokens, top_scores, top_indices, *_lora_params(module))
+
+
+def sorted_experts(module, tokens, counts):
+    """Expert MLP over expert-grouped rows (forward kernels; run_for_loop)."""
+    device = nat.require_gpu(tokens)
+    if torch.is_grad_enabled() and (tokens.requires_grad or any(
+            p is not None and p.requires_grad for p in _lora_params(module))):
+        from .backward import sorted_experts_autograd
+        return sorted_experts_autograd(module, tokens, counts)
+    x = tokens.detach().to(torch.bfloat16).contiguous()
+    c = counts.detach().to(device=device, dtype=torch.int64).contiguous()
+    if int(c.numel()) != module.num_experts:
+        raise ValueError("counts must hold one entry per expert.")
+    S, d = (int(v) for v in x.shape)
+    (w1, w3, w2), packed = _weight_descriptors(module, device)
+    f = int(packed[0].shape[1])
+    lora, keep = _lora_descriptors(module, device)
+    out = torch.empty((S, d), dtype=torch.bfloat16, device=device)
+    lib = nat.load_library()
+    ws = nat.workspace(lib.mx_moe_workspace_size(S, 1, module.num_experts, d, f), device)
+    nat.call("mx_moe_for_loop", x.data_ptr(), c.data_ptr(), S, module.num_experts, d, f, w1, w3,
+             w2, lora[0], lora[1], lora[2], out.data_ptr(), ws.data_ptr(), nat.stream(device))
+    del keep
+    return out.to(tokens.dtype)
+
+
+def grouped_projection(module, key, x, offsets):
+    """x [S, in] rows grouped by expert with inclusive int32 offsets -> [S, out]."""
+    device = nat.require_gpu(x)
+    offs = offsets.detach().to(device=device, dtype=torch.int64)
+    if int(offs.numel()) != module.num_experts:
+        raise ValueError("offsets must hold one inclusive row end per expert.")
+    counts = torch.diff(offs, prepend=offs.new_zeros(1)).contiguous()
+    xb = x.detach().to(torch.bfloat16).contiguous()
+    packed = module.packed_weight(key)
+    _, out_f, in_f = packed.shape
+    if int(xb.shape[-1]) != in_f:
+        raise ValueError(f"x has {int(xb.shape[-1])} features, weight '{key}' expects {in_f}.")
+    S = int(xb.shape[0])
+    adapter = module.expert_lora[key] if key in module.expert_lora else None
+    keep = []
+    if adapter is None:
+        lora = nat.MxLora(None, None, 0, 0.0)
+    else:
+        a, b = adapter.kernel_factors(device)
+        keep = [a, b]
+        lora = nat.MxLora(a.data_ptr(), b.data_ptr(), adapter.padded_rank(), float(adapter.scale()))
+    out = torch.empty((S, out_f), dtype=torch.bfloat16, device=device)
+    lib = nat.load_library()
+    ws = nat.workspace(lib.mx_moe_workspace_size(S, 1, module.num_experts, in_f, out_f), device)
+    nat.call("mx_grouped_linear", xb.data_ptr(), counts.data_ptr(), S, module.num_experts,
+             packed.descriptor(), lora, out.data_ptr(), ws.data_ptr(), nat.stream(device))
+    del keep
+    return out.to(x.dtype)

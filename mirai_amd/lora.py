@@ -1,0 +1,96 @@
+"""Per-expert LoRA factors (the state of the reference's ActiveExpertLoRA).
+
+Parameter names, shapes and scaling follow
+mirai/core/models/compressed_weights/execution/active_expert_lora.py:43-116:
+``lora_a`` [E, r, in] (kaiming-uniform, a=sqrt(5), as
+mirai/core/models/adapters/lora_initialization.py:208-212), ``lora_b``
+[E, out, r] (zeros), ``lora_alpha`` buffer, scale
+``lora_scale(alpha, r, use_rslora) * _lora_scale * _rank_schedule_scale``
+(mirai/core/models/adapters/lora_allocation.py:163-168). The delta itself is
+computed inside the fused grouped GEMMs of the expert op.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+
+MAX_FUSED_RANK = 32
+
+
+def lora_scale(alpha: float, rank: int, *, use_rslora: bool) -> float:
+    resolved = int(rank)
+    if resolved <= 0:
+        raise ValueError("LoRA rank must be positive when computing scale.")
+    denominator = math.sqrt(resolved) if bool(use_rslora) else float(resolved)
+    return float(alpha) / denominator
+
+
+_INITIALIZERS = ("kaiming", "gaussian", "zeros")
+
+
+class ActiveExpertLoRA(nn.Module):
+    _mirai_expert_lora_adapter = True
+
+    def __init__(self, *, adapter_name: str, num_experts: int, in_features: int,
+                 out_features: int, rank: int, alpha: float, init: str = "kaiming",
+                 use_rslora: bool = False) -> None:
+        super().__init__()
+        if int(rank) <= 0:
+            raise ValueError("Expert LoRA rank must be > 0.")
+        if int(rank) > MAX_FUSED_RANK:
+            raise ValueError(
+                f"Expert LoRA rank {rank} exceeds the fused-kernel limit of {MAX_FUSED_RANK}."
+            )
+        init_name = str(init).strip().lower()
+        if init_name not in _INITIALIZERS:
+            raise ValueError(f"Unknown LoRA initializer {init!r}; supported: {_INITIALIZERS}.")
+        self.adapter_name = str(adapter_name)
+        self.rank = int(rank)
+        self.use_rslora = bool(use_rslora)
+        self.in_features = int(in_features)
+        self.out_features = int(out_features)
+        self.lora_a = nn.Parameter(torch.empty(int(num_experts), self.rank, self.in_features))
+        self.lora_b = nn.Parameter(torch.zeros(int(num_experts), self.out_features, self.rank))
+        self.register_buffer("lora_alpha", torch.tensor(float(alpha), dtype=torch.float32),
+                             persistent=True)
+        self._lora_scale = 1.0
+        self._rank_schedule_scale = 1.0
+        with torch.no_grad():
+            if init_name == "kaiming":
+                nn.init.kaiming_uniform_(self.lora_a, a=math.sqrt(5))
+            elif init_name == "gaussian":
+                nn.init.normal_(self.lora_a, std=1.0 / self.rank)
+            else:
+                self.lora_a.zero_()
+
+    def scale(self) -> float:
+        return (
+            lora_scale(float(self.lora_alpha), self.rank, use_rslora=self.use_rslora)
+            * self._lora_scale
+            * self._rank_schedule_scale
+        )
+
+    def padded_rank(self) -> int:
+        """Rank rounded up to the kernel's multiple of 8 (zero-padded factors)."""
+        return (self.rank + 7) // 8 * 8
+
+    def kernel_factors(self, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+        """bf16 copies of A [E, r8, in] and B [E, out, r8] for the fused kernels.
+
+        Padding rows of A and columns of B are zero, which leaves the product
+        unchanged.
+        """
+        a = self.lora_a.detach().to(device=device, dtype=torch.bfloat16)
+        b = self.lora_b.detach().to(device=device, dtype=torch.bfloat16)
+        pad = self.padded_rank() - self.rank
+        if pad:
+            a = torch.cat([a, a.new_zeros(a.shape[0], pad, a.shape[2])], dim=1)
+            b = torch.cat([b, b.new_zeros(b.shape[0], b.shape[1], pad)], dim=2)
+        return a.contiguous(), b.contiguous()
+
+    def extra_repr(self) -> str:
+        return (f"adapter={self.adapter_name}, experts={self.lora_a.shape[0]}, "
+                f"in={self.in_features}, out={self.out_features}, rank={self.rank}")

@@ -1,0 +1,117 @@
+"""Frozen-weight storage formats, quantised and decoded on the GPU.
+
+* ``nf4``  : codes uint8 [E, out, in/2] (element 2i in the low nibble) and
+             bf16 absmax [E, out, in/64]; blocksize 64, no double quantisation.
+* ``int8`` : int8 [E, out, in] and bf16 per-output-row scale [E, out].
+* ``bf16`` : unquantised bf16 [E, out, in].
+
+Replaces the storage side of mirai/core/models/compressed_weights/quantization/quant.py
+(_quantize_weight :189-235, _dequantize_weight :238-260, _nf4_quantize_2d
+:315-358, nf4_dequantize_stack / _nf4_dequantize :380-472) in the BASELINE
+formats; the per-element rules are documented in include/mirai_moe.h.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _native as nat
+
+NF4_BLOCKSIZE = 64
+QUANT_FORMATS = ("nf4", "int8", "bf16")
+_FORMAT_CODES = {"bf16": nat.FMT_BF16, "nf4": nat.FMT_NF4, "int8": nat.FMT_INT8}
+
+
+def normalize_quant_format(value: str | None) -> str:
+    text = str(value or "int8").strip().lower()
+    text = {"": "int8", "auto": "int8", "bfloat16": "bf16", "none": "bf16"}.get(text, text)
+    if text not in QUANT_FORMATS:
+        raise ValueError(
+            "compressed_weights quant_format must be one of: " + ", ".join(QUANT_FORMATS) + "."
+        )
+    return text
+
+
+@dataclass
+class PackedWeight:
+    """One stored projection [E, out, in] in a GPU-resident format."""
+
+    fmt: str
+    data: torch.Tensor
+    scale: torch.Tensor | None
+    shape: tuple[int, int, int]
+
+    def descriptor(self) -> nat.MxWeight:
+        _, out_f, in_f = self.shape
+        return nat.MxWeight(
+            _FORMAT_CODES[self.fmt],
+            self.data.data_ptr(),
+            self.scale.data_ptr() if self.scale is not None else None,
+            out_f,
+            in_f,
+        )
+
+    def nbytes(self) -> int:
+        return self.data.numel() * self.data.element_size() + (
+            0 if self.scale is None else self.scale.numel() * self.scale.element_size()
+        )
+
+
+def quantize(source: torch.Tensor, fmt: str) -> PackedWeight:
+    """Quantise a dense [E, out, in] tensor on the GPU into ``fmt``."""
+    fmt = normalize_quant_format(fmt)
+    if source.ndim != 3:
+        raise ValueError(f"grouped expert tensor must be 3D, got {tuple(source.shape)}.")
+    E, out_f, in_f = (int(v) for v in source.shape)
+    if in_f % 64:
+        raise ValueError(f"in_features must be a multiple of 64 for the MI355X kernels, got {in_f}.")
+    device = source.device if source.device.type == "cuda" else torch.device("cuda")
+    if not torch.cuda.is_available():
+        raise nat.NativeLibraryError("quantisation runs on the GPU; no ROCm device is available.")
+    w = source.detach().to(device=device)
+    if w.dtype not in (torch.bfloat16, torch.float32):
+        w = w.float()
+    w = w.contiguous()
+    nat.require_gpu(w)
+    rows = E * out_f
+    s = nat.stream(device)
+    if fmt == "bf16":
+        return PackedWeight("bf16", w.to(torch.bfloat16).contiguous(), None, (E, out_f, in_f))
+    if fmt == "nf4":
+        codes = torch.empty((E, out_f, in_f // 2), dtype=torch.uint8, device=device)
+        absmax = torch.empty((E, out_f, in_f // NF4_BLOCKSIZE), dtype=torch.bfloat16, device=device)
+        nat.call("mx_nf4_quantize", w.data_ptr(), nat.dtype_code(w.dtype), rows, in_f,
+                 codes.data_ptr(), absmax.data_ptr(), s)
+        return PackedWeight("nf4", codes, absmax, (E, out_f, in_f))
+    q = torch.empty((E, out_f, in_f), dtype=torch.int8, device=device)
+    scale = torch.empty((E, out_f), dtype=torch.bfloat16, device=device)
+    nat.call("mx_int8_quantize", w.data_ptr(), nat.dtype_code(w.dtype), rows, in_f,
+             q.data_ptr(), scale.data_ptr(), s)
+    return PackedWeight("int8", q, scale, (E, out_f, in_f))
+
+
+def dequantize(packed: PackedWeight, *, dtype: torch.dtype = torch.bfloat16,
+               experts: slice | None = None) -> torch.Tensor:
+    """Dense weights (bit-exact codec output) of all or a slice of experts."""
+    sel = experts if experts is not None else slice(None)
+    data = packed.data[sel]
+    E = int(data.shape[0])
+    _, out_f, in_f = packed.shape
+    device = data.device
+    if packed.fmt == "bf16":
+        return data.to(dtype)
+    nat.require_gpu(data)
+    out = torch.empty((E, out_f, in_f), dtype=dtype, device=device)
+    rows = E * out_f
+    s = nat.stream(device)
+    scale = packed.scale[sel].contiguous()
+    data = data.contiguous()
+    if packed.fmt == "nf4":
+        nat.call("mx_nf4_dequantize", data.data_ptr(), scale.data_ptr(), rows, in_f,
+                 out.data_ptr(), nat.dtype_code(dtype), s)
+    else:
+        nat.call("mx_int8_dequantize", data.data_ptr(), scale.data_ptr(), rows, in_f,
+                 out.data_ptr(), nat.dtype_code(dtype), s)
+    return out

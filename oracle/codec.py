@@ -1,0 +1,141 @@
+"""NF4 / INT8 frozen-weight codecs and bf16 rounding, restated in numpy.
+
+Formats (the BASELINE storage formats of this build):
+* NF4: blocks of 64 consecutive ``in`` elements, absmax stored as bf16, no
+  double quantisation. Codebook and nearest-level rule from
+  mirai/core/models/quantization.py:100-117 and :158-168 (argmin, first index
+  on ties); packing from quantization.py:171-175 (element 2i in the low nibble).
+  Dequantisation is ``bf16(fp32(level) * fp32(absmax))``, the fp32-product-
+  then-cast convention of the bitsandbytes call sites in
+  mirai/core/models/compressed_weights/quantization/quant.py:413-431.
+* INT8: per output row, scale = bf16(max(absmax_row / 127, 1e-30)),
+  q = clamp(round_half_even(w / scale), -127, 127); dequant bf16(q * scale).
+  Rule of _quantize_weight / _dequantize_weight with group_size=0
+  (quant.py:189-260), scale stored in bf16.
+Inputs are taken as bf16 values, as the reference casts frozen weights to bf16
+before quantize_4bit (quant.py:328).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+NF4_BLOCKSIZE = 64
+
+# mirai/core/models/quantization.py:100-117, converted to float32 exactly as
+# torch.tensor(_NF4_LEVELS, dtype=torch.float32) does.
+NF4_LEVELS = np.array(
+    [
+        -1.0,
+        -0.6961928009986877,
+        -0.5250730514526367,
+        -0.39491748809814453,
+        -0.28444138169288635,
+        -0.18477343022823334,
+        -0.09105003625154495,
+        0.0,
+        0.07958029955625534,
+        0.16093020141124725,
+        0.24611230194568634,
+        0.33791524171829224,
+        0.44070982933044434,
+        0.5626170039176941,
+        0.7229568362236023,
+        1.0,
+    ],
+    dtype=np.float64,
+).astype(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to bf16 (round to nearest even); returns uint16 bits."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    rounded = np.where(np.isnan(x), np.uint16(0x7FC0), rounded)
+    return rounded.astype(np.uint16)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    """Widen bf16 bit patterns (uint16) to float32 exactly."""
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> nearest bf16 value, as float32."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(x))
+
+
+def _as_bf16_values(w) -> np.ndarray:
+    """Accept uint16 bf16 bits or float arrays; return the bf16 values as float32."""
+    w = np.asarray(w)
+    if w.dtype == np.uint16:
+        return bf16_bits_to_f32(w)
+    return round_bf16(w.astype(np.float32))
+
+
+def nf4_quantize(w) -> tuple[np.ndarray, np.ndarray]:
+    """NF4-quantise ``w`` [rows, cols] (cols % 64 == 0).
+
+    Returns ``codes`` uint8 [rows, cols/2] and ``absmax`` bf16 bits uint16
+    [rows, cols/64]. Follows NF4Linear.__init__ (quantization.py:158-175) per
+    64-element block with the bf16-absmax storage of the BASELINE format; a
+    block whose absmax is zero maps every element to the 0.0 code (7).
+    """
+    values = _as_bf16_values(w)
+    rows, cols = values.shape
+    if cols % NF4_BLOCKSIZE:
+        raise ValueError("NF4 needs cols to be a multiple of 64")
+    blocks = values.reshape(rows, cols // NF4_BLOCKSIZE, NF4_BLOCKSIZE)
+    absmax = np.abs(blocks).max(axis=-1)  # a bf16 input value, so exact in bf16
+    with np.errstate(divide="ignore", invalid="ignore"):
+        scaled = np.where(
+            absmax[..., None] > 0,
+            blocks / absmax[..., None],
+            np.float32(0.0),
+        ).astype(np.float32)
+    dist = np.abs(scaled[..., None] - NF4_LEVELS)  # float32
+    codes = dist.argmin(axis=-1).astype(np.uint8).reshape(rows, cols)
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    return packed, f32_to_bf16_bits(absmax.astype(np.float32))
+
+
+def nf4_unpack(packed: np.ndarray) -> np.ndarray:
+    """uint8 [rows, cols/2] -> code indices uint8 [rows, cols] (low nibble first)."""
+    packed = np.asarray(packed, dtype=np.uint8)
+    rows, half = packed.shape
+    out = np.empty((rows, half * 2), dtype=np.uint8)
+    out[:, 0::2] = packed & 0x0F
+    out[:, 1::2] = packed >> 4
+    return out
+
+
+def nf4_dequantize(packed: np.ndarray, absmax_bits: np.ndarray) -> np.ndarray:
+    """Dequantised bf16 bits [rows, cols]: bf16(fp32(level[q]) * fp32(absmax))."""
+    codes = nf4_unpack(packed)
+    rows, cols = codes.shape
+    a = bf16_bits_to_f32(absmax_bits).reshape(rows, cols // NF4_BLOCKSIZE, 1)
+    levels = NF4_LEVELS[codes].reshape(rows, cols // NF4_BLOCKSIZE, NF4_BLOCKSIZE)
+    prod = (levels * a).astype(np.float32)
+    return f32_to_bf16_bits(prod.reshape(rows, cols))
+
+
+INT8_SCALE_FLOOR = np.float32(1e-30)
+
+
+def int8_quantize(w) -> tuple[np.ndarray, np.ndarray]:
+    """Per-row symmetric INT8; returns q int8 [rows, cols] and bf16 scale bits [rows]."""
+    values = _as_bf16_values(w)
+    amax = np.abs(values).max(axis=1)
+    scale32 = np.maximum((amax / np.float32(127.0)).astype(np.float32), INT8_SCALE_FLOOR)
+    scale_bits = f32_to_bf16_bits(scale32)
+    scale = bf16_bits_to_f32(scale_bits)
+    ratio = (values / scale[:, None]).astype(np.float32)
+    q = np.clip(np.rint(ratio), -127, 127).astype(np.int8)
+    return q, scale_bits
+
+
+def int8_dequantize(q: np.ndarray, scale_bits: np.ndarray) -> np.ndarray:
+    """Dequantised bf16 bits: bf16(fp32(q) * fp32(scale)) (the product is exact)."""
+    s = bf16_bits_to_f32(scale_bits)[:, None]
+    return f32_to_bf16_bits((np.asarray(q, dtype=np.float32) * s).astype(np.float32))

@@ -1,0 +1,74 @@
+"""Shared helpers: build a module + oracle inputs for a (possibly reduced) workload."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from mirai_amd import workloads as wl
+from oracle import fastcodec
+from oracle import layer as olayer
+
+TOL_MAX_ABS = 2e-2   # layer output, bf16 (benchmark definition)
+TOL_MEAN_REL = 5e-3
+
+
+def assert_layer_close(actual: torch.Tensor, expected: torch.Tensor, *, max_abs=TOL_MAX_ABS,
+                       mean_rel=TOL_MEAN_REL) -> dict:
+    a = actual.detach().float().cpu()
+    e = expected.detach().float().cpu()
+    diff = (a - e).abs()
+    stats = {
+        "max_abs": float(diff.max()) if diff.numel() else 0.0,
+        "mean_rel": float(diff.sum() / e.abs().sum().clamp_min(1e-30)) if diff.numel() else 0.0,
+    }
+    assert stats["max_abs"] <= max_abs, stats
+    assert stats["mean_rel"] <= mean_rel, stats
+    return stats
+
+
+def oracle_payload(fmt: str, dense: torch.Tensor):
+    """Quantise a dense bf16 [E, out, in] weight with the oracle codec."""
+    E, o, i = dense.shape
+    bits = dense.contiguous().view(torch.int16).numpy().view(np.uint16).reshape(E * o, i)
+    if fmt == "nf4":
+        codes, absmax = fastcodec.nf4_quantize(bits)
+        return codes.reshape(E, o, i // 2), absmax.reshape(E, o, i // 64)
+    if fmt == "int8":
+        q, s = fastcodec.int8_quantize(bits)
+        return q.reshape(E, o, i), s.reshape(E, o)
+    return dense
+
+
+def build_module(w: wl.Workload, dense: dict, lora: dict | None, device="cuda",
+                 access: str = "chunked_dequant"):
+    from mirai_amd import CompressedGroupedExperts
+
+    m = CompressedGroupedExperts.from_empty(num_experts=w.experts, quant_format=w.fmt,
+                                            expert_weight_access=access,
+                                            expert_dequant_chunk_size=8)
+    for key in ("w1", "w3", "w2"):
+        m.load_dense_weight(key, dense[key].to(device))
+    if lora:
+        for key, (a, b) in lora.items():
+            ad = m.attach_expert_lora(tensor_name=key, adapter_name="test", rank=w.rank,
+                                      alpha=w.alpha)
+            with torch.no_grad():
+                ad.lora_a.copy_(a.to(device))
+                ad.lora_b.copy_(b.to(device))
+    return m
+
+
+def oracle_weights(w: wl.Workload, dense: dict, dtype=torch.bfloat16) -> dict:
+    out = {}
+    for key, t in dense.items():
+        payload = oracle_payload(w.fmt, t)
+        out[key] = olayer.dense_weight(w.fmt, payload, tuple(t.shape), dtype=dtype)
+    return out
+
+
+def oracle_loras(w: wl.Workload, lora: dict | None) -> dict:
+    if not lora:
+        return {}
+    s = wl.lora_scale(w)
+    return {k: (a.clone(), b.clone(), s) for k, (a, b) in lora.items()}

@@ -1,0 +1,113 @@
+"""GPU layer parity: the fused routed expert op vs the reference-order oracle.
+
+Tolerance (benchmark definition): max-abs 2e-2 and mean-relative 5e-3 on the
+bf16 layer output versus the oracle's fp32-accumulated reference path.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from mirai_amd import route_topk
+from mirai_amd import workloads as wl
+from oracle import layer as olayer
+from oracle import routing as oroute
+
+from helpers import assert_layer_close, build_module, oracle_loras, oracle_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def small(fmt, *, T=256, d=256, f=192, E=8, k=2, r=16, alpha=16.0, dtype=torch.bfloat16):
+    return wl.Workload(f"small_{fmt}", 7, T, d, f, E, k, r, alpha, fmt, dtype)
+
+
+def _run_case(w: wl.Workload, *, with_lora=True, token_subset=None):
+    dense = wl.dense_weights(w)
+    lora = wl.lora_factors(w) if with_lora else None
+    x = wl.tokens(w)
+    logits = wl.router_logits(w)
+    idx_np, scores_np = oroute.route_topk(logits.numpy(), w.top_k)
+    idx, scores = torch.from_numpy(idx_np), torch.from_numpy(scores_np)
+    m = build_module(w, dense, lora)
+    with torch.no_grad():
+        out = m.run_direct_routed(x.cuda(), scores.cuda(), idx.cuda())
+    assert out.dtype == x.dtype and tuple(out.shape) == tuple(x.shape)
+    rows = torch.arange(w.tokens) if token_subset is None else token_subset
+    ref = olayer.layer_forward(x[rows], scores[rows], idx[rows],
+                               oracle_weights(w, dense, dtype=w.dtype), oracle_loras(w, lora),
+                               w.experts)
+    stats = assert_layer_close(out.cpu()[rows], ref)
+    print(f"parity {w.name}: {stats}")
+    return stats
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "nf4", "int8"])
+@pytest.mark.parametrize("with_lora", [False, True])
+def test_small_layer_matches_oracle(fmt, with_lora):
+    _run_case(small(fmt), with_lora=with_lora)
+
+
+@pytest.mark.parametrize("r", [8, 24, 32])
+def test_lora_ranks(r):
+    _run_case(small("nf4", r=r, alpha=2.0 * r, E=5, k=3, T=300, f=320, d=192))
+
+
+def test_ragged_and_empty_experts():
+    # Few tokens over many experts: most experts get 0-2 rows, many tiles are partial.
+    _run_case(small("int8", T=37, E=64, k=4, d=128, f=128))
+
+
+@pytest.mark.xfail(strict=True, reason=(
+    "fp32 tokens and fp32 weights run on bf16 MFMA; versus the fp32 reference the "
+    "mean-relative error is ~5.4e-3, above the 5e-3 bound (split-precision path pending)"))
+def test_fp32_tokens_c1_plumbing():
+    w = wl.WORKLOADS["c1"]
+    _run_case(w)
+
+
+def test_c2_full_size_on_token_subset():
+    w = wl.WORKLOADS["c2"]
+    subset = torch.arange(0, w.tokens, 16)
+    _run_case(w, token_subset=subset)
+
+
+def test_run_for_loop_matches_oracle():
+    w = small("nf4", T=200, E=6, k=1)
+    dense = wl.dense_weights(w)
+    lora = wl.lora_factors(w)
+    m = build_module(w, dense, lora)
+    counts = torch.tensor([50, 0, 70, 1, 79, 0])
+    x = wl.tokens(w)
+    with torch.no_grad():
+        out = m.run_for_loop(x.cuda(), counts.cuda())
+    ref = olayer.for_loop_forward(x, counts, oracle_weights(w, dense), oracle_loras(w, lora))
+    assert_layer_close(out.cpu(), ref)
+
+
+def test_grouped_linear_matches_oracle():
+    w = small("int8", T=150, E=4, k=1, d=256, f=320)
+    dense = wl.dense_weights(w)
+    lora = wl.lora_factors(w)
+    m = build_module(w, dense, lora, access="full_dequant")
+    counts = torch.tensor([40, 60, 0, 50])
+    offsets = counts.cumsum(0).to(torch.int32)
+    x = wl.tokens(w)
+    with torch.no_grad():
+        out = m.grouped_linear("w1", x.cuda(), offsets=offsets.cuda())
+    ref = olayer.grouped_linear(x, counts, oracle_weights(w, dense)["w1"],
+                                oracle_loras(w, lora)["w1"])
+    assert_layer_close(out.cpu(), ref)
+
+
+def test_routed_layer_is_deterministic():
+    w = small("nf4", T=512, E=16, k=4)
+    dense = wl.dense_weights(w)
+    m = build_module(w, dense, wl.lora_factors(w))
+    x = wl.tokens(w).cuda()
+    idx, scores = route_topk(wl.router_logits(w).cuda(), w.top_k)
+    with torch.no_grad():
+        a = m.run_direct_routed(x, scores, idx)
+        b = m.run_direct_routed(x, scores, idx)
+    assert torch.equal(a, b)
+    np.testing.assert_array_equal(a.float().cpu().numpy(), b.float().cpu().numpy())
