@@ -1,0 +1,283 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X routed expert layer (one GPU).
+
+A step is one pass of the hot path over one batch: fp32 router logits in ->
+softmax top-k routing -> dispatch plan -> gathered gate/up grouped GEMM (NF4
+decode, LoRA, SwiGLU) -> down grouped GEMM (LoRA) -> gate-weighted combine ->
+[T, d] bf16 out. Inputs are seeded synthetic tensors already resident in HBM
+when the timed region starts. Default workload: the C2 geometry (NF4, E=64,
+top-4, d=2048, ffn=1408, LoRA r=16) at T=32768 tokens.
+
+Prints one JSON line. ``value`` is routed tokens/s (T*k / step time).
+``roofline`` describes the dominant kernel (the gate/up grouped GEMM) from HIP
+events recorded on the library's stream around that kernel; ``cpu_baseline``
+times the oracle's restatement of the reference CPU expert path on a bounded
+token sample on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+STAGES = ("plan", "lora_down_gate_up", "gate_up_gemm", "lora_down_down", "down_gemm", "combine")
+
+
+def _parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="target",
+                    help="workload key: target (default), c2, c3, c4")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="approximate CPU time budget of the baseline sample")
+    return ap.parse_args()
+
+
+def _build_module(w, device):
+    import torch
+
+    from mirai_amd import CompressedGroupedExperts
+    from mirai_amd import workloads as wl
+
+    m = CompressedGroupedExperts.from_empty(num_experts=w.experts, quant_format=w.fmt,
+                                            expert_weight_access="fused_kernel",
+                                            expert_dequant_chunk_size=16)
+    dense = wl.dense_weights(w, device=device)
+    for key in ("w1", "w3", "w2"):
+        m.load_dense_weight(key, dense[key])
+    del dense
+    for key, (a, b) in wl.lora_factors(w, device=device).items():
+        ad = m.attach_expert_lora(tensor_name=key, adapter_name="bench", rank=w.rank,
+                                  alpha=w.alpha)
+        with torch.no_grad():
+            ad.lora_a.copy_(a)
+            ad.lora_b.copy_(b)
+    torch.cuda.synchronize()
+    return m
+
+
+def _stage_times(step, n, device):
+    """Average duration (ms) of each layer stage, from events on the library stream."""
+    import ctypes
+
+    import torch
+
+    from mirai_amd import _native as nat
+
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(7)]
+    for ev in events:
+        ev.record()  # materialise the underlying hipEvent_t
+    torch.cuda.synchronize()
+    handles = (ctypes.c_void_p * 7)(*[ev.cuda_event for ev in events])
+    lib = nat.load_library()
+    sums = [0.0] * 6
+    try:
+        nat.call("mx_set_stage_events", handles, 7)
+        for _ in range(n):
+            step()
+            torch.cuda.synchronize()
+            for i in range(6):
+                sums[i] += events[i].elapsed_time(events[i + 1])
+    finally:
+        lib.mx_set_stage_events(None, 0)
+    return {name: sums[i] / n for i, name in enumerate(STAGES)}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_baseline(w, module, logits_cpu, tokens_cpu, budget_s):
+    """Reference-style CPU expert path (oracle restatement) on a token sample.
+
+    Per call: softmax top-k routing, dequantisation of every projection from
+    the packed format (the reference re-dequantises per call), per-expert
+    gather + bf16 matmuls + LoRA + SwiGLU, fp32 index_add combine.
+    """
+    import numpy as np
+    import torch
+
+    from mirai_amd import workloads as wl
+    from oracle import layer as olayer
+    from oracle import routing as oroute
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    payloads = {}
+    for key in ("w1", "w3", "w2"):
+        p = module.packed_weight(key)
+        if p.fmt == "nf4":
+            payloads[key] = (p.data.cpu().numpy(), p.scale.cpu().view(torch.int16).numpy()
+                             .view(np.uint16))
+        elif p.fmt == "int8":
+            payloads[key] = (p.data.cpu().numpy(), p.scale.cpu().view(torch.int16).numpy()
+                             .view(np.uint16))
+        else:
+            payloads[key] = p.data.cpu()
+    shapes = {k: module.packed_weight(k).shape for k in payloads}
+    loras = {}
+    for key in ("w1", "w3", "w2"):
+        ad = module.expert_lora[key]
+        loras[key] = (ad.lora_a.detach().cpu(), ad.lora_b.detach().cpu(), ad.scale())
+
+    def run(n_tok):
+        lg = logits_cpu[:n_tok].numpy()
+        idx, scores = oroute.route_topk(lg, w.top_k)
+        weights = {k: olayer.dense_weight(w.fmt, payloads[k], shapes[k]) for k in payloads}
+        with torch.no_grad():
+            olayer.layer_forward(tokens_cpu[:n_tok], torch.from_numpy(scores).to(w.dtype),
+                                 torch.from_numpy(idx), weights, loras, w.experts)
+
+    n_tok = min(256, w.tokens)
+    t0 = time.perf_counter()
+    run(n_tok)  # warmup + probe
+    probe = time.perf_counter() - t0
+    # Scale the sample so that ~3 timed calls fit the budget.
+    target = max(1.0, budget_s / 3.0)
+    if probe < target:
+        n_tok = int(min(w.tokens, n_tok * target / max(probe, 1e-3)))
+        n_tok = max(64, n_tok // 64 * 64)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run(n_tok)
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    return {
+        "value": n_tok * w.top_k / sec,
+        "unit": "routed tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{n_tok} of {w.tokens} tokens (x top-{w.top_k} routes), same weights and "
+                   f"LoRA; median of 3 calls incl. per-call dequantisation; torch CPU bf16, "
+                   f"{threads} threads on {_cpu_model()}"),
+        "ms_per_call": sec * 1e3,
+    }
+
+
+def main() -> int:
+    args = _parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); the routed expert layer is built and measured on a "
+              "single MI355X in this build.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from mirai_amd import route_topk
+    from mirai_amd import workloads as wl
+
+    if args.config not in wl.WORKLOADS:
+        print(f"unknown config {args.config!r}; choose from {sorted(wl.WORKLOADS)}",
+              file=sys.stderr)
+        return 2
+    w = wl.WORKLOADS[args.config]
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+
+    logits_cpu = wl.router_logits(w)
+    tokens_cpu = wl.tokens(w)
+    logits = logits_cpu.to(device)
+    x = tokens_cpu.to(device)
+    module = _build_module(w, device)
+
+    state = {}
+
+    def step():
+        with torch.no_grad():
+            idx, scores = route_topk(logits, w.top_k, renorm="clamp", score_dtype=w.dtype)
+            state["out"] = module.run_direct_routed(x, scores, idx)
+            state["idx"] = idx
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+
+    # Routing kernel alone, then the library stages (separate, synchronised passes).
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    r0.record()
+    for _ in range(args.steps):
+        route_topk(logits, w.top_k, renorm="clamp", score_dtype=w.dtype)
+    r1.record()
+    torch.cuda.synchronize()
+    route_ms = r0.elapsed_time(r1) / args.steps
+    stages = _stage_times(step, max(3, args.steps // 2), device)
+
+    counts = torch.bincount(state["idx"].reshape(-1), minlength=w.experts).cpu()
+    R = w.routed_rows
+    flops = w.flops()
+    tflops = flops / (ms * 1e-3) / 1e12
+    gate_up_flops = 2 * R * 2 * w.hidden * w.ffn + 2 * R * 2 * w.ffn * w.rank
+    gu_ms = stages["gate_up_gemm"]
+    achieved = gate_up_flops / (gu_ms * 1e-3) / 1e12
+    down_flops = 2 * R * w.ffn * w.hidden + 2 * R * w.hidden * w.rank
+    result = {
+        "metric": "routed tokens/s + TFLOP/s (% bf16 MFMA peak) for NF4 MoE+LoRA layer, 1 GPU",
+        "value": R / (ms * 1e-3),
+        "unit": "routed tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) tokens and logits, N(0,0.02) weights and LoRA)",
+        "config": {**wl.describe(w), "lora_alpha": w.alpha, "parallelism": "single_gpu"},
+        "tflops": tflops,
+        "pct_bf16_peak": 100.0 * tflops / PEAK_BF16_TFLOPS,
+        "tokens_per_s": w.tokens / (ms * 1e-3),
+        "algorithmic_gflop": flops / 1e9,
+        "empty_experts": int((counts == 0).sum()),
+        "stage_ms": {"route": route_ms, **stages},
+        "down_gemm_tflops": down_flops / (stages["down_gemm"] * 1e-3) / 1e12,
+        "roofline": {
+            "kernel": "grouped_gemm_kernel<NF4, SWIGLU, LoRA> (gate/up)",
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / PEAK_BF16_TFLOPS,
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = _cpu_baseline(w, module, logits_cpu, tokens_cpu,
+                                               args.cpu_seconds)
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

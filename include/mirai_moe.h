@@ -225,6 +225,16 @@ typedef struct mx_lora {
   float scale;          /* alpha / r (or alpha / sqrt(r)) times extra scales */
 } mx_lora;
 
+/*
+ * Profiling hook; no counterpart in the reference (which times whole calls
+ * with CUDA events, scripts/agent/probe_moe_runtime.py:113-146). While set,
+ * each mx_moe_forward call on this thread records events[0..6] (hipEvent_t)
+ * on its stream at the stage boundaries: start, plan, LoRA down-projection of
+ * gate/up, gate/up GEMM, LoRA down-projection of down, down GEMM, combine.
+ * Pass NULL / 0 to clear. count must be 0 or 7.
+ */
+int mx_set_stage_events(void **events, int count);
+
 /* Bytes of scratch for mx_moe_forward / mx_moe_for_loop. */
 size_t mx_moe_workspace_size(int64_t num_tokens, int top_k, int num_experts,
                              int64_t hidden, int64_t ffn);

@@ -75,6 +75,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "mx_nf4_dequantize": (c_int, [_P, _P, c_int64, c_int64, _P, c_int, _P]),
     "mx_int8_quantize": (c_int, [_P, c_int, c_int64, c_int64, _P, _P, _P]),
     "mx_int8_dequantize": (c_int, [_P, _P, c_int64, c_int64, _P, c_int, _P]),
+    "mx_set_stage_events": (c_int, [POINTER(c_void_p), c_int]),
     "mx_moe_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int64]),
     "mx_moe_forward": (
         c_int,

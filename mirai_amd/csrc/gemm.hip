@@ -418,6 +418,15 @@ int launch_any(int fmt, bool lora, const Params &p, int64_t max_row_tiles, hipSt
 }
 
 // ------------------------------------------------------------ host helpers
+constexpr int kStageEvents = 7;
+thread_local void *g_stage_events[kStageEvents] = {};
+thread_local int g_stage_count = 0;
+
+void mark_stage(int i, hipStream_t s) {
+  if (g_stage_count == kStageEvents && g_stage_events[i])
+    (void)hipEventRecord(static_cast<hipEvent_t>(g_stage_events[i]), s);
+}
+
 struct LayerLayout {
   PlanLayout plan;
   size_t off_lora = 0, off_h = 0, off_y = 0, bytes = 0;
@@ -518,6 +527,7 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
     rc = lora_down(v, experts, PL.max_tiles, x, ldx, row_token, hidden, ad, 2, lora_buf, kLoraLd, s);
     if (rc) return rc;
   }
+  mark_stage(2, s);
   {
     Params p = base_params(v);
     p.x = x;
@@ -545,11 +555,13 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
     rc = launch_any<EPI_SWIGLU>(w1->format, lora13, p, PL.max_tiles, s);
     if (rc) return rc;
   }
+  mark_stage(3, s);
   if (lora2) {
     const mx_lora *ad[1] = {l2};
     rc = lora_down(v, experts, PL.max_tiles, h, ffn, nullptr, ffn, ad, 1, lora_buf + 64, kLoraLd, s);
     if (rc) return rc;
   }
+  mark_stage(4, s);
   Params p = base_params(v);
   p.x = h;
   p.ldx = ffn;
@@ -627,9 +639,11 @@ extern "C" int mx_moe_forward(const void *tokens, const int64_t *top_idx, const 
   const LayerLayout L = layer_layout(R, num_experts, hidden, ffn);
   char *ws = static_cast<char *>(workspace);
   const PlanView v = plan_view(ws, L.plan);
+  mark_stage(0, s);
   rc = build_plan(top_idx, nullptr, score_dtype, num_tokens, top_k, num_experts, nullptr, nullptr,
                   nullptr, nullptr, nullptr, nullptr, nullptr, ws, s);
   if (rc) return rc;
+  mark_stage(1, s);
   uint16_t *lora_buf = save_lora ? static_cast<uint16_t *>(save_lora)
                                  : reinterpret_cast<uint16_t *>(ws + L.off_lora);
   uint16_t *h = save_h ? static_cast<uint16_t *>(save_h) : reinterpret_cast<uint16_t *>(ws + L.off_h);
@@ -639,8 +653,22 @@ extern "C" int mx_moe_forward(const void *tokens, const int64_t *top_idx, const 
                   static_cast<uint16_t *>(save_gate), static_cast<uint16_t *>(save_up), y, hidden,
                   v.row_slot, s);
   if (rc) return rc;
-  return mx_combine(y, top_idx, top_scores, score_dtype, num_tokens, top_k, num_experts, hidden,
-                    out, out_dtype, stream);
+  mark_stage(5, s);
+  rc = mx_combine(y, top_idx, top_scores, score_dtype, num_tokens, top_k, num_experts, hidden,
+                  out, out_dtype, stream);
+  mark_stage(6, s);
+  return rc;
+}
+
+extern "C" int mx_set_stage_events(void **events, int count) {
+  clear_error();
+  if (count != 0 && (count != kStageEvents || !events)) {
+    set_error("mx_set_stage_events: pass %d events or none", kStageEvents);
+    return MX_ERR_INVALID;
+  }
+  for (int i = 0; i < kStageEvents; ++i) g_stage_events[i] = count ? events[i] : nullptr;
+  g_stage_count = count;
+  return MX_OK;
 }
 
 extern "C" int mx_moe_for_loop(const void *tokens_sorted, const int64_t *counts, int64_t num_rows,
