@@ -18,18 +18,32 @@
 namespace mx {
 namespace gemm {
 
-constexpr int BM = kPlanTileM;  // rows per tile
-constexpr int BN = 128;         // B rows (output columns) per tile
 constexpr int BK = 64;          // K per pipeline stage (= one NF4 block)
-constexpr int NT = 256;         // 4 wavefronts, 2 x 2, each 64 x 64
-constexpr int kLoraK = 32;      // LoRA rank padded for one MFMA K step
+constexpr int kLoraK = 32;      // LoRA rank padded to two MFMA K steps
 constexpr int kLoraLd = 96;     // low-rank activation row: [gate 32 | up 32 | down 32]
 
 enum { EPI_SWIGLU = 0, EPI_STORE = 1, EPI_LORA_A = 2 };
 
-constexpr int kStageA = BM * BK * 2;
-constexpr int kStageB = BN * BK * 2;
-constexpr int kLdsBytes = 2 * kStageA + 2 * kStageB + NT * 32;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+
+// Macro tile BM x BN x 64 on a WAVES_M x WAVES_N grid of wavefronts; each
+// wave owns a (BM/WAVES_M) x (BN/WAVES_N) sub-tile made of 32 x 32 MFMA blocks
+// (v_mfma_f32_32x32x16_bf16).
+template <int BM_, int BN_, int WAVES_M, int WAVES_N>
+struct Tile {
+  static constexpr int BM = BM_, BN = BN_;
+  static constexpr int NT = 64 * WAVES_M * WAVES_N;
+  static constexpr int WAVES_N_ = WAVES_N;
+  static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  static constexpr int MB = WM / 32, NB = WN / 32;
+  static constexpr int A_CHUNKS = BM * 8 / NT;   // 16-byte A chunks per thread per stage
+  static constexpr int A_ROW_STEP = NT / 8;      // rows between a thread's A chunks
+  static constexpr int B_TPR = NT / BN;          // threads per B row (1, 2 or 4)
+  static constexpr int B_ELEMS = BK / B_TPR;     // B elements decoded per thread per stage
+  static constexpr int STAGE_A = BM * BK * 2;
+  static constexpr int STAGE_B = BN * BK * 2;
+  static constexpr int LDS = 2 * STAGE_A + 2 * STAGE_B;
+};
 
 struct Params {
   const uint16_t *x;
@@ -56,37 +70,103 @@ struct Params {
   float scale[4];
 };
 
+// Per-thread choice among the small kernel-argument arrays by explicit
+// selects: indexing them with a thread-dependent value would copy the
+// argument block to private (scratch) memory.
+template <class V>
+__device__ __forceinline__ V pick(const V (&a)[4], int i) {
+  return i == 0 ? a[0] : i == 1 ? a[1] : i == 2 ? a[2] : a[3];
+}
+template <class V>
+__device__ __forceinline__ V pick2(const V (&a)[2], int i) {
+  return i == 0 ? a[0] : a[1];
+}
+
 // B-tile row j -> (weight group, output column / row of that weight).
-template <int EPI>
+template <int EPI, class T>
 __device__ __forceinline__ void b_row(int j, int nt, int &which, int64_t &n) {
   if (EPI == EPI_SWIGLU) {
-    // 64 ffn columns per tile; each wave's 64 B rows hold 32 gate then 32 up
-    // rows of the same ffn columns, so the SwiGLU pairs land in one lane.
-    which = (j >> 5) & 1;
-    n = static_cast<int64_t>(nt) * 64 + (j >> 6) * 32 + (j & 31);
+    // Each wave's WN columns hold WN/2 gate rows then the WN/2 up rows of the
+    // same ffn columns, so every SwiGLU pair meets in one lane.
+    constexpr int H = T::WN / 2;
+    which = (j / H) & 1;
+    n = static_cast<int64_t>(nt) * (T::BN / 2) + (j / T::WN) * H + (j % H);
   } else if (EPI == EPI_STORE) {
     which = 0;
-    n = static_cast<int64_t>(nt) * BN + j;
+    n = static_cast<int64_t>(nt) * T::BN + j;
   } else {
     which = j >> 5;
     n = j & 31;
   }
 }
 
-__device__ __forceinline__ int swz128(int row, int chunk) {  // 8 x 16 B chunks per row
-  return row * 128 + ((chunk ^ (row & 7)) << 4);
+// 128-byte rows of 8 16-byte chunks. XOR with (row/2)%8 makes any 16
+// consecutive rows at one logical chunk hit 16 distinct bank groups, so both
+// the MFMA fragment reads and the row-owner writes are conflict free.
+__device__ __forceinline__ int swz(int row, int chunk) {
+  return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);
 }
-__device__ __forceinline__ int swz64(int row, int chunk) {  // 4 x 16 B chunks per row
-  return row * 64 + ((chunk ^ (row & 3)) << 4);
+__device__ __forceinline__ int swz64(int row, int chunk) {  // 64-byte rows (LoRA tiles)
+  return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
 }
 
-template <int FMT, int EPI, bool LORA>
-__global__ __launch_bounds__(NT) void grouped_gemm_kernel(Params p) {
+// NF4 decode in registers. `lo`/`hi` hold the low / high bytes of the 16
+// decoded bf16 values bf16(level[q] * absmax) of the current block, 4 per
+// register; v_perm_b32 looks four codes up at once.
+struct Nf4Table {
+  uint32_t lo[4], hi[4];
+};
+
+__device__ __forceinline__ Nf4Table nf4_table(float a) {
+  uint32_t p[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) p[j] = pack_bf16x2(kNF4Levels[2 * j] * a, kNF4Levels[2 * j + 1] * a);
+  Nf4Table t;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    // p[2j] = [lo(4j) hi(4j) lo(4j+1) hi(4j+1)], p[2j+1] likewise for 4j+2, 4j+3.
+    t.lo[j] = __builtin_amdgcn_perm(p[2 * j + 1], p[2 * j], 0x06040200u);
+    t.hi[j] = __builtin_amdgcn_perm(p[2 * j + 1], p[2 * j], 0x07050301u);
+  }
+  return t;
+}
+
+// Table lookup of four 4-bit codes held one per byte of `sel` (values 0..15).
+__device__ __forceinline__ void nf4_lookup4(const Nf4Table &t, uint32_t sel, uint32_t &lo,
+                                            uint32_t &hi) {
+  const uint32_t s7 = sel & 0x07070707u;
+  const uint32_t u = (sel >> 3) & 0x01010101u;
+  const uint32_t m = (u << 8) - u;  // 0xff in every byte whose code is >= 8
+  const uint32_t lo_a = __builtin_amdgcn_perm(t.lo[1], t.lo[0], s7);
+  const uint32_t lo_b = __builtin_amdgcn_perm(t.lo[3], t.lo[2], s7);
+  const uint32_t hi_a = __builtin_amdgcn_perm(t.hi[1], t.hi[0], s7);
+  const uint32_t hi_b = __builtin_amdgcn_perm(t.hi[3], t.hi[2], s7);
+  lo = (lo_b & m) | (lo_a & ~m);
+  hi = (hi_b & m) | (hi_a & ~m);
+}
+
+// Eight codes (one packed dword, element 2i in the low nibble of byte i) ->
+// four dwords of bf16 pairs in element order.
+__device__ __forceinline__ void nf4_decode8(const Nf4Table &t, uint32_t c, uint32_t *out) {
+  uint32_t le, he, lo_, ho;
+  nf4_lookup4(t, c & 0x0f0f0f0fu, le, he);          // elements 0, 2, 4, 6
+  nf4_lookup4(t, (c >> 4) & 0x0f0f0f0fu, lo_, ho);  // elements 1, 3, 5, 7
+  const uint32_t x01 = __builtin_amdgcn_perm(he, le, 0x05010400u);   // e0, e2
+  const uint32_t y01 = __builtin_amdgcn_perm(ho, lo_, 0x05010400u);  // e1, e3
+  const uint32_t x23 = __builtin_amdgcn_perm(he, le, 0x07030602u);   // e4, e6
+  const uint32_t y23 = __builtin_amdgcn_perm(ho, lo_, 0x07030602u);  // e5, e7
+  out[0] = __builtin_amdgcn_perm(y01, x01, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(y01, x01, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(y23, x23, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(y23, x23, 0x07060302u);
+}
+
+template <int FMT, int EPI, bool LORA, class T>
+__global__ __launch_bounds__(T::NT) void grouped_gemm_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t *sA0 = smem;
-  uint8_t *sB0 = smem + 2 * kStageA;
+  uint8_t *sB0 = smem + 2 * T::STAGE_A;
   const int tid = threadIdx.x;
-  uint16_t *lut = reinterpret_cast<uint16_t *>(smem + 2 * kStageA + 2 * kStageB) + tid * 16;
 
   // ---------------------------------------------------------------- tile
   const int num_m = *p.num_tiles;
@@ -104,272 +184,301 @@ __global__ __launch_bounds__(NT) void grouped_gemm_kernel(Params p) {
   const int64_t row_end = p.seg_end[e];
 
   // ----------------------------------------------------- A (activations)
+  // Rows past the segment end re-read the segment's last row: an A row only
+  // feeds its own output row, which the epilogue discards, so the loads need
+  // no guard (and the K loop no branches).
   const int a_chunk = tid & 7;
-  const uint16_t *a_ptr[4];
+  const uint16_t *a_ptr[T::A_CHUNKS];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t grow = row0 + (tid >> 3) + 32 * i;
-    a_ptr[i] = nullptr;
-    if (grow < row_end) {
-      const int64_t src = p.row_token ? static_cast<int64_t>(p.row_token[grow]) : grow;
-      a_ptr[i] = p.x + src * p.ldx + a_chunk * 8;
-    }
+  for (int i = 0; i < T::A_CHUNKS; ++i) {
+    const int64_t grow = min(row0 + (tid >> 3) + T::A_ROW_STEP * i, row_end - 1);
+    const int64_t src = p.row_token ? static_cast<int64_t>(p.row_token[grow]) : grow;
+    a_ptr[i] = p.x + src * p.ldx + a_chunk * 8;
   }
 
   // ------------------------------------------------------- B (weights)
-  const int bj = tid >> 1, bh = tid & 1;
+  const int bj = tid / T::B_TPR, bh = tid % T::B_TPR;
   int which;
   int64_t bn;
-  b_row<EPI>(bj, nt, which, bn);
-  const bool b_valid = bn < p.wn[which];
-  const int64_t wrow = static_cast<int64_t>(e) * p.wn[which] + bn;
+  b_row<EPI, T>(bj, nt, which, bn);
+  // Weight rows past N (a partial column tile) re-read row N-1: they only
+  // feed output columns the epilogue discards. The LoRA down-projection
+  // keeps explicit zeros, as its absent adapters have no rows at all.
+  const int64_t wn_rows = pick(p.wn, which);
+  const bool b_valid = EPI == EPI_LORA_A ? bn < wn_rows : true;
+  if (EPI != EPI_LORA_A) bn = min(bn, wn_rows - 1);
+  const int64_t wrow = static_cast<int64_t>(e) * wn_rows + bn;
   const uint8_t *b_base = nullptr;
   const uint16_t *b_absmax = nullptr;
   float b_scale = 0.0f;
   if (b_valid) {
-    const uint8_t *w = static_cast<const uint8_t *>(p.w[which]);
+    const uint8_t *w = static_cast<const uint8_t *>(pick(p.w, which));
     if (FMT == MX_FMT_NF4) {
-      b_base = w + wrow * (p.K / 2) + bh * 16;
-      b_absmax = p.wscale[which] + wrow * (p.K / BK);
+      b_base = w + wrow * (p.K / 2) + bh * (T::B_ELEMS / 2);
+      b_absmax = pick(p.wscale, which) + wrow * (p.K / BK);
     } else if (FMT == MX_FMT_INT8) {
-      b_base = w + wrow * p.K + bh * 32;
-      b_scale = bf16_bits_to_f32(p.wscale[which][wrow]);
+      b_base = w + wrow * p.K + bh * T::B_ELEMS;
+      b_scale = bf16_bits_to_f32(pick(p.wscale, which)[wrow]);
     } else {
-      b_base = w + wrow * p.K * 2 + bh * 64;
+      b_base = w + wrow * p.K * 2 + bh * T::B_ELEMS * 2;
     }
   }
 
-  constexpr int kBRegs = FMT == MX_FMT_BF16 ? 4 : (FMT == MX_FMT_INT8 ? 2 : 1);
-  uint4 ra[4];
-  uint4 rb[kBRegs];
-  uint32_t rabs = 0;
+  // Bytes of B per thread per stage, in 16-byte registers.
+  constexpr int kBBytes = FMT == MX_FMT_NF4 ? T::B_ELEMS / 2
+                                            : (FMT == MX_FMT_INT8 ? T::B_ELEMS : T::B_ELEMS * 2);
+  constexpr int kBRegs = kBBytes / 16;
+  constexpr int kBStageBytes = FMT == MX_FMT_NF4 ? BK / 2 : (FMT == MX_FMT_INT8 ? BK : BK * 2);
+  // B packed data: two register sets (stage kt+1 is decoded while kt+2 loads).
+  struct BRegs {
+    u32x4 q[kBRegs];
+    uint32_t abs;
+  };
+  u32x4 ra[T::A_CHUNKS];
+  BRegs rb0, rb1;
 
-  auto load_stage = [&](int kt) {
+  auto load_a = [&](int kt) __attribute__((always_inline)) {
     const int64_t k0 = static_cast<int64_t>(kt) * BK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      ra[i] = a_ptr[i] ? *reinterpret_cast<const uint4 *>(a_ptr[i] + k0) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < T::A_CHUNKS; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(a_ptr[i] + k0);
+  };
+  auto load_b = [&](int kt, BRegs &rb) __attribute__((always_inline)) {
     if (b_valid) {
-      if (FMT == MX_FMT_NF4) {
-        rb[0] = *reinterpret_cast<const uint4 *>(b_base + kt * 32);
-        rabs = b_absmax[kt];
-      } else if (FMT == MX_FMT_INT8) {
 #pragma unroll
-        for (int q = 0; q < 2; ++q) rb[q] = *reinterpret_cast<const uint4 *>(b_base + kt * 64 + 16 * q);
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) rb[q] = *reinterpret_cast<const uint4 *>(b_base + kt * 128 + 16 * q);
-      }
+      for (int q = 0; q < kBRegs; ++q)
+        rb.q[q] = *reinterpret_cast<const u32x4 *>(b_base + static_cast<int64_t>(kt) * kBStageBytes + 16 * q);
+      rb.abs = FMT == MX_FMT_NF4 ? b_absmax[kt] : 0u;
     } else {
 #pragma unroll
-      for (int q = 0; q < kBRegs; ++q) rb[q] = make_uint4(0, 0, 0, 0);
-      rabs = 0;
+      for (int q = 0; q < kBRegs; ++q) rb.q[q] = u32x4{0u, 0u, 0u, 0u};
+      rb.abs = 0;
     }
   };
-
-  auto store_stage = [&](int st) {
-    uint8_t *sA = sA0 + st * kStageA;
-    uint8_t *sB = sB0 + st * kStageB;
+  auto store_a = [&](int st) __attribute__((always_inline)) {
+    uint8_t *sA = sA0 + st * T::STAGE_A;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<uint4 *>(sA + swz128((tid >> 3) + 32 * i, a_chunk)) = ra[i];
-    uint32_t dec[16];
-    if (FMT == MX_FMT_NF4) {
-      // Private 16-entry table of this block's decoded values, exactly
-      // bf16(fp32(level) * fp32(absmax)), then one LDS lookup per element.
-      const float a = bf16_bits_to_f32(rabs);
-      uint4 t0, t1;
-      t0.x = pack_bf16x2(kNF4Levels[0] * a, kNF4Levels[1] * a);
-      t0.y = pack_bf16x2(kNF4Levels[2] * a, kNF4Levels[3] * a);
-      t0.z = pack_bf16x2(kNF4Levels[4] * a, kNF4Levels[5] * a);
-      t0.w = pack_bf16x2(kNF4Levels[6] * a, kNF4Levels[7] * a);
-      t1.x = pack_bf16x2(kNF4Levels[8] * a, kNF4Levels[9] * a);
-      t1.y = pack_bf16x2(kNF4Levels[10] * a, kNF4Levels[11] * a);
-      t1.z = pack_bf16x2(kNF4Levels[12] * a, kNF4Levels[13] * a);
-      t1.w = pack_bf16x2(kNF4Levels[14] * a, kNF4Levels[15] * a);
-      reinterpret_cast<uint4 *>(lut)[0] = t0;
-      reinterpret_cast<uint4 *>(lut)[1] = t1;
-      const uint32_t words[4] = {rb[0].x, rb[0].y, rb[0].z, rb[0].w};
+    for (int i = 0; i < T::A_CHUNKS; ++i)
+      *reinterpret_cast<u32x4 *>(sA + swz((tid >> 3) + T::A_ROW_STEP * i, a_chunk)) = ra[i];
+  };
+  // Decode part `part` (of 4) of this thread's B elements into LDS stage st.
+  constexpr int kChunks = T::B_ELEMS / 8;  // 16-byte output chunks per thread
+  constexpr int kChunksPerPart = kChunks / 4 > 0 ? kChunks / 4 : 1;
+  const int chunk0 = bh * kChunks;
+  auto decode_b = [&](const BRegs &rb, const Nf4Table &t, int st, int part) __attribute__((always_inline)) {
+    uint8_t *sB = sB0 + st * T::STAGE_B;
+    if (part * kChunksPerPart >= kChunks) return;
 #pragma unroll
-      for (int wi = 0; wi < 4; ++wi) {
+    for (int cc = 0; cc < kChunksPerPart; ++cc) {
+      const int c = part * kChunksPerPart + cc;  // output chunk: 8 elements
+      uint32_t d[4];
+      if (FMT == MX_FMT_NF4) {
+        // chunk c = code bytes 4c..4c+3 = dword c of the packed registers
+        const u32x4 v = rb.q[c >> 2];
+        const uint32_t word = (c & 3) == 0 ? v[0] : (c & 3) == 1 ? v[1] : (c & 3) == 2 ? v[2] : v[3];
+        nf4_decode8(t, word, d);
+      } else if (FMT == MX_FMT_INT8) {
+        // chunk c = int8 bytes 8c..8c+7 = dwords 2c, 2c+1
+        const u32x4 v = rb.q[c >> 1];
+        const uint32_t w0 = (c & 1) ? v[2] : v[0];
+        const uint32_t w1 = (c & 1) ? v[3] : v[1];
+        const uint32_t ws[2] = {w0, w1};
 #pragma unroll
-        for (int by = 0; by < 4; ++by) {
-          const uint32_t code = (words[wi] >> (8 * by)) & 0xffu;
-          dec[wi * 4 + by] = static_cast<uint32_t>(lut[code & 15u]) |
-                             (static_cast<uint32_t>(lut[code >> 4]) << 16);
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t w = ws[h];
+          const float q0 = static_cast<float>(static_cast<int8_t>(w & 0xffu));
+          const float q1 = static_cast<float>(static_cast<int8_t>((w >> 8) & 0xffu));
+          const float q2 = static_cast<float>(static_cast<int8_t>((w >> 16) & 0xffu));
+          const float q3 = static_cast<float>(static_cast<int8_t>(w >> 24));
+          d[2 * h] = pack_bf16x2(q0 * b_scale, q1 * b_scale);
+          d[2 * h + 1] = pack_bf16x2(q2 * b_scale, q3 * b_scale);
         }
+      } else {
+        const u32x4 v = rb.q[c];
+        d[0] = v[0];
+        d[1] = v[1];
+        d[2] = v[2];
+        d[3] = v[3];
       }
-    } else if (FMT == MX_FMT_INT8) {
-      const uint32_t words[8] = {rb[0].x, rb[0].y, rb[0].z, rb[0].w,
-                                 rb[1].x, rb[1].y, rb[1].z, rb[1].w};
-#pragma unroll
-      for (int wi = 0; wi < 8; ++wi) {
-        const uint32_t w = words[wi];
-        const float q0 = static_cast<float>(static_cast<int8_t>(w & 0xffu));
-        const float q1 = static_cast<float>(static_cast<int8_t>((w >> 8) & 0xffu));
-        const float q2 = static_cast<float>(static_cast<int8_t>((w >> 16) & 0xffu));
-        const float q3 = static_cast<float>(static_cast<int8_t>(w >> 24));
-        dec[2 * wi] = pack_bf16x2(q0 * b_scale, q1 * b_scale);
-        dec[2 * wi + 1] = pack_bf16x2(q2 * b_scale, q3 * b_scale);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        dec[4 * q] = rb[q].x;
-        dec[4 * q + 1] = rb[q].y;
-        dec[4 * q + 2] = rb[q].z;
-        dec[4 * q + 3] = rb[q].w;
-      }
+      *reinterpret_cast<u32x4 *>(sB + swz(bj, chunk0 + c)) = u32x4{d[0], d[1], d[2], d[3]};
     }
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      *reinterpret_cast<uint4 *>(sB + swz128(bj, 4 * bh + q)) =
-          make_uint4(dec[4 * q], dec[4 * q + 1], dec[4 * q + 2], dec[4 * q + 3]);
   };
 
   // -------------------------------------------------------------- MFMA
   const int lane = tid & 63, wid = tid >> 6;
-  const int wm = wid >> 1, wn = wid & 1;
-  f32x4 acc[4][4];
+  const int wm = wid / T::WAVES_N_, wn = wid % T::WAVES_N_;
+  f32x16 acc[T::MB][T::NB];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int mb = 0; mb < T::MB; ++mb)
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int nb = 0; nb < T::NB; ++nb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[mb][nb][j] = 0.0f;
 
-  auto compute_stage = [&](int st) {
-    const uint8_t *sA = sA0 + st * kStageA;
-    const uint8_t *sB = sB0 + st * kStageB;
+  auto mfma_kk = [&](int st, int kk) __attribute__((always_inline)) {
+    const uint8_t *sA = sA0 + st * T::STAGE_A;
+    const uint8_t *sB = sB0 + st * T::STAGE_B;
+    const int ch = kk * 2 + (lane >> 5);
+    bf16x8 a[T::MB], b[T::NB];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int ch = kk * 4 + (lane >> 4);
-      bf16x8 a[4], b[4];
+    for (int mb = 0; mb < T::MB; ++mb)
+      a[mb] = *reinterpret_cast<const bf16x8 *>(sA + swz(wm * T::WM + mb * 32 + (lane & 31), ch));
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-        a[mb] = *reinterpret_cast<const bf16x8 *>(sA + swz128(wm * 64 + mb * 16 + (lane & 15), ch));
+    for (int nb = 0; nb < T::NB; ++nb)
+      b[nb] = *reinterpret_cast<const bf16x8 *>(sB + swz(wn * T::WN + nb * 32 + (lane & 31), ch));
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-        b[nb] = *reinterpret_cast<const bf16x8 *>(sB + swz128(wn * 64 + nb * 16 + (lane & 15), ch));
+    for (int mb = 0; mb < T::MB; ++mb)
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mb], b[nb], acc[mb][nb], 0, 0, 0);
-    }
+      for (int nb = 0; nb < T::NB; ++nb)
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mb], b[nb], acc[mb][nb], 0, 0, 0);
   };
 
+  // One K step: MFMAs on stage `cur` interleaved with the decode of the next
+  // stage's B (loaded one iteration earlier) into the other buffer; the next
+  // A tile and the B tile two steps ahead are in flight meanwhile. Loads past
+  // the end are clamped to the last step, so the body is branch free.
   const int KT = static_cast<int>(p.K / BK);
-  load_stage(0);
-  store_stage(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
+  auto step = [&](int kt, BRegs &b_next, BRegs &b_after) __attribute__((always_inline)) {
     const int cur = kt & 1;
-    if (kt + 1 < KT) load_stage(kt + 1);
-    compute_stage(cur);
-    if (kt + 1 < KT) store_stage(cur ^ 1);
+    load_a(min(kt + 1, KT - 1));
+    load_b(min(kt + 2, KT - 1), b_after);
+    const Nf4Table t = FMT == MX_FMT_NF4 ? nf4_table(bf16_bits_to_f32(b_next.abs)) : Nf4Table{};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      mfma_kk(cur, kk);
+      decode_b(b_next, t, cur ^ 1, kk);
+    }
+    store_a(cur ^ 1);
     __syncthreads();
+  };
+
+  load_a(0);
+  load_b(0, rb0);
+  load_b(min(1, KT - 1), rb1);
+  store_a(0);
+  {
+    const Nf4Table t = FMT == MX_FMT_NF4 ? nf4_table(bf16_bits_to_f32(rb0.abs)) : Nf4Table{};
+#pragma unroll
+    for (int part = 0; part < 4; ++part) decode_b(rb0, t, 0, part);
   }
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    step(kt, rb1, rb0);
+    step(kt + 1, rb0, rb1);
+  }
+  if (kt < KT) step(kt, rb1, rb0);
 
   // ------------------------------------------- LoRA up-projection (K = 32)
-  // Accumulated apart from the frozen projection so the epilogue can round
-  // both to bf16 before adding them, as the reference adds a bf16 LoRA delta
-  // to a bf16 projection output (experts.py:3370-3374).
-  f32x4 acc2[4][4];
+  // Staged in LDS here and multiplied block by block in the epilogue, into
+  // accumulators kept apart from the frozen projection so the epilogue can
+  // round both to bf16 before adding them, as the reference adds a bf16 LoRA
+  // delta to a bf16 projection output (experts.py:3370-3374).
+  constexpr int n_adapt = EPI == EPI_SWIGLU ? 2 : 1;
+  uint8_t *sP = sA0;  // n_adapt x [BM][32] bf16
+  uint8_t *sL = sB0;  // [BN][32] bf16
   if (LORA) {
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) acc2[mb][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    constexpr int n_adapt = EPI == EPI_SWIGLU ? 2 : 1;
-    uint8_t *sP = sA0;  // n_adapt x [BM][32] bf16
-    uint8_t *sL = sB0;  // [BN][32] bf16
-    for (int idx = tid; idx < BM * 4 * n_adapt; idx += NT) {
-      const int ad = idx / (BM * 4);
-      const int rem = idx - ad * BM * 4;
+    for (int idx = tid; idx < T::BM * 4 * n_adapt; idx += T::NT) {
+      const int ad = idx / (T::BM * 4);
+      const int rem = idx - ad * T::BM * 4;
       const int r = rem >> 2, c = rem & 3;
       const int64_t grow = row0 + r;
-      uint4 v = make_uint4(0, 0, 0, 0);
+      u32x4 v = u32x4{0u, 0u, 0u, 0u};
       if (grow < row_end)
-        v = *reinterpret_cast<const uint4 *>(p.lora_p + grow * p.ldp + ad * 32 + c * 8);
-      *reinterpret_cast<uint4 *>(sP + ad * BM * 64 + swz64(r, c)) = v;
+        v = *reinterpret_cast<const u32x4 *>(p.lora_p + grow * p.ldp + ad * 32 + c * 8);
+      *reinterpret_cast<u32x4 *>(sP + ad * T::BM * 64 + swz64(r, c)) = v;
     }
     {
       const int lw = EPI == EPI_SWIGLU ? which : 0;
-      const int r = p.lora_r[lw];
-      const uint16_t *lb = p.lora_b[lw];
+      const int r = pick2(p.lora_r, lw);
+      const uint16_t *lb = pick2(p.lora_b, lw);
+      constexpr int kLChunks = 4 / T::B_TPR > 0 ? 4 / T::B_TPR : 1;
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int c = 2 * bh + q;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (b_valid && lb && c * 8 < r)
-          v = *reinterpret_cast<const uint4 *>(lb + (static_cast<int64_t>(e) * p.N + bn) * r + c * 8);
-        *reinterpret_cast<uint4 *>(sL + swz64(bj, c)) = v;
+      for (int q = 0; q < kLChunks; ++q) {
+        const int c = bh * kLChunks + q;
+        if (c >= 4) break;
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (lb && c * 8 < r)
+          v = *reinterpret_cast<const u32x4 *>(lb + (static_cast<int64_t>(e) * p.N + bn) * r + c * 8);
+        *reinterpret_cast<u32x4 *>(sL + swz64(bj, c)) = v;
       }
     }
     __syncthreads();
-    const int ch = lane >> 4;
-    bf16x8 a[n_adapt][4], b[4];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-      b[nb] = *reinterpret_cast<const bf16x8 *>(sL + swz64(wn * 64 + nb * 16 + (lane & 15), ch));
-#pragma unroll
-    for (int ad = 0; ad < n_adapt; ++ad)
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-        a[ad][mb] = *reinterpret_cast<const bf16x8 *>(sP + ad * BM * 64 +
-                                                      swz64(wm * 64 + mb * 16 + (lane & 15), ch));
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        const int ad = EPI == EPI_SWIGLU ? (nb >> 1) : 0;
-        acc2[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ad][mb], b[nb], acc2[mb][nb], 0, 0, 0);
-      }
   }
-  // Projection output as the reference forms it: bf16(x W^T), plus the bf16
-  // LoRA delta, rounded again.
-  auto proj = [&](int mb, int nb, int i) -> float {
-    const float base = round_bf16(acc[mb][nb][i]);
-    if (!LORA) return base;
-    return round_bf16(base + round_bf16(acc2[mb][nb][i]));
+  auto lora_block = [&](int mb, int nb) -> f32x16 __attribute__((always_inline)) {
+    f32x16 t;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) t[j] = 0.0f;
+    const int ad = EPI == EPI_SWIGLU ? (nb / (T::NB / 2)) : 0;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int ch = kk * 2 + (lane >> 5);
+      const bf16x8 a = *reinterpret_cast<const bf16x8 *>(
+          sP + ad * T::BM * 64 + swz64(wm * T::WM + mb * 32 + (lane & 31), ch));
+      const bf16x8 b = *reinterpret_cast<const bf16x8 *>(
+          sL + swz64(wn * T::WN + nb * 32 + (lane & 31), ch));
+      t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, t, 0, 0, 0);
+    }
+    return t;
   };
 
   // ------------------------------------------------------------ epilogue
-  // Accumulator layout of v_mfma_f32_16x16x32_bf16: lane holds rows
-  // 4*(lane/16) + i (i = 0..3) of column lane%16.
-  const int64_t rbase = row0 + wm * 64 + 4 * (lane >> 4);
+  // v_mfma_f32_32x32x16 accumulator layout: value j of a lane sits at row
+  // 8*(j/4) + 4*(lane/32) + j%4 and column lane%32 of the 32 x 32 block.
+  const int64_t rbase = row0 + wm * T::WM + 4 * (lane >> 5);
+  const int lcol = lane & 31;
+  if (EPI == EPI_SWIGLU) {
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 0; mb < T::MB; ++mb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t r = rbase + mb * 16 + i;
-      if (r >= row_end) continue;
-      if (EPI == EPI_SWIGLU) {
+      for (int nbp = 0; nbp < T::NB / 2; ++nbp) {
+        f32x16 lg, lu;
+        if (LORA) {
+          lg = lora_block(mb, nbp);
+          lu = lora_block(mb, nbp + T::NB / 2);
+        }
+        const int64_t f = static_cast<int64_t>(nt) * (T::BN / 2) + wn * (T::WN / 2) + nbp * 32 + lcol;
 #pragma unroll
-        for (int nbp = 0; nbp < 2; ++nbp) {
-          const int64_t f = static_cast<int64_t>(nt) * 64 + wn * 32 + nbp * 16 + (lane & 15);
-          const float g = proj(mb, nbp, i);
-          const float u = proj(mb, nbp + 2, i);
+        for (int j = 0; j < 16; ++j) {
+          const int64_t r = rbase + mb * 32 + 8 * (j >> 2) + (j & 3);
+          if (r >= row_end || f >= p.N) continue;
+          float g = round_bf16(acc[mb][nbp][j]);
+          float u = round_bf16(acc[mb][nbp + T::NB / 2][j]);
+          if (LORA) {
+            g = round_bf16(g + round_bf16(lg[j]));
+            u = round_bf16(u + round_bf16(lu[j]));
+          }
           // silu(g) rounded to bf16, then the bf16 product (experts.py:289-317).
-          const float sg = round_bf16(g / (1.0f + __expf(-g)));
+          const float sg = round_bf16(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)));
           p.out[r * p.ldo + f] = f32_to_bf16_bits(sg * u);
           if (p.save_gate) p.save_gate[r * p.N + f] = f32_to_bf16_bits(g);
           if (p.save_up) p.save_up[r * p.N + f] = f32_to_bf16_bits(u);
         }
-      } else if (EPI == EPI_STORE) {
-        const int64_t orow = p.out_row ? static_cast<int64_t>(p.out_row[r]) : r;
+      }
+    }
+  } else {
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          const int64_t n = static_cast<int64_t>(nt) * BN + wn * 64 + nb * 16 + (lane & 15);
-          if (n < p.N) p.out[orow * p.ldo + n] = f32_to_bf16_bits(proj(mb, nb, i));
-        }
-      } else {
+    for (int mb = 0; mb < T::MB; ++mb) {
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          const int n = wn * 64 + nb * 16 + (lane & 15);
-          if (n < p.N) {
+      for (int nb = 0; nb < T::NB; ++nb) {
+        f32x16 l2;
+        if (LORA) l2 = lora_block(mb, nb);
+        const int ncol = wn * T::WN + nb * 32 + lcol;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int64_t r = rbase + mb * 32 + 8 * (j >> 2) + (j & 3);
+          if (r >= row_end) continue;
+          if (EPI == EPI_STORE) {
+            const int64_t n = static_cast<int64_t>(nt) * T::BN + ncol;
+            if (n >= p.N) continue;
+            float v = round_bf16(acc[mb][nb][j]);
+            if (LORA) v = round_bf16(v + round_bf16(l2[j]));
+            const int64_t orow = p.out_row ? static_cast<int64_t>(p.out_row[r]) : r;
+            p.out[orow * p.ldo + n] = f32_to_bf16_bits(v);
+          } else {
+            if (ncol >= p.N) continue;
             // bf16(x a^T) first, then the LoRA scale, as low_rank.to(bf16) * scale.
-            const float lr = round_bf16(acc[mb][nb][i]);
-            p.out[r * p.ldo + n] = f32_to_bf16_bits(lr * p.scale[n >> 5]);
+            const float lr = round_bf16(acc[mb][nb][j]);
+            p.out[r * p.ldo + ncol] = f32_to_bf16_bits(lr * pick(p.scale, ncol >> 5));
           }
         }
       }
@@ -377,7 +486,7 @@ __global__ __launch_bounds__(NT) void grouped_gemm_kernel(Params p) {
   }
 }
 
-template <int FMT, int EPI, bool LORA>
+template <int FMT, int EPI, bool LORA, class T>
 int launch(const Params &p, int64_t max_row_tiles, hipStream_t s) {
   const int64_t total = max_row_tiles * p.n_tiles_n;
   if (total <= 0) return MX_OK;
@@ -386,35 +495,54 @@ int launch(const Params &p, int64_t max_row_tiles, hipStream_t s) {
     set_error("grouped GEMM grid too large");
     return MX_ERR_INVALID;
   }
-  auto kern = grouped_gemm_kernel<FMT, EPI, LORA>;
+  auto kern = grouped_gemm_kernel<FMT, EPI, LORA, T>;
   static bool configured = false;
   if (!configured) {
     // Dynamic LDS above 64 KiB; a runtime that needs no opt-in may refuse the
     // attribute, which is harmless, so its status is consumed and dropped.
     if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes) != hipSuccess)
+                            hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS) != hipSuccess)
       (void)hipGetLastError();
     configured = true;
   }
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(NT), kLdsBytes, s, p);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(T::NT), T::LDS, s, p);
   return check_launch("grouped GEMM launch");
 }
 
+// Row-tile height: 256-row tiles when experts average at least 768 rows
+// (their tail waste stays small), else 128-row tiles.
+inline bool use_tall_tiles(int64_t rows, int experts) { return rows >= 768 * static_cast<int64_t>(experts); }
+
 template <int EPI, bool LORA>
-int launch_fmt(int fmt, const Params &p, int64_t max_row_tiles, hipStream_t s) {
+int launch_fmt(int fmt, Params p, const PlanLayout &PL, const PlanView &v, bool tall, hipStream_t s) {
+  // Column tiles are 256 wide (EPI_SWIGLU: 128 ffn columns of gate and of up).
+  using Tall = Tile<256, 256, 2, 4>;
+  using Short = Tile<128, 256, 2, 4>;
+  p.tiles = tall ? v.tiles2 : v.tiles;
+  p.num_tiles = tall ? v.num_tiles2 : v.num_tiles;
+  const int64_t max_tiles = tall ? PL.max_tiles2 : PL.max_tiles;
+  p.n_tiles_n = static_cast<int>(EPI == EPI_SWIGLU ? ceil_div(p.N, 128) : ceil_div(p.N, 256));
   switch (fmt) {
-    case MX_FMT_BF16: return launch<MX_FMT_BF16, EPI, LORA>(p, max_row_tiles, s);
-    case MX_FMT_NF4: return launch<MX_FMT_NF4, EPI, LORA>(p, max_row_tiles, s);
-    case MX_FMT_INT8: return launch<MX_FMT_INT8, EPI, LORA>(p, max_row_tiles, s);
+    case MX_FMT_BF16:
+      return tall ? launch<MX_FMT_BF16, EPI, LORA, Tall>(p, max_tiles, s)
+                  : launch<MX_FMT_BF16, EPI, LORA, Short>(p, max_tiles, s);
+    case MX_FMT_NF4:
+      return tall ? launch<MX_FMT_NF4, EPI, LORA, Tall>(p, max_tiles, s)
+                  : launch<MX_FMT_NF4, EPI, LORA, Short>(p, max_tiles, s);
+    case MX_FMT_INT8:
+      return tall ? launch<MX_FMT_INT8, EPI, LORA, Tall>(p, max_tiles, s)
+                  : launch<MX_FMT_INT8, EPI, LORA, Short>(p, max_tiles, s);
   }
   set_error("unknown weight format %d", fmt);
   return MX_ERR_INVALID;
 }
 
 template <int EPI>
-int launch_any(int fmt, bool lora, const Params &p, int64_t max_row_tiles, hipStream_t s) {
-  return lora ? launch_fmt<EPI, true>(fmt, p, max_row_tiles, s)
-              : launch_fmt<EPI, false>(fmt, p, max_row_tiles, s);
+int launch_any(int fmt, bool lora, const Params &p, const PlanLayout &PL, const PlanView &v,
+               hipStream_t s) {
+  const bool tall = use_tall_tiles(PL.rows, PL.experts);
+  return lora ? launch_fmt<EPI, true>(fmt, p, PL, v, tall, s)
+              : launch_fmt<EPI, false>(fmt, p, PL, v, tall, s);
 }
 
 // ------------------------------------------------------------ host helpers
@@ -509,7 +637,7 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
   p.seg_end = v.seg + experts;
   p.out = out;
   p.ldo = ldo;
-  return launch<MX_FMT_BF16, EPI_LORA_A, false>(p, max_tiles, s);
+  return launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 128, 2, 2>>(p, max_tiles, s);
 }
 
 // gate/up grouped GEMM with SwiGLU epilogue, then the down grouped GEMM.
@@ -540,7 +668,6 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
     p.wscale[1] = static_cast<const uint16_t *>(w3->scale);
     p.wn[0] = p.wn[1] = ffn;
     p.N = ffn;
-    p.n_tiles_n = static_cast<int>(ffn / 64);
     p.lora_p = lora_buf;
     p.ldp = kLoraLd;
     p.lora_b[0] = has_lora(l1) ? static_cast<const uint16_t *>(l1->b) : nullptr;
@@ -552,7 +679,7 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
     p.ldo = ffn;
     p.save_gate = save_gate;
     p.save_up = save_up;
-    rc = launch_any<EPI_SWIGLU>(w1->format, lora13, p, PL.max_tiles, s);
+    rc = launch_any<EPI_SWIGLU>(w1->format, lora13, p, PL, v, s);
     if (rc) return rc;
   }
   mark_stage(3, s);
@@ -571,7 +698,6 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
   p.wscale[0] = static_cast<const uint16_t *>(w2->scale);
   p.wn[0] = hidden;
   p.N = hidden;
-  p.n_tiles_n = static_cast<int>(ceil_div(hidden, BN));
   p.lora_p = lora_buf + 64;
   p.ldp = kLoraLd;
   p.lora_b[0] = lora2 ? static_cast<const uint16_t *>(l2->b) : nullptr;
@@ -580,7 +706,7 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
   p.out = y;
   p.ldo = ldy;
   p.out_row = out_row;
-  return launch_any<EPI_STORE>(w2->format, lora2, p, PL.max_tiles, s);
+  return launch_any<EPI_STORE>(w2->format, lora2, p, PL, v, s);
 }
 
 int check_layer(const char *name, int64_t hidden, int64_t ffn, const mx_weight *w1,
@@ -742,7 +868,6 @@ extern "C" int mx_grouped_linear(const void *x, const int64_t *counts, int64_t n
   p.wscale[0] = static_cast<const uint16_t *>(w->scale);
   p.wn[0] = out_f;
   p.N = out_f;
-  p.n_tiles_n = static_cast<int>(ceil_div(out_f, BN));
   p.lora_p = lora_buf;
   p.ldp = kLoraLd;
   p.lora_b[0] = lr ? static_cast<const uint16_t *>(lora->b) : nullptr;
@@ -750,5 +875,5 @@ extern "C" int mx_grouped_linear(const void *x, const int64_t *counts, int64_t n
   p.seg_end = v.seg + num_experts;
   p.out = static_cast<uint16_t *>(out);
   p.ldo = out_f;
-  return launch_any<EPI_STORE>(w->format, lr, p, L.plan.max_tiles, s);
+  return launch_any<EPI_STORE>(w->format, lr, p, L.plan, v, s);
 }

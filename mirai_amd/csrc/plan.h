@@ -6,28 +6,32 @@
 
 namespace mx {
 
-// Row-tile height of the grouped GEMMs; the plan emits one (expert, first row)
-// work item per tile.
+// Row-tile heights of the grouped GEMMs; the plan emits one (expert, first
+// row) work item per tile for each height.
 constexpr int kPlanTileM = 128;
+constexpr int kPlanTileM2 = 256;
 
 struct PlanLayout {
   int64_t rows = 0;
   int experts = 0;
   int slots_per_block = 0;
   int blocks = 0;
-  int64_t max_tiles = 0;
-  size_t off_block_counts = 0, off_block_base = 0, off_seg = 0, off_tiles = 0;
+  int64_t max_tiles = 0;   // 128-row tiles
+  int64_t max_tiles2 = 0;  // 256-row tiles
+  size_t off_block_counts = 0, off_block_base = 0, off_seg = 0, off_tiles = 0, off_tiles2 = 0;
   size_t off_row_token = 0, off_row_slot = 0;
   size_t bytes = 0;
 };
 
 struct PlanView {
   int32_t *err;            // invalid expert ids / inconsistent counts seen
-  int32_t *num_tiles;      // row tiles emitted
+  int32_t *num_tiles;      // 128-row tiles emitted
+  int32_t *num_tiles2;     // 256-row tiles emitted
   int32_t *block_counts;   // [blocks, E]
   int32_t *block_base;     // [blocks, E]
   int64_t *seg;            // [2, E]: segment start, segment end (sorted rows)
-  int2 *tiles;             // [max_tiles]: (expert, first row)
+  int2 *tiles;             // [max_tiles]: (expert, first row), 128-row tiles
+  int2 *tiles2;            // [max_tiles2]: 256-row tiles
   int32_t *row_token;      // [R]: sorted row -> token
   int32_t *row_slot;       // [R]: sorted row -> flat route slot t*k+j
 };

@@ -76,8 +76,8 @@ __device__ int64_t block_exclusive_scan(int64_t v, int64_t *shared, int64_t *tot
 __global__ __launch_bounds__(1024) void plan_scan_kernel(
     const int32_t *block_counts, int n_blocks, int E, int64_t n_rows, int tile_m,
     const int64_t *counts_in, int32_t *block_base, int64_t *seg, int2 *tiles,
-    int32_t *num_tiles, int32_t *err_counter, int64_t *counts_out, int64_t *starts_out,
-    int32_t *offsets_out) {
+    int32_t *num_tiles, int2 *tiles2, int32_t *num_tiles2, int32_t *err_counter,
+    int64_t *counts_out, int64_t *starts_out, int32_t *offsets_out) {
   __shared__ int64_t scan_tmp[32];
   const int e = threadIdx.x;
   int64_t count = 0;
@@ -116,12 +116,16 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(
     if (starts_out) starts_out[e] = start;
     if (offsets_out) offsets_out[e] = static_cast<int32_t>(start + count);
   }
-  const int64_t my_tiles = e < E ? (seg_hi - seg_lo + tile_m - 1) / tile_m : 0;
-  int64_t n_tiles = 0;
-  const int64_t tile0 = block_exclusive_scan(my_tiles, scan_tmp, &n_tiles);
-  for (int64_t j = 0; j < my_tiles; ++j)
-    tiles[tile0 + j] = make_int2(e, static_cast<int>(seg_lo + j * tile_m));
-  if (threadIdx.x == 0) *num_tiles = static_cast<int32_t>(n_tiles);
+  for (int list = 0; list < 2; ++list) {
+    const int tm = list == 0 ? tile_m : 2 * tile_m;
+    int2 *out = list == 0 ? tiles : tiles2;
+    const int64_t my_tiles = e < E ? (seg_hi - seg_lo + tm - 1) / tm : 0;
+    int64_t n_tiles = 0;
+    const int64_t tile0 = block_exclusive_scan(my_tiles, scan_tmp, &n_tiles);
+    for (int64_t j = 0; j < my_tiles; ++j)
+      out[tile0 + j] = make_int2(e, static_cast<int>(seg_lo + j * tm));
+    if (threadIdx.x == 0) *(list == 0 ? num_tiles : num_tiles2) = static_cast<int32_t>(n_tiles);
+  }
 }
 
 template <int SCORE_DTYPE>
@@ -192,6 +196,7 @@ PlanLayout plan_layout(int64_t num_rows, int num_experts) {
   L.slots_per_block = slots_per_plan_block(num_experts);
   L.blocks = static_cast<int>(ceil_div(num_rows, L.slots_per_block));
   L.max_tiles = ceil_div(num_rows, kPlanTileM) + num_experts;
+  L.max_tiles2 = ceil_div(num_rows, kPlanTileM2) + num_experts;
   size_t off = 256;  // header: error counter, tile count
   L.off_block_counts = off;
   off = align_up(off + sizeof(int32_t) * L.blocks * num_experts, 256);
@@ -201,6 +206,8 @@ PlanLayout plan_layout(int64_t num_rows, int num_experts) {
   off = align_up(off + sizeof(int64_t) * 2 * num_experts, 256);
   L.off_tiles = off;
   off = align_up(off + sizeof(int2) * L.max_tiles, 256);
+  L.off_tiles2 = off;
+  off = align_up(off + sizeof(int2) * L.max_tiles2, 256);
   L.off_row_token = off;
   off = align_up(off + sizeof(int32_t) * num_rows, 256);
   L.off_row_slot = off;
@@ -214,10 +221,12 @@ PlanView plan_view(void *ws, const PlanLayout &L) {
   PlanView v;
   v.err = reinterpret_cast<int32_t *>(b);
   v.num_tiles = reinterpret_cast<int32_t *>(b) + 1;
+  v.num_tiles2 = reinterpret_cast<int32_t *>(b) + 2;
   v.block_counts = reinterpret_cast<int32_t *>(b + L.off_block_counts);
   v.block_base = reinterpret_cast<int32_t *>(b + L.off_block_base);
   v.seg = reinterpret_cast<int64_t *>(b + L.off_seg);
   v.tiles = reinterpret_cast<int2 *>(b + L.off_tiles);
+  v.tiles2 = reinterpret_cast<int2 *>(b + L.off_tiles2);
   v.row_token = reinterpret_cast<int32_t *>(b + L.off_row_token);
   v.row_slot = reinterpret_cast<int32_t *>(b + L.off_row_slot);
   return v;
@@ -230,7 +239,7 @@ int build_plan(const int64_t *top_idx, const void *top_scores, int score_dtype,
   const int64_t R = num_tokens * top_k;
   const PlanLayout L = plan_layout(R, num_experts);
   const PlanView v = plan_view(workspace, L);
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, v.err, 2);
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, v.err, 3);
   if (L.blocks > 0) {
     const size_t lds = sizeof(uint32_t) * num_experts * (L.slots_per_block / 32);
     hipLaunchKernelGGL(plan_count_kernel, dim3(L.blocks), dim3(256), lds, s, top_idx, R,
@@ -238,7 +247,8 @@ int build_plan(const int64_t *top_idx, const void *top_scores, int score_dtype,
   }
   hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, s, v.block_counts, L.blocks,
                      num_experts, R, kPlanTileM, static_cast<const int64_t *>(nullptr),
-                     v.block_base, v.seg, v.tiles, v.num_tiles, v.err, counts, starts, offsets);
+                     v.block_base, v.seg, v.tiles, v.num_tiles, v.tiles2, v.num_tiles2, v.err,
+                     counts, starts, offsets);
   if (L.blocks > 0) {
     const size_t lds = 2 * sizeof(uint32_t) * num_experts * (L.slots_per_block / 32);
     if (score_dtype == MX_DTYPE_BF16)
@@ -261,11 +271,11 @@ int plan_from_counts(const int64_t *counts, int64_t num_rows, int num_experts, v
                      hipStream_t s) {
   const PlanLayout L = plan_layout(num_rows, num_experts);
   const PlanView v = plan_view(workspace, L);
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, v.err, 2);
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, v.err, 3);
   hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, s,
                      static_cast<const int32_t *>(nullptr), 0, num_experts, num_rows,
                      kPlanTileM, counts, static_cast<int32_t *>(nullptr), v.seg, v.tiles,
-                     v.num_tiles, v.err, static_cast<int64_t *>(nullptr),
+                     v.num_tiles, v.tiles2, v.num_tiles2, v.err, static_cast<int64_t *>(nullptr),
                      static_cast<int64_t *>(nullptr), static_cast<int32_t *>(nullptr));
   return check_launch("mx_plan_from_counts");
 }
