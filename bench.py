@@ -18,6 +18,7 @@ token sample on the host cores.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import statistics
@@ -41,6 +42,9 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="target",
                     help="workload key: target (default), c2, c3, c4")
+    ap.add_argument("--weights", choices=("nf4", "int8", "bf16"), default=None,
+                    help="override the workload's frozen-weight format")
+    ap.add_argument("--tokens", type=int, default=None, help="override the token count")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget of the baseline sample")
@@ -194,6 +198,10 @@ def main() -> int:
               file=sys.stderr)
         return 2
     w = wl.WORKLOADS[args.config]
+    if args.weights:
+        w = dataclasses.replace(w, fmt=args.weights, name=f"{w.name}_{args.weights}")
+    if args.tokens:
+        w = dataclasses.replace(w.with_tokens(args.tokens), name=f"{w.name}_T{args.tokens}")
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
 

@@ -12,13 +12,15 @@
 // (workgroups are dispatched round-robin over XCDs), ordered row-tile major,
 // so the column tiles sharing an activation tile, and the row tiles sharing an
 // expert's weights, run on the same XCD and hit its L2.
+#include <stdlib.h>
+
 #include "common.h"
 #include "plan.h"
 
 namespace mx {
 namespace gemm {
 
-constexpr int BK = 64;          // K per pipeline stage (= one NF4 block)
+constexpr int kNf4Block = 64;   // NF4 absmax block along K
 constexpr int kLoraK = 32;      // LoRA rank padded to two MFMA K steps
 constexpr int kLoraLd = 96;     // low-rank activation row: [gate 32 | up 32 | down 32]
 
@@ -26,18 +28,22 @@ enum { EPI_SWIGLU = 0, EPI_STORE = 1, EPI_LORA_A = 2 };
 
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 
-// Macro tile BM x BN x 64 on a WAVES_M x WAVES_N grid of wavefronts; each
+// Macro tile BM x BN x BK on a WAVES_M x WAVES_N grid of wavefronts; each
 // wave owns a (BM/WAVES_M) x (BN/WAVES_N) sub-tile made of 32 x 32 MFMA blocks
-// (v_mfma_f32_32x32x16_bf16).
-template <int BM_, int BN_, int WAVES_M, int WAVES_N>
+// (v_mfma_f32_32x32x16_bf16). BK is 64 (one NF4 block per stage) or 32.
+template <int BM_, int BN_, int WAVES_M, int WAVES_N, int BK_, int WAVES_PER_SIMD_ = 1>
 struct Tile {
-  static constexpr int BM = BM_, BN = BN_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_;
+  // Occupancy the register budget is sized for (waves per SIMD).
+  static constexpr int WAVES_PER_SIMD = WAVES_PER_SIMD_;
   static constexpr int NT = 64 * WAVES_M * WAVES_N;
   static constexpr int WAVES_N_ = WAVES_N;
   static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   static constexpr int MB = WM / 32, NB = WN / 32;
-  static constexpr int A_CHUNKS = BM * 8 / NT;   // 16-byte A chunks per thread per stage
-  static constexpr int A_ROW_STEP = NT / 8;      // rows between a thread's A chunks
+  static constexpr int KSUB = BK / 16;           // MFMA K steps per stage
+  static constexpr int CPR = BK / 8;             // 16-byte chunks per tile row
+  static constexpr int A_CHUNKS = BM * CPR / NT; // A chunks per thread per stage
+  static constexpr int A_ROW_STEP = NT / CPR;    // rows between a thread's A chunks
   static constexpr int B_TPR = NT / BN;          // threads per B row (1, 2 or 4)
   static constexpr int B_ELEMS = BK / B_TPR;     // B elements decoded per thread per stage
   static constexpr int STAGE_A = BM * BK * 2;
@@ -100,11 +106,14 @@ __device__ __forceinline__ void b_row(int j, int nt, int &which, int64_t &n) {
   }
 }
 
-// 128-byte rows of 8 16-byte chunks. XOR with (row/2)%8 makes any 16
-// consecutive rows at one logical chunk hit 16 distinct bank groups, so both
-// the MFMA fragment reads and the row-owner writes are conflict free.
+// Tile rows of BK bf16 = 8 (BK 64) or 4 (BK 32) 16-byte chunks. The chunk is
+// XOR-ed with a row-dependent value so that any 16 consecutive rows at one
+// logical chunk hit 16 distinct 16-byte bank groups: both the MFMA fragment
+// reads and the row-owner writes are conflict free.
+template <int BK>
 __device__ __forceinline__ int swz(int row, int chunk) {
-  return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);
+  if (BK == 64) return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);
+  return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 __device__ __forceinline__ int swz64(int row, int chunk) {  // 64-byte rows (LoRA tiles)
   return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
@@ -162,10 +171,15 @@ __device__ __forceinline__ void nf4_decode8(const Nf4Table &t, uint32_t c, uint3
 }
 
 template <int FMT, int EPI, bool LORA, class T>
-__global__ __launch_bounds__(T::NT) void grouped_gemm_kernel(Params p) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t *sA0 = smem;
-  uint8_t *sB0 = smem + 2 * T::STAGE_A;
+__global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_SIMD)))
+void grouped_gemm_kernel(Params p) {
+  // Four distinct LDS objects (two stages of A and of B): the compiler can
+  // then prove that the A DMA into one stage never aliases the LDS reads and
+  // B writes of the other, and inserts no wait between them.
+  __shared__ __attribute__((aligned(16))) uint8_t sA0[T::STAGE_A];
+  __shared__ __attribute__((aligned(16))) uint8_t sA1[T::STAGE_A];
+  __shared__ __attribute__((aligned(16))) uint8_t sB0[T::STAGE_B];
+  __shared__ __attribute__((aligned(16))) uint8_t sB1[T::STAGE_B];
   const int tid = threadIdx.x;
 
   // ---------------------------------------------------------------- tile
@@ -187,13 +201,25 @@ __global__ __launch_bounds__(T::NT) void grouped_gemm_kernel(Params p) {
   // Rows past the segment end re-read the segment's last row: an A row only
   // feeds its own output row, which the epilogue discards, so the loads need
   // no guard (and the K loop no branches).
-  const int a_chunk = tid & 7;
+  constexpr int BK = T::BK;
+  // A goes global -> LDS by DMA (global_load_lds_dwordx4): one wave
+  // instruction fills 1 KB of the stage, lane l landing at byte 16*l. The lane
+  // that lands on (row, physical chunk) loads the logical chunk the swizzle
+  // maps there, so the stage ends up in the same swizzled layout.
+  const int wave = tid >> 6, lane_id = tid & 63;
+  constexpr int kRowsPerDma = 1024 / (BK * 2);
   const uint16_t *a_ptr[T::A_CHUNKS];
+  int a_lds[T::A_CHUNKS];  // wave-uniform LDS byte offset of each DMA inside a stage
 #pragma unroll
   for (int i = 0; i < T::A_CHUNKS; ++i) {
-    const int64_t grow = min(row0 + (tid >> 3) + T::A_ROW_STEP * i, row_end - 1);
+    const int region = wave * T::A_CHUNKS + i;
+    const int row = region * kRowsPerDma + lane_id / T::CPR;
+    const int phys = lane_id % T::CPR;
+    const int logical = BK == 64 ? (phys ^ ((row >> 1) & 7)) : (phys ^ ((row >> 2) & 3));
+    const int64_t grow = min(row0 + row, row_end - 1);
     const int64_t src = p.row_token ? static_cast<int64_t>(p.row_token[grow]) : grow;
-    a_ptr[i] = p.x + src * p.ldx + a_chunk * 8;
+    a_ptr[i] = p.x + src * p.ldx + logical * 8;
+    a_lds[i] = region * 1024;
   }
 
   // ------------------------------------------------------- B (weights)
@@ -215,7 +241,7 @@ __global__ __launch_bounds__(T::NT) void grouped_gemm_kernel(Params p) {
     const uint8_t *w = static_cast<const uint8_t *>(pick(p.w, which));
     if (FMT == MX_FMT_NF4) {
       b_base = w + wrow * (p.K / 2) + bh * (T::B_ELEMS / 2);
-      b_absmax = pick(p.wscale, which) + wrow * (p.K / BK);
+      b_absmax = pick(p.wscale, which) + wrow * (p.K / kNf4Block);
     } else if (FMT == MX_FMT_INT8) {
       b_base = w + wrow * p.K + bh * T::B_ELEMS;
       b_scale = bf16_bits_to_f32(pick(p.wscale, which)[wrow]);
@@ -234,38 +260,36 @@ __global__ __launch_bounds__(T::NT) void grouped_gemm_kernel(Params p) {
     u32x4 q[kBRegs];
     uint32_t abs;
   };
-  u32x4 ra[T::A_CHUNKS];
   BRegs rb0, rb1;
 
-  auto load_a = [&](int kt) __attribute__((always_inline)) {
+  // DMA of A for step kt into the LDS stage sA.
+  auto load_a = [&](int kt, uint8_t *sA) __attribute__((always_inline)) {
     const int64_t k0 = static_cast<int64_t>(kt) * BK;
 #pragma unroll
-    for (int i = 0; i < T::A_CHUNKS; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(a_ptr[i] + k0);
+    for (int i = 0; i < T::A_CHUNKS; ++i)
+      __builtin_amdgcn_global_load_lds(
+          reinterpret_cast<const void *>(a_ptr[i] + k0),
+          reinterpret_cast<__attribute__((address_space(3))) void *>(
+              reinterpret_cast<uintptr_t>(sA + a_lds[i])),
+          16, 0, 0);
   };
   auto load_b = [&](int kt, BRegs &rb) __attribute__((always_inline)) {
     if (b_valid) {
 #pragma unroll
       for (int q = 0; q < kBRegs; ++q)
         rb.q[q] = *reinterpret_cast<const u32x4 *>(b_base + static_cast<int64_t>(kt) * kBStageBytes + 16 * q);
-      rb.abs = FMT == MX_FMT_NF4 ? b_absmax[kt] : 0u;
+      rb.abs = FMT == MX_FMT_NF4 ? b_absmax[kt * BK / kNf4Block] : 0u;
     } else {
 #pragma unroll
       for (int q = 0; q < kBRegs; ++q) rb.q[q] = u32x4{0u, 0u, 0u, 0u};
       rb.abs = 0;
     }
   };
-  auto store_a = [&](int st) __attribute__((always_inline)) {
-    uint8_t *sA = sA0 + st * T::STAGE_A;
-#pragma unroll
-    for (int i = 0; i < T::A_CHUNKS; ++i)
-      *reinterpret_cast<u32x4 *>(sA + swz((tid >> 3) + T::A_ROW_STEP * i, a_chunk)) = ra[i];
-  };
-  // Decode part `part` (of 4) of this thread's B elements into LDS stage st.
+  // Decode part `part` (of KSUB) of this thread's B elements into LDS stage st.
   constexpr int kChunks = T::B_ELEMS / 8;  // 16-byte output chunks per thread
-  constexpr int kChunksPerPart = kChunks / 4 > 0 ? kChunks / 4 : 1;
+  constexpr int kChunksPerPart = kChunks / T::KSUB > 0 ? kChunks / T::KSUB : 1;
   const int chunk0 = bh * kChunks;
-  auto decode_b = [&](const BRegs &rb, const Nf4Table &t, int st, int part) __attribute__((always_inline)) {
-    uint8_t *sB = sB0 + st * T::STAGE_B;
+  auto decode_b = [&](const BRegs &rb, const Nf4Table &t, uint8_t *sB, int part) __attribute__((always_inline)) {
     if (part * kChunksPerPart >= kChunks) return;
 #pragma unroll
     for (int cc = 0; cc < kChunksPerPart; ++cc) {
@@ -299,7 +323,7 @@ __global__ __launch_bounds__(T::NT) void grouped_gemm_kernel(Params p) {
         d[2] = v[2];
         d[3] = v[3];
       }
-      *reinterpret_cast<u32x4 *>(sB + swz(bj, chunk0 + c)) = u32x4{d[0], d[1], d[2], d[3]};
+      *reinterpret_cast<u32x4 *>(sB + swz<BK>(bj, chunk0 + c)) = u32x4{d[0], d[1], d[2], d[3]};
     }
   };
 
@@ -314,59 +338,70 @@ __global__ __launch_bounds__(T::NT) void grouped_gemm_kernel(Params p) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[mb][nb][j] = 0.0f;
 
-  auto mfma_kk = [&](int st, int kk) __attribute__((always_inline)) {
-    const uint8_t *sA = sA0 + st * T::STAGE_A;
-    const uint8_t *sB = sB0 + st * T::STAGE_B;
-    const int ch = kk * 2 + (lane >> 5);
+  // MFMA operand fragments of one K sub-step, double-buffered so the reads
+  // of sub-step kk+1 are in flight while sub-step kk multiplies.
+  struct Frags {
     bf16x8 a[T::MB], b[T::NB];
+  };
+  auto read_frags = [&](Frags &f, const uint8_t *sA, const uint8_t *sB, int kk) __attribute__((always_inline)) {
+    const int ch = kk * 2 + (lane >> 5);
 #pragma unroll
     for (int mb = 0; mb < T::MB; ++mb)
-      a[mb] = *reinterpret_cast<const bf16x8 *>(sA + swz(wm * T::WM + mb * 32 + (lane & 31), ch));
+      f.a[mb] = *reinterpret_cast<const bf16x8 *>(sA + swz<BK>(wm * T::WM + mb * 32 + (lane & 31), ch));
 #pragma unroll
     for (int nb = 0; nb < T::NB; ++nb)
-      b[nb] = *reinterpret_cast<const bf16x8 *>(sB + swz(wn * T::WN + nb * 32 + (lane & 31), ch));
+      f.b[nb] = *reinterpret_cast<const bf16x8 *>(sB + swz<BK>(wn * T::WN + nb * 32 + (lane & 31), ch));
+  };
+  auto mfma_frags = [&](const Frags &f) __attribute__((always_inline)) {
 #pragma unroll
     for (int mb = 0; mb < T::MB; ++mb)
 #pragma unroll
       for (int nb = 0; nb < T::NB; ++nb)
-        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mb], b[nb], acc[mb][nb], 0, 0, 0);
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[mb], f.b[nb], acc[mb][nb], 0, 0, 0);
   };
+  Frags f0, f1;
 
   // One K step: MFMAs on stage `cur` interleaved with the decode of the next
   // stage's B (loaded one iteration earlier) into the other buffer; the next
   // A tile and the B tile two steps ahead are in flight meanwhile. Loads past
   // the end are clamped to the last step, so the body is branch free.
   const int KT = static_cast<int>(p.K / BK);
-  auto step = [&](int kt, BRegs &b_next, BRegs &b_after) __attribute__((always_inline)) {
-    const int cur = kt & 1;
-    load_a(min(kt + 1, KT - 1));
+  // Stage (sA, sB) is multiplied while stage (nA, nB) is produced. f0 holds
+  // the first sub-step's fragments of (sA, sB) on entry, and of (nA, nB) on
+  // exit (read right after the barrier).
+  auto step = [&](int kt, const uint8_t *sA, const uint8_t *sB, uint8_t *nA, uint8_t *nB,
+                  BRegs &b_next, BRegs &b_after) __attribute__((always_inline)) {
+    load_a(min(kt + 1, KT - 1), nA);
     load_b(min(kt + 2, KT - 1), b_after);
     const Nf4Table t = FMT == MX_FMT_NF4 ? nf4_table(bf16_bits_to_f32(b_next.abs)) : Nf4Table{};
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      mfma_kk(cur, kk);
-      decode_b(b_next, t, cur ^ 1, kk);
+    for (int kk = 0; kk < T::KSUB; ++kk) {
+      Frags &cur = (kk & 1) ? f1 : f0;
+      Frags &nxt = (kk & 1) ? f0 : f1;
+      if (kk + 1 < T::KSUB) read_frags(nxt, sA, sB, kk + 1);
+      mfma_frags(cur);
+      decode_b(b_next, t, nB, kk);
     }
-    store_a(cur ^ 1);
     __syncthreads();
+    read_frags(f0, nA, nB, 0);
   };
 
-  load_a(0);
+  load_a(0, sA0);
   load_b(0, rb0);
   load_b(min(1, KT - 1), rb1);
-  store_a(0);
   {
     const Nf4Table t = FMT == MX_FMT_NF4 ? nf4_table(bf16_bits_to_f32(rb0.abs)) : Nf4Table{};
 #pragma unroll
-    for (int part = 0; part < 4; ++part) decode_b(rb0, t, 0, part);
+    for (int part = 0; part < T::KSUB; ++part) decode_b(rb0, t, sB0, part);
   }
   __syncthreads();
+  read_frags(f0, sA0, sB0, 0);
   int kt = 0;
   for (; kt + 1 < KT; kt += 2) {
-    step(kt, rb1, rb0);
-    step(kt + 1, rb0, rb1);
+    step(kt, sA0, sB0, sA1, sB1, rb1, rb0);
+    step(kt + 1, sA1, sB1, sA0, sB0, rb0, rb1);
   }
-  if (kt < KT) step(kt, rb1, rb0);
+  if (kt < KT) step(kt, sA0, sB0, sA1, sB1, rb1, rb0);
 
   // ------------------------------------------- LoRA up-projection (K = 32)
   // Staged in LDS here and multiplied block by block in the epilogue, into
@@ -374,9 +409,12 @@ __global__ __launch_bounds__(T::NT) void grouped_gemm_kernel(Params p) {
   // round both to bf16 before adding them, as the reference adds a bf16 LoRA
   // delta to a bf16 projection output (experts.py:3370-3374).
   constexpr int n_adapt = EPI == EPI_SWIGLU ? 2 : 1;
+  static_assert(n_adapt * T::BM * 64 <= T::STAGE_A && T::BN * 64 <= T::STAGE_B,
+                "LoRA tiles must fit in one stage buffer");
   uint8_t *sP = sA0;  // n_adapt x [BM][32] bf16
   uint8_t *sL = sB0;  // [BN][32] bf16
   if (LORA) {
+    __syncthreads();  // every wave is done with the stage buffers
     for (int idx = tid; idx < T::BM * 4 * n_adapt; idx += T::NT) {
       const int ad = idx / (T::BM * 4);
       const int rem = idx - ad * T::BM * 4;
@@ -495,17 +533,8 @@ int launch(const Params &p, int64_t max_row_tiles, hipStream_t s) {
     set_error("grouped GEMM grid too large");
     return MX_ERR_INVALID;
   }
-  auto kern = grouped_gemm_kernel<FMT, EPI, LORA, T>;
-  static bool configured = false;
-  if (!configured) {
-    // Dynamic LDS above 64 KiB; a runtime that needs no opt-in may refuse the
-    // attribute, which is harmless, so its status is consumed and dropped.
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS) != hipSuccess)
-      (void)hipGetLastError();
-    configured = true;
-  }
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(T::NT), T::LDS, s, p);
+  hipLaunchKernelGGL((grouped_gemm_kernel<FMT, EPI, LORA, T>), dim3(static_cast<unsigned>(grid)),
+                     dim3(T::NT), 0, s, p);
   return check_launch("grouped GEMM launch");
 }
 
@@ -516,8 +545,8 @@ inline bool use_tall_tiles(int64_t rows, int experts) { return rows >= 768 * sta
 template <int EPI, bool LORA>
 int launch_fmt(int fmt, Params p, const PlanLayout &PL, const PlanView &v, bool tall, hipStream_t s) {
   // Column tiles are 256 wide (EPI_SWIGLU: 128 ffn columns of gate and of up).
-  using Tall = Tile<256, 256, 2, 4>;
-  using Short = Tile<128, 256, 2, 4>;
+  using Tall = Tile<256, 256, 2, 4, 64>;
+  using Short = Tile<128, 256, 2, 4, 64>;
   p.tiles = tall ? v.tiles2 : v.tiles;
   p.num_tiles = tall ? v.num_tiles2 : v.num_tiles;
   const int64_t max_tiles = tall ? PL.max_tiles2 : PL.max_tiles;
@@ -637,7 +666,7 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
   p.seg_end = v.seg + experts;
   p.out = out;
   p.ldo = ldo;
-  return launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 128, 2, 2>>(p, max_tiles, s);
+  return launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 128, 2, 2, 64>>(p, max_tiles, s);
 }
 
 // gate/up grouped GEMM with SwiGLU epilogue, then the down grouped GEMM.
