@@ -152,7 +152,8 @@ int mx_scatter_add_rows(const void *rows_in, const float *row_scale, const int64
  * score[t,j] * y[t*k+j] accumulated in fp32, then cast to out_dtype.
  * Replaces the fp32 output.index_add_ of run_direct_routed
  * (experts.py:1786-1790, 2430-2438) and _CombineRoutedTokens.forward
- * (dispatch_ops.py:23-33); deterministic.
+ * (dispatch_ops.py:23-33); deterministic. top_scores may be NULL for unit
+ * weights (the per-token sum of the slot rows, as the permute backward).
  */
 int mx_combine(const void *y, const int64_t *top_idx, const void *top_scores,
                int score_dtype, int64_t num_tokens, int top_k, int num_experts,

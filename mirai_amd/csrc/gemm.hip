@@ -1,10 +1,14 @@
-// Grouped expert GEMMs on bf16 MFMA (v_mfma_f32_16x16x32_bf16, gfx950) over
+// Grouped expert GEMMs on bf16 MFMA (v_mfma_f32_32x32x16_bf16, gfx950) over
 // expert-sorted rows, with the frozen weights decoded from NF4 / INT8 on the
-// way into LDS, the per-expert LoRA up-projection fused as a K-extension of
-// the same accumulators, and three epilogues:
-//   EPI_SWIGLU : h = silu(x w1^T + dA1) * (x w3^T + dA3)   (gate/up pair)
-//   EPI_STORE  : y = x w^T + dA, rows written through a row map (down proj.)
-//   EPI_LORA_A : p = bf16(s * bf16(x a^T))  (LoRA down-projection, rank <= 32)
+// way into LDS, the per-expert LoRA up-projection fused into the epilogue, and
+// five epilogues. Forward (B = W^T, K along the weight rows' `in` axis):
+//   EPI_SWIGLU  : h = silu(x w1^T + dA1) * (x w3^T + dA3)   (gate/up pair)
+//   EPI_STORE   : y = x w^T + dA, rows written through a row map (down proj.)
+//   EPI_LORA_A  : p = bf16(s * bf16(x a^T))  (LoRA down-projection, rank <= 32)
+// Backward (B = W, K along the weights' `out` axis; the decoded rows land in
+// LDS n-major and reach the MFMA through ds_read_b64_tr_b16):
+//   EPI_DSWIGLU : dh = dy w2 + dz2 a2, then the SwiGLU backward -> [dG | dU]
+//   EPI_STORE2  : dx = [dG | dU] [w1; w3] + dz1 a1 + dz3 a3, through a row map
 //
 // Work decomposition: the dispatch plan lists row tiles (expert, first row) of
 // kTileM rows; a workgroup computes one (row tile, column tile) pair. The
@@ -15,6 +19,7 @@
 #include <stdlib.h>
 
 #include "common.h"
+#include "grads.h"
 #include "plan.h"
 
 namespace mx {
@@ -24,7 +29,10 @@ constexpr int kNf4Block = 64;   // NF4 absmax block along K
 constexpr int kLoraK = 32;      // LoRA rank padded to two MFMA K steps
 constexpr int kLoraLd = 96;     // low-rank activation row: [gate 32 | up 32 | down 32]
 
-enum { EPI_SWIGLU = 0, EPI_STORE = 1, EPI_LORA_A = 2 };
+enum { EPI_SWIGLU = 0, EPI_STORE = 1, EPI_LORA_A = 2, EPI_DSWIGLU = 3, EPI_STORE2 = 4 };
+
+// Backward epilogues multiply by W itself rather than W^T.
+constexpr bool trans_b(int epi) { return epi == EPI_DSWIGLU || epi == EPI_STORE2; }
 
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 
@@ -59,6 +67,7 @@ struct Params {
   const void *w[4];          // per B-row group: weight data
   const uint16_t *wscale[4]; // NF4 absmax / INT8 scale
   int64_t wn[4];             // rows per expert of each weight
+  int64_t k_split;           // transposed B: K rows taken from w[0], the rest from w[1]
   int64_t N;                 // output columns
   int n_tiles_n;
   const uint16_t *lora_p;    // [R, ldp] scaled low-rank activations
@@ -73,6 +82,8 @@ struct Params {
   const int32_t *out_row;    // sorted row -> output row (null: identity)
   uint16_t *save_gate;
   uint16_t *save_up;
+  const uint16_t *gate_in;   // EPI_DSWIGLU: forward gate / up pre-activations [R, N]
+  const uint16_t *up_in;
   float scale[4];
 };
 
@@ -117,6 +128,38 @@ __device__ __forceinline__ int swz(int row, int chunk) {
 }
 __device__ __forceinline__ int swz64(int row, int chunk) {  // 64-byte rows (LoRA tiles)
   return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
+}
+
+// Transposed B stage: [64 k rows][256 n] bf16 (512-byte rows, 32 chunks). The
+// chunk index is XOR-ed with a permutation of the row's low 4 bits so that
+//  * a row-owner ds_write_b128 (16 lanes = 16 consecutive rows, one logical
+//    chunk) hits 16 distinct 16-byte bank groups, and
+//  * a ds_read_b64_tr_b16 half-wave (4 consecutive rows x 4 chunks) does too.
+__device__ __forceinline__ int swz_t(int row, int chunk) {
+  const int x = ((row & 3) << 2) | ((row >> 2) & 3);
+  return row * 512 + ((chunk ^ x) << 4);
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// B fragment of v_mfma_f32_32x32x16_bf16 (lane: column lane%32, k = 8*(lane/32)
+// + 0..7) read from a transposed stage. ds_read_b64_tr_b16 hands lane j of a
+// 16-lane group the elements j, 16+j, 32+j, 48+j of the group's concatenated
+// 8-byte chunks; lane i of the group therefore fetches row k0 + i/4, columns
+// c0 + 4*(i%4) .. +3, and receives column c0 + j of rows k0 .. k0+3.
+__device__ __forceinline__ bf16x8 read_b_trans(const uint8_t *sB, int ncol0, int kk, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const int row = 16 * kk + 8 * (g >> 1) + (i >> 2);
+  const int col = ncol0 + 16 * (g & 1) + 4 * (i & 3);
+  const int chunk = col >> 3, half = ((col >> 2) & 1) * 8;
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4 *>(
+      reinterpret_cast<uintptr_t>(sB + swz_t(row, chunk) + half)));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4 *>(
+      reinterpret_cast<uintptr_t>(sB + swz_t(row + 4, chunk) + half)));
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  const i16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);
 }
 
 // NF4 decode in registers. `lo`/`hi` hold the low / high bytes of the 16
@@ -223,15 +266,22 @@ void grouped_gemm_kernel(Params p) {
   }
 
   // ------------------------------------------------------- B (weights)
+  constexpr bool TRANS = trans_b(EPI);
+  static_assert(!TRANS || (T::NT == 512 && T::BK == 64 && T::BN == 256),
+                "transposed B assumes 8 waves, BK 64 and BN 256");
   const int bj = tid / T::B_TPR, bh = tid % T::B_TPR;
-  int which;
-  int64_t bn;
-  b_row<EPI, T>(bj, nt, which, bn);
+  int which = 0;
+  int64_t bn = 0;
+  if (!TRANS) b_row<EPI, T>(bj, nt, which, bn);
+  // Transposed B: lane = k row of the stage, wave = 32-column slice. Columns
+  // past N re-read the last full 32-column slice (discarded by the epilogue).
+  const int tk = tid & 63, tc = tid >> 6;
+  const int64_t t_col0 = TRANS ? min(static_cast<int64_t>(nt) * T::BN + 32 * tc, p.N - 32) : 0;
   // Weight rows past N (a partial column tile) re-read row N-1: they only
   // feed output columns the epilogue discards. The LoRA down-projection
   // keeps explicit zeros, as its absent adapters have no rows at all.
   const int64_t wn_rows = pick(p.wn, which);
-  const bool b_valid = EPI == EPI_LORA_A ? bn < wn_rows : true;
+  const bool b_valid = EPI == EPI_LORA_A ? bn < wn_rows : !TRANS;
   if (EPI != EPI_LORA_A) bn = min(bn, wn_rows - 1);
   const int64_t wrow = static_cast<int64_t>(e) * wn_rows + bn;
   const uint8_t *b_base = nullptr;
@@ -274,7 +324,28 @@ void grouped_gemm_kernel(Params p) {
           16, 0, 0);
   };
   auto load_b = [&](int kt, BRegs &rb) __attribute__((always_inline)) {
-    if (b_valid) {
+    if (TRANS) {
+      const int64_t kb = static_cast<int64_t>(kt) * BK;
+      const bool second = kb >= p.k_split;
+      const int64_t krow = kb - (second ? p.k_split : 0) + tk;
+      const uint8_t *w = static_cast<const uint8_t *>(second ? p.w[1] : p.w[0]);
+      const uint16_t *ws = second ? p.wscale[1] : p.wscale[0];
+      const int64_t wrow = static_cast<int64_t>(e) * (second ? p.wn[1] : p.wn[0]) + krow;
+      if (FMT == MX_FMT_NF4) {
+        rb.q[0] = *reinterpret_cast<const u32x4 *>(w + wrow * (p.N / 2) + t_col0 / 2);
+        rb.abs = ws[wrow * (p.N / kNf4Block) + t_col0 / kNf4Block];
+      } else if (FMT == MX_FMT_INT8) {
+#pragma unroll
+        for (int q = 0; q < kBRegs; ++q)
+          rb.q[q] = *reinterpret_cast<const u32x4 *>(w + wrow * p.N + t_col0 + 16 * q);
+        rb.abs = ws[wrow];
+      } else {
+#pragma unroll
+        for (int q = 0; q < kBRegs; ++q)
+          rb.q[q] = *reinterpret_cast<const u32x4 *>(w + (wrow * p.N + t_col0) * 2 + 16 * q);
+        rb.abs = 0;
+      }
+    } else if (b_valid) {
 #pragma unroll
       for (int q = 0; q < kBRegs; ++q)
         rb.q[q] = *reinterpret_cast<const u32x4 *>(b_base + static_cast<int64_t>(kt) * kBStageBytes + 16 * q);
@@ -295,6 +366,7 @@ void grouped_gemm_kernel(Params p) {
     for (int cc = 0; cc < kChunksPerPart; ++cc) {
       const int c = part * kChunksPerPart + cc;  // output chunk: 8 elements
       uint32_t d[4];
+      const float sc = TRANS ? bf16_bits_to_f32(rb.abs) : b_scale;
       if (FMT == MX_FMT_NF4) {
         // chunk c = code bytes 4c..4c+3 = dword c of the packed registers
         const u32x4 v = rb.q[c >> 2];
@@ -313,8 +385,8 @@ void grouped_gemm_kernel(Params p) {
           const float q1 = static_cast<float>(static_cast<int8_t>((w >> 8) & 0xffu));
           const float q2 = static_cast<float>(static_cast<int8_t>((w >> 16) & 0xffu));
           const float q3 = static_cast<float>(static_cast<int8_t>(w >> 24));
-          d[2 * h] = pack_bf16x2(q0 * b_scale, q1 * b_scale);
-          d[2 * h + 1] = pack_bf16x2(q2 * b_scale, q3 * b_scale);
+          d[2 * h] = pack_bf16x2(q0 * sc, q1 * sc);
+          d[2 * h + 1] = pack_bf16x2(q2 * sc, q3 * sc);
         }
       } else {
         const u32x4 v = rb.q[c];
@@ -323,7 +395,8 @@ void grouped_gemm_kernel(Params p) {
         d[2] = v[2];
         d[3] = v[3];
       }
-      *reinterpret_cast<u32x4 *>(sB + swz<BK>(bj, chunk0 + c)) = u32x4{d[0], d[1], d[2], d[3]};
+      const int addr = TRANS ? swz_t(tk, 4 * tc + c) : swz<BK>(bj, chunk0 + c);
+      *reinterpret_cast<u32x4 *>(sB + addr) = u32x4{d[0], d[1], d[2], d[3]};
     }
   };
 
@@ -350,7 +423,8 @@ void grouped_gemm_kernel(Params p) {
       f.a[mb] = *reinterpret_cast<const bf16x8 *>(sA + swz<BK>(wm * T::WM + mb * 32 + (lane & 31), ch));
 #pragma unroll
     for (int nb = 0; nb < T::NB; ++nb)
-      f.b[nb] = *reinterpret_cast<const bf16x8 *>(sB + swz<BK>(wn * T::WN + nb * 32 + (lane & 31), ch));
+      f.b[nb] = TRANS ? read_b_trans(sB, wn * T::WN + nb * 32, kk, lane)
+                      : *reinterpret_cast<const bf16x8 *>(sB + swz<BK>(wn * T::WN + nb * 32 + (lane & 31), ch));
   };
   auto mfma_frags = [&](const Frags &f) __attribute__((always_inline)) {
 #pragma unroll
@@ -408,11 +482,14 @@ void grouped_gemm_kernel(Params p) {
   // accumulators kept apart from the frozen projection so the epilogue can
   // round both to bf16 before adding them, as the reference adds a bf16 LoRA
   // delta to a bf16 projection output (experts.py:3370-3374).
-  constexpr int n_adapt = EPI == EPI_SWIGLU ? 2 : 1;
-  static_assert(n_adapt * T::BM * 64 <= T::STAGE_A && T::BN * 64 <= T::STAGE_B,
+  // n_adapt low-rank activation tiles [BM][32] (gate and up for EPI_SWIGLU,
+  // dz1 and dz3 for EPI_STORE2) and n_lb factor tiles [BN][32].
+  constexpr int n_adapt = (EPI == EPI_SWIGLU || EPI == EPI_STORE2) ? 2 : 1;
+  constexpr int n_lb = EPI == EPI_STORE2 ? 2 : 1;
+  static_assert(n_adapt * T::BM * 64 <= T::STAGE_A && n_lb * T::BN * 64 <= T::STAGE_B,
                 "LoRA tiles must fit in one stage buffer");
-  uint8_t *sP = sA0;  // n_adapt x [BM][32] bf16
-  uint8_t *sL = sB0;  // [BN][32] bf16
+  uint8_t *sP = sA0;
+  uint8_t *sL = sB0;
   if (LORA) {
     __syncthreads();  // every wave is done with the stage buffers
     for (int idx = tid; idx < T::BM * 4 * n_adapt; idx += T::NT) {
@@ -421,24 +498,24 @@ void grouped_gemm_kernel(Params p) {
       const int r = rem >> 2, c = rem & 3;
       const int64_t grow = row0 + r;
       u32x4 v = u32x4{0u, 0u, 0u, 0u};
-      if (grow < row_end)
+      // Absent adapters' columns may hold stale data: never read them.
+      if (grow < row_end && c * 8 < pick2(p.lora_r, ad))
         v = *reinterpret_cast<const u32x4 *>(p.lora_p + grow * p.ldp + ad * 32 + c * 8);
       *reinterpret_cast<u32x4 *>(sP + ad * T::BM * 64 + swz64(r, c)) = v;
     }
-    {
-      const int lw = EPI == EPI_SWIGLU ? which : 0;
+    for (int idx = tid; idx < T::BN * 4 * n_lb; idx += T::NT) {
+      const int ad = idx / (T::BN * 4);
+      const int rem = idx - ad * T::BN * 4;
+      const int j = rem >> 2, c = rem & 3;
+      int lw = ad;
+      int64_t n = static_cast<int64_t>(nt) * T::BN + j;
+      if (EPI == EPI_SWIGLU) b_row<EPI, T>(j, nt, lw, n);
       const int r = pick2(p.lora_r, lw);
       const uint16_t *lb = pick2(p.lora_b, lw);
-      constexpr int kLChunks = 4 / T::B_TPR > 0 ? 4 / T::B_TPR : 1;
-#pragma unroll
-      for (int q = 0; q < kLChunks; ++q) {
-        const int c = bh * kLChunks + q;
-        if (c >= 4) break;
-        u32x4 v = u32x4{0u, 0u, 0u, 0u};
-        if (lb && c * 8 < r)
-          v = *reinterpret_cast<const u32x4 *>(lb + (static_cast<int64_t>(e) * p.N + bn) * r + c * 8);
-        *reinterpret_cast<u32x4 *>(sL + swz64(bj, c)) = v;
-      }
+      u32x4 v = u32x4{0u, 0u, 0u, 0u};
+      if (lb && c * 8 < r && n < p.N)
+        v = *reinterpret_cast<const u32x4 *>(lb + (static_cast<int64_t>(e) * p.N + n) * r + c * 8);
+      *reinterpret_cast<u32x4 *>(sL + ad * T::BN * 64 + swz64(j, c)) = v;
     }
     __syncthreads();
   }
@@ -446,15 +523,18 @@ void grouped_gemm_kernel(Params p) {
     f32x16 t;
 #pragma unroll
     for (int j = 0; j < 16; ++j) t[j] = 0.0f;
-    const int ad = EPI == EPI_SWIGLU ? (nb / (T::NB / 2)) : 0;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int ch = kk * 2 + (lane >> 5);
-      const bf16x8 a = *reinterpret_cast<const bf16x8 *>(
-          sP + ad * T::BM * 64 + swz64(wm * T::WM + mb * 32 + (lane & 31), ch));
-      const bf16x8 b = *reinterpret_cast<const bf16x8 *>(
-          sL + swz64(wn * T::WN + nb * 32 + (lane & 31), ch));
-      t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, t, 0, 0, 0);
+    for (int a2 = 0; a2 < n_lb; ++a2) {
+      const int ad = EPI == EPI_SWIGLU ? (nb / (T::NB / 2)) : a2;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int ch = kk * 2 + (lane >> 5);
+        const bf16x8 a = *reinterpret_cast<const bf16x8 *>(
+            sP + ad * T::BM * 64 + swz64(wm * T::WM + mb * 32 + (lane & 31), ch));
+        const bf16x8 b = *reinterpret_cast<const bf16x8 *>(
+            sL + a2 * T::BN * 64 + swz64(wn * T::WN + nb * 32 + (lane & 31), ch));
+        t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, t, 0, 0, 0);
+      }
     }
     return t;
   };
@@ -505,13 +585,30 @@ void grouped_gemm_kernel(Params p) {
         for (int j = 0; j < 16; ++j) {
           const int64_t r = rbase + mb * 32 + 8 * (j >> 2) + (j & 3);
           if (r >= row_end) continue;
-          if (EPI == EPI_STORE) {
+          if (EPI == EPI_STORE || EPI == EPI_STORE2) {
             const int64_t n = static_cast<int64_t>(nt) * T::BN + ncol;
             if (n >= p.N) continue;
             float v = round_bf16(acc[mb][nb][j]);
             if (LORA) v = round_bf16(v + round_bf16(l2[j]));
             const int64_t orow = p.out_row ? static_cast<int64_t>(p.out_row[r]) : r;
             p.out[orow * p.ldo + n] = f32_to_bf16_bits(v);
+          } else if (EPI == EPI_DSWIGLU) {
+            // dh -> (dG, dU) through h = bf16(silu(g)) * u, each op rounded to
+            // bf16 as autograd of the bf16 reference composition does; the
+            // silu derivative is formed in fp32 (silu_backward).
+            const int64_t f = static_cast<int64_t>(nt) * T::BN + ncol;
+            if (f >= p.N) continue;
+            float dh = round_bf16(acc[mb][nb][j]);
+            if (LORA) dh = round_bf16(dh + round_bf16(l2[j]));
+            const float g = bf16_bits_to_f32(p.gate_in[r * p.N + f]);
+            const float u = bf16_bits_to_f32(p.up_in[r * p.N + f]);
+            const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+            const float sg = round_bf16(g * sig);
+            const float dsg = round_bf16(dh * u);
+            const float du = dh * sg;
+            const float dg = dsg * (sig * (1.0f + g * (1.0f - sig)));
+            p.out[r * p.ldo + f] = f32_to_bf16_bits(dg);
+            p.out[r * p.ldo + p.N + f] = f32_to_bf16_bits(du);
           } else {
             if (ncol >= p.N) continue;
             // bf16(x a^T) first, then the LoRA scale, as low_rank.to(bf16) * scale.
@@ -760,11 +857,226 @@ int check_layer(const char *name, int64_t hidden, int64_t ffn, const mx_weight *
   return MX_OK;
 }
 
+// ------------------------------------------------------------ backward
+struct BackLayout {
+  PlanLayout plan;
+  size_t off_dy = 0, off_dgu = 0, off_dz = 0, off_fact[6] = {}, bytes = 0;
+};
+
+// Scratch of the backward: plan, dy [R, d] (slot order; reused for the per-
+// slot dx rows), [dG | dU] [R, 2f] and dz [R, 96] (sorted order), and the six
+// transposed LoRA factors (B2^T, A2^T, B1^T, A1^T, B3^T, A3^T) at rank <= 32.
+BackLayout back_layout(int64_t rows, int num_experts, int64_t hidden, int64_t ffn) {
+  BackLayout L;
+  L.plan = plan_layout(rows, num_experts);
+  size_t off = align_up(L.plan.bytes, 256);
+  L.off_dy = off;
+  off = align_up(off + sizeof(uint16_t) * rows * hidden, 256);
+  L.off_dgu = off;
+  off = align_up(off + sizeof(uint16_t) * rows * 2 * ffn, 256);
+  L.off_dz = off;
+  off = align_up(off + sizeof(uint16_t) * rows * kLoraLd, 256);
+  const int64_t fact[6] = {hidden, ffn, ffn, hidden, ffn, hidden};
+  for (int i = 0; i < 6; ++i) {
+    L.off_fact[i] = off;
+    off = align_up(off + sizeof(uint16_t) * num_experts * kLoraK * fact[i], 256);
+  }
+  L.bytes = off;
+  return L;
+}
+
+struct LoraGradJob {
+  const uint16_t *m;
+  int64_t ldm;
+  const int32_t *map;
+  const uint16_t *v;
+  int64_t cols;
+  float *out;
+  bool a_layout;  // [E, r, cols] (dA) rather than [E, cols, r] (dB)
+};
+
+int run_lora_grad(const LoraGradJob &j, int rank, const PlanView &v, int experts, hipStream_t s) {
+  if (!j.out) return MX_OK;
+  const int64_t se = j.cols * rank;
+  return lora_weight_grad(j.m, j.ldm, j.map, j.v, kLoraLd, rank, j.cols, v.seg, v.seg + experts,
+                          experts, j.out, se, j.a_layout ? 1 : rank, j.a_layout ? j.cols : 1, s);
+}
+
 }  // namespace gemm
 }  // namespace mx
 
 using namespace mx;
 using namespace mx::gemm;
+
+extern "C" size_t mx_moe_backward_workspace_size(int64_t num_tokens, int top_k, int num_experts,
+                                                 int64_t hidden, int64_t ffn) {
+  if (num_tokens < 0 || top_k <= 0 || num_experts <= 0 || hidden <= 0 || ffn <= 0) return 0;
+  return back_layout(num_tokens * top_k, num_experts, hidden, ffn).bytes;
+}
+
+extern "C" int mx_moe_backward(const void *grad_out, int grad_dtype, const void *tokens,
+                               const int64_t *top_idx, const void *top_scores, int score_dtype,
+                               int64_t num_tokens, int top_k, int num_experts, int64_t hidden,
+                               int64_t ffn, const mx_weight *w1, const mx_weight *w3,
+                               const mx_weight *w2, const mx_lora *l1, const mx_lora *l3,
+                               const mx_lora *l2, const void *save_gate, const void *save_up,
+                               const void *save_h, const void *save_y, const void *save_lora,
+                               void *grad_tokens, int grad_tokens_dtype, float *grad_scores,
+                               float *grad_a1, float *grad_b1, float *grad_a3, float *grad_b3,
+                               float *grad_a2, float *grad_b2, void *workspace, void *stream) {
+  clear_error();
+  const char *name = "mx_moe_backward";
+  int rc = validate_plan_args(name, num_tokens, top_k, num_experts);
+  if (rc) return rc;
+  if ((rc = check_layer(name, hidden, ffn, w1, w3, w2, l1, l3, l2))) return rc;
+  if (num_tokens == 0) return MX_OK;
+  const bool lora1 = has_lora(l1), lora3 = has_lora(l3), lora2 = has_lora(l2);
+  if (!grad_out || !tokens || !top_idx || !top_scores || !save_gate || !save_up || !save_h ||
+      !save_y || !grad_tokens || !grad_scores || !workspace ||
+      ((lora1 || lora3 || lora2) && !save_lora)) {
+    set_error("%s: gradients, routes, saved activations and workspace must be non-null", name);
+    return MX_ERR_INVALID;
+  }
+  if ((grad_dtype != MX_DTYPE_BF16 && grad_dtype != MX_DTYPE_F32) ||
+      (grad_tokens_dtype != MX_DTYPE_BF16 && grad_tokens_dtype != MX_DTYPE_F32)) {
+    set_error("%s: gradients must be bf16 or fp32", name);
+    return MX_ERR_INVALID;
+  }
+  hipStream_t s = as_stream(stream);
+  const int64_t R = num_tokens * top_k;
+  const BackLayout L = back_layout(R, num_experts, hidden, ffn);
+  char *ws = static_cast<char *>(workspace);
+  const PlanView v = plan_view(ws, L.plan);
+  uint16_t *dy = reinterpret_cast<uint16_t *>(ws + L.off_dy);
+  uint16_t *dgu = reinterpret_cast<uint16_t *>(ws + L.off_dgu);
+  uint16_t *dz = reinterpret_cast<uint16_t *>(ws + L.off_dz);
+  uint16_t *fact[6];
+  for (int i = 0; i < 6; ++i) fact[i] = reinterpret_cast<uint16_t *>(ws + L.off_fact[i]);
+  const uint16_t *x = static_cast<const uint16_t *>(tokens);
+  const uint16_t *lsave = static_cast<const uint16_t *>(save_lora);
+  const uint16_t *g_in = static_cast<const uint16_t *>(save_gate);
+  const uint16_t *u_in = static_cast<const uint16_t *>(save_up);
+  const uint16_t *h_in = static_cast<const uint16_t *>(save_h);
+
+  // Plan (the forward's, rebuilt: the counting sort is deterministic).
+  mark_stage(0, s);
+  rc = build_plan(top_idx, nullptr, score_dtype, num_tokens, top_k, num_experts, nullptr, nullptr,
+                  nullptr, nullptr, nullptr, nullptr, nullptr, ws, s);
+  if (rc) return rc;
+  // dy = grad_out * score per slot, and the score gradients.
+  rc = mx_combine_backward(grad_out, grad_dtype, save_y, top_idx, top_scores, score_dtype,
+                           num_tokens, top_k, num_experts, hidden, dy, grad_scores, stream);
+  if (rc) return rc;
+  mark_stage(1, s);
+
+  // Down projection: dz2 = s2 * dy B2, then dh = dy W2 + dz2 A2 and the
+  // SwiGLU backward into [dG | dU].
+  if (lora2) {
+    const int r = l2->rank;
+    if ((rc = transpose_factors(static_cast<const uint16_t *>(l2->b), num_experts, hidden, r,
+                                fact[0], s)))
+      return rc;
+    if ((rc = transpose_factors(static_cast<const uint16_t *>(l2->a), num_experts, r, ffn,
+                                fact[1], s)))
+      return rc;
+    const mx_lora t = {fact[0], nullptr, r, l2->scale};
+    const mx_lora *ad[1] = {&t};
+    if ((rc = lora_down(v, num_experts, L.plan.max_tiles, dy, hidden, v.row_slot, hidden, ad, 1,
+                        dz + 64, kLoraLd, s)))
+      return rc;
+  }
+  mark_stage(2, s);
+  {
+    Params p = base_params(v);
+    p.x = dy;
+    p.ldx = hidden;
+    p.row_token = v.row_slot;
+    p.K = hidden;
+    p.w[0] = w2->data;
+    p.wscale[0] = static_cast<const uint16_t *>(w2->scale);
+    p.wn[0] = hidden;
+    p.k_split = hidden;
+    p.N = ffn;
+    p.lora_p = dz + 64;
+    p.ldp = kLoraLd;
+    p.lora_b[0] = lora2 ? fact[1] : nullptr;
+    p.lora_r[0] = lora2 ? l2->rank : 0;
+    p.seg_end = v.seg + num_experts;
+    p.out = dgu;
+    p.ldo = 2 * ffn;
+    p.gate_in = g_in;
+    p.up_in = u_in;
+    if ((rc = launch_any<EPI_DSWIGLU>(w2->format, lora2, p, L.plan, v, s))) return rc;
+  }
+  mark_stage(3, s);
+  if (lora2) {
+    const LoraGradJob jb = {dy, hidden, v.row_slot, lsave + 64, hidden, grad_b2, false};
+    const LoraGradJob ja = {h_in, ffn, nullptr, dz + 64, ffn, grad_a2, true};
+    if ((rc = run_lora_grad(jb, l2->rank, v, num_experts, s))) return rc;
+    if ((rc = run_lora_grad(ja, l2->rank, v, num_experts, s))) return rc;
+  }
+
+  // Gate / up projections: dz1 = s1 * dG B1, dz3 = s3 * dU B3, then per-slot
+  // dx = dG W1 + dU W3 + dz1 A1 + dz3 A3 (written over dy, slot order).
+  const mx_lora *l13[2] = {l1, l3};
+  for (int i = 0; i < 2; ++i) {
+    const mx_lora *l = l13[i];
+    if (!has_lora(l)) continue;
+    const int r = l->rank;
+    uint16_t *bt = fact[2 + 2 * i], *at = fact[3 + 2 * i];
+    if ((rc = transpose_factors(static_cast<const uint16_t *>(l->b), num_experts, ffn, r, bt, s)))
+      return rc;
+    if ((rc = transpose_factors(static_cast<const uint16_t *>(l->a), num_experts, r, hidden, at,
+                                s)))
+      return rc;
+    const mx_lora t = {bt, nullptr, r, l->scale};
+    const mx_lora *ad[1] = {&t};
+    if ((rc = lora_down(v, num_experts, L.plan.max_tiles, dgu + i * ffn, 2 * ffn, nullptr, ffn, ad,
+                        1, dz + 32 * i, kLoraLd, s)))
+      return rc;
+  }
+  mark_stage(4, s);
+  {
+    Params p = base_params(v);
+    p.x = dgu;
+    p.ldx = 2 * ffn;
+    p.row_token = nullptr;
+    p.K = 2 * ffn;
+    p.w[0] = w1->data;
+    p.w[1] = w3->data;
+    p.wscale[0] = static_cast<const uint16_t *>(w1->scale);
+    p.wscale[1] = static_cast<const uint16_t *>(w3->scale);
+    p.wn[0] = p.wn[1] = ffn;
+    p.k_split = ffn;
+    p.N = hidden;
+    p.lora_p = dz;
+    p.ldp = kLoraLd;
+    p.lora_b[0] = lora1 ? fact[3] : nullptr;
+    p.lora_b[1] = lora3 ? fact[5] : nullptr;
+    p.lora_r[0] = lora1 ? l1->rank : 0;
+    p.lora_r[1] = lora3 ? l3->rank : 0;
+    p.seg_end = v.seg + num_experts;
+    p.out = dy;
+    p.ldo = hidden;
+    p.out_row = v.row_slot;
+    if ((rc = launch_any<EPI_STORE2>(w1->format, lora1 || lora3, p, L.plan, v, s))) return rc;
+  }
+  mark_stage(5, s);
+  for (int i = 0; i < 2; ++i) {
+    const mx_lora *l = l13[i];
+    if (!has_lora(l)) continue;
+    const LoraGradJob jb = {dgu + i * ffn, 2 * ffn, nullptr, lsave + 32 * i, ffn,
+                            i ? grad_b3 : grad_b1, false};
+    const LoraGradJob ja = {x, hidden, v.row_token, dz + 32 * i, hidden, i ? grad_a3 : grad_a1, true};
+    if ((rc = run_lora_grad(jb, l->rank, v, num_experts, s))) return rc;
+    if ((rc = run_lora_grad(ja, l->rank, v, num_experts, s))) return rc;
+  }
+  // grad_tokens[t] = sum of its slots' dx rows (fp32, ascending expert order).
+  rc = mx_combine(dy, top_idx, nullptr, score_dtype, num_tokens, top_k, num_experts, hidden,
+                  grad_tokens, grad_tokens_dtype, stream);
+  mark_stage(6, s);
+  return rc;
+}
 
 extern "C" size_t mx_moe_workspace_size(int64_t num_tokens, int top_k, int num_experts,
                                         int64_t hidden, int64_t ffn) {

@@ -1,0 +1,24 @@
+// Small kernels of the layer backward: LoRA factor transposes and the
+// per-expert LoRA weight gradients.
+#pragma once
+
+#include "common.h"
+
+namespace mx {
+
+// dst[e][c][r] = src[e][r][c] for bf16 src [E, rows, cols] (dst [E, cols, rows]).
+int transpose_factors(const uint16_t *src, int64_t experts, int64_t rows, int64_t cols,
+                      uint16_t *dst, hipStream_t s);
+
+// Per-expert outer-product sums over the expert's sorted rows:
+//   G[e, c, j] = sum_{r in [seg_start[e], seg_end[e])} M[map(r), c] * V[r, j]
+// for c < cols, j < rank (fp32 accumulation, fp32 output at
+// out + e*stride_e + c*stride_c + j*stride_j). M and V are bf16 with leading
+// dimensions ldm / ldv; map (null: identity) sends a sorted row to its M row.
+// rank is 8, 16, 24 or 32.
+int lora_weight_grad(const uint16_t *m, int64_t ldm, const int32_t *map, const uint16_t *v,
+                     int64_t ldv, int rank, int64_t cols, const int64_t *seg_start,
+                     const int64_t *seg_end, int experts, float *out, int64_t stride_e,
+                     int64_t stride_c, int64_t stride_j, hipStream_t s);
+
+}  // namespace mx

@@ -69,7 +69,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *y, const i
   int slot[kMaxK];
   const int n = sorted_slots(top_idx + t * k, k, E, slot);
   float sc[kMaxK];
-  for (int j = 0; j < n; ++j) sc[j] = load_score(top_scores, t * k + slot[j], score_dtype);
+  for (int j = 0; j < n; ++j)
+    sc[j] = top_scores ? load_score(top_scores, t * k + slot[j], score_dtype) : 1.0f;
   for (int64_t c0 = static_cast<int64_t>(threadIdx.x) * 8; c0 < cols; c0 += 256 * 8) {
     float acc[8];
 #pragma unroll
@@ -187,8 +188,8 @@ extern "C" int mx_combine(const void *y, const int64_t *top_idx, const void *top
     return MX_ERR_INVALID;
   }
   if (num_tokens == 0) return MX_OK;
-  if (!y || !top_idx || !top_scores || !out) {
-    set_error("mx_combine: buffers must be non-null");
+  if (!y || !top_idx || !out) {
+    set_error("mx_combine: y, top_idx and out must be non-null");
     return MX_ERR_INVALID;
   }
   hipLaunchKernelGGL(combine_kernel, dim3(num_tokens), dim3(256), 0, as_stream(stream),
