@@ -1,0 +1,127 @@
+"""Host-side behaviour of the drop-in module (CPU only): argument validation
+and error types of CompressedGroupedExperts, LoRA adapter state, policy
+normalisation, and that the product path refuses to run without the GPU
+library instead of falling back to a CPU path.
+
+Error types and messages follow
+mirai/core/models/compressed_weights/execution/experts.py:189-196, 544-558,
+756-769, 1662-1666 and 1755-1769.
+"""
+
+import pytest
+import torch
+
+from mirai_amd import CompressedGroupedExperts, route_topk
+from mirai_amd import _native as nat
+from mirai_amd import quant
+from mirai_amd.lora import ActiveExpertLoRA, lora_scale
+from mirai_amd.specs import ExpertMLPExecutionSpec, normalize_expert_weight_access_policy
+
+
+def _module(**kw):
+    kw.setdefault("num_experts", 4)
+    kw.setdefault("expert_weight_access", "chunked_dequant")
+    kw.setdefault("expert_dequant_chunk_size", 2)
+    kw.setdefault("quant_format", "nf4")
+    return CompressedGroupedExperts.from_empty(**kw)
+
+
+def test_from_empty_validation():
+    with pytest.raises(ValueError):
+        _module(num_experts=0)
+    with pytest.raises(ValueError):
+        _module(num_experts=1025)
+    with pytest.raises(ValueError):
+        _module(nf4_blocksize=128)
+    with pytest.raises(ValueError):
+        _module(quant_format="fp8")
+    with pytest.raises(TypeError):
+        _module(execution_spec=object())
+
+
+def test_access_policy_rules():
+    m = _module(expert_weight_access="full_dequant", expert_dequant_chunk_size=0)
+    assert not m.prefers_for_loop()
+    with pytest.raises(ValueError, match="expert_dequant_chunk_size > 0"):
+        m.set_expert_weight_access_policy(expert_weight_access="chunked_dequant",
+                                          expert_dequant_chunk_size=0)
+    m.set_expert_weight_access_policy(expert_weight_access="chunked_dequant",
+                                      expert_dequant_chunk_size=8)
+    assert m.prefers_for_loop() and m.expert_dequant_chunk_size == 8
+    m.set_expert_weight_access_policy(expert_weight_access="active_dequant")
+    assert m.prefers_for_loop()
+    # A module built with a chunked policy and no chunk size gets the default.
+    assert _module(expert_dequant_chunk_size=0).expert_dequant_chunk_size > 0
+    assert normalize_expert_weight_access_policy("auto") == "auto"
+    with pytest.raises(ValueError):
+        normalize_expert_weight_access_policy("nonsense")
+
+
+def test_run_direct_routed_validation_order():
+    tokens = torch.zeros(6, 64)
+    scores = torch.zeros(6, 2)
+    idx = torch.zeros(6, 2, dtype=torch.long)
+    full = _module(expert_weight_access="full_dequant", expert_dequant_chunk_size=0)
+    with pytest.raises(RuntimeError, match="requires active_dequant"):
+        full.run_direct_routed(tokens, scores, idx)
+    m = _module()
+    with pytest.raises(ValueError, match="matching"):
+        m.run_direct_routed(tokens, scores[:, :1], idx)
+    with pytest.raises(ValueError, match="token count"):
+        m.run_direct_routed(tokens[:5], scores, idx)
+    with pytest.raises(RuntimeError, match="missing weights"):
+        m.run_direct_routed(tokens, scores, idx)
+    with pytest.raises(RuntimeError, match="missing weights"):
+        m.run_for_loop(tokens, torch.tensor([6, 0, 0, 0]))
+
+
+def test_attach_lora_validation():
+    m = _module()
+    with pytest.raises(ValueError, match="Unknown grouped expert LoRA tensor"):
+        m.attach_expert_lora(tensor_name="w9", adapter_name="a", rank=8, alpha=16)
+    with pytest.raises(AttributeError):
+        m.attach_expert_lora(tensor_name="w1", adapter_name="a", rank=8, alpha=16)  # not loaded
+
+
+def test_quantisation_needs_the_gpu_and_fails_loudly():
+    m = _module()
+    with pytest.raises(nat.NativeLibraryError):
+        m.load_dense_weight("w1", torch.zeros(4, 128, 64))
+    with pytest.raises(ValueError):
+        quant.quantize(torch.zeros(4, 128, 96), "nf4")  # in_features % 64
+    with pytest.raises(ValueError):
+        m.load_dense_weight("w7", torch.zeros(4, 128, 64))
+
+
+def test_routing_refuses_cpu_tensors():
+    with pytest.raises((nat.NativeLibraryError, ValueError)):
+        route_topk(torch.randn(8, 16), 2)
+
+
+def test_active_expert_lora_state():
+    ad = ActiveExpertLoRA(adapter_name="a", num_experts=3, in_features=64, out_features=32,
+                          rank=12, alpha=24.0)
+    assert ad.lora_a.shape == (3, 12, 64) and ad.lora_b.shape == (3, 32, 12)
+    assert torch.count_nonzero(ad.lora_b) == 0 and torch.count_nonzero(ad.lora_a) > 0
+    assert ad.scale() == pytest.approx(2.0)
+    assert ad.padded_rank() == 16
+    a, b = ad.kernel_factors(torch.device("cpu"))
+    assert a.dtype == torch.bfloat16 and a.shape == (3, 16, 64) and b.shape == (3, 32, 16)
+    assert torch.count_nonzero(a[:, 12:]) == 0 and torch.count_nonzero(b[:, :, 12:]) == 0
+    assert torch.equal(a[:, :12], ad.lora_a.detach().to(torch.bfloat16))
+    rs = ActiveExpertLoRA(adapter_name="r", num_experts=1, in_features=64, out_features=64,
+                          rank=16, alpha=16.0, use_rslora=True)
+    assert rs.scale() == pytest.approx(4.0)
+    with pytest.raises(ValueError):
+        ActiveExpertLoRA(adapter_name="x", num_experts=1, in_features=64, out_features=64,
+                         rank=40, alpha=1.0)
+    with pytest.raises(ValueError):
+        lora_scale(1.0, 0, use_rslora=False)
+
+
+def test_execution_spec_surface():
+    spec = _module().expert_mlp_spec
+    assert isinstance(spec, ExpertMLPExecutionSpec)
+    assert spec.tensor_for_role("gate") == "w1"
+    assert spec.tensor_for_role("up") == "w3"
+    assert spec.tensor_for_role("down") == "w2"
