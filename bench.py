@@ -13,6 +13,11 @@ Prints one JSON line. ``value`` is routed tokens/s (T*k / step time).
 events recorded on the library's stream around that kernel; ``cpu_baseline``
 times the oracle's restatement of the reference CPU expert path on a bounded
 token sample on the host cores.
+
+``--config c5`` (adapter training) times forward + backward per step: the
+forward keeps its activations, the backward produces d tokens, d scores and the
+LoRA factor gradients from dY ~ N(0, 1); forward and backward are also timed
+apart, and the backward's stages are reported next to the forward's.
 """
 
 from __future__ import annotations
@@ -21,6 +26,7 @@ import argparse
 import dataclasses
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -33,6 +39,8 @@ if str(ROOT) not in sys.path:
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 STAGES = ("plan", "lora_down_gate_up", "gate_up_gemm", "lora_down_down", "down_gemm", "combine")
+BACK_STAGES = ("plan_and_combine_bwd", "lora_dz_down", "dh_gemm", "lora_grads_down_and_dz_gate_up",
+               "dx_gemm", "lora_grads_gate_up_and_dx_sum")
 
 
 def _parse():
@@ -48,6 +56,9 @@ def _parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget of the baseline sample")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="after the run, copy this many MiB device-to-device once: a kernel "
+                         "of known traffic that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
     return ap.parse_args()
 
 
@@ -74,8 +85,12 @@ def _build_module(w, device):
     return m
 
 
-def _stage_times(step, n, device):
-    """Average duration (ms) of each layer stage, from events on the library stream."""
+def _stage_times(step, n, device, names=STAGES):
+    """Average duration (ms) of each layer stage, from events on the library stream.
+
+    The library records the seven events at its stage boundaries on every
+    forward / backward call; with both in one step the backward's records win.
+    """
     import ctypes
 
     import torch
@@ -98,7 +113,20 @@ def _stage_times(step, n, device):
                 sums[i] += events[i].elapsed_time(events[i + 1])
     finally:
         lib.mx_set_stage_events(None, 0)
-    return {name: sums[i] / n for i, name in enumerate(STAGES)}
+    return {name: sums[i] / n for i, name in enumerate(names)}
+
+
+def _profiled_traffic(kernel: str, workload: str):
+    """HBM bytes per dispatch of `kernel` on `workload` from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summaries (calibrated against a copy of
+    known size), or None when that pair was not profiled."""
+    pat = re.compile(r"^traffic_bytes_per_dispatch:\s*(\S+)\s+(\S+)\s*=\s*(\d+)\s*$")
+    for path in sorted((ROOT / "profiles").glob("*.md")):
+        for line in path.read_text().splitlines():
+            m = pat.match(line.strip())
+            if m and m.group(1) == kernel and m.group(2) == workload:
+                return int(m.group(3))
+    return None
 
 
 def _cpu_model() -> str:
@@ -144,13 +172,23 @@ def _cpu_baseline(w, module, logits_cpu, tokens_cpu, budget_s):
         ad = module.expert_lora[key]
         loras[key] = (ad.lora_a.detach().cpu(), ad.lora_b.detach().cpu(), ad.scale())
 
+    dy_cpu = wl.upstream_grad(w) if w.backward else None
+
     def run(n_tok):
         lg = logits_cpu[:n_tok].numpy()
         idx, scores = oroute.route_topk(lg, w.top_k)
         weights = {k: olayer.dense_weight(w.fmt, payloads[k], shapes[k]) for k in payloads}
-        with torch.no_grad():
-            olayer.layer_forward(tokens_cpu[:n_tok], torch.from_numpy(scores).to(w.dtype),
-                                 torch.from_numpy(idx), weights, loras, w.experts)
+        if not w.backward:
+            with torch.no_grad():
+                olayer.layer_forward(tokens_cpu[:n_tok], torch.from_numpy(scores).to(w.dtype),
+                                     torch.from_numpy(idx), weights, loras, w.experts)
+            return
+        x = tokens_cpu[:n_tok].clone().requires_grad_(True)
+        sc = torch.from_numpy(scores).requires_grad_(True)
+        lr = {k: (a.clone().requires_grad_(True), b.clone().requires_grad_(True), s)
+              for k, (a, b, s) in loras.items()}
+        out = olayer.layer_forward(x, sc, torch.from_numpy(idx), weights, lr, w.experts)
+        out.backward(dy_cpu[:n_tok])
 
     n_tok = min(256, w.tokens)
     t0 = time.perf_counter()
@@ -173,7 +211,8 @@ def _cpu_baseline(w, module, logits_cpu, tokens_cpu, budget_s):
         "cores": threads,
         "kind": "port",
         "sample": (f"{n_tok} of {w.tokens} tokens (x top-{w.top_k} routes), same weights and "
-                   f"LoRA; median of 3 calls incl. per-call dequantisation; torch CPU bf16, "
+                   f"LoRA; median of 3 calls incl. per-call dequantisation"
+                   f"{' and the autograd backward' if w.backward else ''}; torch CPU bf16, "
                    f"{threads} threads on {_cpu_model()}"),
         "ms_per_call": sec * 1e3,
     }
@@ -212,12 +251,33 @@ def main() -> int:
     module = _build_module(w, device)
 
     state = {}
+    dy = wl.upstream_grad(w, device=device) if w.backward else None
+    lora_params = [p for ad in module.expert_lora.values() for p in (ad.lora_a, ad.lora_b)]
 
-    def step():
+    def forward_only():
         with torch.no_grad():
             idx, scores = route_topk(logits, w.top_k, renorm="clamp", score_dtype=w.dtype)
             state["out"] = module.run_direct_routed(x, scores, idx)
             state["idx"] = idx
+
+    def forward_train():
+        # Routing stays outside the graph here: its backward (d logits) is a
+        # separate, tiny kernel; d scores is what the expert op produces.
+        with torch.no_grad():
+            idx, scores = route_topk(logits, w.top_k, renorm="clamp", score_dtype=w.dtype)
+        xg = x.detach().requires_grad_(True)
+        sg = scores.detach().requires_grad_(True)
+        for p in lora_params:
+            p.grad = None
+        out = module.run_direct_routed(xg, sg, idx)
+        state["idx"] = idx
+        return out
+
+    def step():
+        if not w.backward:
+            forward_only()
+            return
+        forward_train().backward(dy)
 
     for _ in range(args.warmup):
         step()
@@ -239,16 +299,42 @@ def main() -> int:
     r1.record()
     torch.cuda.synchronize()
     route_ms = r0.elapsed_time(r1) / args.steps
-    stages = _stage_times(step, max(3, args.steps // 2), device)
+    stages = _stage_times(forward_only if not w.backward else forward_train,
+                          max(3, args.steps // 2), device)
+    back = {}
+    if w.backward:
+        f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        f0.record()
+        for _ in range(args.steps):
+            out_f = forward_train()
+        f1.record()
+        torch.cuda.synchronize()
+        del out_f
+        fwd_ms = f0.elapsed_time(f1) / args.steps
+        back = {
+            "forward_ms": fwd_ms,
+            "backward_ms": ms - fwd_ms,
+            "backward_stage_ms": _stage_times(step, max(3, args.steps // 2), device, BACK_STAGES),
+        }
 
     counts = torch.bincount(state["idx"].reshape(-1), minlength=w.experts).cpu()
     R = w.routed_rows
     flops = w.flops()
+    if w.backward:
+        # dX through the re-decoded base (2*R*3*d*f) plus about twice the
+        # forward's LoRA FLOPs (dz, dA, dB and the LoRA part of dX).
+        flops += 2 * R * 3 * w.hidden * w.ffn + 2 * (2 * R * w.rank * 3 * (w.hidden + w.ffn))
     tflops = flops / (ms * 1e-3) / 1e12
     gate_up_flops = 2 * R * 2 * w.hidden * w.ffn + 2 * R * 2 * w.ffn * w.rank
     gu_ms = stages["gate_up_gemm"]
     achieved = gate_up_flops / (gu_ms * 1e-3) / 1e12
     down_flops = 2 * R * w.ffn * w.hidden + 2 * R * w.hidden * w.rank
+    if w.backward:
+        bst = back["backward_stage_ms"]
+        dx_flops = 2 * R * 2 * w.ffn * w.hidden + 2 * R * 2 * w.rank * w.hidden
+        back["dx_gemm_tflops"] = dx_flops / (bst["dx_gemm"] * 1e-3) / 1e12
+        dh_flops = 2 * R * w.hidden * w.ffn + 2 * R * w.rank * w.ffn
+        back["dh_gemm_tflops"] = dh_flops / (bst["dh_gemm"] * 1e-3) / 1e12
     result = {
         "metric": "routed tokens/s + TFLOP/s (% bf16 MFMA peak) for NF4 MoE+LoRA layer, 1 GPU",
         "value": R / (ms * 1e-3),
@@ -270,6 +356,7 @@ def main() -> int:
         "empty_experts": int((counts == 0).sum()),
         "stage_ms": {"route": route_ms, **stages},
         "down_gemm_tflops": down_flops / (stages["down_gemm"] * 1e-3) / 1e12,
+        **back,
         "roofline": {
             "kernel": "grouped_gemm_kernel<NF4, SWIGLU, LoRA> (gate/up)",
             "bound": "mfma",
@@ -277,9 +364,18 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / PEAK_BF16_TFLOPS,
-            "traffic": None,
+            "traffic": _profiled_traffic("gate_up", w.name),
         },
     }
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        result["copy_probe_bytes"] = {"read": n * 4, "write": n * 4}
+        del src, dst
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = _cpu_baseline(w, module, logits_cpu, tokens_cpu,
                                                args.cpu_seconds)
