@@ -130,6 +130,21 @@ __device__ __forceinline__ int swz64(int row, int chunk) {  // 64-byte rows (LoR
   return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
 }
 
+// Rounds two fp32 values to bf16 precision with one packed conversion.
+__device__ __forceinline__ void round2(float &a, float &b) {
+  const uint32_t t = pack_bf16x2(a, b);
+  a = __uint_as_float(t << 16);
+  b = __uint_as_float(t & 0xffff0000u);
+}
+
+// Raw buffer over [base, base + bytes): accesses at offsets >= bytes are
+// dropped (stores) or read zero (loads) by the hardware range check. Tile
+// buffers stay far below 2 GiB.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const uint16_t *base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0,
+                                           static_cast<int32_t>(bytes > 0 ? bytes : 0), 0x00020000);
+}
+
 // Transposed B stage: [64 k rows][256 n] bf16 (512-byte rows, 32 chunks). The
 // chunk index is XOR-ed with a permutation of the row's low 4 bits so that
 //  * a row-owner ds_write_b128 (16 lanes = 16 consecutive rows, one logical
@@ -443,9 +458,64 @@ void grouped_gemm_kernel(Params p) {
   // Stage (sA, sB) is multiplied while stage (nA, nB) is produced. f0 holds
   // the first sub-step's fragments of (sA, sB) on entry, and of (nA, nB) on
   // exit (read right after the barrier).
+  // LoRA up-projection tiles for the epilogue: n_adapt low-rank activation
+  // tiles [BM][32] (gate and up for EPI_SWIGLU, dz1 and dz3 for EPI_STORE2)
+  // and n_lb factor tiles [BN][32], both in the swz64 layout. They are DMA'd
+  // during the last K step into the stage buffers that step does not refill.
+  constexpr int n_adapt = (EPI == EPI_SWIGLU || EPI == EPI_STORE2) ? 2 : 1;
+  constexpr int n_lb = EPI == EPI_STORE2 ? 2 : 1;
+  constexpr int kWaves = T::NT / 64;
+  constexpr int kPDma = n_adapt * T::BM * 64 / 1024, kLDma = n_lb * T::BN * 64 / 1024;
+  static_assert(n_adapt * T::BM * 64 <= T::STAGE_A && n_lb * T::BN * 64 <= T::STAGE_B,
+                "LoRA tiles must fit in one stage buffer");
+  static_assert(kPDma % kWaves == 0 && kLDma % kWaves == 0, "LoRA tiles split evenly over waves");
+  auto dma16 = [&](const uint16_t *src, uint8_t *dst) __attribute__((always_inline)) {
+    __builtin_amdgcn_global_load_lds(
+        reinterpret_cast<const void *>(src),
+        reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(dst)),
+        16, 0, 0);
+  };
+  // `zero` is 0 at the call; it is derived from the step index so that the
+  // address arithmetic stays in the last step instead of being hoisted out of
+  // the K loop, where it would hold registers for the whole loop.
+  auto load_lora = [&](uint8_t *dP, uint8_t *dL, int zero) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kPDma / kWaves; ++i) {
+      const int g = i * kWaves + wave;
+      const int pos = g * 1024 + 16 * lane_id + zero;
+      const int ad = pos / (T::BM * 64), rem = pos - ad * T::BM * 64;
+      const int row = rem >> 6, c = ((rem >> 4) & 3) ^ ((row >> 1) & 3);
+      // Rows past the segment end repeat its last row: they feed dropped outputs.
+      const int64_t grow = min(row0 + row, row_end - 1);
+      dma16(p.lora_p + grow * p.ldp + ad * 32 + c * 8, dP + g * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < kLDma / kWaves; ++i) {
+      const int g = i * kWaves + wave;
+      const int pos = g * 1024 + 16 * lane_id + zero;
+      const int ad = pos / (T::BN * 64), rem = pos - ad * T::BN * 64;
+      const int j = rem >> 6, c = ((rem >> 4) & 3) ^ ((j >> 1) & 3);
+      int lw = ad;
+      int64_t n = static_cast<int64_t>(nt) * T::BN + j;
+      if (EPI == EPI_SWIGLU) b_row<EPI, T>(j, nt, lw, n);
+      n = min(n, p.N - 1);
+      const int r = pick2(p.lora_r, lw);
+      const uint16_t *lb = pick2(p.lora_b, lw);
+      // Chunks past the rank re-read an in-rank chunk: the matching columns
+      // of the activation tile are zero. Absent adapters are skipped by the
+      // epilogue and read any valid row.
+      const uint16_t *src = p.lora_p;
+      if (lb && r > 0) src = lb + (static_cast<int64_t>(e) * p.N + n) * r + (c * 8 < r ? c : c % (r >> 3)) * 8;
+      dma16(src, dL + g * 1024);
+    }
+  };
   auto step = [&](int kt, const uint8_t *sA, const uint8_t *sB, uint8_t *nA, uint8_t *nB,
                   BRegs &b_next, BRegs &b_after) __attribute__((always_inline)) {
-    load_a(min(kt + 1, KT - 1), nA);
+    const bool last = LORA && kt + 1 == KT;
+    if (last)
+      load_lora(nA, nB, kt + 1 - KT);
+    else
+      load_a(min(kt + 1, KT - 1), nA);
     load_b(min(kt + 2, KT - 1), b_after);
     const Nf4Table t = FMT == MX_FMT_NF4 ? nf4_table(bf16_bits_to_f32(b_next.abs)) : Nf4Table{};
 #pragma unroll
@@ -454,7 +524,7 @@ void grouped_gemm_kernel(Params p) {
       Frags &nxt = (kk & 1) ? f0 : f1;
       if (kk + 1 < T::KSUB) read_frags(nxt, sA, sB, kk + 1);
       mfma_frags(cur);
-      decode_b(b_next, t, nB, kk);
+      if (!last) decode_b(b_next, t, nB, kk);
     }
     __syncthreads();
     read_frags(f0, nA, nB, 0);
@@ -470,6 +540,7 @@ void grouped_gemm_kernel(Params p) {
   }
   __syncthreads();
   read_frags(f0, sA0, sB0, 0);
+  // Steps alternate the two stages; the final step ends in stage KT & 1.
   int kt = 0;
   for (; kt + 1 < KT; kt += 2) {
     step(kt, sA0, sB0, sA1, sB1, rb1, rb0);
@@ -478,47 +549,13 @@ void grouped_gemm_kernel(Params p) {
   if (kt < KT) step(kt, sA0, sB0, sA1, sB1, rb1, rb0);
 
   // ------------------------------------------- LoRA up-projection (K = 32)
-  // Staged in LDS here and multiplied block by block in the epilogue, into
-  // accumulators kept apart from the frozen projection so the epilogue can
-  // round both to bf16 before adding them, as the reference adds a bf16 LoRA
-  // delta to a bf16 projection output (experts.py:3370-3374).
-  // n_adapt low-rank activation tiles [BM][32] (gate and up for EPI_SWIGLU,
-  // dz1 and dz3 for EPI_STORE2) and n_lb factor tiles [BN][32].
-  constexpr int n_adapt = (EPI == EPI_SWIGLU || EPI == EPI_STORE2) ? 2 : 1;
-  constexpr int n_lb = EPI == EPI_STORE2 ? 2 : 1;
-  static_assert(n_adapt * T::BM * 64 <= T::STAGE_A && n_lb * T::BN * 64 <= T::STAGE_B,
-                "LoRA tiles must fit in one stage buffer");
-  uint8_t *sP = sA0;
-  uint8_t *sL = sB0;
-  if (LORA) {
-    __syncthreads();  // every wave is done with the stage buffers
-    for (int idx = tid; idx < T::BM * 4 * n_adapt; idx += T::NT) {
-      const int ad = idx / (T::BM * 4);
-      const int rem = idx - ad * T::BM * 4;
-      const int r = rem >> 2, c = rem & 3;
-      const int64_t grow = row0 + r;
-      u32x4 v = u32x4{0u, 0u, 0u, 0u};
-      // Absent adapters' columns may hold stale data: never read them.
-      if (grow < row_end && c * 8 < pick2(p.lora_r, ad))
-        v = *reinterpret_cast<const u32x4 *>(p.lora_p + grow * p.ldp + ad * 32 + c * 8);
-      *reinterpret_cast<u32x4 *>(sP + ad * T::BM * 64 + swz64(r, c)) = v;
-    }
-    for (int idx = tid; idx < T::BN * 4 * n_lb; idx += T::NT) {
-      const int ad = idx / (T::BN * 4);
-      const int rem = idx - ad * T::BN * 4;
-      const int j = rem >> 2, c = rem & 3;
-      int lw = ad;
-      int64_t n = static_cast<int64_t>(nt) * T::BN + j;
-      if (EPI == EPI_SWIGLU) b_row<EPI, T>(j, nt, lw, n);
-      const int r = pick2(p.lora_r, lw);
-      const uint16_t *lb = pick2(p.lora_b, lw);
-      u32x4 v = u32x4{0u, 0u, 0u, 0u};
-      if (lb && c * 8 < r && n < p.N)
-        v = *reinterpret_cast<const u32x4 *>(lb + (static_cast<int64_t>(e) * p.N + n) * r + c * 8);
-      *reinterpret_cast<u32x4 *>(sL + ad * T::BN * 64 + swz64(j, c)) = v;
-    }
-    __syncthreads();
-  }
+  // Multiplied block by block in the epilogue, into accumulators kept apart
+  // from the frozen projection so the epilogue can round both to bf16 before
+  // adding them, as the reference adds a bf16 LoRA delta to a bf16
+  // projection output (experts.py:3370-3374). The tiles arrived with the last
+  // K step, in the stage it left free.
+  const uint8_t *sP = (KT & 1) ? sA1 : sA0;
+  const uint8_t *sL = (KT & 1) ? sB1 : sB0;
   auto lora_block = [&](int mb, int nb) -> f32x16 __attribute__((always_inline)) {
     f32x16 t;
 #pragma unroll
@@ -526,6 +563,7 @@ void grouped_gemm_kernel(Params p) {
 #pragma unroll
     for (int a2 = 0; a2 < n_lb; ++a2) {
       const int ad = EPI == EPI_SWIGLU ? (nb / (T::NB / 2)) : a2;
+      if (pick2(p.lora_r, ad) == 0) continue;  // absent adapter: its tiles are not staged
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         const int ch = kk * 2 + (lane >> 5);
@@ -542,9 +580,21 @@ void grouped_gemm_kernel(Params p) {
   // ------------------------------------------------------------ epilogue
   // v_mfma_f32_32x32x16 accumulator layout: value j of a lane sits at row
   // 8*(j/4) + 4*(lane/32) + j%4 and column lane%32 of the 32 x 32 block.
-  const int64_t rbase = row0 + wm * T::WM + 4 * (lane >> 5);
+  // Outputs whose rows are this tile's own sorted rows go through buffer
+  // stores over exactly the tile's valid rows: stores to rows past the
+  // segment end fall outside the buffer and are dropped by the hardware, and
+  // columns past N are sent out of range on purpose, so no store needs a
+  // branch. Offsets are 32-bit byte offsets inside one tile.
   const int lcol = lane & 31;
+  const int lrow = wm * T::WM + 4 * (lane >> 5);  // tile row of value j = 0 in block mb = 0
+  const int64_t tile_rows = min(row_end - row0, static_cast<int64_t>(T::BM));
+  constexpr uint32_t kDrop = 0x80000000u;         // beyond any tile buffer
   if (EPI == EPI_SWIGLU) {
+    const uint32_t ld2 = static_cast<uint32_t>(p.ldo) * 2u, n2 = static_cast<uint32_t>(p.N) * 2u;
+    const auto rs_h = tile_rsrc(p.out + row0 * p.ldo, tile_rows * p.ldo * 2);
+    const bool saves = p.save_gate != nullptr;
+    const auto rs_g = tile_rsrc(saves ? p.save_gate + row0 * p.N : p.out, saves ? tile_rows * p.N * 2 : 0);
+    const auto rs_u = tile_rsrc(saves ? p.save_up + row0 * p.N : p.out, saves ? tile_rows * p.N * 2 : 0);
 #pragma unroll
     for (int mb = 0; mb < T::MB; ++mb) {
 #pragma unroll
@@ -555,66 +605,152 @@ void grouped_gemm_kernel(Params p) {
           lu = lora_block(mb, nbp + T::NB / 2);
         }
         const int64_t f = static_cast<int64_t>(nt) * (T::BN / 2) + wn * (T::WN / 2) + nbp * 32 + lcol;
+        const uint32_t r0 = static_cast<uint32_t>(lrow + mb * 32);
+        const uint32_t off_h = f < p.N ? r0 * ld2 + static_cast<uint32_t>(f) * 2u : kDrop;
+        const uint32_t off_s = f < p.N ? r0 * n2 + static_cast<uint32_t>(f) * 2u : kDrop;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int64_t r = rbase + mb * 32 + 8 * (j >> 2) + (j & 3);
-          if (r >= row_end || f >= p.N) continue;
-          float g = round_bf16(acc[mb][nbp][j]);
-          float u = round_bf16(acc[mb][nbp + T::NB / 2][j]);
+        for (int j = 0; j < 16; j += 2) {
+          // Two adjacent rows at a time: one packed conversion rounds both.
+          float g0 = acc[mb][nbp][j], g1 = acc[mb][nbp][j + 1];
+          float u0 = acc[mb][nbp + T::NB / 2][j], u1 = acc[mb][nbp + T::NB / 2][j + 1];
+          round2(g0, g1);
+          round2(u0, u1);
           if (LORA) {
-            g = round_bf16(g + round_bf16(lg[j]));
-            u = round_bf16(u + round_bf16(lu[j]));
+            float a0 = lg[j], a1 = lg[j + 1], b0 = lu[j], b1 = lu[j + 1];
+            round2(a0, a1);
+            round2(b0, b1);
+            g0 += a0;
+            g1 += a1;
+            u0 += b0;
+            u1 += b1;
+            round2(g0, g1);
+            round2(u0, u1);
           }
           // silu(g) rounded to bf16, then the bf16 product (experts.py:289-317).
-          const float sg = round_bf16(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)));
-          p.out[r * p.ldo + f] = f32_to_bf16_bits(sg * u);
-          if (p.save_gate) p.save_gate[r * p.N + f] = f32_to_bf16_bits(g);
-          if (p.save_up) p.save_up[r * p.N + f] = f32_to_bf16_bits(u);
+          float s0 = g0 * __builtin_amdgcn_rcpf(1.0f + __expf(-g0));
+          float s1 = g1 * __builtin_amdgcn_rcpf(1.0f + __expf(-g1));
+          round2(s0, s1);
+          const uint32_t h = pack_bf16x2(s0 * u0, s1 * u1);
+          const uint32_t dr0 = static_cast<uint32_t>(8 * (j >> 2) + (j & 3));
+          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(h), rs_h, off_h + dr0 * ld2, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(h >> 16), rs_h, off_h + (dr0 + 1) * ld2, 0, 0);
+          if (saves) {
+            const uint32_t gb = pack_bf16x2(g0, g1), ub = pack_bf16x2(u0, u1);
+            __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(gb), rs_g, off_s + dr0 * n2, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(gb >> 16), rs_g, off_s + (dr0 + 1) * n2, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(ub), rs_u, off_s + dr0 * n2, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(ub >> 16), rs_u, off_s + (dr0 + 1) * n2, 0, 0);
+          }
         }
       }
     }
-  } else {
+  } else if (EPI == EPI_STORE || EPI == EPI_STORE2) {
+    // Rows go to out_row[r] (slot order): 64-bit row pointers, loaded once
+    // per row and shared by the column blocks.
+#pragma unroll
+    for (int mb = 0; mb < T::MB; ++mb) {
+      uint16_t *orow[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int64_t r = min(row0 + lrow + mb * 32 + 8 * (j >> 2) + (j & 3), row_end - 1);
+        const int64_t o = p.out_row ? static_cast<int64_t>(p.out_row[r]) : r;
+        orow[j] = p.out + o * p.ldo;
+      }
+#pragma unroll
+      for (int nb = 0; nb < T::NB; ++nb) {
+        f32x16 l2;
+        if (LORA) l2 = lora_block(mb, nb);
+        const int64_t n = static_cast<int64_t>(nt) * T::BN + wn * T::WN + nb * 32 + lcol;
+        const bool nok = n < p.N;
+#pragma unroll
+        for (int j = 0; j < 16; j += 2) {
+          float v0 = acc[mb][nb][j], v1 = acc[mb][nb][j + 1];
+          round2(v0, v1);
+          if (LORA) {
+            float a0 = l2[j], a1 = l2[j + 1];
+            round2(a0, a1);
+            v0 += a0;
+            v1 += a1;
+          }
+          const uint32_t v = pack_bf16x2(v0, v1);
+          const int64_t rr = row0 + lrow + mb * 32 + 8 * (j >> 2) + (j & 3);
+          if (nok && rr < row_end) orow[j][n] = static_cast<uint16_t>(v);
+          if (nok && rr + 1 < row_end) orow[j + 1][n] = static_cast<uint16_t>(v >> 16);
+        }
+      }
+    }
+  } else if (EPI == EPI_DSWIGLU) {
+    // dh -> (dG, dU) through h = bf16(silu(g)) * u, each op rounded to bf16
+    // as autograd of the bf16 reference composition does; the silu
+    // derivative is formed in fp32 (silu_backward). Loads of g and u past
+    // the segment end read zero; their results are dropped.
+    const uint32_t ld2 = static_cast<uint32_t>(p.ldo) * 2u, n2 = static_cast<uint32_t>(p.N) * 2u;
+    const auto rs_o = tile_rsrc(p.out + row0 * p.ldo, tile_rows * p.ldo * 2);
+    const auto rs_g = tile_rsrc(p.gate_in + row0 * p.N, tile_rows * p.N * 2);
+    const auto rs_u = tile_rsrc(p.up_in + row0 * p.N, tile_rows * p.N * 2);
 #pragma unroll
     for (int mb = 0; mb < T::MB; ++mb) {
 #pragma unroll
       for (int nb = 0; nb < T::NB; ++nb) {
         f32x16 l2;
         if (LORA) l2 = lora_block(mb, nb);
-        const int ncol = wn * T::WN + nb * 32 + lcol;
+        const int64_t f = static_cast<int64_t>(nt) * T::BN + wn * T::WN + nb * 32 + lcol;
+        const uint32_t r0 = static_cast<uint32_t>(lrow + mb * 32);
+        const uint32_t off_o = f < p.N ? r0 * ld2 + static_cast<uint32_t>(f) * 2u : kDrop;
+        const uint32_t off_i = f < p.N ? r0 * n2 + static_cast<uint32_t>(f) * 2u : kDrop;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int64_t r = rbase + mb * 32 + 8 * (j >> 2) + (j & 3);
-          if (r >= row_end) continue;
-          if (EPI == EPI_STORE || EPI == EPI_STORE2) {
-            const int64_t n = static_cast<int64_t>(nt) * T::BN + ncol;
-            if (n >= p.N) continue;
-            float v = round_bf16(acc[mb][nb][j]);
-            if (LORA) v = round_bf16(v + round_bf16(l2[j]));
-            const int64_t orow = p.out_row ? static_cast<int64_t>(p.out_row[r]) : r;
-            p.out[orow * p.ldo + n] = f32_to_bf16_bits(v);
-          } else if (EPI == EPI_DSWIGLU) {
-            // dh -> (dG, dU) through h = bf16(silu(g)) * u, each op rounded to
-            // bf16 as autograd of the bf16 reference composition does; the
-            // silu derivative is formed in fp32 (silu_backward).
-            const int64_t f = static_cast<int64_t>(nt) * T::BN + ncol;
-            if (f >= p.N) continue;
-            float dh = round_bf16(acc[mb][nb][j]);
-            if (LORA) dh = round_bf16(dh + round_bf16(l2[j]));
-            const float g = bf16_bits_to_f32(p.gate_in[r * p.N + f]);
-            const float u = bf16_bits_to_f32(p.up_in[r * p.N + f]);
+        for (int j = 0; j < 16; j += 2) {
+          float d0 = acc[mb][nb][j], d1 = acc[mb][nb][j + 1];
+          round2(d0, d1);
+          if (LORA) {
+            float a0 = l2[j], a1 = l2[j + 1];
+            round2(a0, a1);
+            d0 += a0;
+            d1 += a1;
+            round2(d0, d1);
+          }
+          const uint32_t dr0 = static_cast<uint32_t>(8 * (j >> 2) + (j & 3));
+          float dg[2], du[2];
+          const float dh[2] = {d0, d1};
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const uint32_t o = off_i + (dr0 + q) * n2;
+            const float g = bf16_bits_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rs_g, o, 0, 0));
+            const float u = bf16_bits_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rs_u, o, 0, 0));
             const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
             const float sg = round_bf16(g * sig);
-            const float dsg = round_bf16(dh * u);
-            const float du = dh * sg;
-            const float dg = dsg * (sig * (1.0f + g * (1.0f - sig)));
-            p.out[r * p.ldo + f] = f32_to_bf16_bits(dg);
-            p.out[r * p.ldo + p.N + f] = f32_to_bf16_bits(du);
-          } else {
-            if (ncol >= p.N) continue;
-            // bf16(x a^T) first, then the LoRA scale, as low_rank.to(bf16) * scale.
-            const float lr = round_bf16(acc[mb][nb][j]);
-            p.out[r * p.ldo + ncol] = f32_to_bf16_bits(lr * pick(p.scale, ncol >> 5));
+            const float dsg = round_bf16(dh[q] * u);
+            du[q] = dh[q] * sg;
+            dg[q] = dsg * (sig * (1.0f + g * (1.0f - sig)));
           }
+          const uint32_t gb = pack_bf16x2(dg[0], dg[1]), ub = pack_bf16x2(du[0], du[1]);
+          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(gb), rs_o, off_o + dr0 * ld2, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(gb >> 16), rs_o, off_o + (dr0 + 1) * ld2, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(ub), rs_o, off_o + dr0 * ld2 + n2, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(ub >> 16), rs_o, off_o + (dr0 + 1) * ld2 + n2, 0, 0);
+        }
+      }
+    }
+  } else {
+    // EPI_LORA_A: p = bf16(s * bf16(x a^T)), as low_rank.to(bf16) * scale.
+    const uint32_t ld2 = static_cast<uint32_t>(p.ldo) * 2u;
+    const auto rs_o = tile_rsrc(p.out + row0 * p.ldo, tile_rows * p.ldo * 2);
+#pragma unroll
+    for (int mb = 0; mb < T::MB; ++mb) {
+#pragma unroll
+      for (int nb = 0; nb < T::NB; ++nb) {
+        const int ncol = wn * T::WN + nb * 32 + lcol;
+        const float sc = pick(p.scale, ncol >> 5);
+        const uint32_t r0 = static_cast<uint32_t>(lrow + mb * 32);
+        const uint32_t off = ncol < p.N ? r0 * ld2 + static_cast<uint32_t>(ncol) * 2u : kDrop;
+#pragma unroll
+        for (int j = 0; j < 16; j += 2) {
+          float v0 = acc[mb][nb][j], v1 = acc[mb][nb][j + 1];
+          round2(v0, v1);
+          const uint32_t v = pack_bf16x2(v0 * sc, v1 * sc);
+          const uint32_t dr0 = static_cast<uint32_t>(8 * (j >> 2) + (j & 3));
+          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(v), rs_o, off + dr0 * ld2, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(v >> 16), rs_o, off + (dr0 + 1) * ld2, 0, 0);
         }
       }
     }
