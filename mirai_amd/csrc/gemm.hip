@@ -899,6 +899,11 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
   p.seg_end = v.seg + experts;
   p.out = out;
   p.ldo = ldo;
+  // Up to two adapters fill a 64-column tile; the kernel is bound by the
+  // activation reads, so the narrower tile (more workgroups, half the MFMA
+  // and B traffic) is the faster one.
+  if (n_adapt <= 2)
+    return launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 64, 4, 1, 64>>(p, max_tiles, s);
   return launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 128, 2, 2, 64>>(p, max_tiles, s);
 }
 

@@ -60,6 +60,83 @@ __device__ __forceinline__ int sorted_slots(const int64_t *idx_row, int k, int E
   return n;
 }
 
+// One wave per token (four tokens per workgroup) for a compile-time top-k:
+// the slot order (ascending expert id, slot order for ties, invalid ids last)
+// is formed with static indices, and the KC slot rows of each 512-column span
+// are all loaded before the fp32 accumulation, which runs in that order.
+template <int KC>
+__global__ __launch_bounds__(256) void combine_wave_kernel(const uint16_t *y, const int64_t *top_idx,
+                                                          const void *top_scores, int score_dtype,
+                                                          int E, int64_t cols, int64_t num_tokens,
+                                                          void *out, int out_dtype) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= num_tokens) return;
+  const int lane = threadIdx.x & 63;
+  int key[KC];
+#pragma unroll
+  for (int j = 0; j < KC; ++j) {
+    const int64_t e = top_idx[t * KC + j];
+    key[j] = (e < 0 || e >= E) ? 0x7fffffff : static_cast<int>(e);
+  }
+  const uint16_t *row[KC];
+  float sc[KC];
+  bool ok[KC];
+#pragma unroll
+  for (int q = 0; q < KC; ++q) {
+    row[q] = y;
+    sc[q] = 0.0f;
+    ok[q] = false;
+  }
+#pragma unroll
+  for (int j = 0; j < KC; ++j) {
+    int rank = 0;
+#pragma unroll
+    for (int i = 0; i < KC; ++i) rank += (key[i] < key[j] || (key[i] == key[j] && i < j)) ? 1 : 0;
+    const bool valid = key[j] != 0x7fffffff;
+    const float s = valid ? (top_scores ? load_score(top_scores, t * KC + j, score_dtype) : 1.0f) : 0.0f;
+#pragma unroll
+    for (int q = 0; q < KC; ++q) {
+      if (rank == q) {
+        row[q] = y + (t * KC + j) * cols;
+        sc[q] = s;
+        ok[q] = valid;
+      }
+    }
+  }
+  for (int64_t c0 = static_cast<int64_t>(lane) * 8; c0 < cols; c0 += 512) {
+    uint4 v[KC];
+#pragma unroll
+    for (int q = 0; q < KC; ++q)
+      v[q] = ok[q] ? *reinterpret_cast<const uint4 *>(row[q] + c0) : make_uint4(0, 0, 0, 0);
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < KC; ++q) {
+      if (!ok[q]) continue;
+      const uint32_t w[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // Product then sum, each rounded once, as in index_add_(y.float() * score).
+        acc[2 * i] = __fadd_rn(acc[2 * i], __fmul_rn(bf16_bits_to_f32(w[i] & 0xffffu), sc[q]));
+        acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __fmul_rn(bf16_bits_to_f32(w[i] >> 16), sc[q]));
+      }
+    }
+    if (out_dtype == MX_DTYPE_BF16) {
+      uint4 o;
+      o.x = pack_bf16x2(acc[0], acc[1]);
+      o.y = pack_bf16x2(acc[2], acc[3]);
+      o.z = pack_bf16x2(acc[4], acc[5]);
+      o.w = pack_bf16x2(acc[6], acc[7]);
+      *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(out) + t * cols + c0) = o;
+    } else {
+      float4 *o = reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + t * cols + c0);
+      o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    }
+  }
+}
+
 // One workgroup per token; each thread owns 8 consecutive columns per step.
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *y, const int64_t *top_idx,
                                                       const void *top_scores, int score_dtype,
@@ -192,9 +269,26 @@ extern "C" int mx_combine(const void *y, const int64_t *top_idx, const void *top
     set_error("mx_combine: y, top_idx and out must be non-null");
     return MX_ERR_INVALID;
   }
-  hipLaunchKernelGGL(combine_kernel, dim3(num_tokens), dim3(256), 0, as_stream(stream),
-                     static_cast<const uint16_t *>(y), top_idx, top_scores, score_dtype, top_k,
-                     num_experts, cols, out, out_dtype);
+  const dim3 wave_grid(static_cast<unsigned>(ceil_div(num_tokens, 4)));
+  const uint16_t *yb = static_cast<const uint16_t *>(y);
+#define MX_COMBINE_K(KC)                                                                     \
+  case KC:                                                                                   \
+    hipLaunchKernelGGL(combine_wave_kernel<KC>, wave_grid, dim3(256), 0, as_stream(stream), yb, \
+                       top_idx, top_scores, score_dtype, num_experts, cols, num_tokens, out,   \
+                       out_dtype);                                                           \
+    break;
+  switch (top_k) {
+    MX_COMBINE_K(1)
+    MX_COMBINE_K(2)
+    MX_COMBINE_K(3)
+    MX_COMBINE_K(4)
+    MX_COMBINE_K(6)
+    MX_COMBINE_K(8)
+    default:
+      hipLaunchKernelGGL(combine_kernel, dim3(num_tokens), dim3(256), 0, as_stream(stream), yb,
+                         top_idx, top_scores, score_dtype, top_k, num_experts, cols, out, out_dtype);
+  }
+#undef MX_COMBINE_K
   return check_launch("mx_combine");
 }
 
