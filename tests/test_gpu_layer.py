@@ -72,6 +72,20 @@ def test_c2_full_size_on_token_subset():
     _run_case(w, token_subset=subset)
 
 
+def test_c3_zipf_full_size_on_token_subset():
+    # E=128, top-8, Zipf-biased logits: at least 5 experts receive no token.
+    w = wl.WORKLOADS["c3"]
+    logits = wl.router_logits(w)
+    idx_np, _ = oroute.route_topk(logits.numpy(), w.top_k)
+    assert (np.bincount(idx_np.reshape(-1), minlength=w.experts) == 0).sum() >= 5
+    _run_case(w, token_subset=torch.arange(0, w.tokens, 32))
+
+
+def test_c4_int8_rank32_full_size_on_token_subset():
+    w = wl.WORKLOADS["c4"]
+    _run_case(w, token_subset=torch.arange(0, w.tokens, 128))
+
+
 def test_run_for_loop_matches_oracle():
     w = small("nf4", T=200, E=6, k=1)
     dense = wl.dense_weights(w)
