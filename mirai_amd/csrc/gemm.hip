@@ -7,8 +7,8 @@
 //   EPI_LORA_A  : p = bf16(s * bf16(x a^T))  (LoRA down-projection, rank <= 32)
 // Backward (B = W, K along the weights' `out` axis; the decoded rows land in
 // LDS n-major and reach the MFMA through ds_read_b64_tr_b16):
-//   EPI_DSWIGLU : dh = dy w2 + dz2 a2, then the SwiGLU backward -> [dG | dU]
-//   EPI_STORE2  : dx = [dG | dU] [w1; w3] + dz1 a1 + dz3 a3, through a row map
+//   EPI_STORE2  : dh = dy w2 + dz2 a2, and dx = [dG | dU] [w1; w3] + dz1 a1 +
+//                 dz3 a3 through a row map (one or two LoRA terms)
 //
 // Work decomposition: the dispatch plan lists row tiles (expert, first row) of
 // kTileM rows; a workgroup computes one (row tile, column tile) pair. The
@@ -20,6 +20,7 @@
 
 #include "common.h"
 #include "grads.h"
+#include "lds_tr.h"
 #include "plan.h"
 
 namespace mx {
@@ -29,10 +30,10 @@ constexpr int kNf4Block = 64;   // NF4 absmax block along K
 constexpr int kLoraK = 32;      // LoRA rank padded to two MFMA K steps
 constexpr int kLoraLd = 96;     // low-rank activation row: [gate 32 | up 32 | down 32]
 
-enum { EPI_SWIGLU = 0, EPI_STORE = 1, EPI_LORA_A = 2, EPI_DSWIGLU = 3, EPI_STORE2 = 4 };
+enum { EPI_SWIGLU = 0, EPI_STORE = 1, EPI_LORA_A = 2, EPI_STORE2 = 4 };
 
 // Backward epilogues multiply by W itself rather than W^T.
-constexpr bool trans_b(int epi) { return epi == EPI_DSWIGLU || epi == EPI_STORE2; }
+constexpr bool trans_b(int epi) { return epi == EPI_STORE2; }
 
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 
@@ -82,8 +83,6 @@ struct Params {
   const int32_t *out_row;    // sorted row -> output row (null: identity)
   uint16_t *save_gate;
   uint16_t *save_up;
-  const uint16_t *gate_in;   // EPI_DSWIGLU: forward gate / up pre-activations [R, N]
-  const uint16_t *up_in;
   float scale[4];
 };
 
@@ -145,37 +144,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const uint16_t *base
                                            static_cast<int32_t>(bytes > 0 ? bytes : 0), 0x00020000);
 }
 
-// Transposed B stage: [64 k rows][256 n] bf16 (512-byte rows, 32 chunks). The
-// chunk index is XOR-ed with a permutation of the row's low 4 bits so that
-//  * a row-owner ds_write_b128 (16 lanes = 16 consecutive rows, one logical
-//    chunk) hits 16 distinct 16-byte bank groups, and
-//  * a ds_read_b64_tr_b16 half-wave (4 consecutive rows x 4 chunks) does too.
-__device__ __forceinline__ int swz_t(int row, int chunk) {
-  const int x = ((row & 3) << 2) | ((row >> 2) & 3);
-  return row * 512 + ((chunk ^ x) << 4);
-}
-
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-
-// B fragment of v_mfma_f32_32x32x16_bf16 (lane: column lane%32, k = 8*(lane/32)
-// + 0..7) read from a transposed stage. ds_read_b64_tr_b16 hands lane j of a
-// 16-lane group the elements j, 16+j, 32+j, 48+j of the group's concatenated
-// 8-byte chunks; lane i of the group therefore fetches row k0 + i/4, columns
-// c0 + 4*(i%4) .. +3, and receives column c0 + j of rows k0 .. k0+3.
-__device__ __forceinline__ bf16x8 read_b_trans(const uint8_t *sB, int ncol0, int kk, int lane) {
-  const int g = lane >> 4, i = lane & 15;
-  const int row = 16 * kk + 8 * (g >> 1) + (i >> 2);
-  const int col = ncol0 + 16 * (g & 1) + 4 * (i & 3);
-  const int chunk = col >> 3, half = ((col >> 2) & 1) * 8;
-  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4 *>(
-      reinterpret_cast<uintptr_t>(sB + swz_t(row, chunk) + half)));
-  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4 *>(
-      reinterpret_cast<uintptr_t>(sB + swz_t(row + 4, chunk) + half)));
-  typedef short i16x8 __attribute__((ext_vector_type(8)));
-  const i16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-  return __builtin_bit_cast(bf16x8, v);
-}
 
 // NF4 decode in registers. `lo`/`hi` hold the low / high bytes of the 16
 // decoded bf16 values bf16(level[q] * absmax) of the current block, 4 per
@@ -484,6 +452,9 @@ void grouped_gemm_kernel(Params p) {
       const int g = i * kWaves + wave;
       const int pos = g * 1024 + 16 * lane_id + zero;
       const int ad = pos / (T::BM * 64), rem = pos - ad * T::BM * 64;
+      // Each DMA covers 1 KB inside one adapter's tile; absent adapters'
+      // columns are not staged (they may lie past the end of the buffer).
+      if (pick2(p.lora_r, ad) == 0) continue;
       const int row = rem >> 6, c = ((rem >> 4) & 3) ^ ((row >> 1) & 3);
       // Rows past the segment end repeat its last row: they feed dropped outputs.
       const int64_t grow = min(row0 + row, row_end - 1);
@@ -679,58 +650,6 @@ void grouped_gemm_kernel(Params p) {
         }
       }
     }
-  } else if (EPI == EPI_DSWIGLU) {
-    // dh -> (dG, dU) through h = bf16(silu(g)) * u, each op rounded to bf16
-    // as autograd of the bf16 reference composition does; the silu
-    // derivative is formed in fp32 (silu_backward). Loads of g and u past
-    // the segment end read zero; their results are dropped.
-    const uint32_t ld2 = static_cast<uint32_t>(p.ldo) * 2u, n2 = static_cast<uint32_t>(p.N) * 2u;
-    const auto rs_o = tile_rsrc(p.out + row0 * p.ldo, tile_rows * p.ldo * 2);
-    const auto rs_g = tile_rsrc(p.gate_in + row0 * p.N, tile_rows * p.N * 2);
-    const auto rs_u = tile_rsrc(p.up_in + row0 * p.N, tile_rows * p.N * 2);
-#pragma unroll
-    for (int mb = 0; mb < T::MB; ++mb) {
-#pragma unroll
-      for (int nb = 0; nb < T::NB; ++nb) {
-        f32x16 l2;
-        if (LORA) l2 = lora_block(mb, nb);
-        const int64_t f = static_cast<int64_t>(nt) * T::BN + wn * T::WN + nb * 32 + lcol;
-        const uint32_t r0 = static_cast<uint32_t>(lrow + mb * 32);
-        const uint32_t off_o = f < p.N ? r0 * ld2 + static_cast<uint32_t>(f) * 2u : kDrop;
-        const uint32_t off_i = f < p.N ? r0 * n2 + static_cast<uint32_t>(f) * 2u : kDrop;
-#pragma unroll
-        for (int j = 0; j < 16; j += 2) {
-          float d0 = acc[mb][nb][j], d1 = acc[mb][nb][j + 1];
-          round2(d0, d1);
-          if (LORA) {
-            float a0 = l2[j], a1 = l2[j + 1];
-            round2(a0, a1);
-            d0 += a0;
-            d1 += a1;
-            round2(d0, d1);
-          }
-          const uint32_t dr0 = static_cast<uint32_t>(8 * (j >> 2) + (j & 3));
-          float dg[2], du[2];
-          const float dh[2] = {d0, d1};
-#pragma unroll
-          for (int q = 0; q < 2; ++q) {
-            const uint32_t o = off_i + (dr0 + q) * n2;
-            const float g = bf16_bits_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rs_g, o, 0, 0));
-            const float u = bf16_bits_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rs_u, o, 0, 0));
-            const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
-            const float sg = round_bf16(g * sig);
-            const float dsg = round_bf16(dh[q] * u);
-            du[q] = dh[q] * sg;
-            dg[q] = dsg * (sig * (1.0f + g * (1.0f - sig)));
-          }
-          const uint32_t gb = pack_bf16x2(dg[0], dg[1]), ub = pack_bf16x2(du[0], du[1]);
-          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(gb), rs_o, off_o + dr0 * ld2, 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(gb >> 16), rs_o, off_o + (dr0 + 1) * ld2, 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(ub), rs_o, off_o + dr0 * ld2 + n2, 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(ub >> 16), rs_o, off_o + (dr0 + 1) * ld2 + n2, 0, 0);
-        }
-      }
-    }
   } else {
     // EPI_LORA_A: p = bf16(s * bf16(x a^T)), as low_rank.to(bf16) * scale.
     const uint32_t ld2 = static_cast<uint32_t>(p.ldo) * 2u;
@@ -771,9 +690,10 @@ int launch(const Params &p, int64_t max_row_tiles, hipStream_t s) {
   return check_launch("grouped GEMM launch");
 }
 
-// Row-tile height: 256-row tiles when experts average at least 768 rows
-// (their tail waste stays small), else 128-row tiles.
-inline bool use_tall_tiles(int64_t rows, int experts) { return rows >= 768 * static_cast<int64_t>(experts); }
+// Row-tile height: 256-row tiles when experts average at least 256 rows (the
+// taller tile's better MFMA / LDS ratio outweighs its tail waste from there
+// on, measured at C2, C3 and C5), else 128-row tiles.
+inline bool use_tall_tiles(int64_t rows, int experts) { return rows >= 256 * static_cast<int64_t>(experts); }
 
 template <int EPI, bool LORA>
 int launch_fmt(int fmt, Params p, const PlanLayout &PL, const PlanView &v, bool tall, hipStream_t s) {
@@ -809,8 +729,10 @@ int launch_any(int fmt, bool lora, const Params &p, const PlanLayout &PL, const 
 
 // ------------------------------------------------------------ host helpers
 constexpr int kStageEvents = 7;
-thread_local void *g_stage_events[kStageEvents] = {};
-thread_local int g_stage_count = 0;
+// Process-wide, not per thread: the autograd backward calls the library from
+// another host thread than the forward.
+void *g_stage_events[kStageEvents] = {};
+int g_stage_count = 0;
 
 void mark_stage(int i, hipStream_t s) {
   if (g_stage_count == kStageEvents && g_stage_events[i])
@@ -1110,8 +1032,8 @@ extern "C" int mx_moe_backward(const void *grad_out, int grad_dtype, const void 
   if (rc) return rc;
   mark_stage(1, s);
 
-  // Down projection: dz2 = s2 * dy B2, then dh = dy W2 + dz2 A2 and the
-  // SwiGLU backward into [dG | dU].
+  // Down projection: dz2 = s2 * dy B2, then dh = dy W2 + dz2 A2 into the dG
+  // half of [dG | dU], and the SwiGLU backward turns it into [dG | dU].
   if (lora2) {
     const int r = l2->rank;
     if ((rc = transpose_factors(static_cast<const uint16_t *>(l2->b), num_experts, hidden, r,
@@ -1145,9 +1067,8 @@ extern "C" int mx_moe_backward(const void *grad_out, int grad_dtype, const void 
     p.seg_end = v.seg + num_experts;
     p.out = dgu;
     p.ldo = 2 * ffn;
-    p.gate_in = g_in;
-    p.up_in = u_in;
-    if ((rc = launch_any<EPI_DSWIGLU>(w2->format, lora2, p, L.plan, v, s))) return rc;
+    if ((rc = launch_any<EPI_STORE2>(w2->format, lora2, p, L.plan, v, s))) return rc;
+    if ((rc = swiglu_backward(dgu, g_in, u_in, R, ffn, s))) return rc;
   }
   mark_stage(3, s);
   if (lora2) {

@@ -15,10 +15,17 @@ int transpose_factors(const uint16_t *src, int64_t experts, int64_t rows, int64_
 // for c < cols, j < rank (fp32 accumulation, fp32 output at
 // out + e*stride_e + c*stride_c + j*stride_j). M and V are bf16 with leading
 // dimensions ldm / ldv; map (null: identity) sends a sorted row to its M row.
-// rank is 8, 16, 24 or 32.
+// V holds 32 columns (those past `rank`, up to 32, only feed unwritten
+// outputs); rank <= 32, cols a multiple of 8.
 int lora_weight_grad(const uint16_t *m, int64_t ldm, const int32_t *map, const uint16_t *v,
                      int64_t ldv, int rank, int64_t cols, const int64_t *seg_start,
                      const int64_t *seg_end, int experts, float *out, int64_t stride_e,
                      int64_t stride_c, int64_t stride_j, hipStream_t s);
+
+// SwiGLU backward in place over expert-sorted rows: row r of `dgu` (stride
+// 2f) holds dh in its first f columns on entry and [dG | dU] on exit, with
+// h = bf16(silu(g)) * u (g, u: [rows, f]).
+int swiglu_backward(uint16_t *dgu, const uint16_t *g, const uint16_t *u, int64_t rows,
+                    int64_t f, hipStream_t s);
 
 }  // namespace mx

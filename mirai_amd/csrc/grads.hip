@@ -6,6 +6,7 @@
 //   dB_e = sum_rows dOut^T (s * x A_e^T)      dA_e = sum_rows dz^T x,
 // with dz = s * dOut B_e, each a sum over the expert's sorted rows.
 #include "grads.h"
+#include "lds_tr.h"
 
 namespace mx {
 namespace {
@@ -21,55 +22,141 @@ __global__ __launch_bounds__(256) void transpose_factors_kernel(const uint16_t *
   dst[e * per + c * rows + r] = src[i];
 }
 
-// One workgroup per (expert, 512-column slice); each thread owns two adjacent
-// columns and RANK fp32 accumulators per column. The expert's V rows are
-// staged in LDS 64 at a time and read back as broadcasts.
-template <int RANK>
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+
+// V-tile read for v_mfma_f32_32x32x16_bf16's B operand from [64 rows][32]
+// bf16 (64-byte rows): lane j of each 16-lane group receives column
+// 16*(group&1) + j of four consecutive rows (see read_b_trans).
+__device__ __forceinline__ bf16x8 read_v_trans(const uint8_t *sV, int kk, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const int row = 16 * kk + 8 * (g >> 1) + (i >> 2);
+  const int col = 16 * (g & 1) + 4 * (i & 3);
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<lds_i16x4 *>(reinterpret_cast<uintptr_t>(sV + row * 64 + col * 2)));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<lds_i16x4 *>(reinterpret_cast<uintptr_t>(sV + (row + 4) * 64 + col * 2)));
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  const i16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// One workgroup (4 waves) per (expert, 256-column slice): G[c, j] = sum over
+// the expert's rows of M[row, c] * V[row, j] on bf16 MFMA with fp32
+// accumulation. Both operands arrive row-major (the reduction runs along
+// rows), so 64-row tiles of M and V go to LDS as they are and the MFMA
+// fragments are read with ds_read_b64_tr_b16. Each wave owns 64 columns x 32
+// ranks (two 32 x 32 blocks). Rows past the segment and columns past `cols`
+// are zero-filled.
 __global__ __launch_bounds__(256) void lora_weight_grad_kernel(
-    const uint16_t *m, int64_t ldm, const int32_t *map, const uint16_t *v, int64_t ldv,
+    const uint16_t *m, int64_t ldm, const int32_t *map, const uint16_t *v, int64_t ldv, int rank,
     int64_t cols, const int64_t *seg_start, const int64_t *seg_end, float *out, int64_t se,
     int64_t sc, int64_t sj) {
-  constexpr int kRows = 64;
-  __shared__ float sv[kRows][RANK];
+  __shared__ __attribute__((aligned(16))) uint8_t sM[64 * 512];
+  __shared__ __attribute__((aligned(16))) uint8_t sV[64 * 64];
   const int e = blockIdx.y;
-  const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 2;
-  const bool active = c0 < cols;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 256;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t start = seg_start[e], end = seg_end[e];
-  float acc0[RANK], acc1[RANK];
+  f32x16 acc[2];
 #pragma unroll
-  for (int j = 0; j < RANK; ++j) acc0[j] = acc1[j] = 0.0f;
-  for (int64_t r0 = start; r0 < end; r0 += kRows) {
-    const int n = static_cast<int>(min(static_cast<int64_t>(kRows), end - r0));
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < kRows * RANK; idx += 256) {
-      const int rr = idx / RANK, j = idx - rr * RANK;
-      sv[rr][j] = rr < n ? bf16_bits_to_f32(v[(r0 + rr) * ldv + j]) : 0.0f;
-    }
-    __syncthreads();
-    if (!active) continue;
-#pragma unroll 4
-    for (int rr = 0; rr < n; ++rr) {
-      const int64_t row = r0 + rr;
-      const int64_t src = map ? static_cast<int64_t>(map[row]) : row;
-      const uint32_t w = *reinterpret_cast<const uint32_t *>(m + src * ldm + c0);
-      const float x0 = bf16_bits_to_f32(w & 0xffffu), x1 = bf16_bits_to_f32(w >> 16);
+  for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int j = 0; j < RANK; ++j) {
-        acc0[j] = fmaf(x0, sv[rr][j], acc0[j]);
-        acc1[j] = fmaf(x1, sv[rr][j], acc1[j]);
+    for (int j = 0; j < 16; ++j) acc[b][j] = 0.0f;
+  for (int64_t r0 = start; r0 < end; r0 += 64) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int q = tid + 256 * i;  // 16-byte chunk of the 64 x 256 tile
+      const int row = q >> 5, ch = q & 31;
+      const int64_t grow = r0 + row, col = c0 + ch * 8;
+      u32x4 val = u32x4{0u, 0u, 0u, 0u};
+      if (grow < end && col < cols) {
+        const int64_t src = map ? static_cast<int64_t>(map[grow]) : grow;
+        val = *reinterpret_cast<const u32x4 *>(m + src * ldm + col);
       }
+      *reinterpret_cast<u32x4 *>(sM + swz_t(row, ch)) = val;
     }
-  }
-  if (!active) return;
-  float *o = out + e * se;
+    {
+      const int row = tid >> 2, ch = tid & 3;
+      const int64_t grow = r0 + row;
+      u32x4 val = u32x4{0u, 0u, 0u, 0u};
+      if (grow < end) val = *reinterpret_cast<const u32x4 *>(v + grow * ldv + ch * 8);
+      *reinterpret_cast<u32x4 *>(sV + row * 64 + ch * 16) = val;
+    }
+    __syncthreads();
 #pragma unroll
-  for (int j = 0; j < RANK; ++j) {
-    o[c0 * sc + j * sj] = acc0[j];
-    o[(c0 + 1) * sc + j * sj] = acc1[j];
+    for (int kk = 0; kk < 4; ++kk) {
+      const bf16x8 bv = read_v_trans(sV, kk, lane);
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(read_b_trans(sM, wave * 64 + b * 32, kk, lane),
+                                                         bv, acc[b], 0, 0, 0);
+    }
+    __syncthreads();
   }
+  // Accumulator value jj of a lane: column c = 8*(jj/4) + 4*(lane/32) + jj%4 of
+  // the block, rank j = lane % 32.
+  const int j = lane & 31;
+  if (j >= rank) return;
+  float *o = out + e * se + j * sj;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      const int64_t c = c0 + wave * 64 + b * 32 + 8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3);
+      if (c < cols) o[c * sc] = acc[b][jj];
+    }
+}
+
+// One thread per 8 columns of one row. Each op is rounded to bf16 as the
+// autograd of the bf16 reference composition h = bf16(silu(g)) * u does
+// (experts.py:289-317); the silu derivative is formed in fp32, as
+// silu_backward does.
+__global__ __launch_bounds__(256) void swiglu_backward_kernel(uint16_t *dgu, const uint16_t *g,
+                                                              const uint16_t *u, int64_t rows,
+                                                              int64_t f) {
+  const int64_t chunks = f / 8;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= rows * chunks) return;
+  const int64_t r = i / chunks, c = (i - r * chunks) * 8;
+  uint16_t *dg_row = dgu + r * 2 * f + c;
+  const uint4 dv = *reinterpret_cast<const uint4 *>(dg_row);
+  const uint4 gv = *reinterpret_cast<const uint4 *>(g + r * f + c);
+  const uint4 uv = *reinterpret_cast<const uint4 *>(u + r * f + c);
+  const uint32_t dw[4] = {dv.x, dv.y, dv.z, dv.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
+  const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
+  uint32_t og[4], ou[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float dgo[2], duo[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float dh = bf16_bits_to_f32(h ? dw[q] >> 16 : dw[q] & 0xffffu);
+      const float gg = bf16_bits_to_f32(h ? gw[q] >> 16 : gw[q] & 0xffffu);
+      const float uu = bf16_bits_to_f32(h ? uw[q] >> 16 : uw[q] & 0xffffu);
+      const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-gg));
+      const float sg = round_bf16(gg * sig);
+      const float dsg = round_bf16(dh * uu);
+      duo[h] = dh * sg;
+      dgo[h] = dsg * (sig * (1.0f + gg * (1.0f - sig)));
+    }
+    og[q] = pack_bf16x2(dgo[0], dgo[1]);
+    ou[q] = pack_bf16x2(duo[0], duo[1]);
+  }
+  *reinterpret_cast<uint4 *>(dg_row) = make_uint4(og[0], og[1], og[2], og[3]);
+  *reinterpret_cast<uint4 *>(dg_row + f) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
 }
 
 }  // namespace
+
+int swiglu_backward(uint16_t *dgu, const uint16_t *g, const uint16_t *u, int64_t rows,
+                    int64_t f, hipStream_t s) {
+  const int64_t total = rows * (f / 8);
+  if (total <= 0) return MX_OK;
+  hipLaunchKernelGGL(swiglu_backward_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))),
+                     dim3(256), 0, s, dgu, g, u, rows, f);
+  return check_launch("SwiGLU backward");
+}
 
 int transpose_factors(const uint16_t *src, int64_t experts, int64_t rows, int64_t cols,
                       uint16_t *dst, hipStream_t s) {
@@ -84,24 +171,13 @@ int lora_weight_grad(const uint16_t *m, int64_t ldm, const int32_t *map, const u
                      int64_t ldv, int rank, int64_t cols, const int64_t *seg_start,
                      const int64_t *seg_end, int experts, float *out, int64_t stride_e,
                      int64_t stride_c, int64_t stride_j, hipStream_t s) {
-  if (cols % 2 != 0) {
-    set_error("LoRA weight gradient: cols must be even");
+  if (cols % 8 != 0 || rank <= 0 || rank > 32) {
+    set_error("LoRA weight gradient: cols must be a multiple of 8 and rank in [1, 32]");
     return MX_ERR_INVALID;
   }
-  const dim3 grid(static_cast<unsigned>(ceil_div(cols, 512)), static_cast<unsigned>(experts));
-#define MX_LWG(R)                                                                              \
-  hipLaunchKernelGGL(lora_weight_grad_kernel<R>, grid, dim3(256), 0, s, m, ldm, map, v, ldv,   \
-                     cols, seg_start, seg_end, out, stride_e, stride_c, stride_j)
-  switch (rank) {
-    case 8: MX_LWG(8); break;
-    case 16: MX_LWG(16); break;
-    case 24: MX_LWG(24); break;
-    case 32: MX_LWG(32); break;
-    default:
-      set_error("LoRA weight gradient: rank %d not in {8,16,24,32}", rank);
-      return MX_ERR_INVALID;
-  }
-#undef MX_LWG
+  const dim3 grid(static_cast<unsigned>(ceil_div(cols, 256)), static_cast<unsigned>(experts));
+  hipLaunchKernelGGL(lora_weight_grad_kernel, grid, dim3(256), 0, s, m, ldm, map, v, ldv, rank,
+                     cols, seg_start, seg_end, out, stride_e, stride_c, stride_j);
   return check_launch("LoRA weight gradient");
 }
 

@@ -177,6 +177,68 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *y, const i
   }
 }
 
+// One wave per token (four per workgroup) for a compile-time top-k: grad_y
+// rows for every valid slot, 16 bytes per lane, and the score gradients
+// (wave reduction of grad_out . y, fp32).
+template <int KC>
+__global__ __launch_bounds__(256) void combine_backward_wave_kernel(
+    const void *grad_out, int grad_dtype, const uint16_t *y, const int64_t *top_idx,
+    const void *top_scores, int score_dtype, int E, int64_t cols, int64_t num_tokens,
+    uint16_t *grad_y, float *grad_scores) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= num_tokens) return;
+  const int lane = threadIdx.x & 63;
+  bool ok[KC];
+  float sc[KC], part[KC];
+#pragma unroll
+  for (int j = 0; j < KC; ++j) {
+    const int64_t e = top_idx[t * KC + j];
+    ok[j] = e >= 0 && e < E;
+    sc[j] = ok[j] ? load_score(top_scores, t * KC + j, score_dtype) : 0.0f;
+    part[j] = 0.0f;
+  }
+  for (int64_t c0 = static_cast<int64_t>(lane) * 8; c0 < cols; c0 += 512) {
+    float g[8];
+    if (grad_dtype == MX_DTYPE_BF16) {
+      const uint4 v = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(grad_out) + t * cols + c0);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        g[2 * i] = bf16_bits_to_f32(w[i] & 0xffffu);
+        g[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
+      }
+    } else {
+      const float4 *gp = reinterpret_cast<const float4 *>(static_cast<const float *>(grad_out) + t * cols + c0);
+      const float4 a = gp[0], b = gp[1];
+      g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w;
+      g[4] = b.x; g[5] = b.y; g[6] = b.z; g[7] = b.w;
+    }
+    uint4 yv[KC];
+#pragma unroll
+    for (int j = 0; j < KC; ++j)
+      yv[j] = ok[j] ? *reinterpret_cast<const uint4 *>(y + (t * KC + j) * cols + c0) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+      if (!ok[j]) continue;
+      const uint32_t w[4] = {yv[j].x, yv[j].y, yv[j].z, yv[j].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        part[j] += g[2 * i] * bf16_bits_to_f32(w[i] & 0xffffu) + g[2 * i + 1] * bf16_bits_to_f32(w[i] >> 16);
+        o[i] = pack_bf16x2(g[2 * i] * sc[j], g[2 * i + 1] * sc[j]);
+      }
+      *reinterpret_cast<uint4 *>(grad_y + (t * KC + j) * cols + c0) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KC; ++j) {
+    float v = part[j];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    if (lane == 0) grad_scores[t * KC + j] = ok[j] ? v : 0.0f;
+  }
+}
+
 // One workgroup per token: grad_y rows for every valid slot and the score
 // gradients (block reduction of grad_out . y).
 __global__ __launch_bounds__(256) void combine_backward_kernel(
@@ -307,9 +369,28 @@ extern "C" int mx_combine_backward(const void *grad_out, int grad_dtype, const v
     set_error("mx_combine_backward: buffers must be non-null");
     return MX_ERR_INVALID;
   }
+  const uint16_t *yb = static_cast<const uint16_t *>(y);
+  uint16_t *gy = static_cast<uint16_t *>(grad_y);
+  if (cols % 8 == 0) {
+    const dim3 wave_grid(static_cast<unsigned>(ceil_div(num_tokens, 4)));
+#define MX_COMBINE_BWD_K(KC)                                                                  \
+  case KC:                                                                                    \
+    hipLaunchKernelGGL(combine_backward_wave_kernel<KC>, wave_grid, dim3(256), 0,             \
+                       as_stream(stream), grad_out, grad_dtype, yb, top_idx, top_scores,        \
+                       score_dtype, num_experts, cols, num_tokens, gy, grad_scores);           \
+    return check_launch("mx_combine_backward");
+    switch (top_k) {
+      MX_COMBINE_BWD_K(1)
+      MX_COMBINE_BWD_K(2)
+      MX_COMBINE_BWD_K(4)
+      MX_COMBINE_BWD_K(8)
+      default:
+        break;
+    }
+#undef MX_COMBINE_BWD_K
+  }
   hipLaunchKernelGGL(combine_backward_kernel, dim3(num_tokens), dim3(256), 0, as_stream(stream),
-                     grad_out, grad_dtype, static_cast<const uint16_t *>(y), top_idx, top_scores,
-                     score_dtype, top_k, num_experts, cols, static_cast<uint16_t *>(grad_y),
-                     grad_scores);
+                     grad_out, grad_dtype, yb, top_idx, top_scores, score_dtype, top_k,
+                     num_experts, cols, gy, grad_scores);
   return check_launch("mx_combine_backward");
 }
