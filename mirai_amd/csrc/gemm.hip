@@ -208,6 +208,9 @@ void grouped_gemm_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t sA1[T::STAGE_A];
   __shared__ __attribute__((aligned(16))) uint8_t sB0[T::STAGE_B];
   __shared__ __attribute__((aligned(16))) uint8_t sB1[T::STAGE_B];
+  // LoRA factor tiles of the epilogue (one [BN][32] tile per adapter).
+  constexpr int kLTile = LORA ? (EPI == EPI_STORE2 ? 2 : 1) * T::BN * 64 : 16;
+  __shared__ __attribute__((aligned(16))) uint8_t sLt[kLTile];
   const int tid = threadIdx.x;
 
   // ---------------------------------------------------------------- tile
@@ -431,13 +434,15 @@ void grouped_gemm_kernel(Params p) {
   // LoRA up-projection tiles for the epilogue: n_adapt low-rank activation
   // tiles [BM][32] (gate and up for EPI_SWIGLU, dz1 and dz3 for EPI_STORE2)
   // and n_lb factor tiles [BN][32], both in the swz64 layout. They are DMA'd
-  // during the last K step into the stage buffers that step does not refill.
+  // during the last K step: the activation tiles into the A stage that step
+  // does not refill, the factor tiles into their own buffer (the last step
+  // still decodes a B stage, so that no branch splits the step body).
   constexpr int n_adapt = (EPI == EPI_SWIGLU || EPI == EPI_STORE2) ? 2 : 1;
   constexpr int n_lb = EPI == EPI_STORE2 ? 2 : 1;
   constexpr int kWaves = T::NT / 64;
   constexpr int kPDma = n_adapt * T::BM * 64 / 1024, kLDma = n_lb * T::BN * 64 / 1024;
-  static_assert(n_adapt * T::BM * 64 <= T::STAGE_A && n_lb * T::BN * 64 <= T::STAGE_B,
-                "LoRA tiles must fit in one stage buffer");
+  static_assert(n_adapt * T::BM * 64 <= T::STAGE_A && (!LORA || n_lb * T::BN * 64 <= kLTile),
+                "LoRA tiles must fit their buffers");
   static_assert(kPDma % kWaves == 0 && kLDma % kWaves == 0, "LoRA tiles split evenly over waves");
   auto dma16 = [&](const uint16_t *src, uint8_t *dst) __attribute__((always_inline)) {
     __builtin_amdgcn_global_load_lds(
@@ -486,7 +491,7 @@ void grouped_gemm_kernel(Params p) {
                   BRegs &b_next, BRegs &b_after) __attribute__((always_inline)) {
     const bool last = LORA && kt + 1 == KT;
     if (last)
-      load_lora(nA, nB, kt + 1 - KT);
+      load_lora(nA, sLt, kt + 1 - KT);
     else
       load_a(min(kt + 1, KT - 1), nA);
     load_b(min(kt + 2, KT - 1), b_after);
@@ -497,7 +502,7 @@ void grouped_gemm_kernel(Params p) {
       Frags &nxt = (kk & 1) ? f0 : f1;
       if (kk + 1 < T::KSUB) read_frags(nxt, sA, sB, kk + 1);
       mfma_frags(cur);
-      if (!last) decode_b(b_next, t, nB, kk);
+      decode_b(b_next, t, nB, kk);
     }
     __syncthreads();
     read_frags(f0, nA, nB, 0);
@@ -528,7 +533,7 @@ void grouped_gemm_kernel(Params p) {
   // projection output (experts.py:3370-3374). The tiles arrived with the last
   // K step, in the stage it left free.
   const uint8_t *sP = (KT & 1) ? sA1 : sA0;
-  const uint8_t *sL = (KT & 1) ? sB1 : sB0;
+  const uint8_t *sL = sLt;
   auto lora_block = [&](int mb, int nb) -> f32x16 __attribute__((always_inline)) {
     f32x16 t;
 #pragma unroll
