@@ -164,6 +164,9 @@ def _cpu_baseline(w, module, logits_cpu, tokens_cpu, budget_s):
         elif p.fmt == "int8":
             payloads[key] = (p.data.cpu().numpy(), p.scale.cpu().view(torch.int16).numpy()
                              .view(np.uint16))
+        elif p.fmt == "fp32":  # bf16 planes -> the fp32 weight (hi + lo)
+            from mirai_amd import quant
+            payloads[key] = quant.dequantize(p, dtype=torch.float32).cpu()
         else:
             payloads[key] = p.data.cpu()
     shapes = {k: module.packed_weight(k).shape for k in payloads}

@@ -18,7 +18,11 @@
  *                   2i+1 in the high nibble), absmax [E, out, in/64] bf16
  *   INT8 weight     q [E, out, in] int8, scale [E, out] bf16
  *   BF16 weight     w [E, out, in] bf16
- *   LoRA factors    A [E, r, in], B [E, out, r] bf16 (rank r <= 32)
+ *   F32X3 weight    w [E, out, 3*in] bf16: an fp32 weight split into bf16
+ *                   planes [hi | lo | hi] along in (see mx_split_f32)
+ *   LoRA factors    A [E, r, in], B [E, out, r] bf16 (rank r <= 32); with
+ *                   F32X3 weights A [E, r, 3*in] and B [E, out, 3*r] in
+ *                   [hi | lo | hi] planes, r = 8
  *
  * Each declaration cites the reference interface (seruva19/mirai, path:line)
  * whose semantics it implements.
@@ -43,6 +47,11 @@ extern "C" {
 #define MX_FMT_BF16 0
 #define MX_FMT_NF4 1
 #define MX_FMT_INT8 2
+#define MX_FMT_F32X3 3
+
+/* Plane orders of mx_split_f32. */
+#define MX_SPLIT_ACT 0     /* [hi | hi | lo]: activations */
+#define MX_SPLIT_WEIGHT 1  /* [hi | lo | hi]: weights and LoRA factors */
 
 /* Router normalisation modes. */
 #define MX_RENORM_NONE 0      /* scores = softmax probabilities of the picks   */
@@ -236,9 +245,26 @@ typedef struct mx_lora {
  */
 int mx_set_stage_events(void **events, int count);
 
-/* Bytes of scratch for mx_moe_forward / mx_moe_for_loop. */
+/* Bytes of scratch for mx_moe_forward / mx_moe_for_loop (BF16, NF4, INT8 weights). */
 size_t mx_moe_workspace_size(int64_t num_tokens, int top_k, int num_experts,
                              int64_t hidden, int64_t ffn);
+
+/* Bytes of scratch for mx_moe_forward with MX_FMT_F32X3 weights (fp32 tokens). */
+size_t mx_moe_f32x3_workspace_size(int64_t num_tokens, int top_k, int num_experts,
+                                   int64_t hidden, int64_t ffn);
+
+/*
+ * fp32 -> bf16 planes for the fp32 path on bf16 MFMA. Row i of x (cols fp32)
+ * becomes 3*cols bf16 values with hi = bf16(x), lo = bf16(x - hi), in the
+ * order [hi | hi | lo] (MX_SPLIT_ACT) or [hi | lo | hi] (MX_SPLIT_WEIGHT). The
+ * dot product of an activation row and a weight row split this way is
+ * hi*hi + hi*lo + lo*hi: the fp32 product up to the lo*lo term (relative
+ * 2^-16). No reference counterpart: the reference computes its fp32 layer
+ * (run_direct_routed with fp32 tokens, experts.py:1749-1912) on fp32 GEMMs;
+ * this is how the MI355X path reaches the same precision on the matrix cores.
+ */
+int mx_split_f32(const float *x, int64_t rows, int64_t cols, int pattern, void *out,
+                 void *stream);
 
 /*
  * Full routed expert layer: plan -> gathered gate/up grouped GEMM with
@@ -252,6 +278,10 @@ size_t mx_moe_workspace_size(int64_t num_tokens, int top_k, int num_experts,
  *   save_gate/save_up [R, ffn] bf16 pre-activation projections (sorted order),
  *   save_h [R, ffn] bf16, save_y [R, hidden] bf16 (flat slot order t*k+j),
  *   save_lora [R, 3, 32] bf16 scaled low-rank activations.
+ * With MX_FMT_F32X3 weights (all three) the layer runs at fp32 precision:
+ * tokens are fp32 [T, hidden], the workspace comes from
+ * mx_moe_f32x3_workspace_size, no activations are saved (inference only),
+ * and LoRA factors are split as the format list above describes.
  */
 int mx_moe_forward(const void *tokens, const int64_t *top_idx, const void *top_scores,
                    int score_dtype, int64_t num_tokens, int top_k, int num_experts,

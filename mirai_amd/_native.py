@@ -26,6 +26,10 @@ DTYPE_BF16 = 1
 FMT_BF16 = 0
 FMT_NF4 = 1
 FMT_INT8 = 2
+FMT_F32X3 = 3      # fp32 weights as bf16 planes [hi | lo | hi] along in_features
+
+SPLIT_ACT = 0      # mx_split_f32 plane orders
+SPLIT_WEIGHT = 1
 
 RENORM_NONE = 0
 RENORM_CLAMP = 1
@@ -77,6 +81,8 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "mx_int8_dequantize": (c_int, [_P, _P, c_int64, c_int64, _P, c_int, _P]),
     "mx_set_stage_events": (c_int, [POINTER(c_void_p), c_int]),
     "mx_moe_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int64]),
+    "mx_moe_f32x3_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int64]),
+    "mx_split_f32": (c_int, [_P, c_int64, c_int64, c_int, _P, _P]),
     "mx_moe_forward": (
         c_int,
         [_P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, c_int64, _W, _W, _W, _L, _L, _L,

@@ -86,6 +86,7 @@ struct Params {
   uint16_t *save_gate;
   uint16_t *save_up;
   float scale[4];
+  int split_r[4];            // MX_FMT_F32X3 LoRA down-projection: rank of each adapter
 };
 
 // Per-thread choice among the small kernel-argument arrays by explicit
@@ -212,6 +213,9 @@ void grouped_gemm_kernel(Params p) {
   constexpr int kLTile = LORA ? (EPI == EPI_STORE2 ? 2 : 1) * T::BN * 64 : 16;
   __shared__ __attribute__((aligned(16))) uint8_t sLt[kLTile];
   const int tid = threadIdx.x;
+  // MX_FMT_F32X3: bf16 planes with K = 3 * in (loaded as bf16); the
+  // epilogues keep fp32 and write split outputs.
+  constexpr bool kSplit = FMT == MX_FMT_F32X3;
 
   // ---------------------------------------------------------------- tile
   const int num_m = *p.num_tiles;
@@ -588,9 +592,33 @@ void grouped_gemm_kernel(Params p) {
         const uint32_t off_s = f < p.N ? r0 * n2 + static_cast<uint32_t>(f) * 2u : kDrop;
 #pragma unroll
         for (int j = 0; j < 16; j += 2) {
-          // Two adjacent rows at a time: one packed conversion rounds both.
           float g0 = acc[mb][nbp][j], g1 = acc[mb][nbp][j + 1];
           float u0 = acc[mb][nbp + T::NB / 2][j], u1 = acc[mb][nbp + T::NB / 2][j + 1];
+          const uint32_t dr0 = static_cast<uint32_t>(8 * (j >> 2) + (j & 3));
+          if constexpr (kSplit) {
+            // fp32 layer: no intermediate rounding; h goes out as bf16 planes
+            // [hi | hi | lo] (row stride 3N), the down projection's split A.
+            if (LORA) {
+              g0 += lg[j];
+              g1 += lg[j + 1];
+              u0 += lu[j];
+              u1 += lu[j + 1];
+            }
+            const float h0 = g0 * __builtin_amdgcn_rcpf(1.0f + __expf(-g0)) * u0;
+            const float h1 = g1 * __builtin_amdgcn_rcpf(1.0f + __expf(-g1)) * u1;
+            const uint32_t hi = pack_bf16x2(h0, h1);
+            const uint32_t lo = pack_bf16x2(h0 - bf16_bits_to_f32(hi & 0xffffu),
+                                            h1 - bf16_bits_to_f32(hi >> 16));
+            const uint32_t planes[3] = {hi, hi, lo};
+#pragma unroll
+            for (int q = 0; q < 3; ++q) {
+              const uint32_t o = off_h + static_cast<uint32_t>(q) * n2;
+              __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(planes[q]), rs_h, o + dr0 * ld2, 0, 0);
+              __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(planes[q] >> 16), rs_h, o + (dr0 + 1) * ld2, 0, 0);
+            }
+            continue;
+          }
+          // Two adjacent rows at a time: one packed conversion rounds both.
           round2(g0, g1);
           round2(u0, u1);
           if (LORA) {
@@ -609,7 +637,6 @@ void grouped_gemm_kernel(Params p) {
           float s1 = g1 * __builtin_amdgcn_rcpf(1.0f + __expf(-g1));
           round2(s0, s1);
           const uint32_t h = pack_bf16x2(s0 * u0, s1 * u1);
-          const uint32_t dr0 = static_cast<uint32_t>(8 * (j >> 2) + (j & 3));
           __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(h), rs_h, off_h + dr0 * ld2, 0, 0);
           __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(h >> 16), rs_h, off_h + (dr0 + 1) * ld2, 0, 0);
           if (saves) {
@@ -643,12 +670,19 @@ void grouped_gemm_kernel(Params p) {
 #pragma unroll
         for (int j = 0; j < 16; j += 2) {
           float v0 = acc[mb][nb][j], v1 = acc[mb][nb][j + 1];
-          round2(v0, v1);
-          if (LORA) {
-            float a0 = l2[j], a1 = l2[j + 1];
-            round2(a0, a1);
-            v0 += a0;
-            v1 += a1;
+          if constexpr (kSplit) {
+            if (LORA) {  // fp32 layer: one rounding of the sum
+              v0 += l2[j];
+              v1 += l2[j + 1];
+            }
+          } else {
+            round2(v0, v1);
+            if (LORA) {
+              float a0 = l2[j], a1 = l2[j + 1];
+              round2(a0, a1);
+              v0 += a0;
+              v1 += a1;
+            }
           }
           const uint32_t v = pack_bf16x2(v0, v1);
           const int64_t rr = row0 + lrow + mb * 32 + 8 * (j >> 2) + (j & 3);
@@ -669,6 +703,36 @@ void grouped_gemm_kernel(Params p) {
         const float sc = pick(p.scale, ncol >> 5);
         const uint32_t r0 = static_cast<uint32_t>(lrow + mb * 32);
         const uint32_t off = ncol < p.N ? r0 * ld2 + static_cast<uint32_t>(ncol) * 2u : kDrop;
+        if constexpr (kSplit) {
+          // fp32 layer: column j < r of an adapter block leaves as planes
+          // [hi | hi | lo] at columns j, r + j, 2r + j (3r <= 32); columns
+          // from 3r on are zero. The rank-side LoRA factor is split [hi | lo |
+          // hi] likewise, so the epilogue's K = 32 product is fp32-accurate.
+          const int jc = ncol & 31, r = pick(p.split_r, ncol >> 5);
+          const uint32_t base = ncol < p.N ? r0 * ld2 + static_cast<uint32_t>(ncol - jc) * 2u : kDrop;
+          const bool own = jc < r, zero = jc >= 3 * r;
+          const uint32_t o_hi = own ? base + static_cast<uint32_t>(jc) * 2u : kDrop;
+          const uint32_t o_hi2 = own ? base + static_cast<uint32_t>(r + jc) * 2u : kDrop;
+          const uint32_t o_lo = own ? base + static_cast<uint32_t>(2 * r + jc) * 2u
+                                    : (zero ? off : kDrop);
+#pragma unroll
+          for (int j = 0; j < 16; j += 2) {
+            const float v0 = acc[mb][nb][j] * sc, v1 = acc[mb][nb][j + 1] * sc;
+            const uint32_t hi = pack_bf16x2(v0, v1);
+            const uint32_t lo = own ? pack_bf16x2(v0 - bf16_bits_to_f32(hi & 0xffffu),
+                                                  v1 - bf16_bits_to_f32(hi >> 16))
+                                    : 0u;
+            const uint32_t dr0 = static_cast<uint32_t>(8 * (j >> 2) + (j & 3));
+            const uint32_t st[3] = {hi, hi, lo};
+            const uint32_t at[3] = {o_hi, o_hi2, o_lo};
+#pragma unroll
+            for (int q = 0; q < 3; ++q) {
+              __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(st[q]), rs_o, at[q] + dr0 * ld2, 0, 0);
+              __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(st[q] >> 16), rs_o, at[q] + (dr0 + 1) * ld2, 0, 0);
+            }
+          }
+          continue;
+        }
 #pragma unroll
         for (int j = 0; j < 16; j += 2) {
           float v0 = acc[mb][nb][j], v1 = acc[mb][nb][j + 1];
@@ -724,6 +788,11 @@ int launch_fmt(int fmt, Params p, const PlanLayout &PL, const PlanView &v, bool 
     case MX_FMT_INT8:
       return tall ? launch<MX_FMT_INT8, EPI, LORA, Tall>(p, max_tiles, s)
                   : launch<MX_FMT_INT8, EPI, LORA, Short>(p, max_tiles, s);
+    case MX_FMT_F32X3:
+      if constexpr (EPI == EPI_SWIGLU || EPI == EPI_STORE)
+        return tall ? launch<MX_FMT_F32X3, EPI, LORA, Tall>(p, max_tiles, s)
+                    : launch<MX_FMT_F32X3, EPI, LORA, Short>(p, max_tiles, s);
+      break;
   }
   set_error("unknown weight format %d", fmt);
   return MX_ERR_INVALID;
@@ -751,19 +820,25 @@ void mark_stage(int i, hipStream_t s) {
 
 struct LayerLayout {
   PlanLayout plan;
-  size_t off_lora = 0, off_h = 0, off_y = 0, bytes = 0;
+  size_t off_lora = 0, off_h = 0, off_y = 0, off_x = 0, bytes = 0;
 };
 
-LayerLayout layer_layout(int64_t rows, int num_experts, int64_t hidden, int64_t ffn) {
+// Scratch of the layer: plan | low-rank activations [R, 96] | h [R, f] |
+// y [R, d]. The fp32 (MX_FMT_F32X3) layer holds h as planes [R, 3f] and adds
+// the split tokens [T, 3d].
+LayerLayout layer_layout(int64_t rows, int num_experts, int64_t hidden, int64_t ffn,
+                         bool split = false, int64_t tokens = 0) {
   LayerLayout L;
   L.plan = plan_layout(rows, num_experts);
   size_t off = align_up(L.plan.bytes, 256);
   L.off_lora = off;
   off = align_up(off + sizeof(uint16_t) * rows * kLoraLd, 256);
   L.off_h = off;
-  off = align_up(off + sizeof(uint16_t) * rows * ffn, 256);
+  off = align_up(off + sizeof(uint16_t) * rows * ffn * (split ? 3 : 1), 256);
   L.off_y = off;
   off = align_up(off + sizeof(uint16_t) * rows * hidden, 256);
+  L.off_x = off;
+  if (split) off = align_up(off + sizeof(uint16_t) * tokens * hidden * 3, 256);
   L.bytes = off;
   return L;
 }
@@ -782,11 +857,12 @@ int check_weight(const char *name, const char *key, const mx_weight *w, int64_t 
               static_cast<long long>(out_f), static_cast<long long>(in_f));
     return MX_ERR_INVALID;
   }
-  if (w->format != MX_FMT_BF16 && w->format != MX_FMT_NF4 && w->format != MX_FMT_INT8) {
+  if (w->format != MX_FMT_BF16 && w->format != MX_FMT_NF4 && w->format != MX_FMT_INT8 &&
+      w->format != MX_FMT_F32X3) {
     set_error("%s: weight %s has unknown format %d", name, key, w->format);
     return MX_ERR_INVALID;
   }
-  if (w->format != MX_FMT_BF16 && !w->scale) {
+  if ((w->format == MX_FMT_NF4 || w->format == MX_FMT_INT8) && !w->scale) {
     set_error("%s: weight %s needs its scale / absmax buffer", name, key);
     return MX_ERR_INVALID;
   }
@@ -814,7 +890,7 @@ Params base_params(const PlanView &v) {
 // share the same input rows; adapter i lands in columns [32i, 32i+32).
 int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t *x, int64_t ldx,
               const int32_t *row_token, int64_t K, const mx_lora *const *adapters, int n_adapt,
-              uint16_t *out, int64_t ldo, hipStream_t s) {
+              uint16_t *out, int64_t ldo, hipStream_t s, bool split = false) {
   Params p = base_params(v);
   p.x = x;
   p.ldx = ldx;
@@ -825,6 +901,7 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
     p.w[i] = has_lora(l) ? l->a : nullptr;
     p.wn[i] = has_lora(l) ? l->rank : 0;
     p.scale[i] = has_lora(l) ? l->scale : 0.0f;
+    p.split_r[i] = has_lora(l) ? l->rank : 0;
   }
   p.N = 32 * n_adapt;
   p.n_tiles_n = 1;
@@ -834,6 +911,8 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
   // Up to two adapters fill a 64-column tile; the kernel is bound by the
   // activation reads, so the narrower tile (more workgroups, half the MFMA
   // and B traffic) is the faster one.
+  // The fp32 layer (split planes, K = 3 * in) writes split outputs.
+  if (split) return launch<MX_FMT_F32X3, EPI_LORA_A, false, Tile<128, 64, 4, 1, 64>>(p, max_tiles, s);
   if (n_adapt <= 2)
     return launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 64, 4, 1, 64>>(p, max_tiles, s);
   return launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 128, 2, 2, 64>>(p, max_tiles, s);
@@ -848,10 +927,16 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
                const int32_t *out_row, hipStream_t s) {
   const bool lora13 = has_lora(l1) || has_lora(l3);
   const bool lora2 = has_lora(l2);
+  // fp32 layer (MX_FMT_F32X3): K runs over three bf16 planes, h is written as
+  // planes, and the LoRA factors carry 3r split columns.
+  const bool split = w1->format == MX_FMT_F32X3;
+  const int64_t kx = split ? 3 : 1;
+  const int rx = split ? 3 : 1;
   int rc;
   if (lora13) {
     const mx_lora *ad[2] = {l1, l3};
-    rc = lora_down(v, experts, PL.max_tiles, x, ldx, row_token, hidden, ad, 2, lora_buf, kLoraLd, s);
+    rc = lora_down(v, experts, PL.max_tiles, x, ldx, row_token, kx * hidden, ad, 2, lora_buf,
+                   kLoraLd, s, split);
     if (rc) return rc;
   }
   mark_stage(2, s);
@@ -860,7 +945,7 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
     p.x = x;
     p.ldx = ldx;
     p.row_token = row_token;
-    p.K = hidden;
+    p.K = kx * hidden;
     p.w[0] = w1->data;
     p.w[1] = w3->data;
     p.wscale[0] = static_cast<const uint16_t *>(w1->scale);
@@ -871,11 +956,11 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
     p.ldp = kLoraLd;
     p.lora_b[0] = has_lora(l1) ? static_cast<const uint16_t *>(l1->b) : nullptr;
     p.lora_b[1] = has_lora(l3) ? static_cast<const uint16_t *>(l3->b) : nullptr;
-    p.lora_r[0] = has_lora(l1) ? l1->rank : 0;
-    p.lora_r[1] = has_lora(l3) ? l3->rank : 0;
+    p.lora_r[0] = has_lora(l1) ? rx * l1->rank : 0;
+    p.lora_r[1] = has_lora(l3) ? rx * l3->rank : 0;
     p.seg_end = v.seg + experts;
     p.out = h;
-    p.ldo = ffn;
+    p.ldo = kx * ffn;
     p.save_gate = save_gate;
     p.save_up = save_up;
     rc = launch_any<EPI_SWIGLU>(w1->format, lora13, p, PL, v, s);
@@ -884,15 +969,16 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
   mark_stage(3, s);
   if (lora2) {
     const mx_lora *ad[1] = {l2};
-    rc = lora_down(v, experts, PL.max_tiles, h, ffn, nullptr, ffn, ad, 1, lora_buf + 64, kLoraLd, s);
+    rc = lora_down(v, experts, PL.max_tiles, h, kx * ffn, nullptr, kx * ffn, ad, 1, lora_buf + 64,
+                   kLoraLd, s, split);
     if (rc) return rc;
   }
   mark_stage(4, s);
   Params p = base_params(v);
   p.x = h;
-  p.ldx = ffn;
+  p.ldx = kx * ffn;
   p.row_token = nullptr;
-  p.K = ffn;
+  p.K = kx * ffn;
   p.w[0] = w2->data;
   p.wscale[0] = static_cast<const uint16_t *>(w2->scale);
   p.wn[0] = hidden;
@@ -900,7 +986,7 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
   p.lora_p = lora_buf + 64;
   p.ldp = kLoraLd;
   p.lora_b[0] = lora2 ? static_cast<const uint16_t *>(l2->b) : nullptr;
-  p.lora_r[0] = lora2 ? l2->rank : 0;
+  p.lora_r[0] = lora2 ? rx * l2->rank : 0;
   p.seg_end = v.seg + experts;
   p.out = y;
   p.ldo = ldy;
@@ -927,6 +1013,20 @@ int check_layer(const char *name, int64_t hidden, int64_t ffn, const mx_weight *
   if ((rc = check_lora(name, "w1", l1))) return rc;
   if ((rc = check_lora(name, "w3", l3))) return rc;
   if ((rc = check_lora(name, "w2", l2))) return rc;
+  const bool split = w1->format == MX_FMT_F32X3;
+  if (split != (w2->format == MX_FMT_F32X3)) {
+    set_error("%s: MX_FMT_F32X3 (fp32) weights must be used for all three projections", name);
+    return MX_ERR_INVALID;
+  }
+  if (split) {
+    const mx_lora *ls[3] = {l1, l3, l2};
+    for (const mx_lora *l : ls)
+      if (has_lora(l) && l->rank != 8) {
+        set_error("%s: the fp32 (MX_FMT_F32X3) layer takes LoRA factors padded to rank 8 "
+                  "(split into 24 columns); got rank %d", name, l->rank);
+        return MX_ERR_INVALID;
+      }
+  }
   return MX_OK;
 }
 
@@ -1002,6 +1102,10 @@ extern "C" int mx_moe_backward(const void *grad_out, int grad_dtype, const void 
   int rc = validate_plan_args(name, num_tokens, top_k, num_experts);
   if (rc) return rc;
   if ((rc = check_layer(name, hidden, ffn, w1, w3, w2, l1, l3, l2))) return rc;
+  if (w1->format == MX_FMT_F32X3) {
+    set_error("%s: the fp32 (MX_FMT_F32X3) layer is inference-only", name);
+    return MX_ERR_INVALID;
+  }
   if (num_tokens == 0) return MX_OK;
   const bool lora1 = has_lora(l1), lora3 = has_lora(l3), lora2 = has_lora(l2);
   if (!grad_out || !tokens || !top_idx || !top_scores || !save_gate || !save_up || !save_h ||
@@ -1156,6 +1260,12 @@ extern "C" size_t mx_moe_workspace_size(int64_t num_tokens, int top_k, int num_e
   return layer_layout(num_tokens * top_k, num_experts, hidden, ffn).bytes;
 }
 
+extern "C" size_t mx_moe_f32x3_workspace_size(int64_t num_tokens, int top_k, int num_experts,
+                                              int64_t hidden, int64_t ffn) {
+  if (num_tokens < 0 || top_k <= 0 || num_experts <= 0 || hidden <= 0 || ffn <= 0) return 0;
+  return layer_layout(num_tokens * top_k, num_experts, hidden, ffn, true, num_tokens).bytes;
+}
+
 extern "C" int mx_moe_forward(const void *tokens, const int64_t *top_idx, const void *top_scores,
                               int score_dtype, int64_t num_tokens, int top_k, int num_experts,
                               int64_t hidden, int64_t ffn, const mx_weight *w1,
@@ -1175,10 +1285,25 @@ extern "C" int mx_moe_forward(const void *tokens, const int64_t *top_idx, const 
   }
   hipStream_t s = as_stream(stream);
   const int64_t R = num_tokens * top_k;
-  const LayerLayout L = layer_layout(R, num_experts, hidden, ffn);
+  const bool split = w1->format == MX_FMT_F32X3;
+  if (split && (save_gate || save_up || save_h || save_y || save_lora)) {
+    set_error("%s: the fp32 (MX_FMT_F32X3) layer is inference-only and saves no activations",
+              name);
+    return MX_ERR_INVALID;
+  }
+  const LayerLayout L = layer_layout(R, num_experts, hidden, ffn, split, num_tokens);
   char *ws = static_cast<char *>(workspace);
   const PlanView v = plan_view(ws, L.plan);
   mark_stage(0, s);
+  // fp32 tokens -> [hi | hi | lo] bf16 planes, the A side of the split GEMMs.
+  const uint16_t *x = static_cast<const uint16_t *>(tokens);
+  if (split) {
+    uint16_t *xs = reinterpret_cast<uint16_t *>(ws + L.off_x);
+    if ((rc = mx_split_f32(static_cast<const float *>(tokens), num_tokens, hidden, MX_SPLIT_ACT,
+                           xs, stream)))
+      return rc;
+    x = xs;
+  }
   rc = build_plan(top_idx, nullptr, score_dtype, num_tokens, top_k, num_experts, nullptr, nullptr,
                   nullptr, nullptr, nullptr, nullptr, nullptr, ws, s);
   if (rc) return rc;
@@ -1187,7 +1312,7 @@ extern "C" int mx_moe_forward(const void *tokens, const int64_t *top_idx, const 
                                  : reinterpret_cast<uint16_t *>(ws + L.off_lora);
   uint16_t *h = save_h ? static_cast<uint16_t *>(save_h) : reinterpret_cast<uint16_t *>(ws + L.off_h);
   uint16_t *y = save_y ? static_cast<uint16_t *>(save_y) : reinterpret_cast<uint16_t *>(ws + L.off_y);
-  rc = expert_mlp(L.plan, v, num_experts, static_cast<const uint16_t *>(tokens), hidden,
+  rc = expert_mlp(L.plan, v, num_experts, x, (split ? 3 : 1) * hidden,
                   v.row_token, hidden, ffn, w1, w3, w2, l1, l3, l2, lora_buf, h,
                   static_cast<uint16_t *>(save_gate), static_cast<uint16_t *>(save_up), y, hidden,
                   v.row_slot, s);
@@ -1220,6 +1345,10 @@ extern "C" int mx_moe_for_loop(const void *tokens_sorted, const int64_t *counts,
   int rc = validate_plan_args(name, num_rows, 1, num_experts);
   if (rc) return rc;
   if ((rc = check_layer(name, hidden, ffn, w1, w3, w2, l1, l3, l2))) return rc;
+  if (w1->format == MX_FMT_F32X3) {
+    set_error("%s: MX_FMT_F32X3 (fp32) weights are supported by mx_moe_forward only", name);
+    return MX_ERR_INVALID;
+  }
   if (num_rows == 0) return MX_OK;
   if (!tokens_sorted || !counts || !out || !workspace) {
     set_error("%s: tokens, counts, output and workspace must be non-null", name);
@@ -1255,6 +1384,10 @@ extern "C" int mx_grouped_linear(const void *x, const int64_t *counts, int64_t n
   }
   if ((rc = check_weight(name, "w", w, out_f, in_f))) return rc;
   if ((rc = check_lora(name, "w", lora))) return rc;
+  if (w->format == MX_FMT_F32X3) {
+    set_error("%s: MX_FMT_F32X3 (fp32) weights are supported by mx_moe_forward only", name);
+    return MX_ERR_INVALID;
+  }
   if (num_rows == 0) return MX_OK;
   if (!x || !counts || !out || !workspace) {
     set_error("%s: x, counts, output and workspace must be non-null", name);

@@ -276,10 +276,56 @@ __global__ __launch_bounds__(256) void combine_backward_kernel(
   }
 }
 
+// fp32 -> bf16 planes: one thread per 8 values of a row; hi = bf16(x),
+// lo = bf16(x - hi) (x - hi is exact in fp32).
+__global__ __launch_bounds__(256) void split_f32_kernel(const float4 *x, int64_t rows,
+                                                        int64_t chunks, int pattern, uint4 *out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= rows * chunks) return;
+  const int64_t r = i / chunks, c = i - r * chunks;
+  const float4 a = x[2 * i], b = x[2 * i + 1];
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t hi[4], lo[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    hi[q] = pack_bf16x2(v[2 * q], v[2 * q + 1]);
+    lo[q] = pack_bf16x2(v[2 * q] - bf16_bits_to_f32(hi[q] & 0xffffu),
+                        v[2 * q + 1] - bf16_bits_to_f32(hi[q] >> 16));
+  }
+  const uint4 H = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+  const uint4 L = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+  uint4 *o = out + r * 3 * chunks + c;
+  o[0] = H;
+  o[chunks] = pattern == MX_SPLIT_ACT ? H : L;
+  o[2 * chunks] = pattern == MX_SPLIT_ACT ? L : H;
+}
+
 }  // namespace
+
+int split_f32(const float *x, int64_t rows, int64_t cols, int pattern, uint16_t *out,
+              hipStream_t s) {
+  if (!x || !out || rows < 0 || cols <= 0 || cols % 8 != 0 ||
+      (pattern != MX_SPLIT_ACT && pattern != MX_SPLIT_WEIGHT)) {
+    set_error("mx_split_f32: need non-null buffers, cols a multiple of 8 and a known pattern");
+    return MX_ERR_INVALID;
+  }
+  if (rows == 0) return MX_OK;
+  const int64_t chunks = cols / 8;
+  hipLaunchKernelGGL(split_f32_kernel, dim3(static_cast<unsigned>(ceil_div(rows * chunks, 256))),
+                     dim3(256), 0, s, reinterpret_cast<const float4 *>(x), rows, chunks, pattern,
+                     reinterpret_cast<uint4 *>(out));
+  return check_launch("mx_split_f32");
+}
+
 }  // namespace mx
 
 using namespace mx;
+
+extern "C" int mx_split_f32(const float *x, int64_t rows, int64_t cols, int pattern, void *out,
+                            void *stream) {
+  clear_error();
+  return split_f32(x, rows, cols, pattern, static_cast<uint16_t *>(out), as_stream(stream));
+}
 
 extern "C" int mx_gather_rows(const void *tokens, int64_t src_rows, const int64_t *index,
                               int64_t rows, int64_t cols, int dtype, void *out, void *stream) {

@@ -39,6 +39,7 @@ _BUFFER_SUFFIXES = {
     "nf4": ("_nf4", "_nf4_absmax"),
     "int8": ("_int8", "_scale"),
     "bf16": ("_bf16", None),
+    "fp32": ("_f32x3", None),
 }
 
 

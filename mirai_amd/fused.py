@@ -17,14 +17,14 @@ from . import _native as nat
 LORA_ROW = 96  # [gate 32 | up 32 | down 32] scaled low-rank activations per sorted row
 
 
-def _lora_descriptors(module, device):
+def _lora_descriptors(module, device, split=False):
     """MxLora structs for (gate, up, down) plus the bf16 factor tensors they point to."""
     descs, keep = [], []
     for adapter in module._adapters():
         if adapter is None:
             descs.append(nat.MxLora(None, None, 0, 0.0))
             continue
-        a, b = adapter.kernel_factors(device)
+        a, b = adapter.kernel_factors(device, split=split)
         keep += [a, b]
         descs.append(nat.MxLora(a.data_ptr(), b.data_ptr(), adapter.padded_rank(),
                                 float(adapter.scale())))
@@ -48,48 +48,60 @@ def _lora_params(module):
     return params
 
 
+def _forward(module, tokens, top_scores, top_indices, need_grad):
+    """One mx_moe_forward call; returns (out, saved tensors or None)."""
+    device = nat.require_gpu(tokens, top_scores, top_indices)
+    # fp32 weights (quant_format "fp32") run the split-precision layer on
+    # fp32 tokens; the other formats take bf16 tokens.
+    split = module.quant_format == "fp32"
+    x = tokens.detach().to(torch.float32 if split else torch.bfloat16).contiguous()
+    scores = top_scores.detach()
+    if scores.dtype not in (torch.float32, torch.bfloat16):
+        scores = scores.float()
+    scores = scores.contiguous()
+    idx = top_indices.detach().to(torch.int64).contiguous()
+    T, d = (int(v) for v in x.shape)
+    k = int(idx.shape[1])
+    E = module.num_experts
+    (w1, w3, w2), packed = _weight_descriptors(module, device)
+    f = int(packed[0].shape[1])
+    lora, keep = _lora_descriptors(module, device, split)
+    out = torch.empty((T, d), dtype=tokens.dtype if tokens.dtype == torch.float32
+                      else torch.bfloat16, device=device)
+    if need_grad and split:
+        raise NotImplementedError(
+            "the fp32 (quant_format='fp32') expert layer is inference-only; train adapters "
+            "over bf16, nf4 or int8 weights")
+    R = T * k
+    saves = [None] * 5
+    if need_grad:
+        saves = [
+            torch.empty((R, f), dtype=torch.bfloat16, device=device),  # gate
+            torch.empty((R, f), dtype=torch.bfloat16, device=device),  # up
+            torch.empty((R, f), dtype=torch.bfloat16, device=device),  # h
+            torch.empty((R, d), dtype=torch.bfloat16, device=device),  # y (slot order)
+            torch.zeros((R, LORA_ROW), dtype=torch.bfloat16, device=device),
+        ]
+    lib = nat.load_library()
+    size = lib.mx_moe_f32x3_workspace_size if split else lib.mx_moe_workspace_size
+    ws = nat.workspace(size(T, k, E, d, f), device)
+    nat.call("mx_moe_forward", x.data_ptr(), idx.data_ptr(), scores.data_ptr(),
+             nat.dtype_code(scores.dtype), T, k, E, d, f, w1, w3, w2, lora[0], lora[1],
+             lora[2], out.data_ptr(), nat.dtype_code(out.dtype), *[nat.ptr(t) for t in saves],
+             ws.data_ptr(), nat.stream(device))
+    del keep
+    return out.to(tokens.dtype), ((x, scores, idx, *saves) if need_grad else None)
+
+
 class _RoutedExperts(torch.autograd.Function):
     @staticmethod
     def forward(ctx, module, tokens, top_scores, top_indices, *lora_params):
-        device = nat.require_gpu(tokens, top_scores, top_indices)
-        x = tokens.detach().to(torch.bfloat16).contiguous()
-        scores = top_scores.detach()
-        if scores.dtype not in (torch.float32, torch.bfloat16):
-            scores = scores.float()
-        scores = scores.contiguous()
-        idx = top_indices.detach().to(torch.int64).contiguous()
-        T, d = (int(v) for v in x.shape)
-        k = int(idx.shape[1])
-        E = module.num_experts
-        (w1, w3, w2), packed = _weight_descriptors(module, device)
-        f = int(packed[0].shape[1])
-        lora, keep = _lora_descriptors(module, device)
-        out = torch.empty((T, d), dtype=tokens.dtype if tokens.dtype == torch.float32
-                          else torch.bfloat16, device=device)
-        need_grad = any(ctx.needs_input_grad[1:])
-        R = T * k
-        saves = [None] * 5
-        if need_grad:
-            saves = [
-                torch.empty((R, f), dtype=torch.bfloat16, device=device),  # gate
-                torch.empty((R, f), dtype=torch.bfloat16, device=device),  # up
-                torch.empty((R, f), dtype=torch.bfloat16, device=device),  # h
-                torch.empty((R, d), dtype=torch.bfloat16, device=device),  # y (slot order)
-                torch.zeros((R, LORA_ROW), dtype=torch.bfloat16, device=device),
-            ]
-        lib = nat.load_library()
-        ws = nat.workspace(lib.mx_moe_workspace_size(T, k, E, d, f), device)
-        nat.call("mx_moe_forward", x.data_ptr(), idx.data_ptr(), scores.data_ptr(),
-                 nat.dtype_code(scores.dtype), T, k, E, d, f, w1, w3, w2, lora[0], lora[1],
-                 lora[2], out.data_ptr(), nat.dtype_code(out.dtype), *[nat.ptr(t) for t in saves],
-                 ws.data_ptr(), nat.stream(device))
-        del keep
-        if need_grad:
-            ctx.module = module
-            ctx.token_dtype = tokens.dtype
-            ctx.score_dtype = top_scores.dtype
-            ctx.save_for_backward(x, scores, idx, *saves)
-        return out.to(tokens.dtype)
+        out, saved = _forward(module, tokens, top_scores, top_indices, True)
+        ctx.module = module
+        ctx.token_dtype = tokens.dtype
+        ctx.score_dtype = top_scores.dtype
+        ctx.save_for_backward(*saved)
+        return out
 
     @staticmethod
     def backward(ctx, grad_out):
@@ -98,7 +110,13 @@ class _RoutedExperts(torch.autograd.Function):
 
 
 def routed_experts(module, tokens, top_scores, top_indices):
-    return _RoutedExperts.apply(module, tokens, top_scores, top_indices, *_lora_params(module))
+    """The routed layer; with autograd only when a gradient can flow (in
+    inference nothing is saved for a backward)."""
+    params = _lora_params(module)
+    if torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (tokens, top_scores, *params)):
+        return _RoutedExperts.apply(module, tokens, top_scores, top_indices, *params)
+    return _forward(module, tokens, top_scores, top_indices, False)[0]
 
 
 def sorted_experts(module, tokens, counts):

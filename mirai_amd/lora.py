@@ -77,18 +77,25 @@ class ActiveExpertLoRA(nn.Module):
         """Rank rounded up to the kernel's multiple of 8 (zero-padded factors)."""
         return (self.rank + 7) // 8 * 8
 
-    def kernel_factors(self, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    def kernel_factors(self, device: torch.device, *,
+                       split: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
         """bf16 copies of A [E, r8, in] and B [E, out, r8] for the fused kernels.
 
         Padding rows of A and columns of B are zero, which leaves the product
-        unchanged.
+        unchanged. ``split`` (the fp32 layer) returns the fp32 factors as bf16
+        planes [hi | lo | hi] instead: A [E, r8, 3*in], B [E, out, 3*r8].
         """
-        a = self.lora_a.detach().to(device=device, dtype=torch.bfloat16)
-        b = self.lora_b.detach().to(device=device, dtype=torch.bfloat16)
+        dtype = torch.float32 if split else torch.bfloat16
+        a = self.lora_a.detach().to(device=device, dtype=dtype)
+        b = self.lora_b.detach().to(device=device, dtype=dtype)
         pad = self.padded_rank() - self.rank
         if pad:
             a = torch.cat([a, a.new_zeros(a.shape[0], pad, a.shape[2])], dim=1)
             b = torch.cat([b, b.new_zeros(b.shape[0], b.shape[1], pad)], dim=2)
+        if split:
+            from .quant import split_planes
+            from ._native import SPLIT_WEIGHT
+            return split_planes(a, SPLIT_WEIGHT), split_planes(b, SPLIT_WEIGHT)
         return a.contiguous(), b.contiguous()
 
     def extra_repr(self) -> str:

@@ -4,6 +4,9 @@
              bf16 absmax [E, out, in/64]; blocksize 64, no double quantisation.
 * ``int8`` : int8 [E, out, in] and bf16 per-output-row scale [E, out].
 * ``bf16`` : unquantised bf16 [E, out, in].
+* ``fp32`` : unquantised fp32 as bf16 planes [E, out, 3*in] = [hi | lo | hi]
+             (hi = bf16(w), lo = bf16(w - hi)); with fp32 tokens split as
+             [hi | hi | lo] the bf16 MFMA products reach fp32 accuracy.
 
 Replaces the storage side of mirai/core/models/compressed_weights/quantization/quant.py
 (_quantize_weight :189-235, _dequantize_weight :238-260, _nf4_quantize_2d
@@ -20,13 +23,15 @@ import torch
 from . import _native as nat
 
 NF4_BLOCKSIZE = 64
-QUANT_FORMATS = ("nf4", "int8", "bf16")
-_FORMAT_CODES = {"bf16": nat.FMT_BF16, "nf4": nat.FMT_NF4, "int8": nat.FMT_INT8}
+QUANT_FORMATS = ("nf4", "int8", "bf16", "fp32")
+_FORMAT_CODES = {"bf16": nat.FMT_BF16, "nf4": nat.FMT_NF4, "int8": nat.FMT_INT8,
+                 "fp32": nat.FMT_F32X3}
 
 
 def normalize_quant_format(value: str | None) -> str:
     text = str(value or "int8").strip().lower()
-    text = {"": "int8", "auto": "int8", "bfloat16": "bf16", "none": "bf16"}.get(text, text)
+    text = {"": "int8", "auto": "int8", "bfloat16": "bf16", "none": "bf16", "float32": "fp32",
+            "f32": "fp32"}.get(text, text)
     if text not in QUANT_FORMATS:
         raise ValueError(
             "compressed_weights quant_format must be one of: " + ", ".join(QUANT_FORMATS) + "."
@@ -79,6 +84,9 @@ def quantize(source: torch.Tensor, fmt: str) -> PackedWeight:
     s = nat.stream(device)
     if fmt == "bf16":
         return PackedWeight("bf16", w.to(torch.bfloat16).contiguous(), None, (E, out_f, in_f))
+    if fmt == "fp32":
+        return PackedWeight("fp32", split_planes(w.float(), nat.SPLIT_WEIGHT), None,
+                            (E, out_f, in_f))
     if fmt == "nf4":
         codes = torch.empty((E, out_f, in_f // 2), dtype=torch.uint8, device=device)
         absmax = torch.empty((E, out_f, in_f // NF4_BLOCKSIZE), dtype=torch.bfloat16, device=device)
@@ -102,6 +110,8 @@ def dequantize(packed: PackedWeight, *, dtype: torch.dtype = torch.bfloat16,
     device = data.device
     if packed.fmt == "bf16":
         return data.to(dtype)
+    if packed.fmt == "fp32":  # hi + lo planes
+        return (data[..., :in_f].float() + data[..., in_f:2 * in_f].float()).to(dtype)
     nat.require_gpu(data)
     out = torch.empty((E, out_f, in_f), dtype=dtype, device=device)
     rows = E * out_f
@@ -114,4 +124,18 @@ def dequantize(packed: PackedWeight, *, dtype: torch.dtype = torch.bfloat16,
     else:
         nat.call("mx_int8_dequantize", data.data_ptr(), scale.data_ptr(), rows, in_f,
                  out.data_ptr(), nat.dtype_code(dtype), s)
+    return out
+
+
+def split_planes(x: torch.Tensor, pattern: int) -> torch.Tensor:
+    """fp32 [..., n] -> bf16 [..., 3n] planes on the GPU (mx_split_f32):
+    [hi | hi | lo] for ``SPLIT_ACT``, [hi | lo | hi] for ``SPLIT_WEIGHT``."""
+    if x.dtype != torch.float32:
+        raise ValueError(f"split_planes takes fp32, got {x.dtype}")
+    x = x.contiguous()
+    device = nat.require_gpu(x)
+    cols = int(x.shape[-1])
+    rows = x.numel() // max(cols, 1)
+    out = torch.empty((*x.shape[:-1], 3 * cols), dtype=torch.bfloat16, device=device)
+    nat.call("mx_split_f32", x.data_ptr(), rows, cols, pattern, out.data_ptr(), nat.stream(device))
     return out

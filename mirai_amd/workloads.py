@@ -4,7 +4,8 @@ C1-C5 are the five configurations of the benchmark definition; ``target`` is
 the C2 geometry at 32768 tokens on which the throughput goal is stated.
 Seeds: 1000 + config index for logits, +1 weights, +2 LoRA, +3 tokens, +4 dY.
 Inputs: tokens ~ N(0, 1) in the activation dtype, frozen weights ~ N(0, 0.02)
-rounded to bf16, LoRA A, B ~ N(0, 0.02), router logits ~ N(0, 1) (plus a
+(fp32 for C1's unquantised fp32 layer, else rounded to bf16 before any
+quantisation), LoRA A, B ~ N(0, 0.02), router logits ~ N(0, 1) (plus a
 per-expert Zipf(1.2) bias for C3), upstream gradient ~ N(0, 1).
 """
 
@@ -27,7 +28,7 @@ class Workload:
     top_k: int
     rank: int
     alpha: float
-    fmt: str                  # "bf16" | "nf4" | "int8"
+    fmt: str                  # "fp32" | "bf16" | "nf4" | "int8"
     dtype: torch.dtype
     zipf: float = 0.0         # Zipf exponent of the per-expert logit bias (0: none)
     backward: bool = False
@@ -46,7 +47,7 @@ class Workload:
 
 
 WORKLOADS = {
-    "c1": Workload("c1_fp32_plumbing", 0, 512, 512, 1024, 8, 2, 8, 16.0, "bf16", torch.float32),
+    "c1": Workload("c1_fp32_plumbing", 0, 512, 512, 1024, 8, 2, 8, 16.0, "fp32", torch.float32),
     "c2": Workload("c2_nf4_balanced", 1, 4096, 2048, 1408, 64, 4, 16, 16.0, "nf4", torch.bfloat16),
     "c3": Workload("c3_nf4_zipf", 2, 8192, 2048, 768, 128, 8, 8, 16.0, "nf4", torch.bfloat16,
                    zipf=1.2),
@@ -99,15 +100,17 @@ def upstream_grad(w: Workload, device="cpu") -> torch.Tensor:
 
 
 def dense_weights(w: Workload, device="cpu", experts: int | None = None) -> dict[str, torch.Tensor]:
-    """bf16 frozen weights {w1, w3: [E, f, d], w2: [E, d, f]}, ~N(0, 0.02)."""
+    """Frozen weights {w1, w3: [E, f, d], w2: [E, d, f]}, ~N(0, 0.02): fp32 for
+    the fp32 format, else bf16."""
     E = w.experts if experts is None else int(experts)
     g = _gen(1000 + w.index + 1, device)
+    dtype = torch.float32 if w.fmt == "fp32" else torch.bfloat16
     out = {}
     for key, shape in (("w1", (E, w.ffn, w.hidden)), ("w3", (E, w.ffn, w.hidden)),
                        ("w2", (E, w.hidden, w.ffn))):
-        t = torch.empty(shape, dtype=torch.bfloat16, device=device)
+        t = torch.empty(shape, dtype=dtype, device=device)
         for e in range(E):  # per expert keeps the fp32 temporary small
-            t[e] = (torch.randn(shape[1:], generator=g, device=device) * 0.02).to(torch.bfloat16)
+            t[e] = (torch.randn(shape[1:], generator=g, device=device) * 0.02).to(dtype)
         out[key] = t
     return out
 
@@ -132,7 +135,7 @@ def active_weight_bytes(w: Workload, counts) -> int:
     """Packed bytes of the experts that receive at least one row (3 projections)."""
     d, f, r = w.hidden, w.ffn, w.rank
     per = {"nf4": 3 * d * f // 2 + 3 * d * f // 64 * 2, "int8": 3 * d * f + (2 * f + d) * 2,
-           "bf16": 3 * d * f * 2}[w.fmt]
+           "bf16": 3 * d * f * 2, "fp32": 3 * d * f * 4}[w.fmt]
     per += 3 * r * (d + f) * 2
     active = int((torch.as_tensor(counts) > 0).sum())
     return active * per

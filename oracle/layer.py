@@ -37,7 +37,7 @@ def dense_weight(fmt: str, payload, shape, dtype=torch.bfloat16) -> torch.Tensor
     """Dense [E, out, in] tensor of a stored weight, decoded by the oracle codec
     (the C restatement in oracle/codec.c, equal to oracle/codec.py)."""
     E, out_f, in_f = shape
-    if fmt == "bf16":
+    if fmt in ("bf16", "fp32"):
         return payload.to(dtype)
     if fmt == "nf4":
         codes, absmax = payload

@@ -28,7 +28,10 @@ def assert_layer_close(actual: torch.Tensor, expected: torch.Tensor, *, max_abs=
 
 
 def oracle_payload(fmt: str, dense: torch.Tensor):
-    """Quantise a dense bf16 [E, out, in] weight with the oracle codec."""
+    """Quantise a dense bf16 [E, out, in] weight with the oracle codec (fp32 and
+    bf16 weights are stored as they are)."""
+    if fmt in ("bf16", "fp32"):
+        return dense
     E, o, i = dense.shape
     bits = dense.contiguous().view(torch.int16).numpy().view(np.uint16).reshape(E * o, i)
     if fmt == "nf4":

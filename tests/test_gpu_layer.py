@@ -58,12 +58,32 @@ def test_ragged_and_empty_experts():
     _run_case(small("int8", T=37, E=64, k=4, d=128, f=128))
 
 
-@pytest.mark.xfail(strict=True, reason=(
-    "fp32 tokens and fp32 weights run on bf16 MFMA; versus the fp32 reference the "
-    "mean-relative error is ~5.4e-3, above the 5e-3 bound (split-precision path pending)"))
 def test_fp32_tokens_c1_plumbing():
-    w = wl.WORKLOADS["c1"]
-    _run_case(w)
+    # fp32 tokens, fp32 weights (split bf16 planes on MFMA), fp32 LoRA and output.
+    stats = _run_case(wl.WORKLOADS["c1"])
+    # Everything runs at fp32 precision except the one bf16 rounding of each
+    # expert output row y before the fp32 combine (mean-relative ~1.5e-3).
+    assert stats["mean_rel"] < 2.5e-3, stats
+
+
+@pytest.mark.parametrize("with_lora", [False, True])
+def test_fp32_layer_small(with_lora):
+    w = small("fp32", dtype=torch.float32, r=8, alpha=16.0, T=300, E=6, k=2, d=192, f=320)
+    stats = _run_case(w, with_lora=with_lora)
+    assert stats["mean_rel"] < 2.5e-3, stats
+
+
+def test_fp32_layer_is_inference_only():
+    w = small("fp32", dtype=torch.float32, r=8)
+    m = build_module(w, wl.dense_weights(w), wl.lora_factors(w))
+    x = wl.tokens(w).cuda().requires_grad_(True)
+    idx, scores = oroute.route_topk(wl.router_logits(w).numpy(), w.top_k)
+    with pytest.raises(NotImplementedError, match="inference-only"):
+        m.run_direct_routed(x, torch.from_numpy(scores).cuda(), torch.from_numpy(idx).cuda())
+    counts = torch.bincount(torch.from_numpy(idx).reshape(-1), minlength=w.experts)
+    rows = torch.randn(int(counts.sum()), w.hidden).cuda()
+    with pytest.raises(ValueError, match="mx_moe_forward only"), torch.no_grad():
+        m.run_for_loop(rows, counts.cuda())
 
 
 def test_c2_full_size_on_token_subset():
