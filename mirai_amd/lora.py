@@ -85,6 +85,18 @@ class ActiveExpertLoRA(nn.Module):
         unchanged. ``split`` (the fp32 layer) returns the fp32 factors as bf16
         planes [hi | lo | hi] instead: A [E, r8, 3*in], B [E, out, 3*r8].
         """
+        # The packed copies are kept while the parameters are unchanged (same
+        # storage, same in-place version), so inference packs them once.
+        key = (str(device), bool(split), self.lora_a.data_ptr(), self.lora_a._version,
+               self.lora_b.data_ptr(), self.lora_b._version)
+        cached = self.__dict__.get("_kernel_cache")
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        factors = self._pack_factors(device, split)
+        self.__dict__["_kernel_cache"] = (key, factors)
+        return factors
+
+    def _pack_factors(self, device, split):
         dtype = torch.float32 if split else torch.bfloat16
         a = self.lora_a.detach().to(device=device, dtype=dtype)
         b = self.lora_b.detach().to(device=device, dtype=dtype)
