@@ -44,16 +44,22 @@ __device__ __forceinline__ bf16x8 read_v_trans(const uint8_t *sV, int kk, int la
 // One workgroup (4 waves) per (expert, 256-column slice): G[c, j] = sum over
 // the expert's rows of M[row, c] * V[row, j] on bf16 MFMA with fp32
 // accumulation. Both operands arrive row-major (the reduction runs along
-// rows), so 64-row tiles of M and V go to LDS as they are and the MFMA
+// rows), so 64-row chunks of M and V go to LDS as they are and the MFMA
 // fragments are read with ds_read_b64_tr_b16. Each wave owns 64 columns x 32
 // ranks (two 32 x 32 blocks). Rows past the segment and columns past `cols`
-// are zero-filled.
+// are zero-filled. The kernel streams M once, so it is bound by load latency:
+// each thread keeps two chunks of its loads in flight (register sets A and B,
+// alternating), the row map of the chunk after them is fetched one chunk ahead,
+// and two LDS stages alternate, so a chunk's loads are issued two chunks
+// before its MFMAs.
 __global__ __launch_bounds__(256) void lora_weight_grad_kernel(
     const uint16_t *m, int64_t ldm, const int32_t *map, const uint16_t *v, int64_t ldv, int rank,
     int64_t cols, const int64_t *seg_start, const int64_t *seg_end, float *out, int64_t se,
     int64_t sc, int64_t sj) {
-  __shared__ __attribute__((aligned(16))) uint8_t sM[64 * 512];
-  __shared__ __attribute__((aligned(16))) uint8_t sV[64 * 64];
+  __shared__ __attribute__((aligned(16))) uint8_t sM0[64 * 512];
+  __shared__ __attribute__((aligned(16))) uint8_t sM1[64 * 512];
+  __shared__ __attribute__((aligned(16))) uint8_t sV0[64 * 64];
+  __shared__ __attribute__((aligned(16))) uint8_t sV1[64 * 64];
   const int e = blockIdx.y;
   const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 256;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -63,27 +69,43 @@ __global__ __launch_bounds__(256) void lora_weight_grad_kernel(
   for (int b = 0; b < 2; ++b)
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[b][j] = 0.0f;
-  for (int64_t r0 = start; r0 < end; r0 += 64) {
+
+  // This thread's share of a chunk: M pieces q = tid + 256*i (row q/32,
+  // 16-byte chunk q%32) and one 16-byte piece of V (row tid/4, chunk tid%4).
+  struct Loads {
+    u32x4 mr[8];
+    u32x4 vr;
+  };
+  const int vrow = tid >> 2, vch = tid & 3;
+  // M source rows of a chunk (-1 past the segment end).
+  auto rows_of = [&](int64_t r0, int32_t *src) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int q = tid + 256 * i;  // 16-byte chunk of the 64 x 256 tile
-      const int row = q >> 5, ch = q & 31;
-      const int64_t grow = r0 + row, col = c0 + ch * 8;
-      u32x4 val = u32x4{0u, 0u, 0u, 0u};
-      if (grow < end && col < cols) {
-        const int64_t src = map ? static_cast<int64_t>(map[grow]) : grow;
-        val = *reinterpret_cast<const u32x4 *>(m + src * ldm + col);
-      }
-      *reinterpret_cast<u32x4 *>(sM + swz_t(row, ch)) = val;
+      const int64_t grow = r0 + ((tid + 256 * i) >> 5);
+      src[i] = grow < end ? (map ? map[grow] : static_cast<int32_t>(grow)) : -1;
     }
-    {
-      const int row = tid >> 2, ch = tid & 3;
-      const int64_t grow = r0 + row;
-      u32x4 val = u32x4{0u, 0u, 0u, 0u};
-      if (grow < end) val = *reinterpret_cast<const u32x4 *>(v + grow * ldv + ch * 8);
-      *reinterpret_cast<u32x4 *>(sV + row * 64 + ch * 16) = val;
+  };
+  auto load = [&](int64_t r0, const int32_t *src, Loads &L) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t col = c0 + ((tid + 256 * i) & 31) * 8;
+      L.mr[i] = (src[i] >= 0 && col < cols)
+                    ? *reinterpret_cast<const u32x4 *>(m + static_cast<int64_t>(src[i]) * ldm + col)
+                    : u32x4{0u, 0u, 0u, 0u};
     }
-    __syncthreads();
+    const int64_t grow = r0 + vrow;
+    L.vr = grow < end ? *reinterpret_cast<const u32x4 *>(v + grow * ldv + vch * 8)
+                      : u32x4{0u, 0u, 0u, 0u};
+  };
+  auto store = [&](uint8_t *sM, uint8_t *sV, const Loads &L) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int q = tid + 256 * i;
+      *reinterpret_cast<u32x4 *>(sM + swz_t(q >> 5, q & 31)) = L.mr[i];
+    }
+    *reinterpret_cast<u32x4 *>(sV + vrow * 64 + vch * 16) = L.vr;
+  };
+  auto compute = [&](const uint8_t *sM, const uint8_t *sV) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const bf16x8 bv = read_v_trans(sV, kk, lane);
@@ -92,7 +114,34 @@ __global__ __launch_bounds__(256) void lora_weight_grad_kernel(
         acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(read_b_trans(sM, wave * 64 + b * 32, kk, lane),
                                                          bv, acc[b], 0, 0, 0);
     }
+  };
+  // Chunk c (rows start + 64c) is loaded in step c-2 (set c % 2), stored to
+  // stage c % 2 after the MFMAs of step c-1, and multiplied in step c.
+  auto step = [&](int64_t r0, const uint8_t *cM, const uint8_t *cV, uint8_t *nM, uint8_t *nV,
+                  Loads &next, Loads &after, int32_t *src) {
+    if (r0 + 128 < end) load(r0 + 128, src, after);
+    if (r0 + 192 < end) rows_of(r0 + 192, src);
+    compute(cM, cV);
+    if (r0 + 64 < end) store(nM, nV, next);
     __syncthreads();
+  };
+  if (start < end) {
+    Loads la, lb;
+    int32_t src[8];
+    rows_of(start, src);
+    load(start, src, la);
+    if (start + 64 < end) {
+      rows_of(start + 64, src);
+      load(start + 64, src, lb);
+    }
+    if (start + 128 < end) rows_of(start + 128, src);
+    store(sM0, sV0, la);
+    __syncthreads();
+    for (int64_t r0 = start; r0 < end; r0 += 128) {
+      step(r0, sM0, sV0, sM1, sV1, lb, la, src);
+      if (r0 + 64 >= end) break;
+      step(r0 + 64, sM1, sV1, sM0, sV0, la, lb, src);
+    }
   }
   // Accumulator value jj of a lane: column c = 8*(jj/4) + 4*(lane/32) + jj%4 of
   // the block, rank j = lane % 32.
