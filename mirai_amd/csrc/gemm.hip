@@ -24,6 +24,7 @@
 #include "grads.h"
 #include "lds_tr.h"
 #include "plan.h"
+#include "rows.h"
 
 namespace mx {
 namespace gemm {
@@ -688,6 +689,12 @@ void grouped_gemm_kernel(Params p) {
           const int64_t rr = row0 + lrow + mb * 32 + 8 * (j >> 2) + (j & 3);
           if (nok && rr < row_end) orow[j][n] = static_cast<uint16_t>(v);
           if (nok && rr + 1 < row_end) orow[j + 1][n] = static_cast<uint16_t>(v >> 16);
+          if constexpr (kSplit) {  // fp32 layer: y leaves as planes [hi | lo] (row stride 2N)
+            const uint32_t lo = pack_bf16x2(v0 - bf16_bits_to_f32(v & 0xffffu),
+                                            v1 - bf16_bits_to_f32(v >> 16));
+            if (nok && rr < row_end) orow[j][n + p.N] = static_cast<uint16_t>(lo);
+            if (nok && rr + 1 < row_end) orow[j + 1][n + p.N] = static_cast<uint16_t>(lo >> 16);
+          }
         }
       }
     }
@@ -820,12 +827,13 @@ void mark_stage(int i, hipStream_t s) {
 
 struct LayerLayout {
   PlanLayout plan;
-  size_t off_lora = 0, off_h = 0, off_y = 0, off_x = 0, bytes = 0;
+  size_t off_lora = 0, off_h = 0, off_y = 0, off_x = 0, off_sum = 0, bytes = 0;
 };
 
 // Scratch of the layer: plan | low-rank activations [R, 96] | h [R, f] |
-// y [R, d]. The fp32 (MX_FMT_F32X3) layer holds h as planes [R, 3f] and adds
-// the split tokens [T, 3d].
+// y [R, d]. The fp32 (MX_FMT_F32X3) layer holds h as planes [R, 3f] and y as
+// planes [R, 2d], and adds the split tokens [T, 3d] and the fp32 combine of
+// both y planes [T, 2d].
 LayerLayout layer_layout(int64_t rows, int num_experts, int64_t hidden, int64_t ffn,
                          bool split = false, int64_t tokens = 0) {
   LayerLayout L;
@@ -836,9 +844,13 @@ LayerLayout layer_layout(int64_t rows, int num_experts, int64_t hidden, int64_t 
   L.off_h = off;
   off = align_up(off + sizeof(uint16_t) * rows * ffn * (split ? 3 : 1), 256);
   L.off_y = off;
-  off = align_up(off + sizeof(uint16_t) * rows * hidden, 256);
+  off = align_up(off + sizeof(uint16_t) * rows * hidden * (split ? 2 : 1), 256);
   L.off_x = off;
-  if (split) off = align_up(off + sizeof(uint16_t) * tokens * hidden * 3, 256);
+  if (split) {
+    off = align_up(off + sizeof(uint16_t) * tokens * hidden * 3, 256);
+    L.off_sum = off;  // fp32 [T, 2d]: the combine of the two y planes
+    off = align_up(off + sizeof(float) * tokens * hidden * 2, 256);
+  }
   L.bytes = off;
   return L;
 }
@@ -1299,8 +1311,8 @@ extern "C" int mx_moe_forward(const void *tokens, const int64_t *top_idx, const 
   const uint16_t *x = static_cast<const uint16_t *>(tokens);
   if (split) {
     uint16_t *xs = reinterpret_cast<uint16_t *>(ws + L.off_x);
-    if ((rc = mx_split_f32(static_cast<const float *>(tokens), num_tokens, hidden, MX_SPLIT_ACT,
-                           xs, stream)))
+    if ((rc = split_f32(static_cast<const float *>(tokens), num_tokens, hidden, MX_SPLIT_ACT, xs,
+                        s)))
       return rc;
     x = xs;
   }
@@ -1314,12 +1326,20 @@ extern "C" int mx_moe_forward(const void *tokens, const int64_t *top_idx, const 
   uint16_t *y = save_y ? static_cast<uint16_t *>(save_y) : reinterpret_cast<uint16_t *>(ws + L.off_y);
   rc = expert_mlp(L.plan, v, num_experts, x, (split ? 3 : 1) * hidden,
                   v.row_token, hidden, ffn, w1, w3, w2, l1, l3, l2, lora_buf, h,
-                  static_cast<uint16_t *>(save_gate), static_cast<uint16_t *>(save_up), y, hidden,
-                  v.row_slot, s);
+                  static_cast<uint16_t *>(save_gate), static_cast<uint16_t *>(save_up), y,
+                  (split ? 2 : 1) * hidden, v.row_slot, s);
   if (rc) return rc;
   mark_stage(5, s);
-  rc = mx_combine(y, top_idx, top_scores, score_dtype, num_tokens, top_k, num_experts, hidden,
-                  out, out_dtype, stream);
+  if (split) {
+    // fp32 layer: combine both y planes in fp32, then add them.
+    float *sum = reinterpret_cast<float *>(ws + L.off_sum);
+    rc = mx_combine(y, top_idx, top_scores, score_dtype, num_tokens, top_k, num_experts,
+                    2 * hidden, sum, MX_DTYPE_F32, stream);
+    if (!rc) rc = sum_halves(sum, num_tokens, hidden, out, out_dtype, s);
+  } else {
+    rc = mx_combine(y, top_idx, top_scores, score_dtype, num_tokens, top_k, num_experts, hidden,
+                    out, out_dtype, stream);
+  }
   mark_stage(6, s);
   return rc;
 }

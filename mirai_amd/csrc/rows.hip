@@ -1,6 +1,7 @@
 // Row movement between token order and expert-sorted order: gather (permute),
 // scatter-add (permute backward), the gate-weighted combine and its backward.
 #include "common.h"
+#include "rows.h"
 
 namespace mx {
 namespace {
@@ -300,7 +301,36 @@ __global__ __launch_bounds__(256) void split_f32_kernel(const float4 *x, int64_t
   o[2 * chunks] = pattern == MX_SPLIT_ACT ? L : H;
 }
 
+template <int OUT_DTYPE>
+__global__ __launch_bounds__(256) void sum_halves_kernel(const float4 *in, int64_t rows,
+                                                         int64_t chunks, void *out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= rows * chunks) return;
+  const int64_t r = i / chunks, c = i - r * chunks;
+  const float4 a = in[r * 2 * chunks + c], b = in[r * 2 * chunks + chunks + c];
+  const float4 v = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+  if (OUT_DTYPE == MX_DTYPE_F32) {
+    static_cast<float4 *>(out)[i] = v;
+  } else {
+    static_cast<uint2 *>(out)[i] = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+  }
+}
+
 }  // namespace
+
+int sum_halves(const float *in, int64_t rows, int64_t cols, void *out, int out_dtype,
+               hipStream_t s) {
+  if (rows <= 0) return MX_OK;
+  const int64_t chunks = cols / 4;
+  const dim3 grid(static_cast<unsigned>(ceil_div(rows * chunks, 256)));
+  if (out_dtype == MX_DTYPE_F32)
+    hipLaunchKernelGGL(sum_halves_kernel<MX_DTYPE_F32>, grid, dim3(256), 0, s,
+                       reinterpret_cast<const float4 *>(in), rows, chunks, out);
+  else
+    hipLaunchKernelGGL(sum_halves_kernel<MX_DTYPE_BF16>, grid, dim3(256), 0, s,
+                       reinterpret_cast<const float4 *>(in), rows, chunks, out);
+  return check_launch("fp32 layer plane sum");
+}
 
 int split_f32(const float *x, int64_t rows, int64_t cols, int pattern, uint16_t *out,
               hipStream_t s) {
