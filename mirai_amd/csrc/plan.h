@@ -36,7 +36,7 @@ struct PlanView {
   int32_t *row_slot;       // [R]: sorted row -> flat route slot t*k+j
 };
 
-int slots_per_plan_block(int num_experts);
+int slots_per_plan_block(int num_experts, int64_t rows);
 PlanLayout plan_layout(int64_t num_rows, int num_experts);
 PlanView plan_view(void *ws, const PlanLayout &L);
 int validate_plan_args(const char *name, int64_t num_tokens, int top_k, int num_experts);

@@ -72,14 +72,30 @@ __device__ int64_t block_exclusive_scan(int64_t v, int64_t *shared, int64_t *tot
   return r;
 }
 
-// One workgroup of 1024 threads; thread e owns expert e (E <= 1024).
+// One workgroup of 1024 threads; thread e owns expert e (E <= 1024). The
+// per-block counts are summed and turned into per-block bases by G groups of
+// E threads, each over a contiguous range of blocks (G = min(16, 1024 / E)).
 __global__ __launch_bounds__(1024) void plan_scan_kernel(
     const int32_t *block_counts, int n_blocks, int E, int64_t n_rows, int tile_m,
     const int64_t *counts_in, int32_t *block_base, int64_t *seg, int2 *tiles,
     int32_t *num_tiles, int2 *tiles2, int32_t *num_tiles2, int32_t *err_counter,
     int64_t *counts_out, int64_t *starts_out, int32_t *offsets_out) {
   __shared__ int64_t scan_tmp[32];
-  const int e = threadIdx.x;
+  __shared__ int32_t part[1024];     // [group][expert] block-range counts
+  __shared__ int64_t start_s[1024];  // expert starts
+  const int t = threadIdx.x;
+  const int G = counts_in ? 1 : max(1, min(16, 1024 / E));
+  const int ge = t / E, ee = t - ge * E;
+  const bool gact = !counts_in && ge < G;
+  const int b_lo = gact ? static_cast<int>(static_cast<int64_t>(n_blocks) * ge / G) : 0;
+  const int b_hi = gact ? static_cast<int>(static_cast<int64_t>(n_blocks) * (ge + 1) / G) : 0;
+  if (gact) {
+    int32_t c = 0;
+    for (int b = b_lo; b < b_hi; ++b) c += block_counts[static_cast<int64_t>(b) * E + ee];
+    part[t] = c;
+  }
+  __syncthreads();
+  const int e = t;
   int64_t count = 0;
   if (e < E) {
     if (counts_in) {
@@ -89,7 +105,7 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(
         count = count < 0 ? 0 : n_rows;
       }
     } else {
-      for (int b = 0; b < n_blocks; ++b) count += block_counts[static_cast<int64_t>(b) * E + e];
+      for (int gg = 0; gg < G; ++gg) count += part[gg * E + e];
     }
   }
   int64_t total = 0;
@@ -101,15 +117,18 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(
     if (seg_hi > n_rows) seg_hi = n_rows;
     if (e == 0 && total != n_rows) atomicAdd(err_counter, 1);
   }
-  if (e < E) {
-    if (!counts_in) {
-      int64_t run = start;
-      for (int b = 0; b < n_blocks; ++b) {
-        const int64_t i = static_cast<int64_t>(b) * E + e;
-        block_base[i] = static_cast<int32_t>(run);
-        run += block_counts[i];
-      }
+  if (e < E) start_s[e] = start;
+  __syncthreads();
+  if (gact) {
+    int64_t run = start_s[ee];
+    for (int gg = 0; gg < ge; ++gg) run += part[gg * E + ee];
+    for (int b = b_lo; b < b_hi; ++b) {
+      const int64_t i = static_cast<int64_t>(b) * E + ee;
+      block_base[i] = static_cast<int32_t>(run);
+      run += block_counts[i];
     }
+  }
+  if (e < E) {
     seg[e] = seg_lo;
     seg[E + e] = seg_hi;
     if (counts_out) counts_out[e] = count;
@@ -182,10 +201,12 @@ __global__ void zero_i32_kernel(int32_t *p, int n) {
 
 }  // namespace
 
-int slots_per_plan_block(int num_experts) {
-  // Masks + prefixes of E * EB bits each must fit in 64 KiB of LDS.
+int slots_per_plan_block(int num_experts, int64_t rows) {
+  // Masks + prefixes of E * EB bits each must fit in 64 KiB of LDS, and large
+  // route counts are cut into at least 256 blocks (one workgroup per CU).
   int eb = 4096;
-  while (eb > 256 && static_cast<int64_t>(num_experts) * eb > 262144) eb >>= 1;
+  while (eb > 256 && (static_cast<int64_t>(num_experts) * eb > 262144 || ceil_div(rows, eb) < 256))
+    eb >>= 1;
   return eb;
 }
 
@@ -193,7 +214,7 @@ PlanLayout plan_layout(int64_t num_rows, int num_experts) {
   PlanLayout L;
   L.rows = num_rows;
   L.experts = num_experts;
-  L.slots_per_block = slots_per_plan_block(num_experts);
+  L.slots_per_block = slots_per_plan_block(num_experts, num_rows);
   L.blocks = static_cast<int>(ceil_div(num_rows, L.slots_per_block));
   L.max_tiles = ceil_div(num_rows, kPlanTileM) + num_experts;
   L.max_tiles2 = ceil_div(num_rows, kPlanTileM2) + num_experts;
