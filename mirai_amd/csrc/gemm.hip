@@ -170,26 +170,28 @@ __device__ __forceinline__ Nf4Table nf4_table(float a) {
   return t;
 }
 
-// Table lookup of four 4-bit codes held one per byte of `sel` (values 0..15).
-__device__ __forceinline__ void nf4_lookup4(const Nf4Table &t, uint32_t sel, uint32_t &lo,
-                                            uint32_t &hi) {
-  const uint32_t s7 = sel & 0x07070707u;
-  const uint32_t u = (sel >> 3) & 0x01010101u;
-  const uint32_t m = (u << 8) - u;  // 0xff in every byte whose code is >= 8
+// Table lookup of four 4-bit codes. `s7` holds the low three bits of each code
+// (one per byte), `pick` the byte selector i + 4 * bit3 of byte i's code: the
+// halves of the table (codes 0..7 and 8..15) are looked up apart and merged
+// byte by byte with one more v_perm_b32 each, so no per-byte mask is formed.
+__device__ __forceinline__ void nf4_lookup4(const Nf4Table &t, uint32_t s7, uint32_t pick,
+                                            uint32_t &lo, uint32_t &hi) {
   const uint32_t lo_a = __builtin_amdgcn_perm(t.lo[1], t.lo[0], s7);
   const uint32_t lo_b = __builtin_amdgcn_perm(t.lo[3], t.lo[2], s7);
   const uint32_t hi_a = __builtin_amdgcn_perm(t.hi[1], t.hi[0], s7);
   const uint32_t hi_b = __builtin_amdgcn_perm(t.hi[3], t.hi[2], s7);
-  lo = (lo_b & m) | (lo_a & ~m);
-  hi = (hi_b & m) | (hi_a & ~m);
+  lo = __builtin_amdgcn_perm(lo_b, lo_a, pick);
+  hi = __builtin_amdgcn_perm(hi_b, hi_a, pick);
 }
 
 // Eight codes (one packed dword, element 2i in the low nibble of byte i) ->
 // four dwords of bf16 pairs in element order.
 __device__ __forceinline__ void nf4_decode8(const Nf4Table &t, uint32_t c, uint32_t *out) {
   uint32_t le, he, lo_, ho;
-  nf4_lookup4(t, c & 0x0f0f0f0fu, le, he);          // elements 0, 2, 4, 6
-  nf4_lookup4(t, (c >> 4) & 0x0f0f0f0fu, lo_, ho);  // elements 1, 3, 5, 7
+  // Low nibbles (elements 0, 2, 4, 6): bit 3 sits at bit 3 of each byte.
+  nf4_lookup4(t, c & 0x07070707u, ((c >> 1) & 0x04040404u) | 0x03020100u, le, he);
+  // High nibbles (elements 1, 3, 5, 7): bit 3 of the code is bit 7 of the byte.
+  nf4_lookup4(t, (c >> 4) & 0x07070707u, ((c >> 5) & 0x04040404u) | 0x03020100u, lo_, ho);
   const uint32_t x01 = __builtin_amdgcn_perm(he, le, 0x05010400u);   // e0, e2
   const uint32_t y01 = __builtin_amdgcn_perm(ho, lo_, 0x05010400u);  // e1, e3
   const uint32_t x23 = __builtin_amdgcn_perm(he, le, 0x07030602u);   // e4, e6
