@@ -14,8 +14,9 @@
  *   logits          [T, E]          fp32
  *   top_idx         [T, k]          int64   expert id per route slot
  *   top_scores      [T, k]          fp32 or bf16 (score_dtype)
- *   NF4 weight      codes [E, out, in/2] uint8 (element 2i in the low nibble,
- *                   2i+1 in the high nibble), absmax [E, out, in/64] bf16
+ *   NF4 weight      codes [E, out, in/2] uint8 (per group of 8 elements along
+ *                   in, byte i holds element i in the low nibble and element
+ *                   i+4 in the high nibble), absmax [E, out, in/64] bf16
  *   INT8 weight     q [E, out, in] int8, scale [E, out] bf16
  *   BF16 weight     w [E, out, in] bf16
  *   F32X3 weight    w [E, out, 3*in] bf16: an fp32 weight split into bf16

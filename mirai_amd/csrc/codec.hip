@@ -18,8 +18,9 @@ __device__ __forceinline__ float load_weight_as_bf16(const void *w, int64_t i, i
 }
 
 // One wavefront per 64-element block: lane = element. Writes 32 code bytes
-// (lanes with even index pack their odd neighbour as the high nibble) and one
-// absmax.
+// and one absmax. Packing: in each group of 8 elements, byte i holds element
+// i in its low nibble and element i + 4 in its high nibble (lanes whose bit 2
+// is clear pack their neighbour 4 lanes up as the high nibble).
 __global__ __launch_bounds__(256) void nf4_quantize_kernel(const void *w, int w_dtype,
                                                            int64_t num_blocks, uint8_t *codes,
                                                            uint16_t *absmax) {
@@ -42,30 +43,39 @@ __global__ __launch_bounds__(256) void nf4_quantize_kernel(const void *w, int w_
       best = j;
     }
   }
-  const int hi = __shfl_down(best, 1, 64);
-  if ((lane & 1) == 0) codes[block * (kNF4Block / 2) + (lane >> 1)] = static_cast<uint8_t>(best | (hi << 4));
+  const int hi = __shfl_down(best, 4, 64);
+  if ((lane & 4) == 0)
+    codes[block * (kNF4Block / 2) + (lane >> 3) * 4 + (lane & 3)] = static_cast<uint8_t>(best | (hi << 4));
   if (lane == 0) absmax[block] = f32_to_bf16_bits(amax);
 }
 
-// Each thread decodes one code byte (two elements).
-__global__ __launch_bounds__(256) void nf4_dequantize_kernel(const uint8_t *codes,
+// Each thread decodes one packed dword: the 8 elements of one group (byte i
+// holds element i in its low nibble and element i + 4 in its high nibble).
+__global__ __launch_bounds__(256) void nf4_dequantize_kernel(const uint32_t *codes,
                                                              const uint16_t *absmax,
-                                                             int64_t num_bytes, void *out,
+                                                             int64_t num_words, void *out,
                                                              int out_dtype) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= num_bytes) return;
-  const uint32_t byte = codes[i];
-  const float a = bf16_bits_to_f32(absmax[i / (kNF4Block / 2)]);
-  const float lo = kNF4Levels[byte & 15] * a;
-  const float hi = kNF4Levels[byte >> 4] * a;
+  if (i >= num_words) return;
+  const uint32_t word = codes[i];
+  const float a = bf16_bits_to_f32(absmax[i / (kNF4Block / 8)]);
+  float v[8];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t byte = (word >> (8 * b)) & 0xffu;
+    v[b] = kNF4Levels[byte & 15] * a;
+    v[b + 4] = kNF4Levels[byte >> 4] * a;
+  }
   if (out_dtype == MX_DTYPE_BF16) {
-    reinterpret_cast<uint32_t *>(out)[i] = pack_bf16x2(lo, hi);
+    reinterpret_cast<u32x4 *>(out)[i] =
+        u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+              pack_bf16x2(v[6], v[7])};
   } else {
     // fp32 output carries the bf16-rounded value (the codec's dequantized
     // weight is defined in bf16).
-    float *o = reinterpret_cast<float *>(out);
-    o[2 * i] = bf16_bits_to_f32(f32_to_bf16_bits(lo));
-    o[2 * i + 1] = bf16_bits_to_f32(f32_to_bf16_bits(hi));
+    float *o = reinterpret_cast<float *>(out) + 8 * i;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = bf16_bits_to_f32(f32_to_bf16_bits(v[j]));
   }
 }
 
@@ -143,11 +153,16 @@ extern "C" int mx_nf4_dequantize(const uint8_t *codes, const void *absmax, int64
     set_error("mx_nf4_dequantize: need non-null buffers and cols a positive multiple of 64");
     return MX_ERR_INVALID;
   }
-  const int64_t bytes = rows * cols / 2;
-  if (bytes == 0) return MX_OK;
-  hipLaunchKernelGGL(nf4_dequantize_kernel, dim3(ceil_div(bytes, 256)), dim3(256), 0,
-                     as_stream(stream), codes, reinterpret_cast<const uint16_t *>(absmax), bytes,
-                     out, out_dtype);
+  if (reinterpret_cast<uintptr_t>(codes) % 4 != 0 ||
+      (out_dtype == MX_DTYPE_BF16 && reinterpret_cast<uintptr_t>(out) % 16 != 0)) {
+    set_error("mx_nf4_dequantize: codes must be 4-byte aligned and a bf16 output 16-byte aligned");
+    return MX_ERR_INVALID;
+  }
+  const int64_t words = rows * cols / 8;
+  if (words == 0) return MX_OK;
+  hipLaunchKernelGGL(nf4_dequantize_kernel, dim3(ceil_div(words, 256)), dim3(256), 0,
+                     as_stream(stream), reinterpret_cast<const uint32_t *>(codes),
+                     reinterpret_cast<const uint16_t *>(absmax), words, out, out_dtype);
   return check_launch("mx_nf4_dequantize");
 }
 

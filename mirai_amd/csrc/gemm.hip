@@ -184,22 +184,20 @@ __device__ __forceinline__ void nf4_lookup4(const Nf4Table &t, uint32_t s7, uint
   hi = __builtin_amdgcn_perm(hi_b, hi_a, pick);
 }
 
-// Eight codes (one packed dword, element 2i in the low nibble of byte i) ->
-// four dwords of bf16 pairs in element order.
+// Eight codes (one packed dword: byte i holds element i in its low nibble and
+// element i + 4 in its high nibble) -> four dwords of bf16 pairs in element
+// order. The low nibbles give elements 0..3 and the high nibbles 4..7, so one
+// v_perm_b32 per output dword interleaves the looked-up low and high bytes.
 __device__ __forceinline__ void nf4_decode8(const Nf4Table &t, uint32_t c, uint32_t *out) {
   uint32_t le, he, lo_, ho;
-  // Low nibbles (elements 0, 2, 4, 6): bit 3 sits at bit 3 of each byte.
+  // Low nibbles: bit 3 of the code sits at bit 3 of each byte.
   nf4_lookup4(t, c & 0x07070707u, ((c >> 1) & 0x04040404u) | 0x03020100u, le, he);
-  // High nibbles (elements 1, 3, 5, 7): bit 3 of the code is bit 7 of the byte.
+  // High nibbles: bit 3 of the code is bit 7 of the byte.
   nf4_lookup4(t, (c >> 4) & 0x07070707u, ((c >> 5) & 0x04040404u) | 0x03020100u, lo_, ho);
-  const uint32_t x01 = __builtin_amdgcn_perm(he, le, 0x05010400u);   // e0, e2
-  const uint32_t y01 = __builtin_amdgcn_perm(ho, lo_, 0x05010400u);  // e1, e3
-  const uint32_t x23 = __builtin_amdgcn_perm(he, le, 0x07030602u);   // e4, e6
-  const uint32_t y23 = __builtin_amdgcn_perm(ho, lo_, 0x07030602u);  // e5, e7
-  out[0] = __builtin_amdgcn_perm(y01, x01, 0x05040100u);
-  out[1] = __builtin_amdgcn_perm(y01, x01, 0x07060302u);
-  out[2] = __builtin_amdgcn_perm(y23, x23, 0x05040100u);
-  out[3] = __builtin_amdgcn_perm(y23, x23, 0x07060302u);
+  out[0] = __builtin_amdgcn_perm(he, le, 0x05010400u);   // e0, e1
+  out[1] = __builtin_amdgcn_perm(he, le, 0x07030602u);   // e2, e3
+  out[2] = __builtin_amdgcn_perm(ho, lo_, 0x05010400u);  // e4, e5
+  out[3] = __builtin_amdgcn_perm(ho, lo_, 0x07030602u);  // e6, e7
 }
 
 template <int FMT, int EPI, bool LORA, class T>

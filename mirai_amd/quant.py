@@ -1,6 +1,7 @@
 """Frozen-weight storage formats, quantised and decoded on the GPU.
 
-* ``nf4``  : codes uint8 [E, out, in/2] (element 2i in the low nibble) and
+* ``nf4``  : codes uint8 [E, out, in/2] (per group of 8 elements, byte i holds
+  element i in the low nibble and element i + 4 in the high nibble) and
              bf16 absmax [E, out, in/64]; blocksize 64, no double quantisation.
 * ``int8`` : int8 [E, out, in] and bf16 per-output-row scale [E, out].
 * ``bf16`` : unquantised bf16 [E, out, in].

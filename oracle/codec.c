@@ -5,7 +5,8 @@
  *
  * Same rules as oracle/codec.py, which restates
  *   mirai/core/models/quantization.py:100-117 (NF4 codebook), :158-175
- *   (nearest level by argmin with first-index ties, low-nibble-first packing),
+ *   (nearest level by argmin with first-index ties; packed per group of 8
+ *   elements, byte i = element i | element i+4 << 4),
  *   mirai/core/models/compressed_weights/quantization/quant.py:189-260 (INT8
  *   per-row symmetric rule, scale floor 1e-30), :413-431 (fp32 product then
  *   cast on dequantisation),
@@ -66,7 +67,11 @@ void oracle_nf4_quantize(const uint16_t *w, int64_t rows, int64_t cols, uint8_t 
         q[j] = (uint8_t)best;
       }
       uint8_t *dst = codes + r * (cols / 2) + b * 32;
-      for (int j = 0; j < 32; ++j) dst[j] = (uint8_t)(q[2 * j] | (q[2 * j + 1] << 4));
+      /* per group of 8 elements: byte i = element i | element (i + 4) << 4 */
+      for (int j = 0; j < 32; ++j) {
+        const int e = 8 * (j / 4) + j % 4;
+        dst[j] = (uint8_t)(q[e] | (q[e + 4] << 4));
+      }
     }
   }
 }
@@ -78,11 +83,12 @@ void oracle_nf4_dequantize(const uint8_t *codes, const uint16_t *absmax, int64_t
   for (int64_t r = 0; r < rows; ++r) {
     for (int64_t i = 0; i < half; ++i) {
       const uint8_t byte = codes[r * half + i];
-      const float a = bf16_to_f32(absmax[r * (cols / 64) + (2 * i) / 64]);
+      const int64_t e = 8 * (i / 4) + i % 4; /* element of the low nibble */
+      const float a = bf16_to_f32(absmax[r * (cols / 64) + e / 64]);
       const float lo = kLevels[byte & 15] * a;
       const float hi = kLevels[byte >> 4] * a;
-      out[r * cols + 2 * i] = f32_to_bf16(lo);
-      out[r * cols + 2 * i + 1] = f32_to_bf16(hi);
+      out[r * cols + e] = f32_to_bf16(lo);
+      out[r * cols + e + 4] = f32_to_bf16(hi);
     }
   }
 }

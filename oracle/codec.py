@@ -4,7 +4,10 @@ Formats (the BASELINE storage formats of this build):
 * NF4: blocks of 64 consecutive ``in`` elements, absmax stored as bf16, no
   double quantisation. Codebook and nearest-level rule from
   mirai/core/models/quantization.py:100-117 and :158-168 (argmin, first index
-  on ties); packing from quantization.py:171-175 (element 2i in the low nibble).
+  on ties). Packing: in each group of 8 consecutive elements, byte i holds
+  element i in its low nibble and element i + 4 in its high nibble (the build's
+  own layout; NF4Linear, quantization.py:171-175, packs element 2i / 2i+1
+  instead, and the bitsandbytes layout is not available here).
   Dequantisation is ``bf16(fp32(level) * fp32(absmax))``, the fp32-product-
   then-cast convention of the bitsandbytes call sites in
   mirai/core/models/compressed_weights/quantization/quant.py:413-431.
@@ -96,18 +99,27 @@ def nf4_quantize(w) -> tuple[np.ndarray, np.ndarray]:
         ).astype(np.float32)
     dist = np.abs(scaled[..., None] - NF4_LEVELS)  # float32
     codes = dist.argmin(axis=-1).astype(np.uint8).reshape(rows, cols)
-    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
-    return packed, f32_to_bf16_bits(absmax.astype(np.float32))
+    return nf4_pack(codes), f32_to_bf16_bits(absmax.astype(np.float32))
+
+
+def nf4_pack(codes: np.ndarray) -> np.ndarray:
+    """Code indices uint8 [rows, cols] -> packed uint8 [rows, cols/2]: per group of
+    8 elements, byte i = element i | element (i + 4) << 4."""
+    codes = np.asarray(codes, dtype=np.uint8)
+    rows, cols = codes.shape
+    g = codes.reshape(rows, cols // 8, 8)
+    return (g[..., :4] | (g[..., 4:] << 4)).astype(np.uint8).reshape(rows, cols // 2)
 
 
 def nf4_unpack(packed: np.ndarray) -> np.ndarray:
-    """uint8 [rows, cols/2] -> code indices uint8 [rows, cols] (low nibble first)."""
+    """uint8 [rows, cols/2] -> code indices uint8 [rows, cols] (inverse of nf4_pack)."""
     packed = np.asarray(packed, dtype=np.uint8)
     rows, half = packed.shape
-    out = np.empty((rows, half * 2), dtype=np.uint8)
-    out[:, 0::2] = packed & 0x0F
-    out[:, 1::2] = packed >> 4
-    return out
+    p = packed.reshape(rows, half // 4, 4)
+    out = np.empty((rows, half // 4, 8), dtype=np.uint8)
+    out[..., :4] = p & 0x0F
+    out[..., 4:] = p >> 4
+    return out.reshape(rows, half * 2)
 
 
 def nf4_dequantize(packed: np.ndarray, absmax_bits: np.ndarray) -> np.ndarray:

@@ -81,19 +81,25 @@ def test_nf4_quantize_matches_brute_force_search():
 
 def test_nf4_pack_order_and_exact_levels():
     # A block holding the 16 levels themselves (times absmax 1): each maps to
-    # its own code; element 2i sits in the low nibble of byte i.
+    # its own code; in each group of 8 elements, byte i holds element i in the
+    # low nibble and element i + 4 in the high nibble.
     order = np.array([0, 15, 3, 12, 7, 8, 1, 14, 5, 10, 2, 13, 4, 11, 6, 9] * 4)
     w = codec.NF4_LEVELS[order].reshape(1, 64)
     packed, absmax = codec.nf4_quantize(w)
     assert codec.bf16_bits_to_f32(absmax)[0, 0] == 1.0
-    assert packed[0, 0] == 0xF0 and packed[0, 1] == 0xC3 and packed[0, 2] == 0x87
+    # group 0 = codes 0 15 3 12 | 7 8 1 14 -> bytes 0x70 0x8F 0x13 0xEC
+    assert list(packed[0, :4]) == [0x70, 0x8F, 0x13, 0xEC]
+    # group 1 = codes 5 10 2 13 | 4 11 6 9 -> bytes 0x45 0xBA 0x62 0x9D
+    assert list(packed[0, 4:8]) == [0x45, 0xBA, 0x62, 0x9D]
     np.testing.assert_array_equal(codec.nf4_unpack(packed)[0], order)
+    np.testing.assert_array_equal(codec.nf4_pack(order.reshape(1, 64).astype(np.uint8)), packed)
 
 
 def test_nf4_dequantize_is_one_rounding_of_the_exact_product():
     rng = np.random.default_rng(2)
     codes = rng.integers(0, 16, (8, 64)).astype(np.uint8)
-    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    g = codes.reshape(8, 8, 8)
+    packed = (g[..., :4] | (g[..., 4:] << 4)).astype(np.uint8).reshape(8, 32)
     amax = np.abs(rng.standard_normal(8)).astype(np.float32) * np.float32(0.05)
     amax_bits = codec.f32_to_bf16_bits(amax).reshape(8, 1)
     got = codec.nf4_dequantize(packed, amax_bits)
@@ -162,7 +168,7 @@ def test_c_oracle_equals_numpy_oracle():
     np.testing.assert_array_equal(fastcodec.int8_dequantize(c_q, c_s), codec.int8_dequantize(n_q, n_s))
 
 
-@pytest.mark.parametrize("mistake", ["bf16_level_first", "high_nibble_first"])
+@pytest.mark.parametrize("mistake", ["bf16_level_first", "high_nibble_first", "pairwise_packing"])
 def test_planted_mistakes_are_caught(mistake):
     """A plausible codec slip must change the output the checks above compare."""
     rng = np.random.default_rng(6)
@@ -174,8 +180,14 @@ def test_planted_mistakes_are_caught(mistake):
         # NF4Linear's in-tree rule rounds the level to bf16 before the product.
         lv = codec.round_bf16(codec.NF4_LEVELS)
         wrong = codec.f32_to_bf16_bits((lv[codes] * a).astype(np.float32))
-    else:
-        swapped = np.empty_like(codes)
-        swapped[:, 0::2], swapped[:, 1::2] = codes[:, 1::2], codes[:, 0::2]
+    elif mistake == "high_nibble_first":
+        g = codes.reshape(4, 8, 8)
+        swapped = np.concatenate([g[..., 4:], g[..., :4]], axis=-1).reshape(4, 64)
         wrong = codec.f32_to_bf16_bits((codec.NF4_LEVELS[swapped] * a).astype(np.float32))
+    else:
+        # Reading the bytes as element pairs (2i, 2i + 1), NF4Linear's packing.
+        packed = codec.nf4_pack(codes)
+        pairwise = np.empty_like(codes)
+        pairwise[:, 0::2], pairwise[:, 1::2] = packed & 0x0F, packed >> 4
+        wrong = codec.f32_to_bf16_bits((codec.NF4_LEVELS[pairwise] * a).astype(np.float32))
     assert not np.array_equal(right, wrong)
