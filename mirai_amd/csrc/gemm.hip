@@ -424,7 +424,9 @@ void grouped_gemm_kernel(Params p) {
     for (int mb = 0; mb < T::MB; ++mb)
 #pragma unroll
       for (int nb = 0; nb < T::NB; ++nb)
-        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[mb], f.b[nb], acc[mb][nb], 0, 0, 0);
+        // Weight fragment first: the accumulator block is the transposed
+        // product (see the epilogue), which lets a lane store 4 columns at once.
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[nb], f.a[mb], acc[mb][nb], 0, 0, 0);
   };
   Frags f0, f1;
 
@@ -539,7 +541,7 @@ void grouped_gemm_kernel(Params p) {
   // K step, in the stage it left free.
   const uint8_t *sP = (KT & 1) ? sA1 : sA0;
   const uint8_t *sL = sLt;
-  auto lora_block = [&](int mb, int nb) -> f32x16 __attribute__((always_inline)) {
+  auto lora_block = [&](int mb, int nb) -> f32x16 {
     f32x16 t;
 #pragma unroll
     for (int j = 0; j < 16; ++j) t[j] = 0.0f;
@@ -554,24 +556,32 @@ void grouped_gemm_kernel(Params p) {
             sP + ad * T::BM * 64 + swz64(wm * T::WM + mb * 32 + (lane & 31), ch));
         const bf16x8 b = *reinterpret_cast<const bf16x8 *>(
             sL + a2 * T::BN * 64 + swz64(wn * T::WN + nb * 32 + (lane & 31), ch));
-        t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, t, 0, 0, 0);
+        t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, t, 0, 0, 0);
       }
     }
     return t;
   };
 
   // ------------------------------------------------------------ epilogue
-  // v_mfma_f32_32x32x16 accumulator layout: value j of a lane sits at row
-  // 8*(j/4) + 4*(lane/32) + j%4 and column lane%32 of the 32 x 32 block.
-  // Outputs whose rows are this tile's own sorted rows go through buffer
-  // stores over exactly the tile's valid rows: stores to rows past the
-  // segment end fall outside the buffer and are dropped by the hardware, and
-  // columns past N are sent out of range on purpose, so no store needs a
-  // branch. Offsets are 32-bit byte offsets inside one tile.
-  const int lcol = lane & 31;
-  const int lrow = wm * T::WM + 4 * (lane >> 5);  // tile row of value j = 0 in block mb = 0
+  // The MFMAs take the weight fragment first, so each 32 x 32 accumulator
+  // block holds the transposed product: value j of a lane is output row
+  // lane % 32 of the block, column 8 * (j / 4) + 4 * (lane / 32) + j % 4. A lane
+  // thus owns runs of 4 consecutive columns of one row (values 4g .. 4g + 3)
+  // and writes each run with one 8-byte store. Outputs whose rows are this
+  // tile's own sorted rows go through buffer stores over exactly the tile's
+  // valid rows: rows past the segment end fall outside the buffer and are
+  // dropped by the hardware, and columns past N are sent out of range on
+  // purpose, so no store needs a branch. Offsets are 32-bit byte offsets
+  // inside one tile.
+  const int lrow = lane & 31;       // row of the lane inside a block
+  const int lcol = 4 * (lane >> 5); // first column of the lane's run in group 0
   const int64_t tile_rows = min(row_end - row0, static_cast<int64_t>(T::BM));
-  constexpr uint32_t kDrop = 0x80000000u;         // beyond any tile buffer
+  constexpr uint32_t kDrop = 0x80000000u;  // beyond any tile buffer
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  auto st8 = [&](const __amdgpu_buffer_rsrc_t &rs, uint32_t off, uint32_t w0, uint32_t w1)
+      __attribute__((always_inline)) {
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{w0, w1}, rs, off, 0, 0);
+  };
   if (EPI == EPI_SWIGLU) {
     const uint32_t ld2 = static_cast<uint32_t>(p.ldo) * 2u, n2 = static_cast<uint32_t>(p.N) * 2u;
     const auto rs_h = tile_rsrc(p.out + row0 * p.ldo, tile_rows * p.ldo * 2);
@@ -580,6 +590,7 @@ void grouped_gemm_kernel(Params p) {
     const auto rs_u = tile_rsrc(saves ? p.save_up + row0 * p.N : p.out, saves ? tile_rows * p.N * 2 : 0);
 #pragma unroll
     for (int mb = 0; mb < T::MB; ++mb) {
+      const uint32_t r = static_cast<uint32_t>(wm * T::WM + mb * 32 + lrow);
 #pragma unroll
       for (int nbp = 0; nbp < T::NB / 2; ++nbp) {
         f32x16 lg, lu;
@@ -587,167 +598,176 @@ void grouped_gemm_kernel(Params p) {
           lg = lora_block(mb, nbp);
           lu = lora_block(mb, nbp + T::NB / 2);
         }
-        const int64_t f = static_cast<int64_t>(nt) * (T::BN / 2) + wn * (T::WN / 2) + nbp * 32 + lcol;
-        const uint32_t r0 = static_cast<uint32_t>(lrow + mb * 32);
-        const uint32_t off_h = f < p.N ? r0 * ld2 + static_cast<uint32_t>(f) * 2u : kDrop;
-        const uint32_t off_s = f < p.N ? r0 * n2 + static_cast<uint32_t>(f) * 2u : kDrop;
+        const int64_t f0 = static_cast<int64_t>(nt) * (T::BN / 2) + wn * (T::WN / 2) + nbp * 32 + lcol;
 #pragma unroll
-        for (int j = 0; j < 16; j += 2) {
-          float g0 = acc[mb][nbp][j], g1 = acc[mb][nbp][j + 1];
-          float u0 = acc[mb][nbp + T::NB / 2][j], u1 = acc[mb][nbp + T::NB / 2][j + 1];
-          const uint32_t dr0 = static_cast<uint32_t>(8 * (j >> 2) + (j & 3));
+        for (int g = 0; g < 4; ++g) {
+          // N is a multiple of 8: a run of 4 columns is wholly valid or not.
+          const bool fok = f0 + 8 * g < p.N;
+          const uint32_t fc = static_cast<uint32_t>(f0 + 8 * g) * 2u;
+          const uint32_t off_h = fok ? r * ld2 + fc : kDrop;
+          const uint32_t off_s = fok ? r * n2 + fc : kDrop;
+          float gv[4], uv[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            gv[q] = acc[mb][nbp][4 * g + q];
+            uv[q] = acc[mb][nbp + T::NB / 2][4 * g + q];
+          }
           if constexpr (kSplit) {
             // fp32 layer: no intermediate rounding; h goes out as bf16 planes
             // [hi | hi | lo] (row stride 3N), the down projection's split A.
-            if (LORA) {
-              g0 += lg[j];
-              g1 += lg[j + 1];
-              u0 += lu[j];
-              u1 += lu[j + 1];
-            }
-            const float h0 = g0 * __builtin_amdgcn_rcpf(1.0f + __expf(-g0)) * u0;
-            const float h1 = g1 * __builtin_amdgcn_rcpf(1.0f + __expf(-g1)) * u1;
-            const uint32_t hi = pack_bf16x2(h0, h1);
-            const uint32_t lo = pack_bf16x2(h0 - bf16_bits_to_f32(hi & 0xffffu),
-                                            h1 - bf16_bits_to_f32(hi >> 16));
-            const uint32_t planes[3] = {hi, hi, lo};
+            float h[4];
 #pragma unroll
-            for (int q = 0; q < 3; ++q) {
-              const uint32_t o = off_h + static_cast<uint32_t>(q) * n2;
-              __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(planes[q]), rs_h, o + dr0 * ld2, 0, 0);
-              __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(planes[q] >> 16), rs_h, o + (dr0 + 1) * ld2, 0, 0);
+            for (int q = 0; q < 4; ++q) {
+              if (LORA) {
+                gv[q] += lg[4 * g + q];
+                uv[q] += lu[4 * g + q];
+              }
+              h[q] = gv[q] * __builtin_amdgcn_rcpf(1.0f + __expf(-gv[q])) * uv[q];
             }
+            const uint32_t hi0 = pack_bf16x2(h[0], h[1]), hi1 = pack_bf16x2(h[2], h[3]);
+            const uint32_t lo0 = pack_bf16x2(h[0] - bf16_bits_to_f32(hi0 & 0xffffu), h[1] - bf16_bits_to_f32(hi0 >> 16));
+            const uint32_t lo1 = pack_bf16x2(h[2] - bf16_bits_to_f32(hi1 & 0xffffu), h[3] - bf16_bits_to_f32(hi1 >> 16));
+            st8(rs_h, off_h, hi0, hi1);
+            st8(rs_h, off_h + n2, hi0, hi1);
+            st8(rs_h, off_h + 2 * n2, lo0, lo1);
             continue;
           }
-          // Two adjacent rows at a time: one packed conversion rounds both.
-          round2(g0, g1);
-          round2(u0, u1);
+          round2(gv[0], gv[1]);
+          round2(gv[2], gv[3]);
+          round2(uv[0], uv[1]);
+          round2(uv[2], uv[3]);
           if (LORA) {
-            float a0 = lg[j], a1 = lg[j + 1], b0 = lu[j], b1 = lu[j + 1];
-            round2(a0, a1);
-            round2(b0, b1);
-            g0 += a0;
-            g1 += a1;
-            u0 += b0;
-            u1 += b1;
-            round2(g0, g1);
-            round2(u0, u1);
+            float a[4], b[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              a[q] = lg[4 * g + q];
+              b[q] = lu[4 * g + q];
+            }
+            round2(a[0], a[1]);
+            round2(a[2], a[3]);
+            round2(b[0], b[1]);
+            round2(b[2], b[3]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              gv[q] += a[q];
+              uv[q] += b[q];
+            }
+            round2(gv[0], gv[1]);
+            round2(gv[2], gv[3]);
+            round2(uv[0], uv[1]);
+            round2(uv[2], uv[3]);
           }
           // silu(g) rounded to bf16, then the bf16 product (experts.py:289-317).
-          float s0 = g0 * __builtin_amdgcn_rcpf(1.0f + __expf(-g0));
-          float s1 = g1 * __builtin_amdgcn_rcpf(1.0f + __expf(-g1));
-          round2(s0, s1);
-          const uint32_t h = pack_bf16x2(s0 * u0, s1 * u1);
-          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(h), rs_h, off_h + dr0 * ld2, 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(h >> 16), rs_h, off_h + (dr0 + 1) * ld2, 0, 0);
+          float sv[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) sv[q] = gv[q] * __builtin_amdgcn_rcpf(1.0f + __expf(-gv[q]));
+          round2(sv[0], sv[1]);
+          round2(sv[2], sv[3]);
+          st8(rs_h, off_h, pack_bf16x2(sv[0] * uv[0], sv[1] * uv[1]), pack_bf16x2(sv[2] * uv[2], sv[3] * uv[3]));
           if (saves) {
-            const uint32_t gb = pack_bf16x2(g0, g1), ub = pack_bf16x2(u0, u1);
-            __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(gb), rs_g, off_s + dr0 * n2, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(gb >> 16), rs_g, off_s + (dr0 + 1) * n2, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(ub), rs_u, off_s + dr0 * n2, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(ub >> 16), rs_u, off_s + (dr0 + 1) * n2, 0, 0);
+            st8(rs_g, off_s, pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3]));
+            st8(rs_u, off_s, pack_bf16x2(uv[0], uv[1]), pack_bf16x2(uv[2], uv[3]));
           }
         }
       }
     }
   } else if (EPI == EPI_STORE || EPI == EPI_STORE2) {
-    // Rows go to out_row[r] (slot order): 64-bit row pointers, loaded once
-    // per row and shared by the column blocks.
+    // Rows go to out_row[r] (slot order): one row pointer per lane and row
+    // block, shared by the column blocks.
 #pragma unroll
     for (int mb = 0; mb < T::MB; ++mb) {
-      uint16_t *orow[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int64_t r = min(row0 + lrow + mb * 32 + 8 * (j >> 2) + (j & 3), row_end - 1);
-        const int64_t o = p.out_row ? static_cast<int64_t>(p.out_row[r]) : r;
-        orow[j] = p.out + o * p.ldo;
-      }
+      const int64_t rr = row0 + wm * T::WM + mb * 32 + lrow;
+      const bool rok = rr < row_end;
+      const int64_t r = min(rr, row_end - 1);
+      const int64_t o = p.out_row ? static_cast<int64_t>(p.out_row[r]) : r;
+      uint16_t *orow = p.out + o * p.ldo;
 #pragma unroll
       for (int nb = 0; nb < T::NB; ++nb) {
         f32x16 l2;
         if (LORA) l2 = lora_block(mb, nb);
-        const int64_t n = static_cast<int64_t>(nt) * T::BN + wn * T::WN + nb * 32 + lcol;
-        const bool nok = n < p.N;
+        const int64_t n0 = static_cast<int64_t>(nt) * T::BN + wn * T::WN + nb * 32 + lcol;
 #pragma unroll
-        for (int j = 0; j < 16; j += 2) {
-          float v0 = acc[mb][nb][j], v1 = acc[mb][nb][j + 1];
+        for (int g = 0; g < 4; ++g) {
+          // N is a multiple of 8: a run of 4 columns is wholly valid or not.
+          const bool ok = rok && n0 + 8 * g < p.N;
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = acc[mb][nb][4 * g + q];
           if constexpr (kSplit) {
             if (LORA) {  // fp32 layer: one rounding of the sum
-              v0 += l2[j];
-              v1 += l2[j + 1];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) v[q] += l2[4 * g + q];
             }
           } else {
-            round2(v0, v1);
+            round2(v[0], v[1]);
+            round2(v[2], v[3]);
             if (LORA) {
-              float a0 = l2[j], a1 = l2[j + 1];
-              round2(a0, a1);
-              v0 += a0;
-              v1 += a1;
+              float a[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) a[q] = l2[4 * g + q];
+              round2(a[0], a[1]);
+              round2(a[2], a[3]);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) v[q] += a[q];
             }
           }
-          const uint32_t v = pack_bf16x2(v0, v1);
-          const int64_t rr = row0 + lrow + mb * 32 + 8 * (j >> 2) + (j & 3);
-          if (nok && rr < row_end) orow[j][n] = static_cast<uint16_t>(v);
-          if (nok && rr + 1 < row_end) orow[j + 1][n] = static_cast<uint16_t>(v >> 16);
+          const uint32_t w0 = pack_bf16x2(v[0], v[1]), w1 = pack_bf16x2(v[2], v[3]);
+          uint16_t *dst = orow + n0 + 8 * g;
+          if (ok) *reinterpret_cast<u32x2 *>(dst) = u32x2{w0, w1};
           if constexpr (kSplit) {  // fp32 layer: y leaves as planes [hi | lo] (row stride 2N)
-            const uint32_t lo = pack_bf16x2(v0 - bf16_bits_to_f32(v & 0xffffu),
-                                            v1 - bf16_bits_to_f32(v >> 16));
-            if (nok && rr < row_end) orow[j][n + p.N] = static_cast<uint16_t>(lo);
-            if (nok && rr + 1 < row_end) orow[j + 1][n + p.N] = static_cast<uint16_t>(lo >> 16);
+            const uint32_t l0 = pack_bf16x2(v[0] - bf16_bits_to_f32(w0 & 0xffffu), v[1] - bf16_bits_to_f32(w0 >> 16));
+            const uint32_t l1 = pack_bf16x2(v[2] - bf16_bits_to_f32(w1 & 0xffffu), v[3] - bf16_bits_to_f32(w1 >> 16));
+            if (ok) *reinterpret_cast<u32x2 *>(dst + p.N) = u32x2{l0, l1};
           }
         }
       }
     }
   } else {
-    // EPI_LORA_A: p = bf16(s * bf16(x a^T)), as low_rank.to(bf16) * scale.
+    // EPI_LORA_A: p = bf16(s * bf16(x a^T)), as low_rank.to(bf16) * scale. A
+    // 32-column block is one adapter.
     const uint32_t ld2 = static_cast<uint32_t>(p.ldo) * 2u;
     const auto rs_o = tile_rsrc(p.out + row0 * p.ldo, tile_rows * p.ldo * 2);
 #pragma unroll
     for (int mb = 0; mb < T::MB; ++mb) {
+      const uint32_t r = static_cast<uint32_t>(wm * T::WM + mb * 32 + lrow);
 #pragma unroll
       for (int nb = 0; nb < T::NB; ++nb) {
-        const int ncol = wn * T::WN + nb * 32 + lcol;
-        const float sc = pick(p.scale, ncol >> 5);
-        const uint32_t r0 = static_cast<uint32_t>(lrow + mb * 32);
-        const uint32_t off = ncol < p.N ? r0 * ld2 + static_cast<uint32_t>(ncol) * 2u : kDrop;
-        if constexpr (kSplit) {
-          // fp32 layer: column j < r of an adapter block leaves as planes
-          // [hi | hi | lo] at columns j, r + j, 2r + j (3r <= 32); columns
-          // from 3r on are zero. The rank-side LoRA factor is split [hi | lo |
-          // hi] likewise, so the epilogue's K = 32 product is fp32-accurate.
-          const int jc = ncol & 31, r = pick(p.split_r, ncol >> 5);
-          const uint32_t base = ncol < p.N ? r0 * ld2 + static_cast<uint32_t>(ncol - jc) * 2u : kDrop;
-          const bool own = jc < r, zero = jc >= 3 * r;
-          const uint32_t o_hi = own ? base + static_cast<uint32_t>(jc) * 2u : kDrop;
-          const uint32_t o_hi2 = own ? base + static_cast<uint32_t>(r + jc) * 2u : kDrop;
-          const uint32_t o_lo = own ? base + static_cast<uint32_t>(2 * r + jc) * 2u
-                                    : (zero ? off : kDrop);
+        const int nblk = wn * T::WN + nb * 32;
+        const float sc = pick(p.scale, nblk >> 5);
+        const uint32_t base = nblk < p.N ? r * ld2 + static_cast<uint32_t>(nblk) * 2u : kDrop;
 #pragma unroll
-          for (int j = 0; j < 16; j += 2) {
-            const float v0 = acc[mb][nb][j] * sc, v1 = acc[mb][nb][j + 1] * sc;
-            const uint32_t hi = pack_bf16x2(v0, v1);
-            const uint32_t lo = own ? pack_bf16x2(v0 - bf16_bits_to_f32(hi & 0xffffu),
-                                                  v1 - bf16_bits_to_f32(hi >> 16))
-                                    : 0u;
-            const uint32_t dr0 = static_cast<uint32_t>(8 * (j >> 2) + (j & 3));
-            const uint32_t st[3] = {hi, hi, lo};
-            const uint32_t at[3] = {o_hi, o_hi2, o_lo};
+        for (int g = 0; g < 4; ++g) {
+          const int jc = 8 * g + lcol;  // column of the run inside the adapter's block
+          float v[4];
 #pragma unroll
-            for (int q = 0; q < 3; ++q) {
-              __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(st[q]), rs_o, at[q] + dr0 * ld2, 0, 0);
-              __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(st[q] >> 16), rs_o, at[q] + (dr0 + 1) * ld2, 0, 0);
-            }
+          for (int q = 0; q < 4; ++q) v[q] = acc[mb][nb][4 * g + q];
+          if constexpr (kSplit) {
+            // fp32 layer: column j < r of an adapter block leaves as planes
+            // [hi | hi | lo] at columns j, r + j, 2r + j (3r <= 32); columns
+            // from 3r on are zero. The rank-side LoRA factor is split [hi | lo |
+            // hi] likewise, so the epilogue's K = 32 product is fp32-accurate.
+            // r is a multiple of 8, so a run of 4 columns is wholly inside one
+            // of these ranges.
+            const int rk = pick(p.split_r, nblk >> 5);
+            const bool own = jc < rk, zero = jc >= 3 * rk;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] *= sc;
+            const uint32_t hi0 = pack_bf16x2(v[0], v[1]), hi1 = pack_bf16x2(v[2], v[3]);
+            const uint32_t lo0 = own ? pack_bf16x2(v[0] - bf16_bits_to_f32(hi0 & 0xffffu), v[1] - bf16_bits_to_f32(hi0 >> 16)) : 0u;
+            const uint32_t lo1 = own ? pack_bf16x2(v[2] - bf16_bits_to_f32(hi1 & 0xffffu), v[3] - bf16_bits_to_f32(hi1 >> 16)) : 0u;
+            const uint32_t o_hi = own ? base + static_cast<uint32_t>(jc) * 2u : kDrop;
+            const uint32_t o_hi2 = own ? base + static_cast<uint32_t>(rk + jc) * 2u : kDrop;
+            const uint32_t o_lo = own ? base + static_cast<uint32_t>(2 * rk + jc) * 2u
+                                      : (zero ? base + static_cast<uint32_t>(jc) * 2u : kDrop);
+            st8(rs_o, o_hi, hi0, hi1);
+            st8(rs_o, o_hi2, hi0, hi1);
+            st8(rs_o, o_lo, lo0, lo1);
+            continue;
           }
-          continue;
-        }
-#pragma unroll
-        for (int j = 0; j < 16; j += 2) {
-          float v0 = acc[mb][nb][j], v1 = acc[mb][nb][j + 1];
-          round2(v0, v1);
-          const uint32_t v = pack_bf16x2(v0 * sc, v1 * sc);
-          const uint32_t dr0 = static_cast<uint32_t>(8 * (j >> 2) + (j & 3));
-          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(v), rs_o, off + dr0 * ld2, 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(v >> 16), rs_o, off + (dr0 + 1) * ld2, 0, 0);
+          round2(v[0], v[1]);
+          round2(v[2], v[3]);
+          st8(rs_o, base + static_cast<uint32_t>(jc) * 2u, pack_bf16x2(v[0] * sc, v[1] * sc),
+              pack_bf16x2(v[2] * sc, v[3] * sc));
         }
       }
     }
