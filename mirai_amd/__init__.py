@@ -8,6 +8,7 @@ Drop-in for the routed expert op of seruva19/mirai
 from .dispatch import DispatchPlan, build_dispatch_plan, combine_routed_tokens, permute_routed_tokens
 from .experts import CompressedGroupedExperts
 from .lora import ActiveExpertLoRA, lora_scale
+from .magi2 import Magi2FusedMoEBackend, Magi2GroupedExperts, route_topk_heads
 from .routing import route_topk
 from .specs import (
     CANONICAL_PACKED_EXPERT_MLP_SPEC,
@@ -25,6 +26,8 @@ __all__ = [
     "DispatchPlan",
     "ExpertMLPExecutionSpec",
     "ExpertProjectionRole",
+    "Magi2FusedMoEBackend",
+    "Magi2GroupedExperts",
     "MoEOptimizationPolicy",
     "active_moe_optimization_policy",
     "build_dispatch_plan",
@@ -33,4 +36,5 @@ __all__ = [
     "lora_scale",
     "permute_routed_tokens",
     "route_topk",
+    "route_topk_heads",
 ]

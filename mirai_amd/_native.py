@@ -35,6 +35,16 @@ RENORM_NONE = 0
 RENORM_CLAMP = 1
 RENORM_EPS = 2
 
+ACT_SILU = 0       # expert activations
+ACT_SWIGLU7 = 1
+
+SCORE_SOFTMAX = 0  # mx_route_topk_heads score functions and output layouts
+SCORE_SIGMOID = 1
+ROUTE_LAYOUT_HEADS = 0
+ROUTE_LAYOUT_ROWS = 1
+
+PLAN_MAX_EXPERTS = 8192
+
 
 class NativeLibraryError(RuntimeError):
     """The HIP library is not built, not loadable, or no GPU is present."""
@@ -65,6 +75,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "mx_route_topk": (c_int, [_P, c_int64, c_int, c_int, c_int, c_float, _P, _P, c_int, _P]),
     "mx_route_topk_backward": (
         c_int, [_P, c_int64, c_int, c_int, c_int, c_float, _P, _P, _P, _P]),
+    "mx_route_topk_heads": (
+        c_int,
+        [_P, c_int, c_int64, c_int, c_int, c_int, _P, c_int, c_float, c_float, c_int, _P, _P,
+         c_int, _P]),
     "mx_plan_workspace_size": (c_size_t, [c_int64, c_int, c_int]),
     "mx_build_plan": (
         c_int, [_P, _P, c_int, c_int64, c_int, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
@@ -87,6 +101,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         c_int,
         [_P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, c_int64, _W, _W, _W, _L, _L, _L,
          _P, c_int, _P, _P, _P, _P, _P, _P, _P]),
+    "mx_moe_forward_act": (
+        c_int,
+        [_P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, c_int64, c_int, _W, _W, _W, _L, _L,
+         _L, _P, c_int, _P, _P, _P, _P, _P, _P, _P]),
     "mx_moe_for_loop": (
         c_int, [_P, _P, c_int64, c_int, c_int64, c_int64, _W, _W, _W, _L, _L, _L, _P, _P, _P]),
     "mx_grouped_linear": (c_int, [_P, _P, c_int64, c_int, _W, _L, _P, _P, _P]),
@@ -95,6 +113,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         c_int,
         [_P, c_int, _P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, c_int64, _W, _W, _W,
          _L, _L, _L, _P, _P, _P, _P, _P, _P, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "mx_moe_backward_act": (
+        c_int,
+        [_P, c_int, _P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, c_int64, c_int, _W, _W,
+         _W, _L, _L, _L, _P, _P, _P, _P, _P, _P, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
 }
 
 _lib: ctypes.CDLL | None = None

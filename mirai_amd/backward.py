@@ -1,6 +1,6 @@
 """Backward of the fused routed expert layer (adapter training, frozen base).
 
-One ``mx_moe_backward`` call turns grad_out into grad_tokens, grad_scores and
+One ``mx_moe_backward_act`` call turns grad_out into grad_tokens, grad_scores and
 the fp32 LoRA factor gradients. The frozen weights are decoded again inside
 the backward GEMMs (never saved on ctx, never materialised), as the reference's
 _FrozenDequantBatchedLinear(Pair).backward re-dequantises
@@ -15,7 +15,7 @@ from . import _native as nat
 
 
 def routed_experts_backward(ctx, grad_out):
-    from .fused import _lora_descriptors, _weight_descriptors
+    from .fused import _lora_descriptors, _weight_descriptors, kernel_activation
 
     x, scores, idx, gate, up, h, y, lora_rows = ctx.saved_tensors
     module = ctx.module
@@ -46,10 +46,11 @@ def routed_experts_backward(ctx, grad_out):
         raw += [ga, gb]
     lib = nat.load_library()
     ws = nat.workspace(lib.mx_moe_backward_workspace_size(T, k, E, d, f), device)
-    nat.call("mx_moe_backward", g.data_ptr(), nat.dtype_code(g.dtype), x.data_ptr(),
+    nat.call("mx_moe_backward_act", g.data_ptr(), nat.dtype_code(g.dtype), x.data_ptr(),
              idx.data_ptr(), scores.data_ptr(), nat.dtype_code(scores.dtype), T, k, E, d, f,
-             w1, w3, w2, lora[0], lora[1], lora[2], gate.data_ptr(), up.data_ptr(), h.data_ptr(),
-             y.data_ptr(), lora_rows.data_ptr(), grad_tokens.data_ptr(),
+             kernel_activation(module), w1, w3, w2, lora[0], lora[1], lora[2], gate.data_ptr(),
+             up.data_ptr(), h.data_ptr(), y.data_ptr(), lora_rows.data_ptr(),
+             grad_tokens.data_ptr(),
              nat.dtype_code(grad_tokens.dtype), grad_scores.data_ptr(),
              *[nat.ptr(t) for t in raw], ws.data_ptr(), nat.stream(device))
     del keep

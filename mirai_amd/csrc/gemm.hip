@@ -88,6 +88,7 @@ struct Params {
   uint16_t *save_up;
   float scale[4];
   int split_r[4];            // MX_FMT_F32X3 LoRA down-projection: rank of each adapter
+  int act;                   // EPI_SWIGLU: MX_ACT_SILU or MX_ACT_SWIGLU7
 };
 
 // Per-thread choice among the small kernel-argument arrays by explicit
@@ -131,6 +132,16 @@ __device__ __forceinline__ int swz(int row, int chunk) {
 }
 __device__ __forceinline__ int swz64(int row, int chunk) {  // 64-byte rows (LoRA tiles)
   return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
+}
+
+// MAGI-2 swiglu7 of one fp32 gate / up pair (grouped_moe.py:287-306,
+// magi2_preview.py:2785-2787): min(g, 7) * sigmoid(1.702 min(g, 7)) *
+// (clamp(u, -7, 7) + 1), evaluated in fp32 in the reference's order.
+__device__ __forceinline__ float swiglu7(float g, float u) {
+  const float gc = fminf(g, 7.0f);
+  const float uc = fminf(fmaxf(u, -7.0f), 7.0f);
+  const float sig = 1.0f / (1.0f + expf(-(1.702f * gc)));
+  return (gc * sig) * (uc + 1.0f);
 }
 
 // Rounds two fp32 values to bf16 precision with one packed conversion.
@@ -622,7 +633,8 @@ void grouped_gemm_kernel(Params p) {
                 gv[q] += lg[4 * g + q];
                 uv[q] += lu[4 * g + q];
               }
-              h[q] = gv[q] * __builtin_amdgcn_rcpf(1.0f + __expf(-gv[q])) * uv[q];
+              h[q] = p.act == MX_ACT_SWIGLU7 ? swiglu7(gv[q], uv[q])
+                                             : gv[q] * __builtin_amdgcn_rcpf(1.0f + __expf(-gv[q])) * uv[q];
             }
             const uint32_t hi0 = pack_bf16x2(h[0], h[1]), hi1 = pack_bf16x2(h[2], h[3]);
             const uint32_t lo0 = pack_bf16x2(h[0] - bf16_bits_to_f32(hi0 & 0xffffu), h[1] - bf16_bits_to_f32(hi0 >> 16));
@@ -657,13 +669,21 @@ void grouped_gemm_kernel(Params p) {
             round2(uv[0], uv[1]);
             round2(uv[2], uv[3]);
           }
-          // silu(g) rounded to bf16, then the bf16 product (experts.py:289-317).
-          float sv[4];
+          if (p.act == MX_ACT_SWIGLU7) {
+            // bf16 gate / up in, fp32 swiglu7, one rounding (grouped_moe.py:287-306).
+            float hq[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) sv[q] = gv[q] * __builtin_amdgcn_rcpf(1.0f + __expf(-gv[q]));
-          round2(sv[0], sv[1]);
-          round2(sv[2], sv[3]);
-          st8(rs_h, off_h, pack_bf16x2(sv[0] * uv[0], sv[1] * uv[1]), pack_bf16x2(sv[2] * uv[2], sv[3] * uv[3]));
+            for (int q = 0; q < 4; ++q) hq[q] = swiglu7(gv[q], uv[q]);
+            st8(rs_h, off_h, pack_bf16x2(hq[0], hq[1]), pack_bf16x2(hq[2], hq[3]));
+          } else {
+            // silu(g) rounded to bf16, then the bf16 product (experts.py:289-317).
+            float sv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sv[q] = gv[q] * __builtin_amdgcn_rcpf(1.0f + __expf(-gv[q]));
+            round2(sv[0], sv[1]);
+            round2(sv[2], sv[3]);
+            st8(rs_h, off_h, pack_bf16x2(sv[0] * uv[0], sv[1] * uv[1]), pack_bf16x2(sv[2] * uv[2], sv[3] * uv[3]));
+          }
           if (saves) {
             st8(rs_g, off_s, pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3]));
             st8(rs_u, off_s, pack_bf16x2(uv[0], uv[1]), pack_bf16x2(uv[2], uv[3]));
@@ -952,7 +972,7 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
 
 // gate/up grouped GEMM with SwiGLU epilogue, then the down grouped GEMM.
 int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint16_t *x,
-               int64_t ldx, const int32_t *row_token, int64_t hidden, int64_t ffn,
+               int64_t ldx, const int32_t *row_token, int64_t hidden, int64_t ffn, int act,
                const mx_weight *w1, const mx_weight *w3, const mx_weight *w2,
                const mx_lora *l1, const mx_lora *l3, const mx_lora *l2, uint16_t *lora_buf,
                uint16_t *h, uint16_t *save_gate, uint16_t *save_up, uint16_t *y, int64_t ldy,
@@ -995,6 +1015,7 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
     p.ldo = kx * ffn;
     p.save_gate = save_gate;
     p.save_up = save_up;
+    p.act = act;
     rc = launch_any<EPI_SWIGLU>(w1->format, lora13, p, PL, v, s);
     if (rc) return rc;
   }
@@ -1119,10 +1140,10 @@ extern "C" size_t mx_moe_backward_workspace_size(int64_t num_tokens, int top_k, 
   return back_layout(num_tokens * top_k, num_experts, hidden, ffn).bytes;
 }
 
-extern "C" int mx_moe_backward(const void *grad_out, int grad_dtype, const void *tokens,
+extern "C" int mx_moe_backward_act(const void *grad_out, int grad_dtype, const void *tokens,
                                const int64_t *top_idx, const void *top_scores, int score_dtype,
                                int64_t num_tokens, int top_k, int num_experts, int64_t hidden,
-                               int64_t ffn, const mx_weight *w1, const mx_weight *w3,
+                               int64_t ffn, int act, const mx_weight *w1, const mx_weight *w3,
                                const mx_weight *w2, const mx_lora *l1, const mx_lora *l3,
                                const mx_lora *l2, const void *save_gate, const void *save_up,
                                const void *save_h, const void *save_y, const void *save_lora,
@@ -1133,6 +1154,10 @@ extern "C" int mx_moe_backward(const void *grad_out, int grad_dtype, const void 
   const char *name = "mx_moe_backward";
   int rc = validate_plan_args(name, num_tokens, top_k, num_experts);
   if (rc) return rc;
+  if (act != MX_ACT_SILU && act != MX_ACT_SWIGLU7) {
+    set_error("%s: unknown activation %d", name, act);
+    return MX_ERR_INVALID;
+  }
   if ((rc = check_layer(name, hidden, ffn, w1, w3, w2, l1, l3, l2))) return rc;
   if (w1->format == MX_FMT_F32X3) {
     set_error("%s: the fp32 (MX_FMT_F32X3) layer is inference-only", name);
@@ -1214,7 +1239,7 @@ extern "C" int mx_moe_backward(const void *grad_out, int grad_dtype, const void 
     p.out = dgu;
     p.ldo = 2 * ffn;
     if ((rc = launch_any<EPI_STORE2>(w2->format, lora2, p, L.plan, v, s))) return rc;
-    if ((rc = swiglu_backward(dgu, g_in, u_in, R, ffn, s))) return rc;
+    if ((rc = swiglu_backward(dgu, g_in, u_in, R, ffn, act, s))) return rc;
   }
   mark_stage(3, s);
   if (lora2) {
@@ -1286,6 +1311,23 @@ extern "C" int mx_moe_backward(const void *grad_out, int grad_dtype, const void 
   return rc;
 }
 
+extern "C" int mx_moe_backward(const void *grad_out, int grad_dtype, const void *tokens,
+                               const int64_t *top_idx, const void *top_scores, int score_dtype,
+                               int64_t num_tokens, int top_k, int num_experts, int64_t hidden,
+                               int64_t ffn, const mx_weight *w1, const mx_weight *w3,
+                               const mx_weight *w2, const mx_lora *l1, const mx_lora *l3,
+                               const mx_lora *l2, const void *save_gate, const void *save_up,
+                               const void *save_h, const void *save_y, const void *save_lora,
+                               void *grad_tokens, int grad_tokens_dtype, float *grad_scores,
+                               float *grad_a1, float *grad_b1, float *grad_a3, float *grad_b3,
+                               float *grad_a2, float *grad_b2, void *workspace, void *stream) {
+  return mx_moe_backward_act(grad_out, grad_dtype, tokens, top_idx, top_scores, score_dtype,
+                             num_tokens, top_k, num_experts, hidden, ffn, MX_ACT_SILU, w1, w3,
+                             w2, l1, l3, l2, save_gate, save_up, save_h, save_y, save_lora,
+                             grad_tokens, grad_tokens_dtype, grad_scores, grad_a1, grad_b1,
+                             grad_a3, grad_b3, grad_a2, grad_b2, workspace, stream);
+}
+
 extern "C" size_t mx_moe_workspace_size(int64_t num_tokens, int top_k, int num_experts,
                                         int64_t hidden, int64_t ffn) {
   if (num_tokens < 0 || top_k <= 0 || num_experts <= 0 || hidden <= 0 || ffn <= 0) return 0;
@@ -1298,17 +1340,22 @@ extern "C" size_t mx_moe_f32x3_workspace_size(int64_t num_tokens, int top_k, int
   return layer_layout(num_tokens * top_k, num_experts, hidden, ffn, true, num_tokens).bytes;
 }
 
-extern "C" int mx_moe_forward(const void *tokens, const int64_t *top_idx, const void *top_scores,
-                              int score_dtype, int64_t num_tokens, int top_k, int num_experts,
-                              int64_t hidden, int64_t ffn, const mx_weight *w1,
-                              const mx_weight *w3, const mx_weight *w2, const mx_lora *l1,
-                              const mx_lora *l3, const mx_lora *l2, void *out, int out_dtype,
-                              void *save_gate, void *save_up, void *save_h, void *save_y,
-                              void *save_lora, void *workspace, void *stream) {
+extern "C" int mx_moe_forward_act(const void *tokens, const int64_t *top_idx,
+                                  const void *top_scores, int score_dtype, int64_t num_tokens,
+                                  int top_k, int num_experts, int64_t hidden, int64_t ffn,
+                                  int act, const mx_weight *w1, const mx_weight *w3,
+                                  const mx_weight *w2, const mx_lora *l1, const mx_lora *l3,
+                                  const mx_lora *l2, void *out, int out_dtype, void *save_gate,
+                                  void *save_up, void *save_h, void *save_y, void *save_lora,
+                                  void *workspace, void *stream) {
   clear_error();
   const char *name = "mx_moe_forward";
   int rc = validate_plan_args(name, num_tokens, top_k, num_experts);
   if (rc) return rc;
+  if (act != MX_ACT_SILU && act != MX_ACT_SWIGLU7) {
+    set_error("%s: unknown activation %d", name, act);
+    return MX_ERR_INVALID;
+  }
   if ((rc = check_layer(name, hidden, ffn, w1, w3, w2, l1, l3, l2))) return rc;
   if (num_tokens == 0) return MX_OK;
   if (!tokens || !top_idx || !top_scores || !out || !workspace) {
@@ -1345,7 +1392,7 @@ extern "C" int mx_moe_forward(const void *tokens, const int64_t *top_idx, const 
   uint16_t *h = save_h ? static_cast<uint16_t *>(save_h) : reinterpret_cast<uint16_t *>(ws + L.off_h);
   uint16_t *y = save_y ? static_cast<uint16_t *>(save_y) : reinterpret_cast<uint16_t *>(ws + L.off_y);
   rc = expert_mlp(L.plan, v, num_experts, x, (split ? 3 : 1) * hidden,
-                  v.row_token, hidden, ffn, w1, w3, w2, l1, l3, l2, lora_buf, h,
+                  v.row_token, hidden, ffn, act, w1, w3, w2, l1, l3, l2, lora_buf, h,
                   static_cast<uint16_t *>(save_gate), static_cast<uint16_t *>(save_up), y,
                   (split ? 2 : 1) * hidden, v.row_slot, s);
   if (rc) return rc;
@@ -1362,6 +1409,19 @@ extern "C" int mx_moe_forward(const void *tokens, const int64_t *top_idx, const 
   }
   mark_stage(6, s);
   return rc;
+}
+
+extern "C" int mx_moe_forward(const void *tokens, const int64_t *top_idx, const void *top_scores,
+                              int score_dtype, int64_t num_tokens, int top_k, int num_experts,
+                              int64_t hidden, int64_t ffn, const mx_weight *w1,
+                              const mx_weight *w3, const mx_weight *w2, const mx_lora *l1,
+                              const mx_lora *l3, const mx_lora *l2, void *out, int out_dtype,
+                              void *save_gate, void *save_up, void *save_h, void *save_y,
+                              void *save_lora, void *workspace, void *stream) {
+  return mx_moe_forward_act(tokens, top_idx, top_scores, score_dtype, num_tokens, top_k,
+                            num_experts, hidden, ffn, MX_ACT_SILU, w1, w3, w2, l1, l3, l2, out,
+                            out_dtype, save_gate, save_up, save_h, save_y, save_lora, workspace,
+                            stream);
 }
 
 extern "C" int mx_set_stage_events(void **events, int count) {
@@ -1400,7 +1460,7 @@ extern "C" int mx_moe_for_loop(const void *tokens_sorted, const int64_t *counts,
   const PlanView v = plan_view(ws, L.plan);
   if ((rc = plan_from_counts(counts, num_rows, num_experts, ws, s))) return rc;
   return expert_mlp(L.plan, v, num_experts, static_cast<const uint16_t *>(tokens_sorted), hidden,
-                    nullptr, hidden, ffn, w1, w3, w2, l1, l3, l2,
+                    nullptr, hidden, ffn, MX_ACT_SILU, w1, w3, w2, l1, l3, l2,
                     reinterpret_cast<uint16_t *>(ws + L.off_lora),
                     reinterpret_cast<uint16_t *>(ws + L.off_h), nullptr, nullptr,
                     static_cast<uint16_t *>(out), hidden, nullptr, s);

@@ -22,10 +22,11 @@ int lora_weight_grad(const uint16_t *m, int64_t ldm, const int32_t *map, const u
                      const int64_t *seg_end, int experts, float *out, int64_t stride_e,
                      int64_t stride_c, int64_t stride_j, hipStream_t s);
 
-// SwiGLU backward in place over expert-sorted rows: row r of `dgu` (stride
-// 2f) holds dh in its first f columns on entry and [dG | dU] on exit, with
-// h = bf16(silu(g)) * u (g, u: [rows, f]).
+// Gated-activation backward in place over expert-sorted rows: row r of `dgu`
+// (stride 2f) holds dh in its first f columns on entry and [dG | dU] on exit,
+// for h = bf16(silu(g)) * u (MX_ACT_SILU) or h = swiglu7(g, u) (MX_ACT_SWIGLU7),
+// g, u: [rows, f].
 int swiglu_backward(uint16_t *dgu, const uint16_t *g, const uint16_t *u, int64_t rows,
-                    int64_t f, hipStream_t s);
+                    int64_t f, int act, hipStream_t s);
 
 }  // namespace mx

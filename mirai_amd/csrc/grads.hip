@@ -157,10 +157,15 @@ __global__ __launch_bounds__(256) void lora_weight_grad_kernel(
     }
 }
 
-// One thread per 8 columns of one row. Each op is rounded to bf16 as the
-// autograd of the bf16 reference composition h = bf16(silu(g)) * u does
-// (experts.py:289-317); the silu derivative is formed in fp32, as
-// silu_backward does.
+// One thread per 8 columns of one row.
+// MX_ACT_SILU: each op is rounded to bf16 as the autograd of the bf16
+// reference composition h = bf16(silu(g)) * u does (experts.py:289-317); the
+// silu derivative is formed in fp32, as silu_backward does.
+// MX_ACT_SWIGLU7: the fp32 derivative of _memory_bounded_swiglu7_backward
+// (grouped_moe.py:309-335), rounded once per gradient:
+//   dG = dh * (s + 1.702 gc s (1 - s)) [g <= 7] * (uc + 1),
+//   dU = dh * gc s [-7 <= u <= 7], s = sigmoid(1.702 gc).
+template <int ACT>
 __global__ __launch_bounds__(256) void swiglu_backward_kernel(uint16_t *dgu, const uint16_t *g,
                                                               const uint16_t *u, int64_t rows,
                                                               int64_t f) {
@@ -183,6 +188,14 @@ __global__ __launch_bounds__(256) void swiglu_backward_kernel(uint16_t *dgu, con
       const float dh = bf16_bits_to_f32(h ? dw[q] >> 16 : dw[q] & 0xffffu);
       const float gg = bf16_bits_to_f32(h ? gw[q] >> 16 : gw[q] & 0xffffu);
       const float uu = bf16_bits_to_f32(h ? uw[q] >> 16 : uw[q] & 0xffffu);
+      if (ACT == MX_ACT_SWIGLU7) {
+        const float gc = fminf(gg, 7.0f), uc = fminf(fmaxf(uu, -7.0f), 7.0f);
+        const float s7 = 1.0f / (1.0f + expf(-(1.702f * gc)));
+        const float gd = gg <= 7.0f ? s7 + ((1.702f * gc) * s7) * (1.0f - s7) : 0.0f;
+        dgo[h] = (dh * gd) * (uc + 1.0f);
+        duo[h] = uu >= -7.0f && uu <= 7.0f ? dh * (gc * s7) : 0.0f;
+        continue;
+      }
       const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-gg));
       const float sg = round_bf16(gg * sig);
       const float dsg = round_bf16(dh * uu);
@@ -199,11 +212,16 @@ __global__ __launch_bounds__(256) void swiglu_backward_kernel(uint16_t *dgu, con
 }  // namespace
 
 int swiglu_backward(uint16_t *dgu, const uint16_t *g, const uint16_t *u, int64_t rows,
-                    int64_t f, hipStream_t s) {
+                    int64_t f, int act, hipStream_t s) {
   const int64_t total = rows * (f / 8);
   if (total <= 0) return MX_OK;
-  hipLaunchKernelGGL(swiglu_backward_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))),
-                     dim3(256), 0, s, dgu, g, u, rows, f);
+  const dim3 grid(static_cast<unsigned>(ceil_div(total, 256)));
+  if (act == MX_ACT_SWIGLU7)
+    hipLaunchKernelGGL(swiglu_backward_kernel<MX_ACT_SWIGLU7>, grid, dim3(256), 0, s, dgu, g, u,
+                       rows, f);
+  else
+    hipLaunchKernelGGL(swiglu_backward_kernel<MX_ACT_SILU>, grid, dim3(256), 0, s, dgu, g, u,
+                       rows, f);
   return check_launch("SwiGLU backward");
 }
 

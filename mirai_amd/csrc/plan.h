@@ -10,6 +10,15 @@ namespace mx {
 // row) work item per tile for each height.
 constexpr int kPlanTileM = 128;
 constexpr int kPlanTileM2 = 256;
+// Expert (group) count limit of the plan: MAGI-2 flattens heads x experts
+// onto one group axis (12 x 256 = 3072 groups).
+constexpr int kPlanMaxExperts = 8192;
+
+// True when the scatter pass keeps its per-word popcount prefixes in LDS next
+// to the masks (2 * E * EB bits within 64 KiB).
+__host__ __device__ inline bool plan_prefix_in_lds(int num_experts, int slots_per_block) {
+  return static_cast<int64_t>(num_experts) * slots_per_block <= 262144;
+}
 
 struct PlanLayout {
   int64_t rows = 0;

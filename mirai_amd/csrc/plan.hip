@@ -72,21 +72,28 @@ __device__ int64_t block_exclusive_scan(int64_t v, int64_t *shared, int64_t *tot
   return r;
 }
 
-// One workgroup of 1024 threads; thread e owns expert e (E <= 1024). The
+// One workgroup of 1024 threads. Thread t owns experts t, t + 1024, ...
+// (E <= kPlanMaxExperts); the exclusive scans over experts run chunk by chunk
+// of 1024 in expert order, carrying the running total. With E <= 1024 the
 // per-block counts are summed and turned into per-block bases by G groups of
-// E threads, each over a contiguous range of blocks (G = min(16, 1024 / E)).
+// E threads, each over a contiguous range of blocks (G = min(16, 1024 / E));
+// with more experts each thread walks all blocks for each of its experts.
+// kEpt: experts per thread the kernel is compiled for (1 when E <= 1024).
+template <int kEpt>
 __global__ __launch_bounds__(1024) void plan_scan_kernel(
     const int32_t *block_counts, int n_blocks, int E, int64_t n_rows, int tile_m,
     const int64_t *counts_in, int32_t *block_base, int64_t *seg, int2 *tiles,
     int32_t *num_tiles, int2 *tiles2, int32_t *num_tiles2, int32_t *err_counter,
     int64_t *counts_out, int64_t *starts_out, int32_t *offsets_out) {
   __shared__ int64_t scan_tmp[32];
-  __shared__ int32_t part[1024];     // [group][expert] block-range counts
-  __shared__ int64_t start_s[1024];  // expert starts
+  __shared__ int32_t part[1024];     // [group][expert] block-range counts (E <= 1024)
+  __shared__ int64_t start_s[1024];  // expert starts (E <= 1024)
   const int t = threadIdx.x;
-  const int G = counts_in ? 1 : max(1, min(16, 1024 / E));
-  const int ge = t / E, ee = t - ge * E;
-  const bool gact = !counts_in && ge < G;
+  const int ept = (E + 1023) / 1024;
+  const bool small = E <= 1024;
+  const int G = counts_in || !small ? 1 : max(1, min(16, 1024 / E));
+  const int ge = small ? t / E : 0, ee = small ? t - ge * E : 0;
+  const bool gact = !counts_in && small && G > 1 && ge < G;
   const int b_lo = gact ? static_cast<int>(static_cast<int64_t>(n_blocks) * ge / G) : 0;
   const int b_hi = gact ? static_cast<int>(static_cast<int64_t>(n_blocks) * (ge + 1) / G) : 0;
   if (gact) {
@@ -95,29 +102,39 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(
     part[t] = c;
   }
   __syncthreads();
-  const int e = t;
-  int64_t count = 0;
-  if (e < E) {
-    if (counts_in) {
-      count = counts_in[e];
-      if (count < 0 || count > n_rows) {
-        atomicAdd(err_counter, 1);
-        count = count < 0 ? 0 : n_rows;
+  int64_t count[kEpt], start[kEpt], seg_lo[kEpt], seg_hi[kEpt];
+  int64_t carry = 0;
+#pragma unroll
+  for (int c = 0; c < kEpt; ++c) {
+    count[c] = start[c] = seg_lo[c] = seg_hi[c] = 0;
+    if (c >= ept) continue;  // uniform across the workgroup
+    const int e = t + 1024 * c;
+    if (e < E) {
+      if (counts_in) {
+        count[c] = counts_in[e];
+        if (count[c] < 0 || count[c] > n_rows) {
+          atomicAdd(err_counter, 1);
+          count[c] = count[c] < 0 ? 0 : n_rows;
+        }
+      } else if (G > 1) {
+        for (int gg = 0; gg < G; ++gg) count[c] += part[gg * E + e];
+      } else {
+        for (int b = 0; b < n_blocks; ++b) count[c] += block_counts[static_cast<int64_t>(b) * E + e];
       }
-    } else {
-      for (int gg = 0; gg < G; ++gg) count += part[gg * E + e];
+    }
+    int64_t chunk_total = 0;
+    start[c] = carry + block_exclusive_scan(count[c], scan_tmp, &chunk_total);
+    carry += chunk_total;
+    seg_lo[c] = start[c];
+    seg_hi[c] = start[c] + count[c];
+    if (counts_in) {
+      // Rows beyond num_rows are never touched, even if the counts disagree.
+      if (seg_lo[c] > n_rows) seg_lo[c] = n_rows;
+      if (seg_hi[c] > n_rows) seg_hi[c] = n_rows;
     }
   }
-  int64_t total = 0;
-  const int64_t start = block_exclusive_scan(count, scan_tmp, &total);
-  int64_t seg_lo = start, seg_hi = start + count;
-  if (counts_in) {
-    // Rows beyond num_rows are never touched, even if the counts disagree.
-    if (seg_lo > n_rows) seg_lo = n_rows;
-    if (seg_hi > n_rows) seg_hi = n_rows;
-    if (e == 0 && total != n_rows) atomicAdd(err_counter, 1);
-  }
-  if (e < E) start_s[e] = start;
+  if (counts_in && t == 0 && carry != n_rows) atomicAdd(err_counter, 1);
+  if (small && t < E) start_s[t] = start[0];
   __syncthreads();
   if (gact) {
     int64_t run = start_s[ee];
@@ -128,22 +145,40 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(
       run += block_counts[i];
     }
   }
-  if (e < E) {
-    seg[e] = seg_lo;
-    seg[E + e] = seg_hi;
-    if (counts_out) counts_out[e] = count;
-    if (starts_out) starts_out[e] = start;
-    if (offsets_out) offsets_out[e] = static_cast<int32_t>(start + count);
+#pragma unroll
+  for (int c = 0; c < kEpt; ++c) {
+    const int e = t + 1024 * c;
+    if (c >= ept || e >= E) continue;
+    if (!counts_in && G == 1) {
+      int64_t run = start[c];
+      for (int b = 0; b < n_blocks; ++b) {
+        const int64_t i = static_cast<int64_t>(b) * E + e;
+        block_base[i] = static_cast<int32_t>(run);
+        run += block_counts[i];
+      }
+    }
+    seg[e] = seg_lo[c];
+    seg[E + e] = seg_hi[c];
+    if (counts_out) counts_out[e] = count[c];
+    if (starts_out) starts_out[e] = start[c];
+    if (offsets_out) offsets_out[e] = static_cast<int32_t>(start[c] + count[c]);
   }
   for (int list = 0; list < 2; ++list) {
     const int tm = list == 0 ? tile_m : 2 * tile_m;
     int2 *out = list == 0 ? tiles : tiles2;
-    const int64_t my_tiles = e < E ? (seg_hi - seg_lo + tm - 1) / tm : 0;
-    int64_t n_tiles = 0;
-    const int64_t tile0 = block_exclusive_scan(my_tiles, scan_tmp, &n_tiles);
-    for (int64_t j = 0; j < my_tiles; ++j)
-      out[tile0 + j] = make_int2(e, static_cast<int>(seg_lo + j * tm));
-    if (threadIdx.x == 0) *(list == 0 ? num_tiles : num_tiles2) = static_cast<int32_t>(n_tiles);
+    int64_t tcarry = 0;
+#pragma unroll
+    for (int c = 0; c < kEpt; ++c) {
+      if (c >= ept) continue;  // uniform
+      const int e = t + 1024 * c;
+      const int64_t my_tiles = e < E ? (seg_hi[c] - seg_lo[c] + tm - 1) / tm : 0;
+      int64_t chunk_tiles = 0;
+      const int64_t tile0 = tcarry + block_exclusive_scan(my_tiles, scan_tmp, &chunk_tiles);
+      tcarry += chunk_tiles;
+      for (int64_t j = 0; j < my_tiles; ++j)
+        out[tile0 + j] = make_int2(e, static_cast<int>(seg_lo[c] + j * tm));
+    }
+    if (threadIdx.x == 0) *(list == 0 ? num_tiles : num_tiles2) = static_cast<int32_t>(tcarry);
   }
 }
 
@@ -155,18 +190,24 @@ __global__ __launch_bounds__(256) void plan_scatter_kernel(
   extern __shared__ uint32_t lds[];
   const int words = EB >> 5;
   uint32_t *mask = lds;
+  // Per-word popcount prefixes sit in LDS when they fit next to the masks;
+  // otherwise (many experts, EB <= 256: at most 7 words below a slot) each
+  // slot adds up the popcounts of the words below its own.
+  const bool lds_prefix = plan_prefix_in_lds(E, EB);
   uint32_t *prefix = lds + E * words;
   const int64_t slot0 = static_cast<int64_t>(blockIdx.x) * EB;
   const int n_slots = static_cast<int>(min<int64_t>(EB, R - slot0));
   build_masks(top_idx, slot0, n_slots, E, words, mask, nullptr);
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    uint32_t run = 0;
-    for (int w = 0; w < words; ++w) {
-      prefix[e * words + w] = run;
-      run += __popc(mask[e * words + w]);
+  if (lds_prefix) {
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      uint32_t run = 0;
+      for (int w = 0; w < words; ++w) {
+        prefix[e * words + w] = run;
+        run += __popc(mask[e * words + w]);
+      }
     }
+    __syncthreads();
   }
-  __syncthreads();
   const int32_t *base = block_base + static_cast<int64_t>(blockIdx.x) * E;
   for (int p = threadIdx.x; p < n_slots; p += blockDim.x) {
     const int64_t i = slot0 + p;
@@ -177,7 +218,13 @@ __global__ __launch_bounds__(256) void plan_scatter_kernel(
     }
     const int w = p >> 5;
     const uint32_t below = mask[e * words + w] & ((1u << (p & 31)) - 1u);
-    const int64_t pos = base[e] + prefix[e * words + w] + __popc(below);
+    uint32_t pre = 0;
+    if (lds_prefix) {
+      pre = prefix[e * words + w];
+    } else {
+      for (int w2 = 0; w2 < w; ++w2) pre += __popc(mask[e * words + w2]);
+    }
+    const int64_t pos = base[e] + pre + __popc(below);
     const int64_t tok = i / k;
     if (sort_positions) sort_positions[pos] = i;
     if (sorted_token_indices) sorted_token_indices[pos] = tok;
@@ -194,6 +241,8 @@ __global__ __launch_bounds__(256) void plan_scatter_kernel(
   }
 }
 
+constexpr int kPlanMaxEpt = kPlanMaxExperts / 1024;
+
 __global__ void zero_i32_kernel(int32_t *p, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0;
@@ -207,6 +256,10 @@ int slots_per_plan_block(int num_experts, int64_t rows) {
   int eb = 4096;
   while (eb > 256 && (static_cast<int64_t>(num_experts) * eb > 262144 || ceil_div(rows, eb) < 256))
     eb >>= 1;
+  if (static_cast<int64_t>(num_experts) * eb <= 262144) return eb;
+  // More than 1024 experts: the masks alone fill the 64 KiB (prefixes are
+  // recounted per slot), so the blocks shrink to 32..128 slots.
+  while (eb > 32 && static_cast<int64_t>(num_experts) * eb > 524288) eb >>= 1;
   return eb;
 }
 
@@ -266,12 +319,13 @@ int build_plan(const int64_t *top_idx, const void *top_scores, int score_dtype,
     hipLaunchKernelGGL(plan_count_kernel, dim3(L.blocks), dim3(256), lds, s, top_idx, R,
                        num_experts, L.slots_per_block, v.block_counts, v.err);
   }
-  hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, s, v.block_counts, L.blocks,
-                     num_experts, R, kPlanTileM, static_cast<const int64_t *>(nullptr),
-                     v.block_base, v.seg, v.tiles, v.num_tiles, v.tiles2, v.num_tiles2, v.err,
-                     counts, starts, offsets);
+  hipLaunchKernelGGL(num_experts <= 1024 ? plan_scan_kernel<1> : plan_scan_kernel<kPlanMaxEpt>,
+                     dim3(1), dim3(1024), 0, s, v.block_counts, L.blocks, num_experts, R,
+                     kPlanTileM, static_cast<const int64_t *>(nullptr), v.block_base, v.seg,
+                     v.tiles, v.num_tiles, v.tiles2, v.num_tiles2, v.err, counts, starts, offsets);
   if (L.blocks > 0) {
-    const size_t lds = 2 * sizeof(uint32_t) * num_experts * (L.slots_per_block / 32);
+    const size_t lds = (plan_prefix_in_lds(num_experts, L.slots_per_block) ? 2 : 1) *
+                       sizeof(uint32_t) * num_experts * (L.slots_per_block / 32);
     if (score_dtype == MX_DTYPE_BF16)
       hipLaunchKernelGGL(plan_scatter_kernel<MX_DTYPE_BF16>, dim3(L.blocks), dim3(256), lds, s,
                          top_idx, top_scores, R, top_k, num_experts, L.slots_per_block,
@@ -293,7 +347,8 @@ int plan_from_counts(const int64_t *counts, int64_t num_rows, int num_experts, v
   const PlanLayout L = plan_layout(num_rows, num_experts);
   const PlanView v = plan_view(workspace, L);
   hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, v.err, 3);
-  hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, s,
+  hipLaunchKernelGGL(num_experts <= 1024 ? plan_scan_kernel<1> : plan_scan_kernel<kPlanMaxEpt>,
+                     dim3(1), dim3(1024), 0, s,
                      static_cast<const int32_t *>(nullptr), 0, num_experts, num_rows,
                      kPlanTileM, counts, static_cast<int32_t *>(nullptr), v.seg, v.tiles,
                      v.num_tiles, v.tiles2, v.num_tiles2, v.err, static_cast<int64_t *>(nullptr),
@@ -306,8 +361,8 @@ int validate_plan_args(const char *name, int64_t num_tokens, int top_k, int num_
     set_error("%s: need num_tokens >= 0 and top_k in [1, 16]", name);
     return MX_ERR_INVALID;
   }
-  if (num_experts <= 0 || num_experts > 1024) {
-    set_error("%s: num_experts must be in [1, 1024], got %d", name, num_experts);
+  if (num_experts <= 0 || num_experts > kPlanMaxExperts) {
+    set_error("%s: num_experts must be in [1, %d], got %d", name, kPlanMaxExperts, num_experts);
     return MX_ERR_INVALID;
   }
   if (num_tokens * top_k >= (int64_t(1) << 31)) {

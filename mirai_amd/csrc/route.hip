@@ -167,6 +167,112 @@ __global__ __launch_bounds__(256) void route_topk_backward_kernel(
   }
 }
 
+// Multi-head routing (MAGI-2): one wavefront per (head, token) row of fp32
+// logits [H, S, E]. Scores are softmax or sigmoid of the logits; experts are
+// picked by score + expert_bias[h] (the bias steers selection only), ties to
+// the lower expert id; the picks' unbiased scores are renormalised to sum 1
+// (p / max(sum p, floor), the L1 F.normalize of route.py:136-140) when asked
+// and multiplied by route_scale (magi2_preview.py:2735-2742). Follows
+// _compute_topk_probs_and_indices_torch_impl (flash_mh_moe/route.py:28-148)
+// with num_virtual_group = 1.
+template <int PER_LANE>
+__global__ __launch_bounds__(256) void route_heads_kernel(
+    const float *logits, int64_t S, int H, int E, int k, int score_func, const float *bias,
+    int renorm, float renorm_floor, float route_scale, int layout, int64_t *top_idx,
+    void *top_scores, int score_dtype) {
+  const int lane = threadIdx.x & 63;
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // h * S + s
+  if (q >= static_cast<int64_t>(H) * S) return;
+  const int h = static_cast<int>(q / S);
+  const int64_t s = q - static_cast<int64_t>(h) * S;
+  const float *row = logits + q * E;
+  float sc[PER_LANE], key[PER_LANE];
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < PER_LANE; ++j) {
+    const int e = lane + 64 * j;
+    sc[j] = e < E ? row[e] : -INFINITY;
+    m = fmaxf(m, sc[j]);
+  }
+  if (score_func == MX_SCORE_SOFTMAX) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    float z = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j) {
+      sc[j] = lane + 64 * j < E ? expf(sc[j] - m) : 0.0f;
+      z += sc[j];
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) z += __shfl_xor(z, off, 64);
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j) sc[j] = sc[j] / z;
+  } else {
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j) sc[j] = lane + 64 * j < E ? 1.0f / (1.0f + expf(-sc[j])) : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < PER_LANE; ++j) {
+    const int e = lane + 64 * j;
+    key[j] = e < E ? sc[j] + (bias ? bias[static_cast<int64_t>(h) * E + e] : 0.0f) : -INFINITY;
+  }
+  uint32_t taken = 0;
+  int my_e = 0;
+  float my_p = 0.0f;
+  for (int r = 0; r < k; ++r) {
+    float bv = -INFINITY, bp = 0.0f;
+    int be = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E && !((taken >> j) & 1u) && better(key[j], e, bv, be)) {
+        bv = key[j];
+        be = e;
+        bp = sc[j];
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oe = __shfl_xor(be, off, 64);
+      const float op = __shfl_xor(bp, off, 64);
+      if (better(ov, oe, bv, be)) {
+        bv = ov;
+        be = oe;
+        bp = op;
+      }
+    }
+    if ((be & 63) == lane) taken |= 1u << (be >> 6);
+    if (lane == r) {
+      my_e = be;
+      my_p = bp;
+    }
+  }
+  float p = lane < k ? my_p : 0.0f;
+  float sum = p;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  float score = p;
+  if (renorm == MX_RENORM_CLAMP)
+    score = p / fmaxf(sum, renorm_floor);
+  else if (renorm == MX_RENORM_EPS)
+    score = p / (sum + renorm_floor);
+  score *= route_scale;
+  if (lane < k) {
+    int64_t o;
+    int64_t id;
+    if (layout == MX_ROUTE_LAYOUT_ROWS) {
+      o = (s * H + h) * k + lane;
+      id = static_cast<int64_t>(h) * E + my_e;
+    } else {
+      o = q * k + lane;
+      id = my_e;
+    }
+    top_idx[o] = id;
+    store_value(top_scores, o, score, score_dtype);
+  }
+}
+
 }  // namespace
 }  // namespace mx
 
@@ -241,4 +347,48 @@ extern "C" int mx_route_topk_backward(const float *logits, int64_t num_tokens, i
   MX_ROUTE_DISPATCH(route_topk_backward_kernel, logits, num_tokens, num_experts, top_k, renorm,
                     route_scale, top_idx, grad_scores, grad_logits);
   return check_launch("mx_route_topk_backward");
+}
+
+extern "C" int mx_route_topk_heads(const float *logits, int num_heads, int64_t num_tokens,
+                                   int num_experts, int top_k, int score_func,
+                                   const float *expert_bias, int renorm, float renorm_floor,
+                                   float route_scale, int layout, int64_t *top_idx,
+                                   void *top_scores, int score_dtype, void *stream) {
+  clear_error();
+  int rc = validate_route("mx_route_topk_heads", logits, num_tokens, num_experts, top_k, renorm);
+  if (rc) return rc;
+  if (num_heads <= 0 || !top_idx || !top_scores) {
+    set_error("mx_route_topk_heads: need num_heads > 0 and non-null outputs");
+    return MX_ERR_INVALID;
+  }
+  if (score_func != MX_SCORE_SOFTMAX && score_func != MX_SCORE_SIGMOID) {
+    set_error("mx_route_topk_heads: unknown score function %d", score_func);
+    return MX_ERR_INVALID;
+  }
+  if (layout != MX_ROUTE_LAYOUT_HEADS && layout != MX_ROUTE_LAYOUT_ROWS) {
+    set_error("mx_route_topk_heads: unknown output layout %d", layout);
+    return MX_ERR_INVALID;
+  }
+  if (!(renorm_floor >= 0.0f)) {
+    set_error("mx_route_topk_heads: renorm_floor must be >= 0");
+    return MX_ERR_INVALID;
+  }
+  const int64_t rows = num_tokens * num_heads;
+  if (rows == 0) return MX_OK;
+  const int per_lane = (num_experts + 63) / 64;
+  const dim3 grid(static_cast<unsigned>(ceil_div(rows, 4))), block(256);
+  hipStream_t s = as_stream(stream);
+#define MX_HEADS_ARGS logits, num_tokens, num_heads, num_experts, top_k, score_func, expert_bias, \
+    renorm, renorm_floor, route_scale, layout, top_idx, top_scores, score_dtype
+  switch (per_lane) {
+    case 1: hipLaunchKernelGGL(route_heads_kernel<1>, grid, block, 0, s, MX_HEADS_ARGS); break;
+    case 2: hipLaunchKernelGGL(route_heads_kernel<2>, grid, block, 0, s, MX_HEADS_ARGS); break;
+    case 3:
+    case 4: hipLaunchKernelGGL(route_heads_kernel<4>, grid, block, 0, s, MX_HEADS_ARGS); break;
+    case 5: case 6: case 7:
+    case 8: hipLaunchKernelGGL(route_heads_kernel<8>, grid, block, 0, s, MX_HEADS_ARGS); break;
+    default: hipLaunchKernelGGL(route_heads_kernel<16>, grid, block, 0, s, MX_HEADS_ARGS); break;
+  }
+#undef MX_HEADS_ARGS
+  return check_launch("mx_route_topk_heads");
 }

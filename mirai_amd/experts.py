@@ -25,6 +25,7 @@ from . import quant
 from .lora import ActiveExpertLoRA
 from .specs import (
     CANONICAL_PACKED_EXPERT_MLP_SPEC,
+    FUSED_GATED_ACTIVATIONS,
     ExpertMLPExecutionSpec,
     normalize_expert_weight_access_policy,
 )
@@ -81,13 +82,17 @@ class CompressedGroupedExperts(nn.Module):
                     expert_dequant_chunk_size, quant_format, nf4_blocksize, execution_spec):
         if not isinstance(execution_spec, ExpertMLPExecutionSpec):
             raise TypeError("execution_spec must use ExpertMLPExecutionSpec.")
-        if not execution_spec.uses_gated_product or execution_spec.activation != "silu":
+        if (not execution_spec.uses_gated_product
+                or execution_spec.activation not in FUSED_GATED_ACTIVATIONS):
             raise ValueError(
-                "The MI355X fused expert kernels implement the gated SwiGLU expert MLP "
-                "(activation='silu', combiner='gated_product')."
+                "The MI355X fused expert kernels implement the gated expert MLP "
+                "(activation 'silu' or 'swiglu7', combiner='gated_product')."
             )
-        if int(num_experts) <= 0 or int(num_experts) > 1024:
-            raise ValueError("num_experts must be in [1, 1024].")
+        # Activation of the fused gate/up epilogue and of its backward.
+        self._kernel_activation = (nat.ACT_SWIGLU7 if execution_spec.activation == "swiglu7"
+                                   else nat.ACT_SILU)
+        if int(num_experts) <= 0 or int(num_experts) > nat.PLAN_MAX_EXPERTS:
+            raise ValueError(f"num_experts must be in [1, {nat.PLAN_MAX_EXPERTS}].")
         if int(nf4_blocksize) != NF4_BLOCKSIZE:
             raise ValueError("The MI355X NF4 format uses blocksize 64.")
         self.num_experts = int(num_experts)

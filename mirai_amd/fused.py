@@ -1,6 +1,6 @@
 """Autograd wrappers that drive the fused HIP expert kernels.
 
-Forward: one ``mx_moe_forward`` call (plan, gate/up GEMM + LoRA + SwiGLU, down
+Forward: one ``mx_moe_forward_act`` call (plan, gate/up GEMM + LoRA + SwiGLU, down
 GEMM + LoRA, combine). When gradients are needed it also keeps the bf16
 pre-activations, the SwiGLU output, the per-slot expert outputs and the scaled
 low-rank activations for the backward; frozen weights are never saved -- the
@@ -15,6 +15,12 @@ import torch
 from . import _native as nat
 
 LORA_ROW = 96  # [gate 32 | up 32 | down 32] scaled low-rank activations per sorted row
+
+
+def kernel_activation(module) -> int:
+    """Expert activation of the fused kernels: SwiGLU (the canonical packed
+    expert MLP) unless a wrapper such as the MAGI-2 experts selects swiglu7."""
+    return int(getattr(module, "_kernel_activation", nat.ACT_SILU))
 
 
 def _lora_descriptors(module, device, split=False):
@@ -85,10 +91,10 @@ def _forward(module, tokens, top_scores, top_indices, need_grad):
     lib = nat.load_library()
     size = lib.mx_moe_f32x3_workspace_size if split else lib.mx_moe_workspace_size
     ws = nat.workspace(size(T, k, E, d, f), device)
-    nat.call("mx_moe_forward", x.data_ptr(), idx.data_ptr(), scores.data_ptr(),
-             nat.dtype_code(scores.dtype), T, k, E, d, f, w1, w3, w2, lora[0], lora[1],
-             lora[2], out.data_ptr(), nat.dtype_code(out.dtype), *[nat.ptr(t) for t in saves],
-             ws.data_ptr(), nat.stream(device))
+    nat.call("mx_moe_forward_act", x.data_ptr(), idx.data_ptr(), scores.data_ptr(),
+             nat.dtype_code(scores.dtype), T, k, E, d, f, kernel_activation(module), w1, w3, w2,
+             lora[0], lora[1], lora[2], out.data_ptr(), nat.dtype_code(out.dtype),
+             *[nat.ptr(t) for t in saves], ws.data_ptr(), nat.stream(device))
     del keep
     return out.to(tokens.dtype), ((x, scores, idx, *saves) if need_grad else None)
 
@@ -130,6 +136,8 @@ def sorted_experts(module, tokens, counts):
     c = counts.detach().to(device=device, dtype=torch.int64).contiguous()
     if int(c.numel()) != module.num_experts:
         raise ValueError("counts must hold one entry per expert.")
+    if kernel_activation(module) != nat.ACT_SILU:
+        raise NotImplementedError("run_for_loop implements the SwiGLU expert MLP only.")
     S, d = (int(v) for v in x.shape)
     (w1, w3, w2), packed = _weight_descriptors(module, device)
     f = int(packed[0].shape[1])

@@ -13,7 +13,13 @@ from __future__ import annotations
 from contextlib import contextmanager
 from dataclasses import dataclass
 
-EXPERT_MLP_ACTIVATIONS = {"silu", "gelu", "relu", "identity"}
+# "swiglu7" extends the reference set with the MAGI-2 gated activation
+# (mirai/core/models/magi2_preview/grouped_moe.py:287-306), which the reference
+# runs in its separate MAGI-2 grouped backend rather than through this spec.
+EXPERT_MLP_ACTIVATIONS = {"silu", "gelu", "relu", "identity", "swiglu7"}
+# Gated activations the fused MI355X kernels implement (with combiner
+# "gated_product").
+FUSED_GATED_ACTIVATIONS = ("silu", "swiglu7")
 EXPERT_MLP_COMBINERS = {"gated_product", "activated"}
 EXPERT_WEIGHT_ACCESS_POLICIES = {
     "auto",
@@ -130,6 +136,19 @@ CANONICAL_PACKED_EXPERT_MLP_SPEC = ExpertMLPExecutionSpec(
         ExpertProjectionRole("down", "w2"),
     ),
     activation="silu",
+    combiner="gated_product",
+)
+
+
+# MAGI-2 routed experts (CoreMultiHeadMoE, mirai/vendors/magi2_preview/model/
+# magi2_preview.py:2680-2704): gate W_gate, up W_up, down W_down, swiglu7.
+MAGI2_EXPERT_MLP_SPEC = ExpertMLPExecutionSpec(
+    projections=(
+        ExpertProjectionRole("gate", "W_gate"),
+        ExpertProjectionRole("up", "W_up"),
+        ExpertProjectionRole("down", "W_down"),
+    ),
+    activation="swiglu7",
     combiner="gated_product",
 )
 

@@ -48,7 +48,8 @@ def test_plan_known_answer():
 
 
 @pytest.mark.parametrize("T,k,E", [(1, 1, 1), (7, 3, 5), (4097, 2, 1024), (20000, 8, 3),
-                                   (3000, 4, 700)])
+                                   (3000, 4, 700), (3000, 2, 1025), (9000, 3, 3072),
+                                   (500, 4, 8192)])
 def test_plan_random_with_duplicates_and_invalid_ids(T, k, E):
     rng = np.random.default_rng(T + k + E)
     idx = rng.integers(0, E, size=(T, k)).astype(np.int64)

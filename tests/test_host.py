@@ -30,7 +30,7 @@ def test_from_empty_validation():
     with pytest.raises(ValueError):
         _module(num_experts=0)
     with pytest.raises(ValueError):
-        _module(num_experts=1025)
+        _module(num_experts=8193)  # the plan takes up to 8192 (flattened MAGI-2 groups)
     with pytest.raises(ValueError):
         _module(nf4_blocksize=128)
     with pytest.raises(ValueError):
