@@ -17,6 +17,8 @@
  *   NF4 weight      codes [E, out, in/2] uint8 (per group of 8 elements along
  *                   in, byte i holds element i in the low nibble and element
  *                   i+4 in the high nibble), absmax [E, out, in/64] bf16
+ *   NF4_F32 weight  codes as NF4, absmax [E, out, in/64] fp32 (the double-quant
+ *                   absmax of a bitsandbytes payload, decoded by mx_nf4_from_bnb)
  *   INT8 weight     q [E, out, in] int8, scale [E, out] bf16
  *   BF16 weight     w [E, out, in] bf16
  *   F32X3 weight    w [E, out, 3*in] bf16: an fp32 weight split into bf16
@@ -49,6 +51,7 @@ extern "C" {
 #define MX_FMT_NF4 1
 #define MX_FMT_INT8 2
 #define MX_FMT_F32X3 3
+#define MX_FMT_NF4_F32 4  /* NF4 codes with an fp32 absmax per block (ingested bitsandbytes) */
 
 /* Plane orders of mx_split_f32. */
 #define MX_SPLIT_ACT 0     /* [hi | hi | lo]: activations */
@@ -238,6 +241,32 @@ int mx_nf4_quantize(const void *w, int w_dtype, int64_t rows, int64_t cols, uint
  */
 int mx_nf4_dequantize(const uint8_t *codes, const void *absmax, int64_t rows, int64_t cols,
                       void *out, int out_dtype, void *stream);
+
+/* mx_nf4_dequantize with the absmax in bf16 or fp32 (absmax_dtype MX_DTYPE_*;
+ * fp32 is MX_FMT_NF4_F32): w = bf16(fp32(NF4[code]) * absmax). */
+int mx_nf4_dequantize_ex(const uint8_t *codes, const void *absmax, int absmax_dtype,
+                         int64_t rows, int64_t cols, void *out, int out_dtype, void *stream);
+
+/*
+ * Ingests a bitsandbytes double-quantised NF4 payload (quantize_4bit with
+ * compress_statistics=True, blocksize 64, nested blocksize 256, bitsandbytes
+ * 0.49.2) as the reference stores it per expert
+ * (CompressedGroupedExperts._store_nf4_grouped, experts.py:998-1031; buffers
+ * {key}_nf4, _nf4_absmax, _nf4_nabsmax, _nf4_offset, _nf4_ncode):
+ *   packed [E, rows*cols/2] uint8 (byte j: element 2j high nibble, 2j+1 low),
+ *   absmax_q [E, rows*cols/64] uint8, nested_absmax [E, ceil(rows*cols/16384)]
+ *   fp32, offsets [E] fp32, nested_code [256] fp32.
+ * Writes MX_FMT_NF4_F32 weights: codes [E, rows, cols/2] in this library's
+ * nibble order and absmax [E, rows, cols/64] fp32 =
+ * nested_code[absmax_q] * nested_absmax + offset (fp32, two roundings), the
+ * absmax bitsandbytes dequantises with (quant.py:413-431), so the GEMMs decode
+ * the payload's weights without re-quantisation. The 16-entry NF4 code table
+ * of the payload ({key}_nf4_code) must equal the NF4 levels (checked by the
+ * caller). cols a multiple of 64.
+ */
+int mx_nf4_from_bnb(const uint8_t *packed, const uint8_t *absmax_q, const float *nested_absmax,
+                    const float *offsets, const float *nested_code, int64_t experts, int64_t rows,
+                    int64_t cols, uint8_t *codes, float *absmax, void *stream);
 
 /*
  * Symmetric per-output-row INT8: scale = bf16(max(absmax_row/127, 1e-30)),

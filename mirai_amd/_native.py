@@ -27,6 +27,7 @@ FMT_BF16 = 0
 FMT_NF4 = 1
 FMT_INT8 = 2
 FMT_F32X3 = 3      # fp32 weights as bf16 planes [hi | lo | hi] along in_features
+FMT_NF4_F32 = 4    # NF4 codes with an fp32 block absmax (ingested bitsandbytes payloads)
 
 SPLIT_ACT = 0      # mx_split_f32 plane orders
 SPLIT_WEIGHT = 1
@@ -91,6 +92,9 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         c_int, [_P, c_int, _P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, _P, _P, _P]),
     "mx_nf4_quantize": (c_int, [_P, c_int, c_int64, c_int64, _P, _P, _P]),
     "mx_nf4_dequantize": (c_int, [_P, _P, c_int64, c_int64, _P, c_int, _P]),
+    "mx_nf4_dequantize_ex": (c_int, [_P, _P, c_int, c_int64, c_int64, _P, c_int, _P]),
+    "mx_nf4_from_bnb": (
+        c_int, [_P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P]),
     "mx_int8_quantize": (c_int, [_P, c_int, c_int64, c_int64, _P, _P, _P]),
     "mx_int8_dequantize": (c_int, [_P, _P, c_int64, c_int64, _P, c_int, _P]),
     "mx_set_stage_events": (c_int, [POINTER(c_void_p), c_int]),

@@ -51,14 +51,18 @@ __global__ __launch_bounds__(256) void nf4_quantize_kernel(const void *w, int w_
 
 // Each thread decodes one packed dword: the 8 elements of one group (byte i
 // holds element i in its low nibble and element i + 4 in its high nibble).
+// The block absmax is bf16 (the build's quantiser) or fp32 (MX_FMT_NF4_F32).
+template <bool F32_ABSMAX>
 __global__ __launch_bounds__(256) void nf4_dequantize_kernel(const uint32_t *codes,
-                                                             const uint16_t *absmax,
+                                                             const void *absmax,
                                                              int64_t num_words, void *out,
                                                              int out_dtype) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= num_words) return;
   const uint32_t word = codes[i];
-  const float a = bf16_bits_to_f32(absmax[i / (kNF4Block / 8)]);
+  const int64_t blk = i / (kNF4Block / 8);
+  const float a = F32_ABSMAX ? static_cast<const float *>(absmax)[blk]
+                             : bf16_bits_to_f32(static_cast<const uint16_t *>(absmax)[blk]);
   float v[8];
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
@@ -76,6 +80,44 @@ __global__ __launch_bounds__(256) void nf4_dequantize_kernel(const uint32_t *cod
     float *o = reinterpret_cast<float *>(out) + 8 * i;
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = bf16_bits_to_f32(f32_to_bf16_bits(v[j]));
+  }
+}
+
+// bitsandbytes double-quantised NF4 (quantize_4bit with compress_statistics,
+// blocksize 64, nested blocksize 256; bitsandbytes 0.49.2 as called by
+// mirai/core/models/compressed_weights/quantization/quant.py:315-358) ->
+// MX_FMT_NF4_F32. One thread per group of 8 elements: bitsandbytes byte j of
+// a row holds element 2j in its high nibble and 2j + 1 in its low nibble; the
+// group is rewritten as byte i = element i | element i + 4 << 4. The thread
+// that owns the first group of a 64-block also decodes the block's absmax,
+// nested_code[absmax_q] * nested_absmax[block / 256] + offset in fp32 (the
+// dequantize_blockwise + offset step of quant.py:413-424).
+__global__ __launch_bounds__(256) void nf4_from_bnb_kernel(
+    const uint32_t *packed, const uint8_t *absmax_q, const float *nested_absmax,
+    const float *offsets, const float *nested_code, int64_t groups_per_expert,
+    int64_t nested_per_expert, int64_t total_groups, uint32_t *codes, float *absmax) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (g >= total_groups) return;
+  const uint32_t w = packed[g];
+  uint32_t out = 0;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t byte = (w >> (8 * m)) & 0xffu;
+    const uint32_t e_even = byte >> 4, e_odd = byte & 15u;  // elements 2m, 2m + 1
+    // element k of the group goes to byte k % 4, low nibble for k < 4.
+    const int k0 = 2 * m, k1 = 2 * m + 1;
+    out |= e_even << (8 * (k0 & 3) + 4 * (k0 >> 2));
+    out |= e_odd << (8 * (k1 & 3) + 4 * (k1 >> 2));
+  }
+  codes[g] = out;
+  if ((g & 7) == 0) {  // first group of a 64-element block
+#pragma clang fp contract(off)
+    const int64_t e = g / groups_per_expert;
+    const int64_t b = (g - e * groups_per_expert) >> 3;  // block within the expert
+    const int64_t blk = g >> 3;
+    // Two roundings (product, then sum), never one fused multiply-add.
+    const float scaled = nested_code[absmax_q[blk]] * nested_absmax[e * nested_per_expert + (b >> 8)];
+    absmax[blk] = scaled + offsets[e];
   }
 }
 
@@ -146,11 +188,16 @@ extern "C" int mx_nf4_quantize(const void *w, int w_dtype, int64_t rows, int64_t
   return check_launch("mx_nf4_quantize");
 }
 
-extern "C" int mx_nf4_dequantize(const uint8_t *codes, const void *absmax, int64_t rows,
-                                 int64_t cols, void *out, int out_dtype, void *stream) {
+extern "C" int mx_nf4_dequantize_ex(const uint8_t *codes, const void *absmax, int absmax_dtype,
+                                    int64_t rows, int64_t cols, void *out, int out_dtype,
+                                    void *stream) {
   clear_error();
   if (!codes || !absmax || !out || rows < 0 || cols <= 0 || cols % 64 != 0) {
     set_error("mx_nf4_dequantize: need non-null buffers and cols a positive multiple of 64");
+    return MX_ERR_INVALID;
+  }
+  if (absmax_dtype != MX_DTYPE_BF16 && absmax_dtype != MX_DTYPE_F32) {
+    set_error("mx_nf4_dequantize: absmax must be bf16 or fp32");
     return MX_ERR_INVALID;
   }
   if (reinterpret_cast<uintptr_t>(codes) % 4 != 0 ||
@@ -160,10 +207,47 @@ extern "C" int mx_nf4_dequantize(const uint8_t *codes, const void *absmax, int64
   }
   const int64_t words = rows * cols / 8;
   if (words == 0) return MX_OK;
-  hipLaunchKernelGGL(nf4_dequantize_kernel, dim3(ceil_div(words, 256)), dim3(256), 0,
-                     as_stream(stream), reinterpret_cast<const uint32_t *>(codes),
-                     reinterpret_cast<const uint16_t *>(absmax), words, out, out_dtype);
+  const dim3 grid(static_cast<unsigned>(ceil_div(words, 256)));
+  if (absmax_dtype == MX_DTYPE_F32)
+    hipLaunchKernelGGL(nf4_dequantize_kernel<true>, grid, dim3(256), 0, as_stream(stream),
+                       reinterpret_cast<const uint32_t *>(codes), absmax, words, out, out_dtype);
+  else
+    hipLaunchKernelGGL(nf4_dequantize_kernel<false>, grid, dim3(256), 0, as_stream(stream),
+                       reinterpret_cast<const uint32_t *>(codes), absmax, words, out, out_dtype);
   return check_launch("mx_nf4_dequantize");
+}
+
+extern "C" int mx_nf4_dequantize(const uint8_t *codes, const void *absmax, int64_t rows,
+                                 int64_t cols, void *out, int out_dtype, void *stream) {
+  return mx_nf4_dequantize_ex(codes, absmax, MX_DTYPE_BF16, rows, cols, out, out_dtype, stream);
+}
+
+extern "C" int mx_nf4_from_bnb(const uint8_t *packed, const uint8_t *absmax_q,
+                               const float *nested_absmax, const float *offsets,
+                               const float *nested_code, int64_t experts, int64_t rows,
+                               int64_t cols, uint8_t *codes, float *absmax, void *stream) {
+  clear_error();
+  if (!packed || !absmax_q || !nested_absmax || !offsets || !nested_code || !codes || !absmax) {
+    set_error("mx_nf4_from_bnb: buffers must be non-null");
+    return MX_ERR_INVALID;
+  }
+  if (experts < 0 || rows < 0 || cols <= 0 || cols % 64 != 0) {
+    set_error("mx_nf4_from_bnb: need experts, rows >= 0 and cols a positive multiple of 64");
+    return MX_ERR_INVALID;
+  }
+  if (reinterpret_cast<uintptr_t>(packed) % 4 != 0 || reinterpret_cast<uintptr_t>(codes) % 4 != 0) {
+    set_error("mx_nf4_from_bnb: packed and codes must be 4-byte aligned");
+    return MX_ERR_INVALID;
+  }
+  const int64_t groups_per_expert = rows * cols / 8;
+  const int64_t total = experts * groups_per_expert;
+  if (total == 0) return MX_OK;
+  const int64_t nested_per_expert = ceil_div(rows * cols / 64, 256);
+  hipLaunchKernelGGL(nf4_from_bnb_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))),
+                     dim3(256), 0, as_stream(stream), reinterpret_cast<const uint32_t *>(packed),
+                     absmax_q, nested_absmax, offsets, nested_code, groups_per_expert,
+                     nested_per_expert, total, reinterpret_cast<uint32_t *>(codes), absmax);
+  return check_launch("mx_nf4_from_bnb");
 }
 
 extern "C" int mx_int8_quantize(const void *w, int w_dtype, int64_t rows, int64_t cols,

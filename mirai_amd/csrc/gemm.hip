@@ -35,6 +35,21 @@ constexpr int kLoraLd = 96;     // low-rank activation row: [gate 32 | up 32 | d
 
 enum { EPI_SWIGLU = 0, EPI_STORE = 1, EPI_LORA_A = 2, EPI_STORE2 = 4 };
 
+// NF4 codes with a bf16 absmax (the build's own quantiser) or an fp32 absmax
+// (bitsandbytes payloads, whose double-quantised absmax decodes to fp32).
+constexpr bool is_nf4(int fmt) { return fmt == MX_FMT_NF4 || fmt == MX_FMT_NF4_F32; }
+
+// Block absmax i of a row as raw bits (a bf16 in the low half, or fp32 bits).
+template <int FMT>
+__device__ __forceinline__ uint32_t load_absmax(const void *row, int64_t i) {
+  if (FMT == MX_FMT_NF4_F32) return static_cast<const uint32_t *>(row)[i];
+  return static_cast<const uint16_t *>(row)[i];
+}
+template <int FMT>
+__device__ __forceinline__ float absmax_value(uint32_t raw) {
+  return FMT == MX_FMT_NF4_F32 ? __uint_as_float(raw) : bf16_bits_to_f32(raw);
+}
+
 // Backward epilogues multiply by W itself rather than W^T.
 constexpr bool trans_b(int epi) { return epi == EPI_STORE2; }
 
@@ -69,7 +84,7 @@ struct Params {
   const int32_t *row_token;  // sorted row -> activation row (null: identity)
   int64_t K;
   const void *w[4];          // per B-row group: weight data
-  const uint16_t *wscale[4]; // NF4 absmax / INT8 scale
+  const void *wscale[4];     // NF4 absmax (bf16 or fp32) / INT8 scale (bf16)
   int64_t wn[4];             // rows per expert of each weight
   int64_t k_split;           // transposed B: K rows taken from w[0], the rest from w[1]
   int64_t N;                 // output columns
@@ -289,26 +304,27 @@ void grouped_gemm_kernel(Params p) {
   if (EPI != EPI_LORA_A) bn = min(bn, wn_rows - 1);
   const int64_t wrow = static_cast<int64_t>(e) * wn_rows + bn;
   const uint8_t *b_base = nullptr;
-  const uint16_t *b_absmax = nullptr;
+  const void *b_absmax = nullptr;  // the row's absmax entries
   float b_scale = 0.0f;
   if (b_valid) {
     const uint8_t *w = static_cast<const uint8_t *>(pick(p.w, which));
-    if (FMT == MX_FMT_NF4) {
+    if (is_nf4(FMT)) {
       b_base = w + wrow * (p.K / 2) + bh * (T::B_ELEMS / 2);
-      b_absmax = pick(p.wscale, which) + wrow * (p.K / kNf4Block);
+      b_absmax = static_cast<const uint8_t *>(pick(p.wscale, which)) +
+                 wrow * (p.K / kNf4Block) * (FMT == MX_FMT_NF4_F32 ? 4 : 2);
     } else if (FMT == MX_FMT_INT8) {
       b_base = w + wrow * p.K + bh * T::B_ELEMS;
-      b_scale = bf16_bits_to_f32(pick(p.wscale, which)[wrow]);
+      b_scale = bf16_bits_to_f32(static_cast<const uint16_t *>(pick(p.wscale, which))[wrow]);
     } else {
       b_base = w + wrow * p.K * 2 + bh * T::B_ELEMS * 2;
     }
   }
 
   // Bytes of B per thread per stage, in 16-byte registers.
-  constexpr int kBBytes = FMT == MX_FMT_NF4 ? T::B_ELEMS / 2
+  constexpr int kBBytes = is_nf4(FMT) ? T::B_ELEMS / 2
                                             : (FMT == MX_FMT_INT8 ? T::B_ELEMS : T::B_ELEMS * 2);
   constexpr int kBRegs = kBBytes / 16;
-  constexpr int kBStageBytes = FMT == MX_FMT_NF4 ? BK / 2 : (FMT == MX_FMT_INT8 ? BK : BK * 2);
+  constexpr int kBStageBytes = is_nf4(FMT) ? BK / 2 : (FMT == MX_FMT_INT8 ? BK : BK * 2);
   // B packed data: two register sets (stage kt+1 is decoded while kt+2 loads).
   struct BRegs {
     u32x4 q[kBRegs];
@@ -333,16 +349,16 @@ void grouped_gemm_kernel(Params p) {
       const bool second = kb >= p.k_split;
       const int64_t krow = kb - (second ? p.k_split : 0) + tk;
       const uint8_t *w = static_cast<const uint8_t *>(second ? p.w[1] : p.w[0]);
-      const uint16_t *ws = second ? p.wscale[1] : p.wscale[0];
+      const void *ws = second ? p.wscale[1] : p.wscale[0];
       const int64_t wrow = static_cast<int64_t>(e) * (second ? p.wn[1] : p.wn[0]) + krow;
-      if (FMT == MX_FMT_NF4) {
+      if (is_nf4(FMT)) {
         rb.q[0] = *reinterpret_cast<const u32x4 *>(w + wrow * (p.N / 2) + t_col0 / 2);
-        rb.abs = ws[wrow * (p.N / kNf4Block) + t_col0 / kNf4Block];
+        rb.abs = load_absmax<FMT>(ws, wrow * (p.N / kNf4Block) + t_col0 / kNf4Block);
       } else if (FMT == MX_FMT_INT8) {
 #pragma unroll
         for (int q = 0; q < kBRegs; ++q)
           rb.q[q] = *reinterpret_cast<const u32x4 *>(w + wrow * p.N + t_col0 + 16 * q);
-        rb.abs = ws[wrow];
+        rb.abs = static_cast<const uint16_t *>(ws)[wrow];
       } else {
 #pragma unroll
         for (int q = 0; q < kBRegs; ++q)
@@ -353,7 +369,7 @@ void grouped_gemm_kernel(Params p) {
 #pragma unroll
       for (int q = 0; q < kBRegs; ++q)
         rb.q[q] = *reinterpret_cast<const u32x4 *>(b_base + static_cast<int64_t>(kt) * kBStageBytes + 16 * q);
-      rb.abs = FMT == MX_FMT_NF4 ? b_absmax[kt * BK / kNf4Block] : 0u;
+      rb.abs = is_nf4(FMT) ? load_absmax<FMT>(b_absmax, kt * BK / kNf4Block) : 0u;
     } else {
 #pragma unroll
       for (int q = 0; q < kBRegs; ++q) rb.q[q] = u32x4{0u, 0u, 0u, 0u};
@@ -371,7 +387,7 @@ void grouped_gemm_kernel(Params p) {
       const int c = part * kChunksPerPart + cc;  // output chunk: 8 elements
       uint32_t d[4];
       const float sc = TRANS ? bf16_bits_to_f32(rb.abs) : b_scale;
-      if (FMT == MX_FMT_NF4) {
+      if (is_nf4(FMT)) {
         // chunk c = code bytes 4c..4c+3 = dword c of the packed registers
         const u32x4 v = rb.q[c >> 2];
         const uint32_t word = (c & 3) == 0 ? v[0] : (c & 3) == 1 ? v[1] : (c & 3) == 2 ? v[2] : v[3];
@@ -513,7 +529,7 @@ void grouped_gemm_kernel(Params p) {
     else
       load_a(min(kt + 1, KT - 1), nA);
     load_b(min(kt + 2, KT - 1), b_after);
-    const Nf4Table t = FMT == MX_FMT_NF4 ? nf4_table(bf16_bits_to_f32(b_next.abs)) : Nf4Table{};
+    const Nf4Table t = is_nf4(FMT) ? nf4_table(absmax_value<FMT>(b_next.abs)) : Nf4Table{};
 #pragma unroll
     for (int kk = 0; kk < T::KSUB; ++kk) {
       Frags &cur = (kk & 1) ? f1 : f0;
@@ -530,7 +546,7 @@ void grouped_gemm_kernel(Params p) {
   load_b(0, rb0);
   load_b(min(1, KT - 1), rb1);
   {
-    const Nf4Table t = FMT == MX_FMT_NF4 ? nf4_table(bf16_bits_to_f32(rb0.abs)) : Nf4Table{};
+    const Nf4Table t = is_nf4(FMT) ? nf4_table(absmax_value<FMT>(rb0.abs)) : Nf4Table{};
 #pragma unroll
     for (int part = 0; part < T::KSUB; ++part) decode_b(rb0, t, sB0, part);
   }
@@ -832,6 +848,9 @@ int launch_fmt(int fmt, Params p, const PlanLayout &PL, const PlanView &v, bool 
     case MX_FMT_NF4:
       return tall ? launch<MX_FMT_NF4, EPI, LORA, Tall>(p, max_tiles, s)
                   : launch<MX_FMT_NF4, EPI, LORA, Short>(p, max_tiles, s);
+    case MX_FMT_NF4_F32:
+      return tall ? launch<MX_FMT_NF4_F32, EPI, LORA, Tall>(p, max_tiles, s)
+                  : launch<MX_FMT_NF4_F32, EPI, LORA, Short>(p, max_tiles, s);
     case MX_FMT_INT8:
       return tall ? launch<MX_FMT_INT8, EPI, LORA, Tall>(p, max_tiles, s)
                   : launch<MX_FMT_INT8, EPI, LORA, Short>(p, max_tiles, s);
@@ -910,11 +929,12 @@ int check_weight(const char *name, const char *key, const mx_weight *w, int64_t 
     return MX_ERR_INVALID;
   }
   if (w->format != MX_FMT_BF16 && w->format != MX_FMT_NF4 && w->format != MX_FMT_INT8 &&
-      w->format != MX_FMT_F32X3) {
+      w->format != MX_FMT_F32X3 && w->format != MX_FMT_NF4_F32) {
     set_error("%s: weight %s has unknown format %d", name, key, w->format);
     return MX_ERR_INVALID;
   }
-  if ((w->format == MX_FMT_NF4 || w->format == MX_FMT_INT8) && !w->scale) {
+  if ((w->format == MX_FMT_NF4 || w->format == MX_FMT_NF4_F32 || w->format == MX_FMT_INT8) &&
+      !w->scale) {
     set_error("%s: weight %s needs its scale / absmax buffer", name, key);
     return MX_ERR_INVALID;
   }
@@ -1000,8 +1020,8 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
     p.K = kx * hidden;
     p.w[0] = w1->data;
     p.w[1] = w3->data;
-    p.wscale[0] = static_cast<const uint16_t *>(w1->scale);
-    p.wscale[1] = static_cast<const uint16_t *>(w3->scale);
+    p.wscale[0] = w1->scale;
+    p.wscale[1] = w3->scale;
     p.wn[0] = p.wn[1] = ffn;
     p.N = ffn;
     p.lora_p = lora_buf;
@@ -1033,7 +1053,7 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
   p.row_token = nullptr;
   p.K = kx * ffn;
   p.w[0] = w2->data;
-  p.wscale[0] = static_cast<const uint16_t *>(w2->scale);
+  p.wscale[0] = w2->scale;
   p.wn[0] = hidden;
   p.N = hidden;
   p.lora_p = lora_buf + 64;
@@ -1227,7 +1247,7 @@ extern "C" int mx_moe_backward_act(const void *grad_out, int grad_dtype, const v
     p.row_token = v.row_slot;
     p.K = hidden;
     p.w[0] = w2->data;
-    p.wscale[0] = static_cast<const uint16_t *>(w2->scale);
+    p.wscale[0] = w2->scale;
     p.wn[0] = hidden;
     p.k_split = hidden;
     p.N = ffn;
@@ -1277,8 +1297,8 @@ extern "C" int mx_moe_backward_act(const void *grad_out, int grad_dtype, const v
     p.K = 2 * ffn;
     p.w[0] = w1->data;
     p.w[1] = w3->data;
-    p.wscale[0] = static_cast<const uint16_t *>(w1->scale);
-    p.wscale[1] = static_cast<const uint16_t *>(w3->scale);
+    p.wscale[0] = w1->scale;
+    p.wscale[1] = w3->scale;
     p.wn[0] = p.wn[1] = ffn;
     p.k_split = ffn;
     p.N = hidden;
@@ -1511,7 +1531,7 @@ extern "C" int mx_grouped_linear(const void *x, const int64_t *counts, int64_t n
   p.ldx = in_f;
   p.K = in_f;
   p.w[0] = w->data;
-  p.wscale[0] = static_cast<const uint16_t *>(w->scale);
+  p.wscale[0] = w->scale;
   p.wn[0] = out_f;
   p.N = out_f;
   p.lora_p = lora_buf;

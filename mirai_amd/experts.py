@@ -177,6 +177,45 @@ class CompressedGroupedExperts(nn.Module):
         self._shapes[key] = packed.shape
         self._loaded_dense_keys.add(key)
 
+    def load_packed_nf4(self, key: str, *, packed: torch.Tensor, absmax: torch.Tensor,
+                        nested_absmax: torch.Tensor, offset: torch.Tensor, code: torch.Tensor,
+                        nested_code: torch.Tensor, shape: tuple[int, int, int]) -> None:
+        """Adopt a bitsandbytes double-quantised NF4 stack as the reference stores it
+        (the {key}_nf4* buffers of _store_nf4_grouped, experts.py:998-1031) without
+        re-quantising: the GEMMs decode the payload's weights (fp32 absmax)."""
+        if self._quant_format != "nf4":
+            raise ValueError("packed NF4 payloads load into a module with quant_format='nf4'.")
+        if key not in self.expert_mlp_spec.tensor_names:
+            raise ValueError(f"Unknown compressed_weights grouped expert tensor '{key}'.")
+        if int(shape[0]) != self.num_experts:
+            raise ValueError(
+                f"compressed_weights grouped expert tensor {key} has {int(shape[0])} experts, "
+                f"expected {self.num_experts}.")
+        packed_w = quant.from_bnb_nf4(packed=packed, absmax=absmax, nested_absmax=nested_absmax,
+                                      offset=offset, code=code, nested_code=nested_code,
+                                      shape=tuple(int(v) for v in shape))
+        data_suffix, scale_suffix = _BUFFER_SUFFIXES["nf4"]
+        self._set_buffer(f"{key}{data_suffix}", packed_w.data)
+        self._set_buffer(f"{key}{scale_suffix}", packed_w.scale)
+        self._shapes[key] = packed_w.shape
+        self._loaded_dense_keys.add(key)
+
+    def load_bnb_state_dict(self, state: dict, shapes: dict, *, prefix: str = "") -> None:
+        """Load every expert tensor of ``shapes`` ({key: (E, out, in)}) from a
+        reference state dict holding its {key}_nf4, _nf4_absmax, _nf4_nabsmax,
+        _nf4_offset, _nf4_code and _nf4_ncode buffers."""
+        for key, shape in shapes.items():
+            base = f"{prefix}{key}_nf4"
+            missing = [n for n in ("", "_absmax", "_nabsmax", "_offset", "_code", "_ncode")
+                       if base + n not in state]
+            if missing:
+                raise RuntimeError(f"packed NF4 state for '{key}' lacks "
+                                   + ", ".join(base + n for n in missing) + ".")
+            self.load_packed_nf4(key, packed=state[base], absmax=state[base + "_absmax"],
+                                 nested_absmax=state[base + "_nabsmax"],
+                                 offset=state[base + "_offset"], code=state[base + "_code"],
+                                 nested_code=state[base + "_ncode"], shape=shape)
+
     def packed_weight(self, key: str) -> quant.PackedWeight:
         if key not in self._loaded_dense_keys:
             raise RuntimeError(f"compressed_weights grouped experts are missing weight '{key}'.")

@@ -3,6 +3,9 @@
 * ``nf4``  : codes uint8 [E, out, in/2] (per group of 8 elements, byte i holds
   element i in the low nibble and element i + 4 in the high nibble) and
              bf16 absmax [E, out, in/64]; blocksize 64, no double quantisation.
+             A bitsandbytes double-quantised payload ingested with
+             ``from_bnb_nf4`` keeps the same codes with an fp32 absmax
+             (kernel format MX_FMT_NF4_F32).
 * ``int8`` : int8 [E, out, in] and bf16 per-output-row scale [E, out].
 * ``bf16`` : unquantised bf16 [E, out, in].
 * ``fp32`` : unquantised fp32 as bf16 planes [E, out, 3*in] = [hi | lo | hi]
@@ -49,10 +52,15 @@ class PackedWeight:
     scale: torch.Tensor | None
     shape: tuple[int, int, int]
 
+    def format_code(self) -> int:
+        if self.fmt == "nf4" and self.scale is not None and self.scale.dtype == torch.float32:
+            return nat.FMT_NF4_F32
+        return _FORMAT_CODES[self.fmt]
+
     def descriptor(self) -> nat.MxWeight:
         _, out_f, in_f = self.shape
         return nat.MxWeight(
-            _FORMAT_CODES[self.fmt],
+            self.format_code(),
             self.data.data_ptr(),
             self.scale.data_ptr() if self.scale is not None else None,
             out_f,
@@ -120,12 +128,67 @@ def dequantize(packed: PackedWeight, *, dtype: torch.dtype = torch.bfloat16,
     scale = packed.scale[sel].contiguous()
     data = data.contiguous()
     if packed.fmt == "nf4":
-        nat.call("mx_nf4_dequantize", data.data_ptr(), scale.data_ptr(), rows, in_f,
-                 out.data_ptr(), nat.dtype_code(dtype), s)
+        nat.call("mx_nf4_dequantize_ex", data.data_ptr(), scale.data_ptr(),
+                 nat.dtype_code(scale.dtype), rows, in_f, out.data_ptr(), nat.dtype_code(dtype), s)
     else:
         nat.call("mx_int8_dequantize", data.data_ptr(), scale.data_ptr(), rows, in_f,
                  out.data_ptr(), nat.dtype_code(dtype), s)
     return out
+
+
+def from_bnb_nf4(*, packed: torch.Tensor, absmax: torch.Tensor, nested_absmax: torch.Tensor,
+                 offset: torch.Tensor, code: torch.Tensor, nested_code: torch.Tensor,
+                 shape: tuple[int, int, int], blocksize: int = NF4_BLOCKSIZE,
+                 nested_blocksize: int = 256) -> PackedWeight:
+    """Ingest a bitsandbytes double-quantised NF4 expert stack without
+    re-quantising (mx_nf4_from_bnb).
+
+    The arguments are the reference's per-key buffers
+    (CompressedGroupedExperts._store_nf4_grouped, experts.py:998-1031):
+    ``{key}_nf4`` packed codes [E, out*in/2(, 1)] uint8, ``{key}_nf4_absmax``
+    quantised absmax [E, out*in/64] uint8, ``{key}_nf4_nabsmax`` [E, n2] fp32,
+    ``{key}_nf4_offset`` [E] fp32, ``{key}_nf4_code`` (the 16 NF4 levels) and
+    ``{key}_nf4_ncode`` (256 fp32). Returns the codes in this library's layout
+    with the decoded fp32 absmax.
+    """
+    E, out_f, in_f = (int(v) for v in shape)
+    if int(blocksize) != NF4_BLOCKSIZE or int(nested_blocksize) != 256:
+        raise ValueError("bitsandbytes NF4 payloads are ingested with blocksize 64 and "
+                         "nested blocksize 256.")
+    if in_f % NF4_BLOCKSIZE:
+        raise ValueError(f"in_features must be a multiple of 64, got {in_f}.")
+    device = packed.device
+    nat.require_gpu(packed)
+    levels = code.detach().to(device="cpu", dtype=torch.float32).reshape(-1)
+    if levels.numel() != 16 or not torch.equal(levels, nf4_levels()):
+        raise ValueError("the payload's 4-bit code table is not the NF4 table (quant_type='nf4').")
+    n = out_f * in_f
+    n2 = -(-(n // NF4_BLOCKSIZE) // 256)
+    want = {"packed": (packed, E * n // 2, torch.uint8), "absmax": (absmax, E * n // 64, torch.uint8),
+            "nested_absmax": (nested_absmax, E * n2, torch.float32),
+            "offset": (offset, E, torch.float32), "nested_code": (nested_code, 256, torch.float32)}
+    flat = {}
+    for name, (t, numel, dtype) in want.items():
+        if int(t.numel()) != numel or t.dtype != dtype:
+            raise ValueError(f"bitsandbytes field {name} must hold {numel} {dtype} values, got "
+                             f"{int(t.numel())} {t.dtype}.")
+        flat[name] = t.detach().to(device).reshape(-1).contiguous()
+    codes = torch.empty((E, out_f, in_f // 2), dtype=torch.uint8, device=device)
+    amax = torch.empty((E, out_f, in_f // NF4_BLOCKSIZE), dtype=torch.float32, device=device)
+    nat.call("mx_nf4_from_bnb", flat["packed"].data_ptr(), flat["absmax"].data_ptr(),
+             flat["nested_absmax"].data_ptr(), flat["offset"].data_ptr(),
+             flat["nested_code"].data_ptr(), E, out_f, in_f, codes.data_ptr(), amax.data_ptr(),
+             nat.stream(device))
+    return PackedWeight("nf4", codes, amax, (E, out_f, in_f))
+
+
+def nf4_levels() -> torch.Tensor:
+    """The 16 NF4 levels as fp32 (mirai/core/models/quantization.py:100-117)."""
+    return torch.tensor([
+        -1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+        -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0.0,
+        0.07958029955625534, 0.16093020141124725, 0.24611230194568634, 0.33791524171829224,
+        0.44070982933044434, 0.5626170039176941, 0.7229568362236023, 1.0], dtype=torch.float32)
 
 
 def split_planes(x: torch.Tensor, pattern: int) -> torch.Tensor:

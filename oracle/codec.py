@@ -151,3 +151,64 @@ def int8_dequantize(q: np.ndarray, scale_bits: np.ndarray) -> np.ndarray:
     """Dequantised bf16 bits: bf16(fp32(q) * fp32(scale)) (the product is exact)."""
     s = bf16_bits_to_f32(scale_bits)[:, None]
     return f32_to_bf16_bits((np.asarray(q, dtype=np.float32) * s).astype(np.float32))
+
+
+# --------------------------------------------------------------------------
+# bitsandbytes double-quantised NF4 (the reference's NF4 storage, quant.py:
+# 315-358 / 407-431, through bitsandbytes==0.49.2, which is not installed
+# here: parity with bitsandbytes itself is unpinned). Restated from its
+# published format: per 64-element block an absmax, stored as a uint8 code
+# of a 256-entry table with an fp32 absmax per 256 blocks and a per-tensor
+# fp32 offset; 4-bit codes packed two per byte with element 2j in the HIGH
+# nibble of byte j.
+
+def bnb_nf4_absmax(absmax_q: np.ndarray, nested_absmax: np.ndarray, offset, nested_code):
+    """Decoded fp32 block absmax: fp32(fp32(code2[q] * nested[b // 256]) + offset)."""
+    q = np.asarray(absmax_q, dtype=np.uint8).reshape(-1)
+    nested = np.asarray(nested_absmax, dtype=np.float32).reshape(-1)
+    code2 = np.asarray(nested_code, dtype=np.float32).reshape(-1)
+    scaled = (code2[q] * nested[np.arange(q.size) // 256]).astype(np.float32)
+    return (scaled + np.float32(offset)).astype(np.float32)
+
+
+def bnb_nf4_unpack(packed: np.ndarray) -> np.ndarray:
+    """uint8 [n/2] -> codes [n], element 2j in the high nibble of byte j."""
+    p = np.asarray(packed, dtype=np.uint8).reshape(-1)
+    out = np.empty(p.size * 2, dtype=np.uint8)
+    out[0::2] = p >> 4
+    out[1::2] = p & 0x0F
+    return out
+
+
+def bnb_nf4_dequantize(packed, absmax_q, nested_absmax, offset, nested_code, rows, cols):
+    """One expert's weights as bf16 bits [rows, cols]: bf16(fp32(NF4[c] * absmax))."""
+    codes = bnb_nf4_unpack(packed).reshape(-1, NF4_BLOCKSIZE)
+    a = bnb_nf4_absmax(absmax_q, nested_absmax, offset, nested_code)
+    prod = (NF4_LEVELS[codes] * a[:, None]).astype(np.float32)
+    return f32_to_bf16_bits(prod.reshape(rows, cols))
+
+
+def bnb_nf4_quantize(w, nested_code) -> dict:
+    """A double-quantised payload of one expert [rows, cols] for fixtures:
+    fp32 absmax per 64 block, nearest NF4 level (first index on ties), offset =
+    mean absmax, nested absmax per 256 blocks, nearest code of the table."""
+    values = _as_bf16_values(w).astype(np.float32)
+    rows, cols = values.shape
+    blocks = values.reshape(-1, NF4_BLOCKSIZE)
+    absmax = np.abs(blocks).max(axis=1).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        scaled = np.where(absmax[:, None] > 0, blocks / absmax[:, None], 0.0).astype(np.float32)
+    codes = np.abs(scaled[..., None] - NF4_LEVELS).argmin(axis=-1).astype(np.uint8).reshape(-1)
+    packed = ((codes[0::2] << 4) | codes[1::2]).astype(np.uint8)
+    offset = np.float32(absmax.mean(dtype=np.float64))
+    centered = (absmax - offset).astype(np.float32)
+    n2 = -(-centered.size // 256)
+    pad = np.zeros(n2 * 256, dtype=np.float32)
+    pad[:centered.size] = centered
+    nested = np.abs(pad.reshape(n2, 256)).max(axis=1).astype(np.float32)
+    nested = np.where(nested > 0, nested, np.float32(1.0)).astype(np.float32)
+    norm = (centered / nested[np.arange(centered.size) // 256]).astype(np.float32)
+    code2 = np.asarray(nested_code, dtype=np.float32)
+    absmax_q = np.abs(norm[:, None] - code2[None, :]).argmin(axis=1).astype(np.uint8)
+    return {"packed": packed, "absmax": absmax_q, "nested_absmax": nested, "offset": offset,
+            "code": NF4_LEVELS.copy(), "nested_code": code2}

@@ -4,6 +4,7 @@ import numpy as np
 import pytest
 import torch
 
+from mirai_amd import _native as nat
 from mirai_amd import quant
 from oracle import codec
 
@@ -73,3 +74,81 @@ def test_nf4_full_expert_stack_round_trip_bound():
     half_gap = float(np.max(np.diff(codec.NF4_LEVELS.astype(np.float64))) / 2)
     # bf16 rounding of the product adds at most 2^-9 relative to |w| <= absmax.
     assert bool((err <= amax * (half_gap + 2.0**-8) + 1e-12).all())
+
+
+def _bnb_payload(E, rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    table = np.sort(np.concatenate([np.linspace(-1, 1, 255), [0.0]])).astype(np.float32)
+    w = (rng.standard_normal((E, rows, cols)) * 0.02).astype(np.float32)
+    parts = [codec.bnb_nf4_quantize(w[e], table) for e in range(E)]
+    stacked = {
+        "packed": np.stack([p["packed"] for p in parts]),
+        "absmax": np.stack([p["absmax"] for p in parts]),
+        "nested_absmax": np.stack([p["nested_absmax"] for p in parts]),
+        "offset": np.array([p["offset"] for p in parts], dtype=np.float32),
+        "code": parts[0]["code"],
+        "nested_code": table,
+    }
+    return stacked, parts, table
+
+
+def test_bnb_nf4_ingest_is_bit_exact():
+    # 96 x 384 per expert = 576 absmax blocks: the last nested block is partial.
+    E, rows, cols = 3, 96, 384
+    stacked, parts, table = _bnb_payload(E, rows, cols, 21)
+    t = {k: torch.from_numpy(np.asarray(v)).cuda() for k, v in stacked.items()}
+    pw = quant.from_bnb_nf4(packed=t["packed"], absmax=t["absmax"],
+                            nested_absmax=t["nested_absmax"], offset=t["offset"], code=t["code"],
+                            nested_code=t["nested_code"], shape=(E, rows, cols))
+    assert pw.format_code() == nat.FMT_NF4_F32
+    for e, p in enumerate(parts):
+        want_codes = codec.nf4_pack(codec.bnb_nf4_unpack(p["packed"]).reshape(rows, cols))
+        np.testing.assert_array_equal(pw.data[e].cpu().numpy(), want_codes)
+        want_abs = codec.bnb_nf4_absmax(p["absmax"], p["nested_absmax"], p["offset"], table)
+        np.testing.assert_array_equal(pw.scale[e].cpu().numpy().reshape(-1), want_abs)
+    deq = quant.dequantize(pw).view(torch.int16).cpu().numpy().view(np.uint16)
+    for e, p in enumerate(parts):
+        want = codec.bnb_nf4_dequantize(p["packed"], p["absmax"], p["nested_absmax"], p["offset"],
+                                        table, rows, cols)
+        np.testing.assert_array_equal(deq[e], want)
+
+
+def test_bnb_nf4_ingest_rejects_a_non_nf4_code_table():
+    stacked, _, _ = _bnb_payload(1, 64, 64, 3)
+    t = {k: torch.from_numpy(np.asarray(v)).cuda() for k, v in stacked.items()}
+    with pytest.raises(ValueError, match="NF4 table"):
+        quant.from_bnb_nf4(packed=t["packed"], absmax=t["absmax"],
+                           nested_absmax=t["nested_absmax"], offset=t["offset"],
+                           code=torch.linspace(-1, 1, 16).cuda(), nested_code=t["nested_code"],
+                           shape=(1, 64, 64))
+
+
+def test_layer_runs_on_ingested_bnb_nf4_weights():
+    from mirai_amd import CompressedGroupedExperts, route_topk
+    from oracle import layer as olayer
+    from helpers import assert_layer_close
+
+    E, d, f, T, k = 8, 256, 192, 200, 2
+    shapes = {"w1": (E, f, d), "w3": (E, f, d), "w2": (E, d, f)}
+    state, dense = {}, {}
+    for i, (key, (e_, o, n)) in enumerate(shapes.items()):
+        stacked, parts, table = _bnb_payload(e_, o, n, 40 + i)
+        for name, suffix in (("packed", ""), ("absmax", "_absmax"), ("nested_absmax", "_nabsmax"),
+                             ("offset", "_offset"), ("code", "_code"),
+                             ("nested_code", "_ncode")):
+            state[f"{key}_nf4{suffix}"] = torch.from_numpy(np.asarray(stacked[name])).cuda()
+        bits = np.stack([codec.bnb_nf4_dequantize(p["packed"], p["absmax"], p["nested_absmax"],
+                                                  p["offset"], table, o, n) for p in parts])
+        dense[key] = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+    m = CompressedGroupedExperts.from_empty(num_experts=E, quant_format="nf4",
+                                            expert_weight_access="fused_kernel",
+                                            expert_dequant_chunk_size=8)
+    m.load_bnb_state_dict(state, shapes)
+    assert m.is_fully_loaded()
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(T, d, generator=g).to(torch.bfloat16)
+    idx, scores = route_topk(torch.randn(T, E, generator=g).cuda(), k)
+    with torch.no_grad():
+        out = m.run_direct_routed(x.cuda(), scores, idx)
+    ref = olayer.layer_forward(x, scores.cpu(), idx.cpu(), dense, {}, E)
+    print(f"ingested bnb nf4 layer: {assert_layer_close(out.cpu(), ref)}")

@@ -191,3 +191,46 @@ def test_planted_mistakes_are_caught(mistake):
         pairwise[:, 0::2], pairwise[:, 1::2] = packed & 0x0F, packed >> 4
         wrong = codec.f32_to_bf16_bits((codec.NF4_LEVELS[pairwise] * a).astype(np.float32))
     assert not np.array_equal(right, wrong)
+
+
+def test_bnb_nf4_dequantize_known_answer_and_nibble_order():
+    # One block of 64: byte 0 = 0xF0 holds element 0 = code 15 (high nibble)
+    # and element 1 = code 0 (low nibble); absmax code 5 with table value 0.5,
+    # nested absmax 0.5 and offset 0.25 gives absmax 0.5 * 0.5 + 0.25 = 0.5.
+    packed = np.full(32, 0x77, dtype=np.uint8)  # codes 7 (level 0.0) elsewhere
+    packed[0] = 0xF0
+    table = np.linspace(-1.0, 1.0, 256).astype(np.float32)
+    table[5] = 0.5
+    out = codec.bnb_nf4_dequantize(packed, np.array([5], np.uint8), np.array([0.5], np.float32),
+                                   np.float32(0.25), table, 1, 64)
+    vals = codec.bf16_bits_to_f32(out)[0]
+    assert vals[0] == 0.5 and vals[1] == -0.5 and np.all(vals[2:] == 0.0)
+    assert list(codec.bnb_nf4_unpack(packed)[:2]) == [15, 0]
+    # A plausible slip (reading the pair low nibble first) swaps the two.
+    low_first = np.empty(64, dtype=np.uint8)
+    low_first[0::2], low_first[1::2] = packed & 0x0F, packed >> 4
+    assert list(low_first[:2]) == [0, 15]
+
+
+def test_bnb_nf4_absmax_rounds_product_then_sum():
+    # fp32(fp32(a * b) + c) differs from one fused rounding for these values.
+    a, b, c = np.float32(1.0000001), np.float32(3.0000002), np.float32(-3.0000005)
+    got = codec.bnb_nf4_absmax(np.array([0], np.uint8), np.array([b], np.float32), c,
+                               np.array([a], np.float32))
+    prod = np.float32(a * b)
+    assert got[0] == np.float32(prod + c)
+    assert got[0] != np.float32(np.float64(a) * np.float64(b) + np.float64(c))
+
+
+def test_bnb_nf4_quantize_round_trip_error_bound():
+    rng = np.random.default_rng(8)
+    w = (rng.standard_normal((6, 4096)) * 0.02).astype(np.float32)
+    table = np.sort(np.concatenate([np.linspace(-1, 1, 255), [0.0]])).astype(np.float32)
+    p = codec.bnb_nf4_quantize(w, table)
+    got = codec.bf16_bits_to_f32(codec.bnb_nf4_dequantize(
+        p["packed"], p["absmax"], p["nested_absmax"], p["offset"], p["nested_code"], 6, 4096))
+    err = np.abs(got - codec.round_bf16(w)).reshape(-1, 64).max(axis=1)
+    amax = np.abs(codec.round_bf16(w)).reshape(-1, 64).max(axis=1)
+    # NF4 half-gap (0.16) plus the absmax code error (table step 1/127 of the
+    # nested absmax) bounds the per-block error.
+    assert np.all(err <= 0.16 * amax + 0.02 * amax + 1e-3)
