@@ -132,6 +132,42 @@ int mx_route_topk_heads(const float *logits, int num_heads, int64_t num_tokens, 
                         void *top_scores, int score_dtype, void *stream);
 
 /* ------------------------------------------------------------------------ */
+/* Fused router front end (router GEMM + scores + selection)                 */
+/* ------------------------------------------------------------------------ */
+
+/* Experts padded to the router kernel's column tile (32, 64, 128 or 256);
+ * -1 when num_experts is outside [1, 256]. */
+int mx_router_padded_experts(int num_experts);
+/* Bytes of the router weight planes [3][EP][hidden] bf16 (0 on bad sizes). */
+size_t mx_router_planes_size(int num_experts, int64_t hidden);
+/* Split the fp32 router weight W [E, hidden] (LingBotVideoRouter.weight,
+ * transformer_lingbot_video.py:520) into bf16 planes hi, mid, lo with
+ * W == hi + mid + lo exactly, rows E..EP-1 zero. Done once per weight value;
+ * mx_router_forward reads the planes. hidden % 64 == 0. */
+int mx_router_weight_planes(const float *weight, int num_experts, int64_t hidden, void *planes,
+                            void *stream);
+/* Replaces LingBotVideoRouter.forward (transformer_lingbot_video.py:962-1033,
+ * group-limited choice :865-890) without its optional extensions:
+ *   logits = tokens.float() @ W.T (+ logit_delta)      fp32 products, fp32 sums
+ *   scores = softmax(logits) or sigmoid(logits)         (score_func)
+ *   picks  = top_k of scores + expert_bias, optionally within the topk_group
+ *            best of n_group expert groups (group score = sum of its two
+ *            largest biased scores); ties go to the lower expert / group id
+ *   top_scores = scores[picks] / (sum + 1e-20) if top_k > 1 && norm_topk_prob,
+ *                times route_scale, stored as score_dtype
+ * Picks are written in descending order of the selection key. tokens [T, hidden]
+ * bf16 or fp32 (token_dtype); planes from mx_router_weight_planes; expert_bias
+ * [E] fp32 and logit_delta [T, E] fp32 may be NULL; n_group <= 1 disables group
+ * limiting. Optional outputs logits_out / scores_out [T, E] fp32 (may be NULL).
+ * E <= 256, 1 <= top_k <= 16, hidden % 64 == 0. */
+int mx_router_forward(const void *tokens, int token_dtype, int64_t num_tokens, int64_t hidden,
+                      int num_experts, const void *planes, const float *expert_bias,
+                      const float *logit_delta, int top_k, int score_func, int n_group,
+                      int topk_group, int norm_topk_prob, float route_scale, float *logits_out,
+                      float *scores_out, int64_t *top_idx, void *top_scores, int score_dtype,
+                      void *stream);
+
+/* ------------------------------------------------------------------------ */
 /* Dispatch plan (stable counting sort of routes by expert)                  */
 /* ------------------------------------------------------------------------ */
 

@@ -9,6 +9,7 @@ from .dispatch import DispatchPlan, build_dispatch_plan, combine_routed_tokens, 
 from .experts import CompressedGroupedExperts
 from .lora import ActiveExpertLoRA, lora_scale
 from .magi2 import Magi2FusedMoEBackend, Magi2GroupedExperts, route_topk_heads
+from .router import FusedRouter, fused_router_forward, router_weight_planes
 from .routing import route_topk
 from .specs import (
     CANONICAL_PACKED_EXPERT_MLP_SPEC,
@@ -24,6 +25,7 @@ __all__ = [
     "CANONICAL_PACKED_EXPERT_MLP_SPEC",
     "CompressedGroupedExperts",
     "DispatchPlan",
+    "FusedRouter",
     "ExpertMLPExecutionSpec",
     "ExpertProjectionRole",
     "Magi2FusedMoEBackend",
@@ -32,9 +34,11 @@ __all__ = [
     "active_moe_optimization_policy",
     "build_dispatch_plan",
     "combine_routed_tokens",
+    "fused_router_forward",
     "get_active_moe_optimization_policy",
     "lora_scale",
     "permute_routed_tokens",
     "route_topk",
     "route_topk_heads",
+    "router_weight_planes",
 ]

@@ -45,6 +45,7 @@ ROUTE_LAYOUT_HEADS = 0
 ROUTE_LAYOUT_ROWS = 1
 
 PLAN_MAX_EXPERTS = 8192
+ROUTER_MAX_EXPERTS = 256  # mx_router_forward
 
 
 class NativeLibraryError(RuntimeError):
@@ -80,6 +81,13 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         c_int,
         [_P, c_int, c_int64, c_int, c_int, c_int, _P, c_int, c_float, c_float, c_int, _P, _P,
          c_int, _P]),
+    "mx_router_padded_experts": (c_int, [c_int]),
+    "mx_router_planes_size": (c_size_t, [c_int, c_int64]),
+    "mx_router_weight_planes": (c_int, [_P, c_int, c_int64, _P, _P]),
+    "mx_router_forward": (
+        c_int,
+        [_P, c_int, c_int64, c_int64, c_int, _P, _P, _P, c_int, c_int, c_int, c_int, c_int,
+         c_float, _P, _P, _P, _P, c_int, _P]),
     "mx_plan_workspace_size": (c_size_t, [c_int64, c_int, c_int]),
     "mx_build_plan": (
         c_int, [_P, _P, c_int, c_int64, c_int, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P]),

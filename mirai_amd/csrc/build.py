@@ -17,7 +17,7 @@ LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libmirai_moe.so"
 OBJ_DIR = CSRC / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ("api.hip", "codec.hip", "route.hip", "plan.hip", "rows.hip", "grads.hip", "gemm.hip")
+SOURCES = ("api.hip", "codec.hip", "route.hip", "router.hip", "plan.hip", "rows.hip", "grads.hip", "gemm.hip")
 
 COMMON_FLAGS = [
     "--offload-arch=gfx950",
