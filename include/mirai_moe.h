@@ -413,6 +413,25 @@ int mx_moe_forward_act(const void *tokens, const int64_t *top_idx, const void *t
                        void *save_lora, void *workspace, void *stream);
 
 /*
+ * mx_moe_forward_act with the block's shared-expert sum fused into the
+ * combine: with addend [T, hidden] (out's dtype) the output is
+ * out_dtype(out_dtype(routed sum) + addend), the `out + shared_output` of
+ * LingBotVideoSparseMoeBlock (transformer_lingbot_video.py:2374-2377, shared
+ * expert LingBotVideoMLP :491-499). addend_ready (a hipEvent_t, may be NULL)
+ * is waited on by `stream` right before the combine, so a producer of the
+ * addend on another stream overlaps the whole routed path. addend NULL gives
+ * mx_moe_forward_act. Not with MX_FMT_F32X3 weights.
+ */
+int mx_moe_forward_ex(const void *tokens, const int64_t *top_idx, const void *top_scores,
+                      int score_dtype, int64_t num_tokens, int top_k, int num_experts,
+                      int64_t hidden, int64_t ffn, int act, const mx_weight *w1,
+                      const mx_weight *w3, const mx_weight *w2, const mx_lora *l1,
+                      const mx_lora *l3, const mx_lora *l2, void *out, int out_dtype,
+                      const void *addend, void *addend_ready, void *save_gate, void *save_up,
+                      void *save_h, void *save_y, void *save_lora, void *workspace,
+                      void *stream);
+
+/*
  * Expert MLP over rows already sorted by expert (no gate weighting):
  * out[i] = (silu(x w1^T + dA1) * (x w3^T + dA3)) w2^T + dA2 for the expert that
  * owns row i. Replaces CompressedGroupedExperts.run_for_loop

@@ -117,6 +117,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         c_int,
         [_P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, c_int64, c_int, _W, _W, _W, _L, _L,
          _L, _P, c_int, _P, _P, _P, _P, _P, _P, _P]),
+    "mx_moe_forward_ex": (
+        c_int,
+        [_P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, c_int64, c_int, _W, _W, _W, _L, _L,
+         _L, _P, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "mx_moe_for_loop": (
         c_int, [_P, _P, c_int64, c_int, c_int64, c_int64, _W, _W, _W, _L, _L, _L, _P, _P, _P]),
     "mx_grouped_linear": (c_int, [_P, _P, c_int64, c_int, _W, _L, _P, _P, _P]),

@@ -1360,14 +1360,15 @@ extern "C" size_t mx_moe_f32x3_workspace_size(int64_t num_tokens, int top_k, int
   return layer_layout(num_tokens * top_k, num_experts, hidden, ffn, true, num_tokens).bytes;
 }
 
-extern "C" int mx_moe_forward_act(const void *tokens, const int64_t *top_idx,
-                                  const void *top_scores, int score_dtype, int64_t num_tokens,
-                                  int top_k, int num_experts, int64_t hidden, int64_t ffn,
-                                  int act, const mx_weight *w1, const mx_weight *w3,
-                                  const mx_weight *w2, const mx_lora *l1, const mx_lora *l3,
-                                  const mx_lora *l2, void *out, int out_dtype, void *save_gate,
-                                  void *save_up, void *save_h, void *save_y, void *save_lora,
-                                  void *workspace, void *stream) {
+extern "C" int mx_moe_forward_ex(const void *tokens, const int64_t *top_idx,
+                                 const void *top_scores, int score_dtype, int64_t num_tokens,
+                                 int top_k, int num_experts, int64_t hidden, int64_t ffn, int act,
+                                 const mx_weight *w1, const mx_weight *w3, const mx_weight *w2,
+                                 const mx_lora *l1, const mx_lora *l3, const mx_lora *l2,
+                                 void *out, int out_dtype, const void *addend,
+                                 void *addend_ready, void *save_gate, void *save_up,
+                                 void *save_h, void *save_y, void *save_lora, void *workspace,
+                                 void *stream) {
   clear_error();
   const char *name = "mx_moe_forward";
   int rc = validate_plan_args(name, num_tokens, top_k, num_experts);
@@ -1388,6 +1389,14 @@ extern "C" int mx_moe_forward_act(const void *tokens, const int64_t *top_idx,
   if (split && (save_gate || save_up || save_h || save_y || save_lora)) {
     set_error("%s: the fp32 (MX_FMT_F32X3) layer is inference-only and saves no activations",
               name);
+    return MX_ERR_INVALID;
+  }
+  if (split && addend) {
+    set_error("%s: an addend is supported with bf16 / NF4 / INT8 weights only", name);
+    return MX_ERR_INVALID;
+  }
+  if (addend_ready && !addend) {
+    set_error("%s: addend_ready needs an addend", name);
     return MX_ERR_INVALID;
   }
   const LayerLayout L = layer_layout(R, num_experts, hidden, ffn, split, num_tokens);
@@ -1424,11 +1433,34 @@ extern "C" int mx_moe_forward_act(const void *tokens, const int64_t *top_idx,
                     2 * hidden, sum, MX_DTYPE_F32, stream);
     if (!rc) rc = sum_halves(sum, num_tokens, hidden, out, out_dtype, s);
   } else {
-    rc = mx_combine(y, top_idx, top_scores, score_dtype, num_tokens, top_k, num_experts, hidden,
-                    out, out_dtype, stream);
+    // The addend (e.g. a shared expert computed on another stream) is needed
+    // only here: the routed path above runs concurrently with its producer.
+    if (addend_ready) {
+      const hipError_t err = hipStreamWaitEvent(s, static_cast<hipEvent_t>(addend_ready), 0);
+      if (err != hipSuccess) {
+        set_error("%s: hipStreamWaitEvent: %s", name, hipGetErrorString(err));
+        return MX_ERR_HIP;
+      }
+    }
+    rc = combine_ex(y, top_idx, top_scores, score_dtype, num_tokens, top_k, num_experts, hidden,
+                    out, out_dtype, addend, stream);
   }
   mark_stage(6, s);
   return rc;
+}
+
+extern "C" int mx_moe_forward_act(const void *tokens, const int64_t *top_idx,
+                                  const void *top_scores, int score_dtype, int64_t num_tokens,
+                                  int top_k, int num_experts, int64_t hidden, int64_t ffn,
+                                  int act, const mx_weight *w1, const mx_weight *w3,
+                                  const mx_weight *w2, const mx_lora *l1, const mx_lora *l3,
+                                  const mx_lora *l2, void *out, int out_dtype, void *save_gate,
+                                  void *save_up, void *save_h, void *save_y, void *save_lora,
+                                  void *workspace, void *stream) {
+  return mx_moe_forward_ex(tokens, top_idx, top_scores, score_dtype, num_tokens, top_k,
+                           num_experts, hidden, ffn, act, w1, w3, w2, l1, l3, l2, out, out_dtype,
+                           nullptr, nullptr, save_gate, save_up, save_h, save_y, save_lora,
+                           workspace, stream);
 }
 
 extern "C" int mx_moe_forward(const void *tokens, const int64_t *top_idx, const void *top_scores,

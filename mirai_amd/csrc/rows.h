@@ -14,4 +14,10 @@ int split_f32(const float *x, int64_t rows, int64_t cols, int pattern, uint16_t 
 int sum_halves(const float *in, int64_t rows, int64_t cols, void *out, int out_dtype,
                hipStream_t s);
 
+// mx_combine with an optional addend [T, cols] of out's dtype:
+// out = out_dtype(out_dtype(sum) + addend).
+int combine_ex(const void *y, const int64_t *top_idx, const void *top_scores, int score_dtype,
+               int64_t num_tokens, int top_k, int num_experts, int64_t cols, void *out,
+               int out_dtype, const void *addend, void *stream);
+
 }  // namespace mx

@@ -61,6 +61,47 @@ __device__ __forceinline__ int sorted_slots(const int64_t *idx_row, int k, int E
   return n;
 }
 
+// Stores 8 combined columns at element offset `off`. With an addend (same
+// dtype and layout as out) the value is out_dtype(out_dtype(sum) + addend):
+// the routed sum is rounded to the output dtype first and then added, as the
+// reference's `out + shared_output` on the block output
+// (transformer_lingbot_video.py:2374-2377).
+__device__ __forceinline__ void store_combined(void *out, int out_dtype, const void *addend,
+                                               int64_t off, const float (&acc)[8]) {
+  if (out_dtype == MX_DTYPE_BF16) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = acc[i];
+    if (addend) {
+      const uint4 a = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(addend) + off);
+      const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v[2 * q] = round_bf16(v[2 * q]) + bf16_bits_to_f32(aw[q] & 0xffffu);
+        v[2 * q + 1] = round_bf16(v[2 * q + 1]) + bf16_bits_to_f32(aw[q] >> 16);
+      }
+    }
+    uint4 o;
+    o.x = pack_bf16x2(v[0], v[1]);
+    o.y = pack_bf16x2(v[2], v[3]);
+    o.z = pack_bf16x2(v[4], v[5]);
+    o.w = pack_bf16x2(v[6], v[7]);
+    *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + off) = o;
+  } else {
+    float4 *o = reinterpret_cast<float4 *>(static_cast<float *>(out) + off);
+    float4 lo = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    float4 hi = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    if (addend) {
+      const float4 *a = reinterpret_cast<const float4 *>(static_cast<const float *>(addend) + off);
+      const float4 a0 = a[0], a1 = a[1];
+      lo = make_float4(lo.x + a0.x, lo.y + a0.y, lo.z + a0.z, lo.w + a0.w);
+      hi = make_float4(hi.x + a1.x, hi.y + a1.y, hi.z + a1.z, hi.w + a1.w);
+    }
+    o[0] = lo;
+    o[1] = hi;
+  }
+}
+
 // One wave per token (four tokens per workgroup) for a compile-time top-k:
 // the slot order (ascending expert id, slot order for ties, invalid ids last)
 // is formed with static indices, and the KC slot rows of each 512-column span
@@ -69,7 +110,8 @@ template <int KC>
 __global__ __launch_bounds__(256) void combine_wave_kernel(const uint16_t *y, const int64_t *top_idx,
                                                           const void *top_scores, int score_dtype,
                                                           int E, int64_t cols, int64_t num_tokens,
-                                                          void *out, int out_dtype) {
+                                                          void *out, int out_dtype,
+                                                          const void *addend) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (t >= num_tokens) return;
   const int lane = threadIdx.x & 63;
@@ -123,18 +165,7 @@ __global__ __launch_bounds__(256) void combine_wave_kernel(const uint16_t *y, co
         acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __fmul_rn(bf16_bits_to_f32(w[i] >> 16), sc[q]));
       }
     }
-    if (out_dtype == MX_DTYPE_BF16) {
-      uint4 o;
-      o.x = pack_bf16x2(acc[0], acc[1]);
-      o.y = pack_bf16x2(acc[2], acc[3]);
-      o.z = pack_bf16x2(acc[4], acc[5]);
-      o.w = pack_bf16x2(acc[6], acc[7]);
-      *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(out) + t * cols + c0) = o;
-    } else {
-      float4 *o = reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + t * cols + c0);
-      o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-      o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
-    }
+    store_combined(out, out_dtype, addend, t * cols + c0, acc);
   }
 }
 
@@ -142,7 +173,7 @@ __global__ __launch_bounds__(256) void combine_wave_kernel(const uint16_t *y, co
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *y, const int64_t *top_idx,
                                                       const void *top_scores, int score_dtype,
                                                       int k, int E, int64_t cols, void *out,
-                                                      int out_dtype) {
+                                                      int out_dtype, const void *addend) {
   const int64_t t = blockIdx.x;
   int slot[kMaxK];
   const int n = sorted_slots(top_idx + t * k, k, E, slot);
@@ -163,18 +194,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *y, const i
         acc[2 * q + 1] = __fadd_rn(acc[2 * q + 1], __fmul_rn(bf16_bits_to_f32(w[q] >> 16), sc[j]));
       }
     }
-    if (out_dtype == MX_DTYPE_BF16) {
-      uint4 o;
-      o.x = pack_bf16x2(acc[0], acc[1]);
-      o.y = pack_bf16x2(acc[2], acc[3]);
-      o.z = pack_bf16x2(acc[4], acc[5]);
-      o.w = pack_bf16x2(acc[6], acc[7]);
-      *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(out) + t * cols + c0) = o;
-    } else {
-      float *o = reinterpret_cast<float *>(out) + t * cols + c0;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) o[q] = acc[q];
-    }
+    store_combined(out, out_dtype, addend, t * cols + c0, acc);
   }
 }
 
@@ -393,10 +413,11 @@ extern "C" int mx_scatter_add_rows(const void *rows_in, const float *row_scale,
   return check_launch("mx_scatter_add_rows");
 }
 
-extern "C" int mx_combine(const void *y, const int64_t *top_idx, const void *top_scores,
-                          int score_dtype, int64_t num_tokens, int top_k, int num_experts,
-                          int64_t cols, void *out, int out_dtype, void *stream) {
-  clear_error();
+namespace mx {
+
+int combine_ex(const void *y, const int64_t *top_idx, const void *top_scores, int score_dtype,
+               int64_t num_tokens, int top_k, int num_experts, int64_t cols, void *out,
+               int out_dtype, const void *addend, void *stream) {
   if (num_tokens < 0 || top_k <= 0 || top_k > kMaxK || cols <= 0 || cols % 8 != 0 ||
       num_experts <= 0) {
     set_error("mx_combine: need top_k in [1,16], cols a positive multiple of 8");
@@ -413,7 +434,7 @@ extern "C" int mx_combine(const void *y, const int64_t *top_idx, const void *top
   case KC:                                                                                   \
     hipLaunchKernelGGL(combine_wave_kernel<KC>, wave_grid, dim3(256), 0, as_stream(stream), yb, \
                        top_idx, top_scores, score_dtype, num_experts, cols, num_tokens, out,   \
-                       out_dtype);                                                           \
+                       out_dtype, addend);                                                   \
     break;
   switch (top_k) {
     MX_COMBINE_K(1)
@@ -424,10 +445,21 @@ extern "C" int mx_combine(const void *y, const int64_t *top_idx, const void *top
     MX_COMBINE_K(8)
     default:
       hipLaunchKernelGGL(combine_kernel, dim3(num_tokens), dim3(256), 0, as_stream(stream), yb,
-                         top_idx, top_scores, score_dtype, top_k, num_experts, cols, out, out_dtype);
+                         top_idx, top_scores, score_dtype, top_k, num_experts, cols, out, out_dtype,
+                         addend);
   }
 #undef MX_COMBINE_K
   return check_launch("mx_combine");
+}
+
+}  // namespace mx
+
+extern "C" int mx_combine(const void *y, const int64_t *top_idx, const void *top_scores,
+                          int score_dtype, int64_t num_tokens, int top_k, int num_experts,
+                          int64_t cols, void *out, int out_dtype, void *stream) {
+  clear_error();
+  return combine_ex(y, top_idx, top_scores, score_dtype, num_tokens, top_k, num_experts, cols, out,
+                    out_dtype, nullptr, stream);
 }
 
 extern "C" int mx_combine_backward(const void *grad_out, int grad_dtype, const void *y,

@@ -54,8 +54,10 @@ def _lora_params(module):
     return params
 
 
-def _forward(module, tokens, top_scores, top_indices, need_grad):
-    """One mx_moe_forward call; returns (out, saved tensors or None)."""
+def _forward(module, tokens, top_scores, top_indices, need_grad, addend=None, addend_ready=None):
+    """One mx_moe_forward call; returns (out, saved tensors or None). With an
+    addend [T, d] (bf16) the combine adds it to the rounded routed sum, after
+    waiting for the event ``addend_ready`` (torch.cuda.Event or None)."""
     device = nat.require_gpu(tokens, top_scores, top_indices)
     # fp32 weights (quant_format "fp32") run the split-precision layer on
     # fp32 tokens; the other formats take bf16 tokens.
@@ -91,9 +93,14 @@ def _forward(module, tokens, top_scores, top_indices, need_grad):
     lib = nat.load_library()
     size = lib.mx_moe_f32x3_workspace_size if split else lib.mx_moe_workspace_size
     ws = nat.workspace(size(T, k, E, d, f), device)
-    nat.call("mx_moe_forward_act", x.data_ptr(), idx.data_ptr(), scores.data_ptr(),
+    if addend is not None:
+        if need_grad or split or addend.dtype != out.dtype or tuple(addend.shape) != (T, d):
+            raise ValueError("the fused addend is a bf16 [tokens, hidden] inference input.")
+        addend = addend.contiguous()
+    nat.call("mx_moe_forward_ex", x.data_ptr(), idx.data_ptr(), scores.data_ptr(),
              nat.dtype_code(scores.dtype), T, k, E, d, f, kernel_activation(module), w1, w3, w2,
              lora[0], lora[1], lora[2], out.data_ptr(), nat.dtype_code(out.dtype),
+             nat.ptr(addend), addend_ready.cuda_event if addend_ready is not None else None,
              *[nat.ptr(t) for t in saves], ws.data_ptr(), nat.stream(device))
     del keep
     return out.to(tokens.dtype), ((x, scores, idx, *saves) if need_grad else None)
@@ -123,6 +130,22 @@ def routed_experts(module, tokens, top_scores, top_indices):
             t is not None and t.requires_grad for t in (tokens, top_scores, *params)):
         return _RoutedExperts.apply(module, tokens, top_scores, top_indices, *params)
     return _forward(module, tokens, top_scores, top_indices, False)[0]
+
+
+def routed_experts_plus(module, tokens, top_scores, top_indices, addend, addend_ready=None):
+    """routed_experts(...) + addend, the add fused into the combine in inference
+    (the combine waits for ``addend_ready``); with autograd a plain add."""
+    params = _lora_params(module)
+    if torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (tokens, top_scores, addend, *params)):
+        if addend_ready is not None:
+            torch.cuda.current_stream(tokens.device).wait_event(addend_ready)
+        return routed_experts(module, tokens, top_scores, top_indices) + addend
+    if tokens.dtype != torch.bfloat16 or module.quant_format == "fp32":
+        if addend_ready is not None:
+            torch.cuda.current_stream(tokens.device).wait_event(addend_ready)
+        return routed_experts(module, tokens, top_scores, top_indices) + addend
+    return _forward(module, tokens, top_scores, top_indices, False, addend, addend_ready)[0]
 
 
 def sorted_experts(module, tokens, counts):

@@ -125,3 +125,44 @@ def test_execution_spec_surface():
     assert spec.tensor_for_role("gate") == "w1"
     assert spec.tensor_for_role("up") == "w3"
     assert spec.tensor_for_role("down") == "w2"
+
+
+def test_token_chunk_policy_surface():
+    from mirai_amd.chunking import MoETokenChunkPolicy
+
+    with pytest.raises(ValueError):
+        MoETokenChunkPolicy(-1)
+    p = MoETokenChunkPolicy(100)
+    assert p.enabled and not MoETokenChunkPolicy(0).enabled
+    assert [p.chunk_count(n) for n in (0, 1, 100, 101, 250)] == [1, 1, 1, 2, 3]
+    calls = []
+
+    def runner(t, s, i, off):
+        calls.append((int(t.shape[0]), off))
+        return t * 2
+
+    x = torch.arange(250.0).view(250, 1)
+    s, i = torch.ones(250, 2), torch.zeros(250, 2, dtype=torch.long)
+    with torch.no_grad():
+        out = p.execute(x, s, i, runner=runner, training=True)
+    assert calls == [(100, 0), (100, 100), (50, 200)] and torch.equal(out, x * 2)
+    calls.clear()
+    p.execute(x, s, i, runner=runner, training=False)  # eval: one call
+    assert calls == [(250, 0)]
+    with pytest.raises(ValueError):
+        p.execute(x, s[:, :1], i, runner=runner, training=True)
+
+
+def test_block_builds_the_reference_submodules():
+    from mirai_amd.block import FusedSparseMoeBlock
+
+    blk = FusedSparseMoeBlock(128, 512, 8, 2, 64, "sigmoid", True, None, None, 1.0, 1)
+    assert blk.router.weight.shape == (8, 128) and blk.router.weight.dtype == torch.float32
+    assert blk.router.e_score_correction_bias.shape == (8,)
+    assert blk.shared_experts.gate_proj.weight.shape == (64, 128)
+    assert blk.shared_experts.down_proj.weight.shape == (128, 64)
+    assert blk.experts.num_experts == 8
+    assert FusedSparseMoeBlock(128, 512, 8, 2, 64, "softmax", True, None, None, 1.0,
+                               0).shared_experts is None
+    with pytest.raises((nat.NativeLibraryError, ValueError)):
+        blk(torch.zeros(1, 4, 128))
