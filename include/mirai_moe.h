@@ -432,6 +432,55 @@ int mx_moe_forward_ex(const void *tokens, const int64_t *top_idx, const void *to
                       void *stream);
 
 /*
+ * Expert-choice routes: expert_token_indices / expert_token_scores [B, L, C]
+ * (each of L logical experts picks C tokens of each of B samples; token ids
+ * in [0, tokens_per_sample)). The flat slots s = (b, l, c) map to physical
+ * expert logical_to_physical[l] (NULL: l, with L == num_experts) and token
+ * idx + b * tokens_per_sample.
+ *
+ * mx_build_expert_choice_plan replaces build_expert_choice_dispatch_plan
+ * (mirai/core/models/compressed_weights/execution/dispatch_preprocess.py:182-278):
+ * the plan fields of mx_build_plan over the slots sorted stably by physical
+ * expert, with sorted_token_indices the slots' flat token ids.
+ */
+size_t mx_expert_choice_plan_workspace_size(int batch, int logical_experts, int capacity,
+                                            int num_experts);
+int mx_build_expert_choice_plan(const int64_t *expert_token_indices,
+                                const void *expert_token_scores, int score_dtype, int batch,
+                                int logical_experts, int capacity, int64_t tokens_per_sample,
+                                const int32_t *logical_to_physical, int num_experts,
+                                int64_t *counts, int64_t *starts, int32_t *offsets,
+                                int64_t *sort_positions, int64_t *sorted_token_indices,
+                                void *sorted_scores, int64_t *inverse_order, void *workspace,
+                                void *stream);
+
+/*
+ * Expert-choice routed layer, replacing run_compressed_expert_choice
+ * (execution/expert_choice.py:16-152, run_expert_choice_routed
+ * experts.py:1954-1974): the expert MLP of every slot (same kernels as
+ * mx_moe_forward_act) and out[t] = sum over t's slots of score * y in fp32,
+ * in ascending order of (physical expert, logical expert) -- the order the
+ * reference's index_add_ visits the sorted slots on the CPU -- cast to
+ * out_dtype. combine_order [L] lists the logical experts in that order (NULL:
+ * 0..L-1, right when logical_to_physical is NULL or monotone). Tokens no
+ * expert picked get 0. Preconditions: a token appears at most once per
+ * (sample, logical expert); token ids outside [0, tokens_per_sample) are
+ * skipped. L <= 1024. Inference (no saved activations).
+ */
+size_t mx_moe_expert_choice_workspace_size(int batch, int logical_experts, int capacity,
+                                           int64_t tokens_per_sample, int num_experts,
+                                           int64_t hidden, int64_t ffn);
+int mx_moe_forward_expert_choice(const void *tokens, const int64_t *expert_token_indices,
+                                 const void *expert_token_scores, int score_dtype, int batch,
+                                 int logical_experts, int capacity, int64_t tokens_per_sample,
+                                 const int32_t *logical_to_physical,
+                                 const int32_t *combine_order, int num_experts, int64_t hidden,
+                                 int64_t ffn, int act, const mx_weight *w1, const mx_weight *w3,
+                                 const mx_weight *w2, const mx_lora *l1, const mx_lora *l3,
+                                 const mx_lora *l2, void *out, int out_dtype, void *workspace,
+                                 void *stream);
+
+/*
  * Expert MLP over rows already sorted by expert (no gate weighting):
  * out[i] = (silu(x w1^T + dA1) * (x w3^T + dA3)) w2^T + dA2 for the expert that
  * owns row i. Replaces CompressedGroupedExperts.run_for_loop

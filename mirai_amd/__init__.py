@@ -5,7 +5,13 @@ Drop-in for the routed expert op of seruva19/mirai
 ``mirai_amd.experts``.
 """
 
-from .dispatch import DispatchPlan, build_dispatch_plan, combine_routed_tokens, permute_routed_tokens
+from .dispatch import (
+    DispatchPlan,
+    build_dispatch_plan,
+    build_expert_choice_dispatch_plan,
+    combine_routed_tokens,
+    permute_routed_tokens,
+)
 from .experts import CompressedGroupedExperts
 from .lora import ActiveExpertLoRA, lora_scale
 from .magi2 import Magi2FusedMoEBackend, Magi2GroupedExperts, route_topk_heads
@@ -33,6 +39,7 @@ __all__ = [
     "MoEOptimizationPolicy",
     "active_moe_optimization_policy",
     "build_dispatch_plan",
+    "build_expert_choice_dispatch_plan",
     "combine_routed_tokens",
     "fused_router_forward",
     "get_active_moe_optimization_policy",

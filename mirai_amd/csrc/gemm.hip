@@ -1575,3 +1575,274 @@ extern "C" int mx_grouped_linear(const void *x, const int64_t *counts, int64_t n
   p.ldo = out_f;
   return launch_any<EPI_STORE>(w->format, lr, p, L.plan, v, s);
 }
+
+// ------------------------------------------------------------ expert choice
+// Expert-choice routes [B, L, C] (each of L logical experts picks C tokens of
+// each sample) through the same plan and grouped GEMMs: the flat slots
+// s = (b, l, c) are counting-sorted by physical expert (k = 1), each sorted
+// row reads token idx[s] + b * tokens_per_sample, and the combine adds every
+// token's contributions in ascending (physical expert, logical expert) order.
+namespace mx {
+namespace gemm {
+
+struct EcLayout {
+  LayerLayout layer;
+  size_t off_phys = 0, off_tok = 0, off_map = 0, bytes = 0;
+};
+
+EcLayout ec_layout(int64_t slots, int num_experts, int64_t hidden, int64_t ffn, int64_t tokens,
+                   int logical) {
+  EcLayout L;
+  L.layer = layer_layout(slots, num_experts, hidden, ffn);
+  size_t off = align_up(L.layer.bytes, 256);
+  L.off_phys = off;
+  off = align_up(off + sizeof(int64_t) * slots, 256);
+  L.off_tok = off;
+  off = align_up(off + sizeof(int64_t) * slots, 256);
+  L.off_map = off;
+  off = align_up(off + sizeof(int32_t) * tokens * logical, 256);
+  L.bytes = off;
+  return L;
+}
+
+// phys[s] = logical_to_physical[l] (or l), tok[s] = idx[s] + b * tps.
+__global__ __launch_bounds__(256) void ec_slots_kernel(const int64_t *idx, int64_t slots, int L,
+                                                       int C, int64_t tps, const int32_t *l2p,
+                                                       int64_t *phys, int64_t *tok) {
+  const int64_t s = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (s >= slots) return;
+  const int64_t b = s / (static_cast<int64_t>(L) * C);
+  const int l = static_cast<int>((s / C) % L);
+  phys[s] = l2p ? l2p[l] : l;
+  tok[s] = idx[s] + b * tps;
+}
+
+// dst[r] = tok[src[r]] (sorted token indices / sorted-row tokens) for slot
+// indices src[r] in [0, rows); with clamp, tokens outside [0, T) read token 0
+// (their slots are not combined).
+template <typename D, typename S>
+__global__ __launch_bounds__(256) void ec_gather_tok_kernel(const S *src, const int64_t *tok,
+                                                            int64_t rows, int64_t T, bool clamp,
+                                                            D *dst) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (r >= rows) return;
+  const int64_t i = static_cast<int64_t>(src[r]);
+  int64_t t = (i >= 0 && i < rows) ? tok[i] : -1;
+  if (clamp && (t < 0 || t >= T)) t = 0;
+  dst[r] = static_cast<D>(t);
+}
+
+__global__ __launch_bounds__(256) void ec_map_kernel(const int64_t *tok, int64_t slots, int L,
+                                                     int C, int64_t T, int32_t *map) {
+  const int64_t s = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (s >= slots) return;
+  const int64_t t = tok[s];
+  if (t < 0 || t >= T) return;
+  map[t * L + (s / C) % L] = static_cast<int32_t>(s);
+}
+
+__global__ __launch_bounds__(256) void ec_fill_kernel(int32_t *p, int64_t n, int32_t v) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// One wave per token: the token's slots are collected in the given logical
+// order into LDS, then each 512-column span sums score * y over them in fp32
+// (product and sum each rounded once, as index_add_(y.float() * score)).
+__global__ __launch_bounds__(256) void ec_combine_kernel(const uint16_t *y, const void *scores,
+                                                         int score_dtype, const int32_t *map,
+                                                         const int32_t *order, int64_t T, int L,
+                                                         int64_t cols, void *out, int out_dtype) {
+  __shared__ int32_t s_slot[4][1024];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + w;
+  if (t >= T) return;
+  int n = 0;
+  for (int i0 = 0; i0 < L; i0 += 64) {
+    const int i = i0 + lane;
+    int32_t s = -1;
+    if (i < L) s = map[t * L + (order ? order[i] : i)];
+    const uint64_t present = __ballot(s >= 0);
+    const int pos = n + __popcll(present & ((1ull << lane) - 1ull));
+    if (s >= 0) s_slot[w][pos] = s;
+    n += __popcll(present);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  for (int64_t c0 = static_cast<int64_t>(lane) * 8; c0 < cols; c0 += 512) {
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    for (int j = 0; j < n; ++j) {
+      const int32_t s = s_slot[w][j];
+      const float sc = load_score(scores, s, score_dtype);
+      const uint4 v = *reinterpret_cast<const uint4 *>(y + static_cast<int64_t>(s) * cols + c0);
+      const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] = __fadd_rn(acc[2 * i], __fmul_rn(bf16_bits_to_f32(q[i] & 0xffffu), sc));
+        acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __fmul_rn(bf16_bits_to_f32(q[i] >> 16), sc));
+      }
+    }
+    if (out_dtype == MX_DTYPE_BF16) {
+      uint4 o;
+      o.x = pack_bf16x2(acc[0], acc[1]);
+      o.y = pack_bf16x2(acc[2], acc[3]);
+      o.z = pack_bf16x2(acc[4], acc[5]);
+      o.w = pack_bf16x2(acc[6], acc[7]);
+      *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + t * cols + c0) = o;
+    } else {
+      float4 *o = reinterpret_cast<float4 *>(static_cast<float *>(out) + t * cols + c0);
+      o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    }
+  }
+}
+
+int validate_ec(const char *name, int batch, int logical, int capacity, int64_t tps,
+                int num_experts, const int32_t *l2p) {
+  if (batch < 0 || logical <= 0 || logical > 1024 || capacity <= 0 || tps <= 0 ||
+      num_experts <= 0 || num_experts > kPlanMaxExperts) {
+    set_error("%s: need batch >= 0, 1 <= logical experts <= 1024, capacity > 0, "
+              "tokens_per_sample > 0 and 1 <= num_experts <= %d", name, kPlanMaxExperts);
+    return MX_ERR_INVALID;
+  }
+  if (!l2p && logical != num_experts) {
+    set_error("%s: logical and physical expert counts differ without an alias map", name);
+    return MX_ERR_INVALID;
+  }
+  const int64_t slots = static_cast<int64_t>(batch) * logical * capacity;
+  if (slots >= (int64_t(1) << 31)) {
+    set_error("%s: expert-choice slot count exceeds the int32 range", name);
+    return MX_ERR_INVALID;
+  }
+  return MX_OK;
+}
+
+}  // namespace gemm
+}  // namespace mx
+
+extern "C" size_t mx_expert_choice_plan_workspace_size(int batch, int logical_experts,
+                                                       int capacity, int num_experts) {
+  if (batch < 0 || logical_experts <= 0 || capacity <= 0 || num_experts <= 0) return 0;
+  const int64_t slots = static_cast<int64_t>(batch) * logical_experts * capacity;
+  return align_up(plan_layout(slots, num_experts).bytes, 256) + 2 * align_up(8 * slots, 256);
+}
+
+extern "C" int mx_build_expert_choice_plan(
+    const int64_t *expert_token_indices, const void *expert_token_scores, int score_dtype,
+    int batch, int logical_experts, int capacity, int64_t tokens_per_sample,
+    const int32_t *logical_to_physical, int num_experts, int64_t *counts, int64_t *starts,
+    int32_t *offsets, int64_t *sort_positions, int64_t *sorted_token_indices,
+    void *sorted_scores, int64_t *inverse_order, void *workspace, void *stream) {
+  clear_error();
+  const char *name = "mx_build_expert_choice_plan";
+  int rc = validate_ec(name, batch, logical_experts, capacity, tokens_per_sample, num_experts,
+                       logical_to_physical);
+  if (rc) return rc;
+  const int64_t slots = static_cast<int64_t>(batch) * logical_experts * capacity;
+  if (slots > 0 && (!expert_token_indices || !expert_token_scores || !workspace ||
+                    !sort_positions || !sorted_token_indices)) {
+    set_error("%s: routes, workspace, sort_positions and sorted_token_indices must be non-null",
+              name);
+    return MX_ERR_INVALID;
+  }
+  hipStream_t s = as_stream(stream);
+  char *ws = static_cast<char *>(workspace);
+  const size_t plan_bytes = align_up(plan_layout(slots, num_experts).bytes, 256);
+  int64_t *phys = reinterpret_cast<int64_t *>(ws + plan_bytes);
+  int64_t *tok = reinterpret_cast<int64_t *>(ws + plan_bytes + align_up(8 * slots, 256));
+  const dim3 grid(static_cast<unsigned>(ceil_div(slots > 0 ? slots : 1, 256)));
+  if (slots > 0) {
+    hipLaunchKernelGGL(ec_slots_kernel, grid, dim3(256), 0, s, expert_token_indices, slots,
+                       logical_experts, capacity, tokens_per_sample, logical_to_physical, phys,
+                       tok);
+    if ((rc = check_launch(name))) return rc;
+  }
+  rc = build_plan(phys, expert_token_scores, score_dtype, slots, 1, num_experts, counts, starts,
+                  offsets, sort_positions, sorted_token_indices, sorted_scores, inverse_order,
+                  workspace, s);
+  if (rc || slots == 0) return rc;
+  hipLaunchKernelGGL((ec_gather_tok_kernel<int64_t, int64_t>), grid, dim3(256), 0, s,
+                     sort_positions, tok, slots, int64_t(0), false, sorted_token_indices);
+  return check_launch(name);
+}
+
+extern "C" size_t mx_moe_expert_choice_workspace_size(int batch, int logical_experts,
+                                                      int capacity, int64_t tokens_per_sample,
+                                                      int num_experts, int64_t hidden,
+                                                      int64_t ffn) {
+  if (batch < 0 || logical_experts <= 0 || capacity <= 0 || tokens_per_sample <= 0 ||
+      num_experts <= 0 || hidden <= 0 || ffn <= 0)
+    return 0;
+  const int64_t slots = static_cast<int64_t>(batch) * logical_experts * capacity;
+  return ec_layout(slots, num_experts, hidden, ffn, batch * tokens_per_sample, logical_experts)
+      .bytes;
+}
+
+extern "C" int mx_moe_forward_expert_choice(
+    const void *tokens, const int64_t *expert_token_indices, const void *expert_token_scores,
+    int score_dtype, int batch, int logical_experts, int capacity, int64_t tokens_per_sample,
+    const int32_t *logical_to_physical, const int32_t *combine_order, int num_experts,
+    int64_t hidden, int64_t ffn, int act, const mx_weight *w1, const mx_weight *w3,
+    const mx_weight *w2, const mx_lora *l1, const mx_lora *l3, const mx_lora *l2, void *out,
+    int out_dtype, void *workspace, void *stream) {
+  clear_error();
+  const char *name = "mx_moe_forward_expert_choice";
+  int rc = validate_ec(name, batch, logical_experts, capacity, tokens_per_sample, num_experts,
+                       logical_to_physical);
+  if (rc) return rc;
+  if (act != MX_ACT_SILU && act != MX_ACT_SWIGLU7) {
+    set_error("%s: unknown activation %d", name, act);
+    return MX_ERR_INVALID;
+  }
+  if ((rc = check_layer(name, hidden, ffn, w1, w3, w2, l1, l3, l2))) return rc;
+  if (w1->format == MX_FMT_F32X3) {
+    set_error("%s: MX_FMT_F32X3 (fp32) weights are supported by mx_moe_forward only", name);
+    return MX_ERR_INVALID;
+  }
+  const int64_t T = static_cast<int64_t>(batch) * tokens_per_sample;
+  const int64_t slots = static_cast<int64_t>(batch) * logical_experts * capacity;
+  if (T == 0) return MX_OK;
+  if (!tokens || !out || !workspace || (slots > 0 && (!expert_token_indices ||
+                                                      !expert_token_scores))) {
+    set_error("%s: tokens, routes, output and workspace must be non-null", name);
+    return MX_ERR_INVALID;
+  }
+  hipStream_t s = as_stream(stream);
+  const EcLayout L = ec_layout(slots, num_experts, hidden, ffn, T, logical_experts);
+  char *ws = static_cast<char *>(workspace);
+  int64_t *phys = reinterpret_cast<int64_t *>(ws + L.off_phys);
+  int64_t *tok = reinterpret_cast<int64_t *>(ws + L.off_tok);
+  int32_t *map = reinterpret_cast<int32_t *>(ws + L.off_map);
+  const dim3 sgrid(static_cast<unsigned>(ceil_div(slots > 0 ? slots : 1, 256)));
+  hipLaunchKernelGGL(ec_fill_kernel, dim3(static_cast<unsigned>(ceil_div(T * logical_experts, 256))),
+                     dim3(256), 0, s, map, T * logical_experts, -1);
+  if (slots > 0) {
+    hipLaunchKernelGGL(ec_slots_kernel, sgrid, dim3(256), 0, s, expert_token_indices, slots,
+                       logical_experts, capacity, tokens_per_sample, logical_to_physical, phys,
+                       tok);
+    hipLaunchKernelGGL(ec_map_kernel, sgrid, dim3(256), 0, s, tok, slots, logical_experts,
+                       capacity, T, map);
+    if ((rc = check_launch(name))) return rc;
+    rc = build_plan(phys, nullptr, score_dtype, slots, 1, num_experts, nullptr, nullptr, nullptr,
+                    nullptr, nullptr, nullptr, nullptr, ws, s);
+    if (rc) return rc;
+    const PlanView v = plan_view(ws, L.layer.plan);
+    // Sorted rows carry slots (k = 1); the GEMM reads each slot's token.
+    hipLaunchKernelGGL((ec_gather_tok_kernel<int32_t, int32_t>), sgrid, dim3(256), 0, s,
+                       v.row_token, tok, slots, T, true, v.row_token);
+    if ((rc = check_launch(name))) return rc;
+    uint16_t *y = reinterpret_cast<uint16_t *>(ws + L.layer.off_y);
+    rc = expert_mlp(L.layer.plan, v, num_experts, static_cast<const uint16_t *>(tokens), hidden,
+                    v.row_token, hidden, ffn, act, w1, w3, w2, l1, l3, l2,
+                    reinterpret_cast<uint16_t *>(ws + L.layer.off_lora),
+                    reinterpret_cast<uint16_t *>(ws + L.layer.off_h), nullptr, nullptr, y, hidden,
+                    v.row_slot, s);
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(ec_combine_kernel, dim3(static_cast<unsigned>(ceil_div(T, 4))), dim3(256), 0,
+                     s, reinterpret_cast<const uint16_t *>(ws + L.layer.off_y), expert_token_scores,
+                     score_dtype, map, combine_order, T, logical_experts, hidden, out, out_dtype);
+  return check_launch(name);
+}

@@ -68,6 +68,68 @@ def build_dispatch_plan(top_indices: torch.Tensor, top_scores: torch.Tensor, num
                         top_k=k, max_count_bound=T)
 
 
+def build_expert_choice_dispatch_plan(expert_token_indices: torch.Tensor,
+                                      expert_token_scores: torch.Tensor, *,
+                                      tokens_per_sample: int, num_physical_experts: int,
+                                      logical_to_physical: tuple[int, ...] = ()) -> DispatchPlan:
+    """Expert-contiguous plan from [batch, expert, capacity] routes
+    (dispatch_preprocess.py:182-278), device-resident: the flat slots sorted
+    stably by physical expert, sorted_token_indices = idx + b * tokens_per_sample."""
+    if expert_token_indices.shape != expert_token_scores.shape:
+        raise ValueError("Expert-choice indices and scores must have matching shapes.")
+    if expert_token_indices.ndim != 3:
+        raise ValueError("Expert-choice routes must have shape [batch, expert, capacity].")
+    B, L, C = (int(v) for v in expert_token_indices.shape)
+    if expert_token_indices.device != expert_token_scores.device:
+        raise ValueError("Expert-choice indices and scores must share a device.")
+    if expert_token_indices.dtype.is_floating_point:
+        raise TypeError("Expert-choice token indices must use an integer dtype.")
+    if L <= 0 or C <= 0:
+        raise ValueError("Expert-choice routes require experts and positive capacity.")
+    if int(tokens_per_sample) <= 0:
+        raise ValueError("tokens_per_sample must be > 0.")
+    E = int(num_physical_experts)
+    if E <= 0:
+        raise ValueError("num_physical_experts must be > 0.")
+    aliases = tuple(int(v) for v in logical_to_physical)
+    if aliases and len(aliases) != L:
+        raise ValueError("Logical expert alias map does not match Expert-Choice routes.")
+    if aliases and any(v < 0 or v >= E for v in aliases):
+        raise ValueError("Logical expert alias map contains an invalid physical id.")
+    if not aliases and L != E:
+        raise ValueError("Logical and physical expert counts differ without an alias map.")
+    S = B * L * C
+    if S >= 2**31:
+        raise ValueError("Expert-choice dispatch plan exceeds the int32 slot range.")
+    device = nat.require_gpu(expert_token_indices, expert_token_scores)
+    idx = expert_token_indices.to(torch.int64).contiguous()
+    scores = expert_token_scores.contiguous()
+    if scores.dtype not in (torch.float32, torch.bfloat16):
+        scores = scores.float()
+    l2p = torch.tensor(aliases, dtype=torch.int32, device=device) if aliases else None
+    counts = torch.empty(E, dtype=torch.int64, device=device)
+    starts = torch.empty(E, dtype=torch.int64, device=device)
+    offsets = torch.empty(E, dtype=torch.int32, device=device)
+    sort_positions = torch.empty(S, dtype=torch.int64, device=device)
+    sorted_tokens = torch.empty(S, dtype=torch.int64, device=device)
+    sorted_scores = torch.empty(S, dtype=scores.dtype, device=device)
+    inverse = torch.empty(S, dtype=torch.int64, device=device)
+    ws = nat.workspace(nat.load_library().mx_expert_choice_plan_workspace_size(B, L, C, E), device)
+    nat.call("mx_build_expert_choice_plan", idx.data_ptr(), scores.data_ptr(),
+             nat.dtype_code(scores.dtype), B, L, C, int(tokens_per_sample), nat.ptr(l2p), E,
+             counts.data_ptr(), starts.data_ptr(), offsets.data_ptr(), sort_positions.data_ptr(),
+             sorted_tokens.data_ptr(), sorted_scores.data_ptr(), inverse.data_ptr(),
+             ws.data_ptr(), nat.stream(device))
+    if aliases:
+        bound = B * C * max(aliases.count(i) for i in range(E))
+    else:
+        bound = B * C
+    return DispatchPlan(counts=counts, starts=starts, offsets=offsets,
+                        sort_positions=sort_positions, sorted_token_indices=sorted_tokens,
+                        sorted_scores=sorted_scores, inverse_order=inverse, total_slots=S,
+                        top_k=0, max_count_bound=bound)
+
+
 def _gather(tokens: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
     device = nat.require_gpu(tokens, index)
     src = tokens.contiguous()

@@ -303,6 +303,34 @@ class CompressedGroupedExperts(nn.Module):
         from .fused import routed_experts
         return routed_experts(self, tokens, top_scores, top_indices)
 
+    def logical_to_physical_map(self) -> tuple[int, ...]:
+        """Logical -> physical expert aliases of expert-choice routes (empty: identity)."""
+        return tuple(getattr(self, "_logical_to_physical", ()))
+
+    def set_logical_to_physical_map(self, aliases) -> None:
+        aliases = tuple(int(v) for v in aliases)
+        if any(v < 0 or v >= self.num_experts for v in aliases):
+            raise ValueError("Logical expert alias map contains an invalid physical id.")
+        self._logical_to_physical = aliases
+
+    def run_expert_choice_routed(self, tokens: torch.Tensor, expert_token_scores: torch.Tensor,
+                                 expert_token_indices: torch.Tensor, *,
+                                 tokens_per_sample: int) -> torch.Tensor:
+        """Expert-choice routes [B, L, C] through the fused kernels
+        (experts.py:1954-1974, expert_choice.py:16-152): [B * tokens_per_sample, d]
+        in ``tokens.dtype``, each token the fp32 sum of score * expert output
+        over the (sample, expert, slot) entries that picked it."""
+        if self.expert_weight_access not in {"active_dequant", "chunked_dequant", "fused_kernel"}:
+            raise RuntimeError(
+                "Expert-Choice compressed dispatch requires active_dequant or "
+                "chunked_dequant expert access.")
+        if int(tokens.shape[0]) != int(expert_token_indices.shape[0]) * int(tokens_per_sample):
+            raise ValueError("Expert-Choice batch/token dimensions do not match tokens.")
+        self._require_loaded()
+        from .fused import expert_choice_experts
+        return expert_choice_experts(self, tokens, expert_token_scores, expert_token_indices,
+                                     int(tokens_per_sample), self.logical_to_physical_map())
+
     def run_for_loop(self, tokens: torch.Tensor, counts: torch.Tensor) -> torch.Tensor:
         """Expert MLP of rows already grouped by expert (experts.py:1656-1747)."""
         self._require_loaded()

@@ -148,6 +148,65 @@ def routed_experts_plus(module, tokens, top_scores, top_indices, addend, addend_
     return _forward(module, tokens, top_scores, top_indices, False, addend, addend_ready)[0]
 
 
+def _expert_choice_meta(aliases, logical, num_experts, device):
+    """Device alias map and the combine's logical order: ascending (physical, logical)."""
+    if not aliases:
+        if logical != num_experts:
+            raise ValueError("Logical and physical expert counts differ without an alias map.")
+        return None, None
+    if len(aliases) != logical:
+        raise ValueError("Logical expert alias map does not match Expert-Choice routes.")
+    order = sorted(range(logical), key=lambda l: (aliases[l], l))
+    l2p = torch.tensor(aliases, dtype=torch.int32, device=device)
+    return l2p, torch.tensor(order, dtype=torch.int32, device=device)
+
+
+def expert_choice_experts(module, tokens, expert_token_scores, expert_token_indices,
+                          tokens_per_sample, aliases=()):
+    """Expert-choice routed layer (inference) through mx_moe_forward_expert_choice."""
+    params = _lora_params(module)
+    if torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad
+            for t in (tokens, expert_token_scores, *params)):
+        raise NotImplementedError(
+            "the fused expert-choice layer is inference-only; call it under torch.no_grad()")
+    if expert_token_indices.shape != expert_token_scores.shape:
+        raise ValueError("Expert-choice indices and scores must have matching shapes.")
+    if expert_token_indices.ndim != 3:
+        raise ValueError("Expert-choice routes must have shape [batch, expert, capacity].")
+    if expert_token_indices.dtype.is_floating_point:
+        raise TypeError("Expert-choice token indices must use an integer dtype.")
+    if module.quant_format == "fp32":
+        raise NotImplementedError("expert-choice routes run over bf16, nf4 or int8 weights")
+    device = nat.require_gpu(tokens, expert_token_scores, expert_token_indices)
+    B, L, C = (int(v) for v in expert_token_indices.shape)
+    l2p, order = _expert_choice_meta(tuple(aliases), L, module.num_experts, device)
+    x = tokens.detach().to(torch.bfloat16).contiguous()
+    T, d = (int(v) for v in x.shape)
+    idx = expert_token_indices.detach().to(torch.int64).contiguous()
+    scores = expert_token_scores.detach()
+    if scores.dtype not in (torch.float32, torch.bfloat16):
+        scores = scores.float()
+    scores = scores.contiguous()
+    (w1, w3, w2), packed = _weight_descriptors(module, device)
+    f = int(packed[0].shape[1])
+    lora, keep = _lora_descriptors(module, device)
+    # fp32 sums are kept for fp32 tokens (the reference casts its fp32 buffer
+    # to the token dtype).
+    out = torch.empty((T, d), dtype=torch.float32 if tokens.dtype == torch.float32
+                      else torch.bfloat16, device=device)
+    lib = nat.load_library()
+    ws = nat.workspace(lib.mx_moe_expert_choice_workspace_size(B, L, C, tokens_per_sample,
+                                                               module.num_experts, d, f), device)
+    nat.call("mx_moe_forward_expert_choice", x.data_ptr(), idx.data_ptr(), scores.data_ptr(),
+             nat.dtype_code(scores.dtype), B, L, C, int(tokens_per_sample), nat.ptr(l2p),
+             nat.ptr(order), module.num_experts, d, f, kernel_activation(module), w1, w3, w2,
+             lora[0], lora[1], lora[2], out.data_ptr(), nat.dtype_code(out.dtype), ws.data_ptr(),
+             nat.stream(device))
+    del keep
+    return out.to(tokens.dtype)
+
+
 def sorted_experts(module, tokens, counts):
     """Expert MLP over expert-grouped rows (forward kernels; run_for_loop)."""
     device = nat.require_gpu(tokens)
