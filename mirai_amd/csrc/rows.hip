@@ -146,12 +146,8 @@ __global__ __launch_bounds__(256) void combine_wave_kernel(const uint16_t *y, co
       }
     }
   }
-  for (int64_t c0 = static_cast<int64_t>(lane) * 8; c0 < cols; c0 += 512) {
-    uint4 v[KC];
-#pragma unroll
-    for (int q = 0; q < KC; ++q)
-      v[q] = ok[q] ? *reinterpret_cast<const uint4 *>(row[q] + c0) : make_uint4(0, 0, 0, 0);
-    float acc[8];
+  // Sums the KC rows of one 8-column span into acc, in rank order.
+  auto span_sum = [&](const uint4 (&v)[KC], float (&acc)[8]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
 #pragma unroll
@@ -165,6 +161,32 @@ __global__ __launch_bounds__(256) void combine_wave_kernel(const uint16_t *y, co
         acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __fmul_rn(bf16_bits_to_f32(w[i] >> 16), sc[q]));
       }
     }
+  };
+  // Four 512-column spans per round: all 4 * KC row loads are in flight
+  // before the first sum.
+  int64_t c0 = static_cast<int64_t>(lane) * 8;
+  for (; c0 + 3 * 512 < cols; c0 += 4 * 512) {
+    uint4 v[4][KC];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int q = 0; q < KC; ++q)
+        v[u][q] = ok[q] ? *reinterpret_cast<const uint4 *>(row[q] + c0 + 512 * u)
+                        : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float acc[8];
+      span_sum(v[u], acc);
+      store_combined(out, out_dtype, addend, t * cols + c0 + 512 * u, acc);
+    }
+  }
+  for (; c0 < cols; c0 += 512) {
+    uint4 v[KC];
+#pragma unroll
+    for (int q = 0; q < KC; ++q)
+      v[q] = ok[q] ? *reinterpret_cast<const uint4 *>(row[q] + c0) : make_uint4(0, 0, 0, 0);
+    float acc[8];
+    span_sum(v, acc);
     store_combined(out, out_dtype, addend, t * cols + c0, acc);
   }
 }
