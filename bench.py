@@ -18,6 +18,13 @@ token sample on the host cores.
 forward keeps its activations, the backward produces d tokens, d scores and the
 LoRA factor gradients from dY ~ N(0, 1); forward and backward are also timed
 apart, and the backward's stages are reported next to the forward's.
+
+``--path`` measures the paths next to the layer on the same geometry (one JSON
+line each, not the headline): ``router`` (the fused router front end, tokens ->
+routes, LingBot's sigmoid router with correction bias), ``block`` (LingBot's
+sparse-MoE block: fused router, routed layer, and a shared expert of the same
+width overlapped on a side stream), ``expert_choice`` (the same experts under
+expert-choice routes with capacity T * k / E).
 """
 
 from __future__ import annotations
@@ -56,6 +63,8 @@ def _parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget of the baseline sample")
+    ap.add_argument("--path", choices=("layer", "router", "block", "expert_choice"),
+                    default="layer", help="the path to time (layer: the headline)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the run, copy this many MiB device-to-device once: a kernel "
                          "of known traffic that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -221,6 +230,115 @@ def _cpu_baseline(w, module, logits_cpu, tokens_cpu, budget_s):
     }
 
 
+def _timed(fn, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def _bench_path(args, w, device) -> dict:
+    """One JSON record for a path next to the layer (see the module docstring)."""
+    import torch
+
+    from mirai_amd import fused_router_forward, router_weight_planes
+    from mirai_amd import workloads as wl
+
+    T, d, E, k = w.tokens, w.hidden, w.experts, w.top_k
+    g = torch.Generator(device=device).manual_seed(7)
+    x = wl.tokens(w).to(device)
+    router_w = torch.randn(E, d, generator=g, device=device) * 0.02
+    bias = torch.randn(E, generator=g, device=device) * 0.01
+    base = {"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded N(0,1) tokens, N(0,0.02) weights)"}
+    if args.path == "router":
+        planes = router_weight_planes(router_w)
+
+        def fused():
+            fused_router_forward(x, planes, E, k, score_func="sigmoid", expert_bias=bias,
+                                 return_logits=False, return_scores=False)
+
+        ms = _timed(fused, args.steps, args.warmup)
+
+        def unfused():  # torch's fp32 GEMM, then the routing kernel
+            from mirai_amd import route_topk
+            route_topk(torch.nn.functional.linear(x.float(), router_w), k, renorm="eps")
+
+        ms_unfused = _timed(unfused, args.steps, args.warmup)
+        EP = 32 * -(-E // 32)
+        traffic = T * d * 2 + 3 * EP * d * 2 + T * k * (8 + 2)
+        gbs = traffic / (ms * 1e-3) / 1e9
+        return {**base, "metric": "router tokens/s (fused router front end), 1 GPU",
+                "value": T / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms,
+                "config": {"workload": f"router_{w.name}", "tokens": T, "hidden": d,
+                           "experts": E, "top_k": k, "score_func": "sigmoid"},
+                "unfused_torch_gemm_plus_route_ms": ms_unfused,
+                "roofline": {"kernel": "router_fused_kernel", "bound": "hbm", "achieved": gbs,
+                             "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                             "traffic": None}}
+    module = _build_module(w, device)
+    if args.path == "block":
+        from mirai_amd.block import FusedSparseMoeBlock
+
+        blk = FusedSparseMoeBlock(d, 4 * d, E, k, w.ffn, "sigmoid", True, None, None, 1.0, 1,
+                                  quant_format=w.fmt).to(device)
+        blk.experts = module
+        with torch.no_grad():
+            blk.router.weight.copy_(router_w)
+            blk.router.e_score_correction_bias.copy_(bias)
+        blk.shared_experts.to(torch.bfloat16).requires_grad_(False)
+        for lin in (blk.shared_experts.gate_proj, blk.shared_experts.up_proj,
+                    blk.shared_experts.down_proj):
+            with torch.no_grad():
+                lin.weight.copy_(torch.randn(lin.weight.shape, generator=g, device=device) * 0.02)
+        hs = x.view(1, T, d)
+        with torch.no_grad():
+            ms = _timed(lambda: blk(hs), args.steps, args.warmup)
+            idx, top, _, _, _ = blk.router(x)
+            ms_routed = _timed(lambda: module.run_direct_routed(x, top, idx), args.steps,
+                               args.warmup)
+            ms_shared = _timed(lambda: blk.shared_experts(x), args.steps, args.warmup)
+            ms_router = _timed(lambda: blk.router(x), args.steps, args.warmup)
+        flops = w.flops() + 2 * T * 3 * d * w.ffn + 2 * T * d * E  # routed + shared + router
+        return {**base, "metric": "tokens/s (LingBot sparse-MoE block: router + routed NF4 "
+                "experts + shared expert), 1 GPU",
+                "value": T / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms,
+                "config": {"workload": f"block_{w.name}", "tokens": T, "hidden": d,
+                           "experts": E, "top_k": k, "ffn": w.ffn, "shared_ffn": w.ffn,
+                           "weights": w.fmt, "lora_rank": w.rank},
+                "tflops": flops / (ms * 1e-3) / 1e12,
+                "parts_ms": {"router": ms_router, "routed_layer": ms_routed,
+                             "shared_expert": ms_shared,
+                             "sum": ms_router + ms_routed + ms_shared}}
+    # expert choice: capacity T * k / E per expert, one sample
+    C = T * k // E
+    gi = torch.Generator().manual_seed(11)
+    idx = torch.stack([torch.randperm(T, generator=gi)[:C] for _ in range(E)]).view(1, E, C)
+    scores = torch.rand(1, E, C, generator=gi)
+    idx, scores = idx.to(device), scores.to(device)
+    with torch.no_grad():
+        ms = _timed(lambda: module.run_expert_choice_routed(x, scores, idx, tokens_per_sample=T),
+                    args.steps, args.warmup)
+    R = E * C
+    flops = 2 * R * 3 * d * w.ffn + 2 * R * w.rank * 3 * (d + w.ffn)
+    return {**base, "metric": "routed slots/s (expert-choice routes, NF4 experts + LoRA), 1 GPU",
+            "value": R / (ms * 1e-3), "unit": "routed slots/s", "ms_per_step": ms,
+            "config": {"workload": f"expert_choice_{w.name}", "tokens": T, "hidden": d,
+                       "experts": E, "capacity": C, "ffn": w.ffn, "weights": w.fmt,
+                       "lora_rank": w.rank},
+            "tflops": flops / (ms * 1e-3) / 1e12,
+            "pct_bf16_peak": 100.0 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+
+
 def main() -> int:
     args = _parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -246,6 +364,9 @@ def main() -> int:
         w = dataclasses.replace(w.with_tokens(args.tokens), name=f"{w.name}_T{args.tokens}")
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.path != "layer":
+        print(json.dumps(_bench_path(args, w, device)))
+        return 0
 
     logits_cpu = wl.router_logits(w)
     tokens_cpu = wl.tokens(w)

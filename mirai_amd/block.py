@@ -25,16 +25,16 @@ import torch.nn as nn
 from . import _native as nat
 from .chunking import MoETokenChunkPolicy
 from .experts import CompressedGroupedExperts
-from .fused import routed_experts, routed_experts_plus
+from .fused import routed_experts, routed_experts_plus, sorted_experts
 from .router import FusedRouter
 
 
 class SharedExpertMLP(nn.Module):
     """LingBotVideoMLP (down(silu(gate(x)) * up(x)), bf16 nn.Linear weights
-    gate_proj / up_proj / down_proj) as a one-expert layer of the grouped
-    kernels: every token is routed to expert 0 with weight 1, so the combine
-    returns the down projection unchanged and the gate/up epilogue rounds
-    exactly where the reference's bf16 linears and silu do."""
+    gate_proj / up_proj / down_proj) as one expert of the grouped kernels over
+    rows already in order (mx_moe_for_loop with one segment of all tokens): no
+    plan, no combine, and the gate/up epilogue rounds exactly where the
+    reference's bf16 linears and silu do."""
 
     def __init__(self, hidden_size: int, intermediate_size: int):
         super().__init__()
@@ -43,6 +43,7 @@ class SharedExpertMLP(nn.Module):
         self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
         self._packed = None
         self._packed_key = None
+        self._counts = {}
 
     def _experts(self) -> CompressedGroupedExperts:
         projs = (self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight)
@@ -60,10 +61,12 @@ class SharedExpertMLP(nn.Module):
             raise NotImplementedError(
                 "the shared expert runs over frozen weights; freeze gate_proj / up_proj / "
                 "down_proj (adapter training) or call it under torch.no_grad()")
-        T = int(x.shape[0])
-        ones = torch.ones((T, 1), dtype=torch.float32, device=x.device)
-        zeros = torch.zeros((T, 1), dtype=torch.int64, device=x.device)
-        return routed_experts(self._experts(), x, ones, zeros)
+        key = (int(x.shape[0]), x.device)
+        counts = self._counts.get(key)
+        if counts is None:  # one segment of all rows, kept on the device
+            counts = self._counts[key] = torch.tensor([key[0]], dtype=torch.int64,
+                                                      device=x.device)
+        return sorted_experts(self._experts(), x, counts)
 
 
 class FusedSparseMoeBlock(nn.Module):
