@@ -63,6 +63,9 @@ def _parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget of the baseline sample")
+    ap.add_argument("--graph", action="store_true",
+                    help="inference configs: also replay the step as one HIP graph and report "
+                         "that time (the graph's output is checked against the eager step)")
     ap.add_argument("--path", choices=("layer", "router", "block", "expert_choice"),
                     default="layer", help="the path to time (layer: the headline)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -403,17 +406,42 @@ def main() -> int:
             return
         forward_train().backward(dy)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(args.steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.steps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / args.steps
+
+    eager_ms = timed(step)
+    ms = eager_ms
+    execution = "eager"
+    if not w.backward and args.graph:
+        # The inference step (route + layer: about a dozen kernels) replayed as
+        # one HIP graph: the same kernels on the same inputs, without the
+        # per-launch gaps. Nothing on this path records a memset.
+        forward_only()
+        torch.cuda.synchronize()
+        eager_out = state["out"].clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                forward_only()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            forward_only()
+        ms = timed(graph.replay)
+        if not torch.equal(state["out"], eager_out):
+            print("graph replay differs from the eager step", file=sys.stderr)
+            return 1
+        execution = "hip_graph"
 
     # Routing kernel alone, then the library stages (separate, synchronised passes).
     r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -478,6 +506,8 @@ def main() -> int:
         "tokens_per_s": w.tokens / (ms * 1e-3),
         "algorithmic_gflop": flops / 1e9,
         "empty_experts": int((counts == 0).sum()),
+        "execution": execution,
+        "eager_ms_per_step": eager_ms,
         "stage_ms": {"route": route_ms, **stages},
         "down_gemm_tflops": down_flops / (stages["down_gemm"] * 1e-3) / 1e12,
         **back,

@@ -66,9 +66,21 @@ class ActiveExpertLoRA(nn.Module):
             else:
                 self.lora_a.zero_()
 
+    def _alpha(self) -> float:
+        """lora_alpha as a Python float, read from the (device) buffer only when
+        the buffer changes: a read per call would synchronise the host with the
+        GPU on every forward, and cannot happen under HIP graph capture."""
+        buf = self.lora_alpha
+        key = (buf.data_ptr(), buf._version, str(buf.device))
+        cached = self.__dict__.get("_alpha_cache")
+        if cached is None or cached[0] != key:
+            cached = (key, float(buf))
+            self.__dict__["_alpha_cache"] = cached
+        return cached[1]
+
     def scale(self) -> float:
         return (
-            lora_scale(float(self.lora_alpha), self.rank, use_rslora=self.use_rslora)
+            lora_scale(self._alpha(), self.rank, use_rslora=self.use_rslora)
             * self._lora_scale
             * self._rank_schedule_scale
         )

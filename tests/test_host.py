@@ -166,3 +166,14 @@ def test_block_builds_the_reference_submodules():
                                0).shared_experts is None
     with pytest.raises((nat.NativeLibraryError, ValueError)):
         blk(torch.zeros(1, 4, 128))
+
+
+def test_lora_scale_follows_alpha_buffer_updates():
+    ad = ActiveExpertLoRA(adapter_name="a", num_experts=2, in_features=64, out_features=32,
+                          rank=8, alpha=16.0)
+    assert ad.scale() == pytest.approx(2.0)
+    with torch.no_grad():
+        ad.lora_alpha.fill_(32.0)  # in place: the cached value must not go stale
+    assert ad.scale() == pytest.approx(4.0)
+    ad.load_state_dict({**ad.state_dict(), "lora_alpha": torch.tensor(8.0)})
+    assert ad.scale() == pytest.approx(1.0)
