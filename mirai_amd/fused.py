@@ -148,17 +148,24 @@ def routed_experts_plus(module, tokens, top_scores, top_indices, addend, addend_
     return _forward(module, tokens, top_scores, top_indices, False, addend, addend_ready)[0]
 
 
+_EC_META: dict = {}
+
+
 def _expert_choice_meta(aliases, logical, num_experts, device):
-    """Device alias map and the combine's logical order: ascending (physical, logical)."""
+    """Device alias map and the combine's logical order (ascending (physical,
+    logical)); built once per (map, device): they are static checkpoint metadata."""
     if not aliases:
         if logical != num_experts:
             raise ValueError("Logical and physical expert counts differ without an alias map.")
         return None, None
     if len(aliases) != logical:
         raise ValueError("Logical expert alias map does not match Expert-Choice routes.")
-    order = sorted(range(logical), key=lambda l: (aliases[l], l))
-    l2p = torch.tensor(aliases, dtype=torch.int32, device=device)
-    return l2p, torch.tensor(order, dtype=torch.int32, device=device)
+    key = (aliases, str(device))
+    if key not in _EC_META:
+        order = sorted(range(logical), key=lambda l: (aliases[l], l))
+        _EC_META[key] = (torch.tensor(aliases, dtype=torch.int32, device=device),
+                         torch.tensor(order, dtype=torch.int32, device=device))
+    return _EC_META[key]
 
 
 def expert_choice_experts(module, tokens, expert_token_scores, expert_token_indices,
