@@ -89,6 +89,68 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float *logits, in
   }
 }
 
+// The same routing with one LANE per token for E <= 64: the lane holds its
+// token's logits in registers, so the max, the softmax sum and the k selection
+// rounds need no cross-lane exchange. Taken experts become NaN keys (never
+// better); the scan runs in increasing expert order, so a strict > keeps the
+// lower id on ties.
+template <int EC>
+__global__ __launch_bounds__(256) void route_topk_lane_kernel(const float *logits, int64_t T,
+                                                              int E, int k, int renorm,
+                                                              float route_scale, int64_t *top_idx,
+                                                              void *top_scores, int score_dtype) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= T) return;
+  const float *row = logits + t * E;
+  float v[EC];
+  float m = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < EC; ++e) {
+    v[e] = e < E ? row[e] : -INFINITY;
+    m = fmaxf(m, v[e]);
+  }
+  float z = 0.0f;
+#pragma unroll
+  for (int e = 0; e < EC; ++e)
+    if (e < E) z += __expf(v[e] - m);
+  int sel[kMaxTopK];
+  float p[kMaxTopK];
+  float sum = 0.0f;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    sel[r] = 0;
+    p[r] = 0.0f;
+    if (r < k) {
+      float bv = -INFINITY;
+      int be = -1;
+#pragma unroll
+      for (int e = 0; e < EC; ++e)
+        if (e < E && (v[e] > bv || (be < 0 && v[e] == bv))) {
+          bv = v[e];
+          be = e;
+        }
+#pragma unroll
+      for (int e = 0; e < EC; ++e)
+        if (e == be) v[e] = __builtin_nanf("");
+      sel[r] = be;
+      p[r] = __expf(bv - m) / z;
+      sum += p[r];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    if (r >= k) break;
+    float score = p[r];
+    if (renorm == MX_RENORM_CLAMP)
+      score = p[r] / fmaxf(sum, 1e-20f);
+    else if (renorm == MX_RENORM_EPS)
+      score = p[r] / (sum + 1e-20f);
+    score *= route_scale;
+    top_idx[t * k + r] = sel[r];
+    store_value(top_scores, t * k + r, score, score_dtype);
+  }
+}
+
 // d(logits) for the selected experts of each token; one wavefront per token.
 template <int PER_LANE>
 __global__ __launch_bounds__(256) void route_topk_backward_kernel(
@@ -326,6 +388,23 @@ extern "C" int mx_route_topk(const float *logits, int64_t num_tokens, int num_ex
     return MX_ERR_INVALID;
   }
   if (num_tokens == 0) return MX_OK;
+  if (num_experts <= 64) {
+    const dim3 grid(static_cast<unsigned>(ceil_div(num_tokens, 256)));
+    hipStream_t s = as_stream(stream);
+#define MX_ROUTE_LANE(EC)                                                                    \
+  hipLaunchKernelGGL(route_topk_lane_kernel<EC>, grid, dim3(256), 0, s, logits, num_tokens,   \
+                     num_experts, top_k, renorm, route_scale, top_idx, top_scores, score_dtype)
+    if (num_experts <= 8)
+      MX_ROUTE_LANE(8);
+    else if (num_experts <= 16)
+      MX_ROUTE_LANE(16);
+    else if (num_experts <= 32)
+      MX_ROUTE_LANE(32);
+    else
+      MX_ROUTE_LANE(64);
+#undef MX_ROUTE_LANE
+    return check_launch("mx_route_topk");
+  }
   MX_ROUTE_DISPATCH(route_topk_kernel, logits, num_tokens, num_experts, top_k, renorm,
                     route_scale, top_idx, top_scores, score_dtype);
   return check_launch("mx_route_topk");
