@@ -829,18 +829,8 @@ int launch(const Params &p, int64_t max_row_tiles, hipStream_t s) {
 // on, measured at C2, C3 and C5), else 128-row tiles.
 inline bool use_tall_tiles(int64_t rows, int experts) { return rows >= 256 * static_cast<int64_t>(experts); }
 
-template <int EPI, bool LORA>
-int launch_fmt(int fmt, Params p, const PlanLayout &PL, const PlanView &v, bool tall, hipStream_t s) {
-  // Column tiles are 256 wide (EPI_SWIGLU: 128 ffn columns of gate and of up).
-  // The forward down projection (store epilogue) runs faster with its 8
-  // waves as 4 x 2 (64 x 128 per wave); the others as 2 x 4 (measured).
-  using Tall = typename std::conditional<EPI == EPI_STORE, Tile<256, 256, 4, 2, 64>,
-                                         Tile<256, 256, 2, 4, 64>>::type;
-  using Short = Tile<128, 256, 2, 4, 64>;
-  p.tiles = tall ? v.tiles2 : v.tiles;
-  p.num_tiles = tall ? v.num_tiles2 : v.num_tiles;
-  const int64_t max_tiles = tall ? PL.max_tiles2 : PL.max_tiles;
-  p.n_tiles_n = static_cast<int>(EPI == EPI_SWIGLU ? ceil_div(p.N, 128) : ceil_div(p.N, 256));
+template <int EPI, bool LORA, class Tall, class Short>
+int launch_tile(int fmt, bool tall, const Params &p, int64_t max_tiles, hipStream_t s) {
   switch (fmt) {
     case MX_FMT_BF16:
       return tall ? launch<MX_FMT_BF16, EPI, LORA, Tall>(p, max_tiles, s)
@@ -862,6 +852,32 @@ int launch_fmt(int fmt, Params p, const PlanLayout &PL, const PlanView &v, bool 
   }
   set_error("unknown weight format %d", fmt);
   return MX_ERR_INVALID;
+}
+
+template <int EPI, bool LORA>
+int launch_fmt(int fmt, Params p, const PlanLayout &PL, const PlanView &v, bool tall, hipStream_t s) {
+  // Column tiles are 256 wide (EPI_SWIGLU: 128 ffn columns of gate and of up).
+  // The forward down projection (store epilogue) runs faster with its 8
+  // waves as 4 x 2 (64 x 128 per wave); the others as 2 x 4 (measured).
+  using Tall = typename std::conditional<EPI == EPI_STORE, Tile<256, 256, 4, 2, 64>,
+                                         Tile<256, 256, 2, 4, 64>>::type;
+  using Short = Tile<128, 256, 2, 4, 64>;
+  p.n_tiles_n = static_cast<int>(EPI == EPI_SWIGLU ? ceil_div(p.N, 128) : ceil_div(p.N, 256));
+  if (!tall) {
+    p.tiles = v.tiles;
+    p.num_tiles = v.num_tiles;
+    return launch_tile<EPI, LORA, Tall, Short>(fmt, false, p, PL.max_tiles, s);
+  }
+  // 256-row tiles over each expert's rows except a final remainder of at most
+  // 128 rows, then one launch of 128-row tiles for those remainders: a short
+  // remainder costs about half a tall tile instead of a whole one.
+  p.tiles = v.tiles2m;
+  p.num_tiles = v.num_tiles2m;
+  int rc = launch_tile<EPI, LORA, Tall, Short>(fmt, true, p, PL.max_tiles2, s);
+  if (rc) return rc;
+  p.tiles = v.tilesr;
+  p.num_tiles = v.num_tilesr;
+  return launch_tile<EPI, LORA, Tall, Short>(fmt, false, p, PL.experts, s);
 }
 
 template <int EPI>

@@ -28,6 +28,7 @@ struct PlanLayout {
   int64_t max_tiles = 0;   // 128-row tiles
   int64_t max_tiles2 = 0;  // 256-row tiles
   size_t off_block_counts = 0, off_block_base = 0, off_seg = 0, off_tiles = 0, off_tiles2 = 0;
+  size_t off_tiles2m = 0, off_tilesr = 0;
   size_t off_row_token = 0, off_row_slot = 0;
   size_t bytes = 0;
 };
@@ -41,6 +42,12 @@ struct PlanView {
   int64_t *seg;            // [2, E]: segment start, segment end (sorted rows)
   int2 *tiles;             // [max_tiles]: (expert, first row), 128-row tiles
   int2 *tiles2;            // [max_tiles2]: 256-row tiles
+  // Split covering: 256-row tiles over each expert's rows except a final
+  // remainder of at most 128 rows, which gets one 128-row tile of its own.
+  int32_t *num_tiles2m;    // 256-row tiles of the split covering
+  int32_t *num_tilesr;     // 128-row remainder tiles (at most one per expert)
+  int2 *tiles2m;           // [max_tiles2]
+  int2 *tilesr;            // [experts]
   int32_t *row_token;      // [R]: sorted row -> token
   int32_t *row_slot;       // [R]: sorted row -> flat route slot t*k+j
 };

@@ -83,8 +83,9 @@ template <int kEpt>
 __global__ __launch_bounds__(1024) void plan_scan_kernel(
     const int32_t *block_counts, int n_blocks, int E, int64_t n_rows, int tile_m,
     const int64_t *counts_in, int32_t *block_base, int64_t *seg, int2 *tiles,
-    int32_t *num_tiles, int2 *tiles2, int32_t *num_tiles2, int32_t *err_counter,
-    int64_t *counts_out, int64_t *starts_out, int32_t *offsets_out) {
+    int32_t *num_tiles, int2 *tiles2, int32_t *num_tiles2, int2 *tiles2m, int32_t *num_tiles2m,
+    int2 *tilesr, int32_t *num_tilesr, int32_t *err_counter, int64_t *counts_out,
+    int64_t *starts_out, int32_t *offsets_out) {
   __shared__ int64_t scan_tmp[32];
   __shared__ int32_t part[1024];     // [group][expert] block-range counts (E <= 1024)
   __shared__ int64_t start_s[1024];  // expert starts (E <= 1024)
@@ -163,22 +164,39 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(
     if (starts_out) starts_out[e] = start[c];
     if (offsets_out) offsets_out[e] = static_cast<int32_t>(start[c] + count[c]);
   }
-  for (int list = 0; list < 2; ++list) {
-    const int tm = list == 0 ? tile_m : 2 * tile_m;
-    int2 *out = list == 0 ? tiles : tiles2;
+  // Lists: 0 = tile_m-row tiles, 1 = 2*tile_m-row tiles over all rows;
+  // 2 = 2*tile_m-row tiles over each expert's rows but a final remainder of
+  // at most tile_m rows, 3 = one tile_m-row tile for that remainder.
+  for (int list = 0; list < 4; ++list) {
+    const int tm = list == 0 || list == 3 ? tile_m : 2 * tile_m;
+    int2 *out = list == 0 ? tiles : list == 1 ? tiles2 : list == 2 ? tiles2m : tilesr;
     int64_t tcarry = 0;
 #pragma unroll
     for (int c = 0; c < kEpt; ++c) {
       if (c >= ept) continue;  // uniform
       const int e = t + 1024 * c;
-      const int64_t my_tiles = e < E ? (seg_hi[c] - seg_lo[c] + tm - 1) / tm : 0;
+      const int64_t n = e < E ? seg_hi[c] - seg_lo[c] : 0;
+      const int64_t full = n / (2 * tile_m), rem = n - full * 2 * tile_m;
+      int64_t my_tiles, first = seg_lo[c];
+      if (list <= 1)
+        my_tiles = (n + tm - 1) / tm;
+      else if (list == 2)
+        my_tiles = full + (rem > tile_m ? 1 : 0);
+      else {
+        my_tiles = rem > 0 && rem <= tile_m ? 1 : 0;
+        first = seg_lo[c] + full * 2 * tile_m;
+      }
       int64_t chunk_tiles = 0;
       const int64_t tile0 = tcarry + block_exclusive_scan(my_tiles, scan_tmp, &chunk_tiles);
       tcarry += chunk_tiles;
       for (int64_t j = 0; j < my_tiles; ++j)
-        out[tile0 + j] = make_int2(e, static_cast<int>(seg_lo[c] + j * tm));
+        out[tile0 + j] = make_int2(e, static_cast<int>(first + j * tm));
     }
-    if (threadIdx.x == 0) *(list == 0 ? num_tiles : num_tiles2) = static_cast<int32_t>(tcarry);
+    if (threadIdx.x == 0) {
+      int32_t *num = list == 0 ? num_tiles : list == 1 ? num_tiles2 : list == 2 ? num_tiles2m
+                                                                               : num_tilesr;
+      *num = static_cast<int32_t>(tcarry);
+    }
   }
 }
 
@@ -282,6 +300,10 @@ PlanLayout plan_layout(int64_t num_rows, int num_experts) {
   off = align_up(off + sizeof(int2) * L.max_tiles, 256);
   L.off_tiles2 = off;
   off = align_up(off + sizeof(int2) * L.max_tiles2, 256);
+  L.off_tiles2m = off;
+  off = align_up(off + sizeof(int2) * L.max_tiles2, 256);
+  L.off_tilesr = off;
+  off = align_up(off + sizeof(int2) * num_experts, 256);
   L.off_row_token = off;
   off = align_up(off + sizeof(int32_t) * num_rows, 256);
   L.off_row_slot = off;
@@ -296,11 +318,15 @@ PlanView plan_view(void *ws, const PlanLayout &L) {
   v.err = reinterpret_cast<int32_t *>(b);
   v.num_tiles = reinterpret_cast<int32_t *>(b) + 1;
   v.num_tiles2 = reinterpret_cast<int32_t *>(b) + 2;
+  v.num_tiles2m = reinterpret_cast<int32_t *>(b) + 3;
+  v.num_tilesr = reinterpret_cast<int32_t *>(b) + 4;
   v.block_counts = reinterpret_cast<int32_t *>(b + L.off_block_counts);
   v.block_base = reinterpret_cast<int32_t *>(b + L.off_block_base);
   v.seg = reinterpret_cast<int64_t *>(b + L.off_seg);
   v.tiles = reinterpret_cast<int2 *>(b + L.off_tiles);
   v.tiles2 = reinterpret_cast<int2 *>(b + L.off_tiles2);
+  v.tiles2m = reinterpret_cast<int2 *>(b + L.off_tiles2m);
+  v.tilesr = reinterpret_cast<int2 *>(b + L.off_tilesr);
   v.row_token = reinterpret_cast<int32_t *>(b + L.off_row_token);
   v.row_slot = reinterpret_cast<int32_t *>(b + L.off_row_slot);
   return v;
@@ -313,7 +339,7 @@ int build_plan(const int64_t *top_idx, const void *top_scores, int score_dtype,
   const int64_t R = num_tokens * top_k;
   const PlanLayout L = plan_layout(R, num_experts);
   const PlanView v = plan_view(workspace, L);
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, v.err, 3);
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, v.err, 5);
   if (L.blocks > 0) {
     const size_t lds = sizeof(uint32_t) * num_experts * (L.slots_per_block / 32);
     hipLaunchKernelGGL(plan_count_kernel, dim3(L.blocks), dim3(256), lds, s, top_idx, R,
@@ -322,7 +348,8 @@ int build_plan(const int64_t *top_idx, const void *top_scores, int score_dtype,
   hipLaunchKernelGGL(num_experts <= 1024 ? plan_scan_kernel<1> : plan_scan_kernel<kPlanMaxEpt>,
                      dim3(1), dim3(1024), 0, s, v.block_counts, L.blocks, num_experts, R,
                      kPlanTileM, static_cast<const int64_t *>(nullptr), v.block_base, v.seg,
-                     v.tiles, v.num_tiles, v.tiles2, v.num_tiles2, v.err, counts, starts, offsets);
+                     v.tiles, v.num_tiles, v.tiles2, v.num_tiles2, v.tiles2m, v.num_tiles2m,
+                     v.tilesr, v.num_tilesr, v.err, counts, starts, offsets);
   if (L.blocks > 0) {
     const size_t lds = (plan_prefix_in_lds(num_experts, L.slots_per_block) ? 2 : 1) *
                        sizeof(uint32_t) * num_experts * (L.slots_per_block / 32);
@@ -346,12 +373,13 @@ int plan_from_counts(const int64_t *counts, int64_t num_rows, int num_experts, v
                      hipStream_t s) {
   const PlanLayout L = plan_layout(num_rows, num_experts);
   const PlanView v = plan_view(workspace, L);
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, v.err, 3);
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, v.err, 5);
   hipLaunchKernelGGL(num_experts <= 1024 ? plan_scan_kernel<1> : plan_scan_kernel<kPlanMaxEpt>,
                      dim3(1), dim3(1024), 0, s,
                      static_cast<const int32_t *>(nullptr), 0, num_experts, num_rows,
                      kPlanTileM, counts, static_cast<int32_t *>(nullptr), v.seg, v.tiles,
-                     v.num_tiles, v.tiles2, v.num_tiles2, v.err, static_cast<int64_t *>(nullptr),
+                     v.num_tiles, v.tiles2, v.num_tiles2, v.tiles2m, v.num_tiles2m, v.tilesr,
+                     v.num_tilesr, v.err, static_cast<int64_t *>(nullptr),
                      static_cast<int64_t *>(nullptr), static_cast<int32_t *>(nullptr));
   return check_launch("mx_plan_from_counts");
 }
