@@ -1240,16 +1240,30 @@ extern "C" int mx_moe_backward_act(const void *grad_out, int grad_dtype, const v
   if (rc) return rc;
   mark_stage(1, s);
 
+  // The six LoRA factor transposes (B2^T, A2^T, B1^T, A1^T, B3^T, A3^T) in one launch.
+  {
+    FactorTransposes jobs = {};
+    auto add = [&](const void *src, int64_t rows, int64_t cols, uint16_t *dst) {
+      jobs.job[jobs.n++] = {static_cast<const uint16_t *>(src), dst, rows, cols,
+                            static_cast<int64_t>(num_experts) * rows * cols};
+    };
+    if (lora2) {
+      add(l2->b, hidden, l2->rank, fact[0]);
+      add(l2->a, l2->rank, ffn, fact[1]);
+    }
+    const mx_lora *l13t[2] = {l1, l3};
+    for (int i = 0; i < 2; ++i)
+      if (has_lora(l13t[i])) {
+        add(l13t[i]->b, ffn, l13t[i]->rank, fact[2 + 2 * i]);
+        add(l13t[i]->a, l13t[i]->rank, hidden, fact[3 + 2 * i]);
+      }
+    if ((rc = transpose_factors_multi(jobs, s))) return rc;
+  }
+
   // Down projection: dz2 = s2 * dy B2, then dh = dy W2 + dz2 A2 into the dG
   // half of [dG | dU], and the SwiGLU backward turns it into [dG | dU].
   if (lora2) {
     const int r = l2->rank;
-    if ((rc = transpose_factors(static_cast<const uint16_t *>(l2->b), num_experts, hidden, r,
-                                fact[0], s)))
-      return rc;
-    if ((rc = transpose_factors(static_cast<const uint16_t *>(l2->a), num_experts, r, ffn,
-                                fact[1], s)))
-      return rc;
     const mx_lora t = {fact[0], nullptr, r, l2->scale};
     const mx_lora *ad[1] = {&t};
     if ((rc = lora_down(v, num_experts, L.plan.max_tiles, dy, hidden, v.row_slot, hidden, ad, 1,
@@ -1294,11 +1308,6 @@ extern "C" int mx_moe_backward_act(const void *grad_out, int grad_dtype, const v
     if (!has_lora(l)) continue;
     const int r = l->rank;
     uint16_t *bt = fact[2 + 2 * i], *at = fact[3 + 2 * i];
-    if ((rc = transpose_factors(static_cast<const uint16_t *>(l->b), num_experts, ffn, r, bt, s)))
-      return rc;
-    if ((rc = transpose_factors(static_cast<const uint16_t *>(l->a), num_experts, r, hidden, at,
-                                s)))
-      return rc;
     const mx_lora t = {bt, nullptr, r, l->scale};
     const mx_lora *ad[1] = {&t};
     if ((rc = lora_down(v, num_experts, L.plan.max_tiles, dgu + i * ffn, 2 * ffn, nullptr, ffn, ad,

@@ -6,9 +6,18 @@
 
 namespace mx {
 
-// dst[e][c][r] = src[e][r][c] for bf16 src [E, rows, cols] (dst [E, cols, rows]).
-int transpose_factors(const uint16_t *src, int64_t experts, int64_t rows, int64_t cols,
-                      uint16_t *dst, hipStream_t s);
+// One [E, rows, cols] -> [E, cols, rows] bf16 transpose (total = E*rows*cols).
+struct FactorTranspose {
+  const uint16_t *src;
+  uint16_t *dst;
+  int64_t rows, cols, total;
+};
+struct FactorTransposes {
+  FactorTranspose job[6];
+  int n;
+};
+// All jobs in one launch.
+int transpose_factors_multi(const FactorTransposes &jobs, hipStream_t s);
 
 // Per-expert outer-product sums over the expert's sorted rows:
 //   G[e, c, j] = sum_{r in [seg_start[e], seg_end[e])} M[map(r), c] * V[r, j]

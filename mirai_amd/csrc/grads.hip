@@ -11,15 +11,21 @@
 namespace mx {
 namespace {
 
-__global__ __launch_bounds__(256) void transpose_factors_kernel(const uint16_t *src, int64_t rows,
-                                                                int64_t cols, int64_t total,
-                                                                uint16_t *dst) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= total) return;
-  const int64_t per = rows * cols;
+// Several [E, rows, cols] -> [E, cols, rows] transposes in one launch: thread
+// i belongs to the first job whose element range ends past i.
+__global__ __launch_bounds__(256) void transpose_factors_multi_kernel(FactorTransposes jobs) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  int j = 0;
+  while (j < jobs.n && i >= jobs.job[j].total) {
+    i -= jobs.job[j].total;
+    ++j;
+  }
+  if (j >= jobs.n) return;
+  const FactorTranspose &t = jobs.job[j];
+  const int64_t per = t.rows * t.cols;
   const int64_t e = i / per, rem = i - e * per;
-  const int64_t r = rem / cols, c = rem - r * cols;
-  dst[e * per + c * rows + r] = src[i];
+  const int64_t r = rem / t.cols, c = rem - r * t.cols;
+  t.dst[e * per + c * t.rows + r] = t.src[i];
 }
 
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
@@ -225,13 +231,13 @@ int swiglu_backward(uint16_t *dgu, const uint16_t *g, const uint16_t *u, int64_t
   return check_launch("SwiGLU backward");
 }
 
-int transpose_factors(const uint16_t *src, int64_t experts, int64_t rows, int64_t cols,
-                      uint16_t *dst, hipStream_t s) {
-  const int64_t total = experts * rows * cols;
+int transpose_factors_multi(const FactorTransposes &jobs, hipStream_t s) {
+  int64_t total = 0;
+  for (int j = 0; j < jobs.n; ++j) total += jobs.job[j].total;
   if (total <= 0) return MX_OK;
-  hipLaunchKernelGGL(transpose_factors_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))),
-                     dim3(256), 0, s, src, rows, cols, total, dst);
-  return check_launch("LoRA factor transpose");
+  hipLaunchKernelGGL(transpose_factors_multi_kernel,
+                     dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0, s, jobs);
+  return check_launch("LoRA factor transposes");
 }
 
 int lora_weight_grad(const uint16_t *m, int64_t ldm, const int32_t *map, const uint16_t *v,
