@@ -61,6 +61,12 @@ __device__ __forceinline__ int sorted_slots(const int64_t *idx_row, int k, int E
   return n;
 }
 
+// 16-byte load that bypasses cache retention: each y row is read exactly once.
+__device__ __forceinline__ uint4 nt_load16(const uint16_t *p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 // Stores 8 combined columns at element offset `off`. With an addend (same
 // dtype and layout as out) the value is out_dtype(out_dtype(sum) + addend):
 // the routed sum is rounded to the output dtype first and then added, as the
@@ -171,8 +177,7 @@ __global__ __launch_bounds__(256) void combine_wave_kernel(const uint16_t *y, co
     for (int u = 0; u < 4; ++u)
 #pragma unroll
       for (int q = 0; q < KC; ++q)
-        v[u][q] = ok[q] ? *reinterpret_cast<const uint4 *>(row[q] + c0 + 512 * u)
-                        : make_uint4(0, 0, 0, 0);
+        v[u][q] = ok[q] ? nt_load16(row[q] + c0 + 512 * u) : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       float acc[8];
