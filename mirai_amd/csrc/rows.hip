@@ -87,12 +87,9 @@ __device__ __forceinline__ void store_combined(void *out, int out_dtype, const v
         v[2 * q + 1] = round_bf16(v[2 * q + 1]) + bf16_bits_to_f32(aw[q] >> 16);
       }
     }
-    uint4 o;
-    o.x = pack_bf16x2(v[0], v[1]);
-    o.y = pack_bf16x2(v[2], v[3]);
-    o.z = pack_bf16x2(v[4], v[5]);
-    o.w = pack_bf16x2(v[6], v[7]);
-    *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + off) = o;
+    const u32x4 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                     pack_bf16x2(v[6], v[7])};
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(out) + off));
   } else {
     float4 *o = reinterpret_cast<float4 *>(static_cast<float *>(out) + off);
     float4 lo = make_float4(acc[0], acc[1], acc[2], acc[3]);
