@@ -501,6 +501,11 @@ extern "C" int mx_router_forward(const void *tokens, int token_dtype, int64_t nu
     set_error("mx_router_forward: num_experts must be in [1, 256], got %d", num_experts);
     return MX_ERR_INVALID;
   }
+  if (static_cast<int64_t>(3) * router_padded_experts(num_experts) * hidden >= (int64_t(1) << 31)) {
+    set_error("mx_router_forward: the weight planes (3 x %d x %lld) exceed the 32-bit offsets of "
+              "the kernel", router_padded_experts(num_experts), static_cast<long long>(hidden));
+    return MX_ERR_INVALID;
+  }
   if (top_k <= 0 || top_k > kRouterMaxTopK || top_k > num_experts) {
     set_error("mx_router_forward: top_k must be in [1, min(16, num_experts)], got %d", top_k);
     return MX_ERR_INVALID;
