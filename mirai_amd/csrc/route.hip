@@ -95,20 +95,31 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float *logits, in
 // better); the scan runs in increasing expert order, so a strict > keeps the
 // lower id on ties.
 template <int EC>
-__global__ __launch_bounds__(256) void route_topk_lane_kernel(const float *logits, int64_t T,
+__global__ __launch_bounds__(64) void route_topk_lane_kernel(const float *logits, int64_t T,
                                                               int E, int k, int renorm,
                                                               float route_scale, int64_t *top_idx,
                                                               void *top_scores, int score_dtype) {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= T) return;
   const float *row = logits + t * E;
   float v[EC];
+  if ((E & 3) == 0) {  // 16-byte row loads (rows are 16-byte aligned)
+#pragma unroll
+    for (int e = 0; e < EC; e += 4) {
+      const float4 q = e < E ? *reinterpret_cast<const float4 *>(row + e)
+                             : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      v[e] = q.x;
+      v[e + 1] = q.y;
+      v[e + 2] = q.z;
+      v[e + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EC; ++e) v[e] = e < E ? row[e] : -INFINITY;
+  }
   float m = -INFINITY;
 #pragma unroll
-  for (int e = 0; e < EC; ++e) {
-    v[e] = e < E ? row[e] : -INFINITY;
-    m = fmaxf(m, v[e]);
-  }
+  for (int e = 0; e < EC; ++e) m = fmaxf(m, v[e]);
   float z = 0.0f;
 #pragma unroll
   for (int e = 0; e < EC; ++e)
@@ -389,10 +400,11 @@ extern "C" int mx_route_topk(const float *logits, int64_t num_tokens, int num_ex
   }
   if (num_tokens == 0) return MX_OK;
   if (num_experts <= 64) {
-    const dim3 grid(static_cast<unsigned>(ceil_div(num_tokens, 256)));
+    // One-wave workgroups spread the tokens over every CU.
+    const dim3 grid(static_cast<unsigned>(ceil_div(num_tokens, 64)));
     hipStream_t s = as_stream(stream);
 #define MX_ROUTE_LANE(EC)                                                                    \
-  hipLaunchKernelGGL(route_topk_lane_kernel<EC>, grid, dim3(256), 0, s, logits, num_tokens,   \
+  hipLaunchKernelGGL(route_topk_lane_kernel<EC>, grid, dim3(64), 0, s, logits, num_tokens,    \
                      num_experts, top_k, renorm, route_scale, top_idx, top_scores, score_dtype)
     if (num_experts <= 8)
       MX_ROUTE_LANE(8);
