@@ -11,21 +11,78 @@
 namespace mx {
 namespace {
 
-// Several [E, rows, cols] -> [E, cols, rows] transposes in one launch: thread
-// i belongs to the first job whose element range ends past i.
-__global__ __launch_bounds__(256) void transpose_factors_multi_kernel(FactorTransposes jobs) {
-  int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+// Several [E, rows, cols] -> [E, cols, rows] transposes in one launch. One of
+// rows / cols is a LoRA rank (at most 32): a thread moves the rank-long run at
+// one position of the other (long) dimension, so the long dimension runs
+// across the lanes of a wave and both the loads and the stores are coalesced.
+// Runs are moved as 16-byte vectors when the rank is a multiple of 8 and both
+// buffers are 16-byte aligned. Workgroups [block0[j], block0[j + 1]) serve job j.
+struct TransposeLaunch {
+  FactorTranspose job[6];
+  int64_t block0[7];
+  int vec[6];
+  int n;
+};
+
+__global__ __launch_bounds__(256) void transpose_factors_multi_kernel(TransposeLaunch L) {
   int j = 0;
-  while (j < jobs.n && i >= jobs.job[j].total) {
-    i -= jobs.job[j].total;
-    ++j;
+  while (j + 1 < L.n && static_cast<int64_t>(blockIdx.x) >= L.block0[j + 1]) ++j;
+  const FactorTranspose &t = L.job[j];
+  const bool small_rows = t.rows <= t.cols;
+  const uint32_t S = static_cast<uint32_t>(small_rows ? t.rows : t.cols);
+  const uint32_t Lg = static_cast<uint32_t>(small_rows ? t.cols : t.rows);
+  const uint32_t idx = static_cast<uint32_t>(
+      (static_cast<int64_t>(blockIdx.x) - L.block0[j]) * 256 + threadIdx.x);
+  if (static_cast<int64_t>(idx) * S >= t.total) return;
+  const uint32_t e = idx / Lg, l = idx - e * Lg;
+  const int64_t base = static_cast<int64_t>(e) * S * Lg;
+  const uint16_t *src = t.src + base;
+  uint16_t *dst = t.dst + base;
+  const bool vec = L.vec[j] != 0;
+  uint16_t v[32];
+  if (small_rows) {  // src [S][Lg] -> dst [Lg][S]: gather the column, store the run
+#pragma unroll
+    for (int s = 0; s < 32; ++s)
+      if (s < static_cast<int>(S)) v[s] = src[static_cast<int64_t>(s) * Lg + l];
+    uint16_t *run = dst + static_cast<int64_t>(l) * S;
+    if (vec) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (q * 8 < static_cast<int>(S)) {
+          u32x4 w;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            w[i] = static_cast<uint32_t>(v[q * 8 + 2 * i]) |
+                   (static_cast<uint32_t>(v[q * 8 + 2 * i + 1]) << 16);
+          *reinterpret_cast<u32x4 *>(run + q * 8) = w;
+        }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 32; ++s)
+        if (s < static_cast<int>(S)) run[s] = v[s];
+    }
+  } else {  // src [Lg][S] -> dst [S][Lg]: load the run, scatter it down the column
+    const uint16_t *run = src + static_cast<int64_t>(l) * S;
+    if (vec) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (q * 8 < static_cast<int>(S)) {
+          const u32x4 w = *reinterpret_cast<const u32x4 *>(run + q * 8);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[q * 8 + 2 * i] = static_cast<uint16_t>(w[i] & 0xFFFFu);
+            v[q * 8 + 2 * i + 1] = static_cast<uint16_t>(w[i] >> 16);
+          }
+        }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 32; ++s)
+        if (s < static_cast<int>(S)) v[s] = run[s];
+    }
+#pragma unroll
+    for (int s = 0; s < 32; ++s)
+      if (s < static_cast<int>(S)) dst[static_cast<int64_t>(s) * Lg + l] = v[s];
   }
-  if (j >= jobs.n) return;
-  const FactorTranspose &t = jobs.job[j];
-  const int64_t per = t.rows * t.cols;
-  const int64_t e = i / per, rem = i - e * per;
-  const int64_t r = rem / t.cols, c = rem - r * t.cols;
-  t.dst[e * per + c * t.rows + r] = t.src[i];
 }
 
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
@@ -232,11 +289,28 @@ int swiglu_backward(uint16_t *dgu, const uint16_t *g, const uint16_t *u, int64_t
 }
 
 int transpose_factors_multi(const FactorTransposes &jobs, hipStream_t s) {
-  int64_t total = 0;
-  for (int j = 0; j < jobs.n; ++j) total += jobs.job[j].total;
-  if (total <= 0) return MX_OK;
-  hipLaunchKernelGGL(transpose_factors_multi_kernel,
-                     dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0, s, jobs);
+  TransposeLaunch L = {};
+  int64_t blocks = 0;
+  for (int j = 0; j < jobs.n; ++j) {
+    const FactorTranspose &t = jobs.job[j];
+    const int64_t small = t.rows < t.cols ? t.rows : t.cols;
+    if (t.total < 0 || (t.total > 0 && (small < 1 || small > 32 || t.total / small >= (int64_t{1} << 31)))) {
+      set_error("LoRA factor transposes: one dimension must be a rank in [1, 32] and the other "
+                "times the experts below 2^31 (got %lld x %lld)",
+                static_cast<long long>(t.rows), static_cast<long long>(t.cols));
+      return MX_ERR_INVALID;
+    }
+    L.job[L.n] = t;
+    L.block0[L.n] = blocks;
+    L.vec[L.n] = small % 8 == 0 && reinterpret_cast<uintptr_t>(t.src) % 16 == 0 &&
+                 reinterpret_cast<uintptr_t>(t.dst) % 16 == 0;
+    blocks += t.total > 0 ? ceil_div(t.total / small, 256) : 0;
+    ++L.n;
+  }
+  L.block0[L.n] = blocks;
+  if (blocks <= 0) return MX_OK;
+  hipLaunchKernelGGL(transpose_factors_multi_kernel, dim3(static_cast<unsigned>(blocks)),
+                     dim3(256), 0, s, L);
   return check_launch("LoRA factor transposes");
 }
 
