@@ -98,7 +98,10 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(
   const int b_lo = gact ? static_cast<int>(static_cast<int64_t>(n_blocks) * ge / G) : 0;
   const int b_hi = gact ? static_cast<int>(static_cast<int64_t>(n_blocks) * (ge + 1) / G) : 0;
   if (gact) {
+    // Unrolled so that several block counts are in flight at once: the loop is
+    // latency bound (one workgroup, 16+ loads per thread).
     int32_t c = 0;
+#pragma unroll 8
     for (int b = b_lo; b < b_hi; ++b) c += block_counts[static_cast<int64_t>(b) * E + ee];
     part[t] = c;
   }
@@ -140,6 +143,7 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(
   if (gact) {
     int64_t run = start_s[ee];
     for (int gg = 0; gg < ge; ++gg) run += part[gg * E + ee];
+#pragma unroll 8
     for (int b = b_lo; b < b_hi; ++b) {
       const int64_t i = static_cast<int64_t>(b) * E + ee;
       block_base[i] = static_cast<int32_t>(run);
