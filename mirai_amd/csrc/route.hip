@@ -89,6 +89,91 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float *logits, in
   }
 }
 
+// The same routing with four lanes per token for 32 < E <= 64 (E a multiple
+// of 4): lane q of a quad holds experts [16q, 16q + 16), one 64-byte run of the
+// row, so a wave reads 16 whole rows and a token's serial chains are a quarter
+// as long. The row max, the softmax sum (four partial sums added in a fixed
+// tree) and each round's pick are combined across the quad by lane exchanges.
+// A pick is the largest remaining value, the lowest id on ties (the serial
+// scan's rule: NaN keys never win, and the first valid id stands in when all
+// remaining values are -inf); the quad's owner of the pick marks it NaN.
+__global__ __launch_bounds__(256) void route_topk_quad_kernel(const float *logits, int64_t T,
+                                                              int E, int k, int renorm,
+                                                              float route_scale, int64_t *top_idx,
+                                                              void *top_scores, int score_dtype) {
+  const int64_t t = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 2;
+  if (t >= T) return;  // whole quads leave together
+  const int q = threadIdx.x & 3, e0 = 16 * q;
+  const float *row = logits + t * E + e0;
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; i += 4) {
+    const float4 x = e0 + i < E ? *reinterpret_cast<const float4 *>(row + i)
+                                : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    v[i] = x.x;
+    v[i + 1] = x.y;
+    v[i + 2] = x.z;
+    v[i + 3] = x.w;
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) m = fmaxf(m, v[i]);
+  m = fmaxf(m, __shfl_xor(m, 1));
+  m = fmaxf(m, __shfl_xor(m, 2));
+  float z = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (e0 + i < E) z += __expf(v[i] - m);
+  z += __shfl_xor(z, 1);
+  z += __shfl_xor(z, 2);
+  int sel[kMaxTopK];
+  float p[kMaxTopK];
+  float sum = 0.0f;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    sel[r] = 0;
+    p[r] = 0.0f;
+    if (r < k) {
+      float bv = -INFINITY;
+      int be = -1;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (e0 + i < E && (v[i] > bv || (be < 0 && v[i] == bv))) {
+          bv = v[i];
+          be = e0 + i;
+        }
+#pragma unroll
+      for (int off = 1; off <= 2; off <<= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oe = __shfl_xor(be, off);
+        if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) {
+          bv = ov;
+          be = oe;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (e0 + i == be) v[i] = __builtin_nanf("");
+      sel[r] = be;
+      p[r] = __expf(bv - m) / z;
+      sum += p[r];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    if (r >= k) break;
+    if ((r & 3) != q) continue;
+    float score = p[r];
+    if (renorm == MX_RENORM_CLAMP)
+      score = p[r] / fmaxf(sum, 1e-20f);
+    else if (renorm == MX_RENORM_EPS)
+      score = p[r] / (sum + 1e-20f);
+    score *= route_scale;
+    top_idx[t * k + r] = sel[r];
+    store_value(top_scores, t * k + r, score, score_dtype);
+  }
+}
+
 // The same routing with one LANE per token for E <= 64: the lane holds its
 // token's logits in registers, so the max, the softmax sum and the k selection
 // rounds need no cross-lane exchange. Taken experts become NaN keys (never
@@ -399,6 +484,12 @@ extern "C" int mx_route_topk(const float *logits, int64_t num_tokens, int num_ex
     return MX_ERR_INVALID;
   }
   if (num_tokens == 0) return MX_OK;
+  if (num_experts > 32 && num_experts <= 64 && (num_experts & 3) == 0) {
+    hipLaunchKernelGGL(route_topk_quad_kernel, dim3(static_cast<unsigned>(ceil_div(num_tokens, 64))),
+                       dim3(256), 0, as_stream(stream), logits, num_tokens, num_experts, top_k,
+                       renorm, route_scale, top_idx, top_scores, score_dtype);
+    return check_launch("mx_route_topk");
+  }
   if (num_experts <= 64) {
     // One-wave workgroups spread the tokens over every CU.
     const dim3 grid(static_cast<unsigned>(ceil_div(num_tokens, 64)));

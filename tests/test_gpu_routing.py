@@ -24,11 +24,13 @@ def test_route_matches_oracle_on_benchmark_logits(name):
 
 
 @pytest.mark.parametrize("renorm", ["clamp", "eps", "none"])
-@pytest.mark.parametrize("experts,k", [(8, 2), (100, 3), (128, 8), (1024, 16), (5, 5)])
+@pytest.mark.parametrize("experts,k", [(8, 2), (100, 3), (128, 8), (1024, 16), (5, 5), (64, 4),
+                                        (40, 6), (36, 16), (48, 1)])
 def test_route_modes_and_shapes(renorm, experts, k):
     g = torch.Generator().manual_seed(experts * 31 + k)
     logits = torch.randn(333, experts, generator=g)
     logits[::7, : experts // 2] = 0.25  # ties: equal logits go to the lower expert id
+    logits[3::11, experts // 3:] = -float("inf")  # -inf logits, taken last in id order
     idx, scores = route_topk(logits.cuda(), k, renorm=renorm, route_scale=2.5,
                              score_dtype=torch.float32)
     ref_idx, ref_scores = oroute.route_topk(logits.numpy(), k, renorm=RENORMS[renorm],
