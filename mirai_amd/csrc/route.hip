@@ -126,50 +126,55 @@ __global__ __launch_bounds__(256) void route_topk_quad_kernel(const float *logit
     if (e0 + i < E) z += __expf(v[i] - m);
   z += __shfl_xor(z, 1);
   z += __shfl_xor(z, 2);
-  int sel[kMaxTopK];
-  float p[kMaxTopK];
+  // Lane q keeps the picks of rounds q, q + 4, q + 8, q + 12 (the ones it
+  // stores); the rounds loop stays rolled, so the registers stay few.
+  int my_sel[4] = {0, 0, 0, 0};
+  float my_p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   float sum = 0.0f;
+#pragma unroll 1
+  for (int r = 0; r < k; ++r) {
+    float bv = -INFINITY;
+    int be = -1;
 #pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r) {
-    sel[r] = 0;
-    p[r] = 0.0f;
-    if (r < k) {
-      float bv = -INFINITY;
-      int be = -1;
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (e0 + i < E && (v[i] > bv || (be < 0 && v[i] == bv))) {
-          bv = v[i];
-          be = e0 + i;
-        }
-#pragma unroll
-      for (int off = 1; off <= 2; off <<= 1) {
-        const float ov = __shfl_xor(bv, off);
-        const int oe = __shfl_xor(be, off);
-        if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) {
-          bv = ov;
-          be = oe;
-        }
+    for (int i = 0; i < 16; ++i)
+      if (e0 + i < E && (v[i] > bv || (be < 0 && v[i] == bv))) {
+        bv = v[i];
+        be = e0 + i;
       }
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (e0 + i == be) v[i] = __builtin_nanf("");
-      sel[r] = be;
-      p[r] = __expf(bv - m) / z;
-      sum += p[r];
+    for (int off = 1; off <= 2; off <<= 1) {
+      const float ov = __shfl_xor(bv, off);
+      const int oe = __shfl_xor(be, off);
+      if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) {
+        bv = ov;
+        be = oe;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (e0 + i == be) v[i] = __builtin_nanf("");
+    const float pr = __expf(bv - m) / z;
+    sum += pr;
+    if ((r & 3) == q) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if ((r >> 2) == j) {
+          my_sel[j] = be;
+          my_p[j] = pr;
+        }
     }
   }
 #pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r) {
+  for (int j = 0; j < 4; ++j) {
+    const int r = 4 * j + q;
     if (r >= k) break;
-    if ((r & 3) != q) continue;
-    float score = p[r];
+    float score = my_p[j];
     if (renorm == MX_RENORM_CLAMP)
-      score = p[r] / fmaxf(sum, 1e-20f);
+      score = my_p[j] / fmaxf(sum, 1e-20f);
     else if (renorm == MX_RENORM_EPS)
-      score = p[r] / (sum + 1e-20f);
+      score = my_p[j] / (sum + 1e-20f);
     score *= route_scale;
-    top_idx[t * k + r] = sel[r];
+    top_idx[t * k + r] = my_sel[j];
     store_value(top_scores, t * k + r, score, score_dtype);
   }
 }
