@@ -92,6 +92,8 @@ int mx_abi_version(void);
  * renorm MX_RENORM_EPS when norm_topk_prob, else MX_RENORM_NONE).
  * Selection is by logit (softmax is monotone); ties go to the lower expert id;
  * slots are written in descending-score order. E <= 1024, 1 <= k <= 16.
+ * `logits` needs only fp32 alignment; a 16-byte aligned base with E % 4 == 0
+ * takes 16-byte row loads.
  */
 int mx_route_topk(const float *logits, int64_t num_tokens, int num_experts, int top_k,
                   int renorm, float route_scale, int64_t *top_idx, void *top_scores,

@@ -12,6 +12,7 @@ from .dispatch import (
     combine_routed_tokens,
     permute_routed_tokens,
 )
+from ._native import RouteIndexError, check_route_errors, set_route_check
 from .experts import CompressedGroupedExperts
 from .lora import ActiveExpertLoRA, lora_scale
 from .magi2 import Magi2FusedMoEBackend, Magi2GroupedExperts, route_topk_heads
@@ -21,9 +22,7 @@ from .specs import (
     CANONICAL_PACKED_EXPERT_MLP_SPEC,
     ExpertMLPExecutionSpec,
     ExpertProjectionRole,
-    MoEOptimizationPolicy,
-    active_moe_optimization_policy,
-    get_active_moe_optimization_policy,
+    as_execution_spec,
 )
 
 __all__ = [
@@ -32,20 +31,21 @@ __all__ = [
     "CompressedGroupedExperts",
     "DispatchPlan",
     "FusedRouter",
+    "RouteIndexError",
     "ExpertMLPExecutionSpec",
     "ExpertProjectionRole",
     "Magi2FusedMoEBackend",
     "Magi2GroupedExperts",
-    "MoEOptimizationPolicy",
-    "active_moe_optimization_policy",
+    "as_execution_spec",
     "build_dispatch_plan",
     "build_expert_choice_dispatch_plan",
+    "check_route_errors",
     "combine_routed_tokens",
     "fused_router_forward",
-    "get_active_moe_optimization_policy",
     "lora_scale",
     "permute_routed_tokens",
     "route_topk",
     "route_topk_heads",
     "router_weight_planes",
+    "set_route_check",
 ]

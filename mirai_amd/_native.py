@@ -8,6 +8,7 @@ raises :class:`NativeLibraryError` when the library or a GPU is missing.
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
 from pathlib import Path
 from typing import Any
@@ -221,3 +222,103 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+# --------------------------------------------------------- route errors
+# The dispatch plan counts route slots whose expert id lies outside
+# [0, num_experts) (and, for count-driven plans, counts that do not add up)
+# into the workspace's error counter; such slots are left out of every
+# expert. The reference's torch.bincount raises on such ids
+# (dispatch_preprocess.py:155-157). Reading the counter needs the GPU to have
+# run the plan, so by default ("deferred") each call copies it into a pinned
+# host slot on its stream and the count is read once that copy has landed:
+# at the start of a later call, or by check_route_errors(), which waits. With
+# "sync" the call itself waits for its plan and raises; "off" skips the copy.
+# Calls captured into a HIP graph are not watched.
+ROUTE_CHECK_MODES = ("deferred", "sync", "off")
+_route_check = os.environ.get("MIRAI_ROUTE_CHECK", "deferred").strip().lower()
+if _route_check not in ROUTE_CHECK_MODES:  # pragma: no cover - environment
+    _route_check = "deferred"
+_SLOTS = 256
+_slot_buf: torch.Tensor | None = None
+_slot_next = 0
+_pending: list = []  # (event, slot index, what)
+
+
+class RouteIndexError(ValueError):
+    """Routed expert ids outside [0, num_experts) reached the dispatch plan."""
+
+
+def set_route_check(mode: str) -> None:
+    """Select how invalid route ids are reported: "deferred" (default),
+    "sync" (raise at the call, after a wait for its plan) or "off"."""
+    global _route_check
+    mode = str(mode).strip().lower()
+    if mode not in ROUTE_CHECK_MODES:
+        raise ValueError(f"route check mode must be one of {ROUTE_CHECK_MODES}.")
+    _route_check = mode
+
+
+def route_check_mode() -> str:
+    return _route_check
+
+
+def _raise_for(count: int, what: str, deferred: bool) -> None:
+    when = "an earlier " if deferred else ""
+    raise RouteIndexError(
+        f"{count} route slot(s) of {when}{what} carry an expert id outside "
+        f"[0, num_experts) or counts that do not match the rows; those slots were left "
+        f"out of the expert computation.")
+
+
+def _drain(block: bool) -> None:
+    while _pending:
+        event, slot, what = _pending[0]
+        if block:
+            event.synchronize()
+        elif not event.query():
+            return
+        _pending.pop(0)
+        count = int(_slot_buf[slot])
+        if count:
+            _pending.clear()
+            _raise_for(count, what, deferred=True)
+
+
+def poll_route_errors() -> None:
+    """Raise for an earlier call whose plan found invalid routes (no wait)."""
+    if _pending and not torch.cuda.is_current_stream_capturing():
+        _drain(block=False)
+
+
+def check_route_errors() -> None:
+    """Wait for every watched call's plan and raise if any found invalid routes."""
+    _drain(block=True)
+
+
+def watch_plan_errors(workspace: torch.Tensor, device: torch.device, what: str) -> None:
+    """Queue the plan error counter at the head of ``workspace`` for reading
+    (see ROUTE_CHECK_MODES); in "sync" mode wait for it and raise now."""
+    global _slot_buf, _slot_next
+    # Calls captured into a HIP graph are not watched: a capture may neither
+    # query events nor wait, and a replay would not refresh the slot.
+    if _route_check == "off" or torch.cuda.is_current_stream_capturing():
+        return
+    if _slot_buf is None:
+        _slot_buf = torch.zeros(_SLOTS, dtype=torch.int32, pin_memory=True)
+    slot = _slot_next
+    _slot_next = (_slot_next + 1) % _SLOTS
+    # A slot is reused only after its previous copy has been read.
+    while any(p[1] == slot for p in _pending):
+        _drain(block=True)
+    counter = workspace[:4].view(torch.int32)
+    _slot_buf[slot:slot + 1].copy_(counter, non_blocking=True)
+    event = torch.cuda.Event()
+    event.record(torch.cuda.current_stream(device))
+    if _route_check == "sync":
+        event.synchronize()
+        count = int(_slot_buf[slot])
+        if count:
+            _raise_for(count, what, deferred=False)
+        return
+    _pending.append((event, slot, what))

@@ -188,12 +188,13 @@ template <int EC>
 __global__ __launch_bounds__(64) void route_topk_lane_kernel(const float *logits, int64_t T,
                                                               int E, int k, int renorm,
                                                               float route_scale, int64_t *top_idx,
-                                                              void *top_scores, int score_dtype) {
+                                                              void *top_scores, int score_dtype,
+                                                              bool vec4) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= T) return;
   const float *row = logits + t * E;
   float v[EC];
-  if ((E & 3) == 0) {  // 16-byte row loads (rows are 16-byte aligned)
+  if (vec4) {  // 16-byte row loads: E % 4 == 0 and a 16-byte aligned base
 #pragma unroll
     for (int e = 0; e < EC; e += 4) {
       const float4 q = e < E ? *reinterpret_cast<const float4 *>(row + e)
@@ -489,7 +490,11 @@ extern "C" int mx_route_topk(const float *logits, int64_t num_tokens, int num_ex
     return MX_ERR_INVALID;
   }
   if (num_tokens == 0) return MX_OK;
-  if (num_experts > 32 && num_experts <= 64 && (num_experts & 3) == 0) {
+  // The quad kernel and the vector path of the lane kernel read rows as
+  // float4: E % 4 == 0 and a 16-byte aligned base (a view with a storage
+  // offset may not be); otherwise the lane kernel reads scalars.
+  const bool vec4 = (num_experts & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0;
+  if (num_experts > 32 && num_experts <= 64 && vec4) {
     hipLaunchKernelGGL(route_topk_quad_kernel, dim3(static_cast<unsigned>(ceil_div(num_tokens, 64))),
                        dim3(256), 0, as_stream(stream), logits, num_tokens, num_experts, top_k,
                        renorm, route_scale, top_idx, top_scores, score_dtype);
@@ -501,7 +506,8 @@ extern "C" int mx_route_topk(const float *logits, int64_t num_tokens, int num_ex
     hipStream_t s = as_stream(stream);
 #define MX_ROUTE_LANE(EC)                                                                    \
   hipLaunchKernelGGL(route_topk_lane_kernel<EC>, grid, dim3(64), 0, s, logits, num_tokens,    \
-                     num_experts, top_k, renorm, route_scale, top_idx, top_scores, score_dtype)
+                     num_experts, top_k, renorm, route_scale, top_idx, top_scores, score_dtype, \
+                     vec4)
     if (num_experts <= 8)
       MX_ROUTE_LANE(8);
     else if (num_experts <= 16)

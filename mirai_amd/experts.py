@@ -27,6 +27,7 @@ from .specs import (
     CANONICAL_PACKED_EXPERT_MLP_SPEC,
     FUSED_GATED_ACTIVATIONS,
     ExpertMLPExecutionSpec,
+    as_execution_spec,
     normalize_expert_weight_access_policy,
 )
 
@@ -59,7 +60,7 @@ class CompressedGroupedExperts(nn.Module):
                          expert_dequant_chunk_size=expert_dequant_chunk_size,
                          quant_format=quant_format, nf4_blocksize=nf4_blocksize,
                          execution_spec=spec)
-        for key in spec.tensor_names:
+        for key in self._spec.tensor_names:
             self.load_dense_weight(key, getattr(base, key))
 
     @classmethod
@@ -80,16 +81,17 @@ class CompressedGroupedExperts(nn.Module):
     # ------------------------------------------------------------------ state
     def _init_empty(self, *, num_experts, group_sizes, expert_weight_access,
                     expert_dequant_chunk_size, quant_format, nf4_blocksize, execution_spec):
-        if not isinstance(execution_spec, ExpertMLPExecutionSpec):
-            raise TypeError("execution_spec must use ExpertMLPExecutionSpec.")
-        if (not execution_spec.uses_gated_product
-                or execution_spec.activation not in FUSED_GATED_ACTIVATIONS):
+        # The provider's spec object may be the reference's own class: it is
+        # kept as given (provider code re-reads it and checks its type), and
+        # this module works from a validated copy of its fields.
+        spec = as_execution_spec(execution_spec)
+        if not spec.uses_gated_product or spec.activation not in FUSED_GATED_ACTIVATIONS:
             raise ValueError(
                 "The MI355X fused expert kernels implement the gated expert MLP "
                 "(activation 'silu' or 'swiglu7', combiner='gated_product')."
             )
         # Activation of the fused gate/up epilogue and of its backward.
-        self._kernel_activation = (nat.ACT_SWIGLU7 if execution_spec.activation == "swiglu7"
+        self._kernel_activation = (nat.ACT_SWIGLU7 if spec.activation == "swiglu7"
                                    else nat.ACT_SILU)
         if int(num_experts) <= 0 or int(num_experts) > nat.PLAN_MAX_EXPERTS:
             raise ValueError(f"num_experts must be in [1, {nat.PLAN_MAX_EXPERTS}].")
@@ -97,12 +99,15 @@ class CompressedGroupedExperts(nn.Module):
             raise ValueError("The MI355X NF4 format uses blocksize 64.")
         self.num_experts = int(num_experts)
         self.mirai_expert_mlp_spec = execution_spec
+        self._spec = spec
         self._group_sizes = group_sizes
         self._quant_format = quant.normalize_quant_format(quant_format)
         self._nf4_blocksize = int(nf4_blocksize)
         self._shapes: dict[str, tuple[int, int, int]] = {}
         self._loaded_dense_keys: set[str] = set()
         self.expert_lora = nn.ModuleDict()
+        self.logical_num_experts = int(num_experts)
+        self.prototype_logical_ids: tuple[int, ...] = ()
         self.set_expert_weight_access_policy(
             expert_weight_access=expert_weight_access,
             expert_dequant_chunk_size=expert_dequant_chunk_size,
@@ -110,7 +115,8 @@ class CompressedGroupedExperts(nn.Module):
         )
 
     @property
-    def expert_mlp_spec(self) -> ExpertMLPExecutionSpec:
+    def expert_mlp_spec(self):
+        """The spec object the module was built with (experts.py:282-284)."""
         return self.mirai_expert_mlp_spec
 
     @property
@@ -118,7 +124,7 @@ class CompressedGroupedExperts(nn.Module):
         return self._quant_format
 
     def projection_for_role(self, role: str) -> str:
-        return self.expert_mlp_spec.tensor_for_role(role)
+        return self._spec.tensor_for_role(role)
 
     def set_expert_weight_access_policy(self, *, expert_weight_access: str,
                                         expert_dequant_chunk_size: int = 0,
@@ -140,7 +146,7 @@ class CompressedGroupedExperts(nn.Module):
         return self.expert_weight_access in {"active_dequant", "chunked_dequant", "fused_kernel"}
 
     def is_fully_loaded(self) -> bool:
-        return self._loaded_dense_keys.issuperset(self.expert_mlp_spec.tensor_names)
+        return self._loaded_dense_keys.issuperset(self._spec.tensor_names)
 
     def expert_weight_shape(self, key: str) -> tuple[int, ...]:
         if str(key) in self._shapes:
@@ -157,7 +163,7 @@ class CompressedGroupedExperts(nn.Module):
                           rotation: torch.Tensor | None = None) -> None:
         """Quantise a dense [E, out, in] expert tensor into this module's format
         (experts.py:940-996; the MI355X formats of mirai_amd.quant)."""
-        if key not in self.expert_mlp_spec.tensor_names:
+        if key not in self._spec.tensor_names:
             raise ValueError(f"Unknown compressed_weights grouped expert tensor '{key}'.")
         if source.ndim != 3:
             raise ValueError(
@@ -185,7 +191,7 @@ class CompressedGroupedExperts(nn.Module):
         re-quantising: the GEMMs decode the payload's weights (fp32 absmax)."""
         if self._quant_format != "nf4":
             raise ValueError("packed NF4 payloads load into a module with quant_format='nf4'.")
-        if key not in self.expert_mlp_spec.tensor_names:
+        if key not in self._spec.tensor_names:
             raise ValueError(f"Unknown compressed_weights grouped expert tensor '{key}'.")
         if int(shape[0]) != self.num_experts:
             raise ValueError(
@@ -232,7 +238,7 @@ class CompressedGroupedExperts(nn.Module):
                            init: str = "kaiming", use_rslora: bool = False) -> nn.Module:
         """experts.py:544-571."""
         key = str(tensor_name)
-        if key not in self.expert_mlp_spec.tensor_names:
+        if key not in self._spec.tensor_names:
             raise ValueError(f"Unknown grouped expert LoRA tensor '{key}'.")
         if key in self.expert_lora:
             raise ValueError(f"Grouped expert LoRA is already attached to '{key}'.")
@@ -274,7 +280,7 @@ class CompressedGroupedExperts(nn.Module):
     # ----------------------------------------------------------- execution
     def _require_loaded(self) -> None:
         if not self.is_fully_loaded():
-            missing = sorted(set(self.expert_mlp_spec.tensor_names) - self._loaded_dense_keys)
+            missing = sorted(set(self._spec.tensor_names) - self._loaded_dense_keys)
             raise RuntimeError(
                 f"compressed_weights grouped experts are missing weights: {missing}.")
 
@@ -300,18 +306,85 @@ class CompressedGroupedExperts(nn.Module):
         if int(top_indices.shape[0]) != int(tokens.shape[0]):
             raise ValueError("Direct routed expert indices do not match token count.")
         self._require_loaded()
+        top_scores, top_indices = self._coalesce_logical_routes(top_scores, top_indices)
         from .fused import routed_experts
         return routed_experts(self, tokens, top_scores, top_indices)
 
     def logical_to_physical_map(self) -> tuple[int, ...]:
-        """Logical -> physical expert aliases of expert-choice routes (empty: identity)."""
+        """Logical -> physical expert aliases (empty: identity)."""
         return tuple(getattr(self, "_logical_to_physical", ()))
+
+    def has_logical_expert_aliases(self) -> bool:
+        return bool(self.logical_to_physical_map())
+
+    def configure_logical_expert_aliases(self, logical_to_physical, *,
+                                         prototype_logical_ids=None) -> None:
+        """Attach a validated logical-router -> physical-expert map
+        (experts.py:392-431 with validate_logical_to_physical,
+        storage/aliases.py:85-107): more logical than physical experts, every
+        physical id referenced, one prototype logical id per physical expert."""
+        values = tuple(int(v) for v in logical_to_physical)
+        if len(values) <= self.num_experts:
+            raise ValueError("A consolidated mapping must have more logical than physical experts.")
+        invalid = sorted({v for v in values if v < 0 or v >= self.num_experts})
+        if invalid:
+            raise ValueError(f"Logical-to-physical mapping contains invalid ids: {invalid}.")
+        missing = sorted(set(range(self.num_experts)) - set(values))
+        if missing:
+            raise ValueError(
+                f"Logical-to-physical mapping does not reference physical ids: {missing}.")
+        if prototype_logical_ids is None:
+            prototypes = tuple(values.index(p) for p in range(self.num_experts))
+        else:
+            prototypes = tuple(int(v) for v in prototype_logical_ids)
+        if len(prototypes) != self.num_experts or len(set(prototypes)) != len(prototypes):
+            raise ValueError(
+                "prototype_logical_ids must contain one unique id per physical expert.")
+        if any(v < 0 or v >= len(values) for v in prototypes):
+            raise ValueError("prototype_logical_ids contains an out-of-range logical id.")
+        if any(values[lid] != pid for pid, lid in enumerate(prototypes)):
+            raise ValueError("Each prototype logical id must map to its corresponding physical id.")
+        self.set_logical_to_physical_map(values)
+        self.logical_num_experts = len(values)
+        self.prototype_logical_ids = prototypes
 
     def set_logical_to_physical_map(self, aliases) -> None:
         aliases = tuple(int(v) for v in aliases)
         if any(v < 0 or v >= self.num_experts for v in aliases):
             raise ValueError("Logical expert alias map contains an invalid physical id.")
         self._logical_to_physical = aliases
+        self._alias_device_maps = {}
+
+    def _coalesce_logical_routes(self, top_scores: torch.Tensor, top_indices: torch.Tensor):
+        """Token-choice routes over logical experts -> physical routes
+        (experts.py:529-542 with coalesce_alias_routes, storage/aliases.py:156-199):
+        each slot takes its logical expert's physical id, and the scores of a
+        token's slots that land on one physical expert are summed into the
+        first such slot (the others keep the id with score 0). A logical id
+        outside the map becomes an invalid physical id, which the dispatch plan
+        reports (mirai_amd.check_route_errors) instead of a host sync here."""
+        aliases = self.logical_to_physical_map()
+        if not aliases:
+            return top_scores, top_indices
+        device = top_indices.device
+        maps = self.__dict__.setdefault("_alias_device_maps", {})
+        mapping = maps.get(str(device))
+        if mapping is None:
+            mapping = maps[str(device)] = torch.tensor(aliases, dtype=torch.long, device=device)
+        logical = top_indices.long()
+        valid = (logical >= 0) & (logical < len(aliases))
+        physical = torch.where(valid, mapping[logical.clamp(0, len(aliases) - 1)],
+                               torch.full_like(logical, -1))
+        k = int(physical.shape[1])
+        if k == 0:
+            return top_scores, physical
+        current = torch.arange(k, device=device).view(1, k, 1)
+        candidate = torch.arange(k, device=device).view(1, 1, k)
+        eligible = (physical.unsqueeze(2) == physical.unsqueeze(1)) & (candidate <= current)
+        first = torch.where(eligible, candidate.expand_as(eligible),
+                            torch.full_like(eligible, k, dtype=torch.long)).amin(dim=2)
+        coalesced = torch.zeros_like(top_scores).scatter_add(1, first, top_scores)
+        return coalesced, physical
 
     def run_expert_choice_routed(self, tokens: torch.Tensor, expert_token_scores: torch.Tensor,
                                  expert_token_indices: torch.Tensor, *,

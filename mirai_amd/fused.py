@@ -59,6 +59,7 @@ def _forward(module, tokens, top_scores, top_indices, need_grad, addend=None, ad
     addend [T, d] (bf16) the combine adds it to the rounded routed sum, after
     waiting for the event ``addend_ready`` (torch.cuda.Event or None)."""
     device = nat.require_gpu(tokens, top_scores, top_indices)
+    nat.poll_route_errors()
     # fp32 weights (quant_format "fp32") run the split-precision layer on
     # fp32 tokens; the other formats take bf16 tokens.
     split = module.quant_format == "fp32"
@@ -103,6 +104,7 @@ def _forward(module, tokens, top_scores, top_indices, need_grad, addend=None, ad
              nat.ptr(addend), addend_ready.cuda_event if addend_ready is not None else None,
              *[nat.ptr(t) for t in saves], ws.data_ptr(), nat.stream(device))
     del keep
+    nat.watch_plan_errors(ws, device, "a routed expert layer call")
     return out.to(tokens.dtype), ((x, scores, idx, *saves) if need_grad else None)
 
 
@@ -237,6 +239,7 @@ def sorted_experts(module, tokens, counts):
     nat.call("mx_moe_for_loop", x.data_ptr(), c.data_ptr(), S, module.num_experts, d, f, w1, w3,
              w2, lora[0], lora[1], lora[2], out.data_ptr(), ws.data_ptr(), nat.stream(device))
     del keep
+    nat.watch_plan_errors(ws, device, "a run_for_loop call")
     return out.to(tokens.dtype)
 
 
@@ -267,4 +270,5 @@ def grouped_projection(module, key, x, offsets):
     nat.call("mx_grouped_linear", xb.data_ptr(), counts.data_ptr(), S, module.num_experts,
              packed.descriptor(), lora, out.data_ptr(), ws.data_ptr(), nat.stream(device))
     del keep
+    nat.watch_plan_errors(ws, device, "a grouped_linear call")
     return out.to(x.dtype)

@@ -1,16 +1,15 @@
-"""Expert-MLP layout spec and the MoE runtime policy read by the expert op.
+"""Expert-MLP layout spec read by the expert op.
 
 Mirrors the names and validation of mirai/core/moe/runtime/specs.py
 (ExpertProjectionRole :111-127, ExpertMLPExecutionSpec :129-213,
 CANONICAL_PACKED_EXPERT_MLP_SPEC :222-231, normalize_expert_weight_access_policy
-:483-506, MoEOptimizationPolicy :234-267 and the active-policy helpers
-:555-600). Only the fields the expert op consumes are interpreted; the rest of
-the reference policy surface (storage, streaming, autotune) is out of scope.
+:483-506). Provider code hands the expert module its own spec objects
+(prepare.py:46-48, lingbot_video/pipeline.py:1678), so ``as_execution_spec``
+accepts any object with the same fields and converts it.
 """
 
 from __future__ import annotations
 
-from contextlib import contextmanager
 from dataclasses import dataclass
 
 # "swiglu7" extends the reference set with the MAGI-2 gated activation
@@ -29,9 +28,6 @@ EXPERT_WEIGHT_ACCESS_POLICIES = {
     "chunked_dequant",
     "fused_kernel",
 }
-MOE_DISPATCH_MODES = ("vectorized", "legacy", "triton", "triton_persistent")
-MOE_DISPATCH_PREPROCESS_MODES = ("host", "device", "sonic")
-MOE_GEMM_BACKENDS = ("auto", "bmm", "persistent", "torch_grouped", "deepgemm_fp8")
 
 _ACCESS_ALIASES = {
     "": "auto",
@@ -153,66 +149,19 @@ MAGI2_EXPERT_MLP_SPEC = ExpertMLPExecutionSpec(
 )
 
 
-@dataclass(frozen=True)
-class MoEOptimizationPolicy:
-    """The hot-path subset of the reference MoE runtime policy.
-
-    The dispatch / GEMM-backend fields are accepted for call-site
-    compatibility: on this build every setting runs the same fused MI355X
-    kernels, so they only have to name a valid reference mode.
-    """
-
-    expert_weight_access: str = "auto"
-    expert_dequant_chunk_size: int = 0
-    moe_dispatch: str = "vectorized"
-    moe_dispatch_preprocess: str = "host"
-    moe_gemm_backend: str = "auto"
-    moe_batched_dequant: bool = True
-    moe_pair_dequant: bool = True
-
-    def __post_init__(self) -> None:
-        access = normalize_expert_weight_access_policy(self.expert_weight_access)
-        dispatch = str(self.moe_dispatch or "vectorized").strip().lower()
-        if dispatch not in MOE_DISPATCH_MODES:
-            raise ValueError(
-                "memory.moe_dispatch must be one of: " + ", ".join(MOE_DISPATCH_MODES) + "."
-            )
-        preprocess = str(self.moe_dispatch_preprocess or "host").strip().lower()
-        if preprocess not in MOE_DISPATCH_PREPROCESS_MODES:
-            raise ValueError(
-                "memory.moe_dispatch_preprocess must be one of: "
-                + ", ".join(MOE_DISPATCH_PREPROCESS_MODES) + "."
-            )
-        backend = str(self.moe_gemm_backend or "auto").strip().lower()
-        if backend not in MOE_GEMM_BACKENDS:
-            raise ValueError(
-                "memory.moe_gemm_backend must be one of: " + ", ".join(MOE_GEMM_BACKENDS) + "."
-            )
-        if int(self.expert_dequant_chunk_size) < 0:
-            raise ValueError("memory.expert_dequant_chunk_size must be >= 0.")
-        object.__setattr__(self, "expert_weight_access", access)
-        object.__setattr__(self, "moe_dispatch", dispatch)
-        object.__setattr__(self, "moe_dispatch_preprocess", preprocess)
-        object.__setattr__(self, "moe_gemm_backend", backend)
-
-
-_ACTIVE_POLICY: MoEOptimizationPolicy | None = None
-
-
-def set_active_moe_optimization_policy(policy: MoEOptimizationPolicy | None) -> None:
-    global _ACTIVE_POLICY
-    _ACTIVE_POLICY = policy
-
-
-@contextmanager
-def active_moe_optimization_policy(policy: MoEOptimizationPolicy):
-    previous = _ACTIVE_POLICY
-    set_active_moe_optimization_policy(policy)
+def as_execution_spec(spec) -> ExpertMLPExecutionSpec:
+    """This package's spec for ``spec``: the object itself, or a validated copy
+    of any spec object exposing ``projections`` (items with ``role`` and
+    ``tensor_name``), ``activation`` and ``combiner`` -- the reference's own
+    ExpertMLPExecutionSpec included. Anything else raises TypeError, as the
+    reference's isinstance check does (experts.py:164-165)."""
+    if isinstance(spec, ExpertMLPExecutionSpec):
+        return spec
     try:
-        yield policy
-    finally:
-        set_active_moe_optimization_policy(previous)
-
-
-def get_active_moe_optimization_policy() -> MoEOptimizationPolicy:
-    return _ACTIVE_POLICY or MoEOptimizationPolicy()
+        projections = tuple(spec.projections)
+        roles = tuple(ExpertProjectionRole(str(p.role), str(p.tensor_name)) for p in projections)
+        activation = str(spec.activation)
+        combiner = str(spec.combiner)
+    except (AttributeError, TypeError) as exc:
+        raise TypeError("execution_spec must use ExpertMLPExecutionSpec.") from exc
+    return ExpertMLPExecutionSpec(projections=roles, activation=activation, combiner=combiner)

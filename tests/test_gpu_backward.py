@@ -8,9 +8,16 @@ the bf16 reference composition does, but the reference's autograd also sums
 the k routes of a token and the base/LoRA parts of each gradient in bf16, in
 an order torch does not fix. Bounds (stated per gradient, relative to the
 oracle): mean-relative error <= 1e-2 and max-abs error <= 3e-2 * max|oracle|.
-Size-independent checks at full C5 size: linearity in the upstream gradient
-(scaling dY by 2 scales every gradient by exactly 2) and run-to-run
-determinism (bit-identical gradients).
+Production tile shapes: experts averaging >= 256 rows run 256-row tiles plus
+one 128-row remainder tile per expert whose last rows number 1..128 (an
+expert whose last rows number 129..255 gets a partial 256-row tile). The
+tall-tile cases below meet that threshold and assert which tiles they cover;
+full C5 runs on every token (so on the production tiles) and is compared with
+the oracle on a token subset for d tokens / d scores, and per expert for the
+LoRA gradients (an expert's LoRA gradients sum only its own rows, so the
+oracle reproduces them from that expert's routes alone). Size-independent
+checks at full C5 size: linearity in the upstream gradient (scaling dY by 2
+scales every gradient by exactly 2) and run-to-run determinism.
 """
 
 import pytest
@@ -61,7 +68,7 @@ def _gpu_grads(m, x, scores, idx, dy):
     return out, {k: v.detach().clone() for k, v in grads.items()}
 
 
-def _oracle_grads(w, dense, lora, x, scores, idx, dy, rows):
+def _oracle_grads(w, dense, lora, x, scores, idx, dy, rows, weights=None):
     xo = x[rows].clone().requires_grad_(True)
     so = scores[rows].clone().requires_grad_(True)
     loras = {}
@@ -71,8 +78,9 @@ def _oracle_grads(w, dense, lora, x, scores, idx, dy, rows):
         b = b.clone().float().requires_grad_(True)
         leaves[key] = (a, b)
         loras[key] = (a, b, wl.lora_scale(w))
-    out = olayer.layer_forward(xo, so, idx[rows], oracle_weights(w, dense, dtype=torch.bfloat16),
-                               loras, w.experts)
+    if weights is None:
+        weights = oracle_weights(w, dense, dtype=torch.bfloat16)
+    out = olayer.layer_forward(xo, so, idx[rows], weights, loras, w.experts)
     out.backward(dy[rows])
     grads = {"tokens": xo.grad, "scores": so.grad}
     for key, (a, b) in leaves.items():
@@ -113,6 +121,87 @@ def test_backward_lora_ranks(r):
 
 def test_backward_ragged_experts():
     _case(small("int8", T=37, E=64, k=4, d=128, f=128))
+
+
+def _routes(w, bias=None):
+    logits = wl.router_logits(w)
+    if bias is not None:
+        logits = logits + bias
+    idx_np, scores_np = oroute.route_topk(logits.numpy(), w.top_k)
+    return torch.from_numpy(idx_np), torch.from_numpy(scores_np)
+
+
+def _tile_kinds(idx, E):
+    """(tall tiles used, experts with a 128-row remainder tile, experts whose
+    last rows need a partial 256-row tile) -- the plan's tile rule."""
+    counts = torch.bincount(idx.reshape(-1), minlength=E)
+    tall = int(counts.sum()) >= 256 * E
+    rem = counts % 256
+    return tall, int(((rem > 0) & (rem <= 128)).sum()), int((rem > 128).sum())
+
+
+def _case_routes(w, idx, scores, rows=None):
+    dense = wl.dense_weights(w)
+    lora = wl.lora_factors(w)
+    x = wl.tokens(w)
+    dy = wl.upstream_grad(w)
+    m = build_module(w, dense, lora)
+    rows = torch.arange(w.tokens) if rows is None else rows
+    _, g = _gpu_grads(m, x[rows], scores[rows], idx[rows], dy[rows])
+    _, ref = _oracle_grads(w, dense, lora, x, scores, idx, dy, rows)
+    for name, e in ref.items():
+        _close(name, g[name], e)
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "nf4", "int8"])
+def test_tall_tile_backward_matches_oracle(fmt):
+    # R = 4096 >= 256 * E: 256-row tiles; every gradient over all rows.
+    w = small(fmt, T=2048, E=8, k=2, d=256, f=192)
+    idx, scores = _routes(w)
+    tall, _, _ = _tile_kinds(idx, w.experts)
+    assert tall
+    _case_routes(w, idx, scores)
+
+
+def test_tall_tile_remainders_backward_matches_oracle():
+    # Skewed routes over 4 experts: remainders of both kinds.
+    w = small("nf4", T=700, E=4, k=2, d=192, f=256)
+    idx, scores = _routes(w, bias=torch.tensor([1.2, 0.45, 0.0, -0.9]))
+    tall, short_rem, long_rem = _tile_kinds(idx, w.experts)
+    assert tall and short_rem >= 1 and long_rem >= 1, torch.bincount(idx.reshape(-1))
+    _case_routes(w, idx, scores)
+
+
+def test_c5_full_size_backward_matches_oracle():
+    """Full C5 on the GPU (production tiles); oracle on a token subset for d
+    tokens / d scores and on each of three experts' routes for their LoRA
+    gradients."""
+    w = wl.WORKLOADS["c5"]
+    dense = wl.dense_weights(w)
+    lora = wl.lora_factors(w)
+    x = wl.tokens(w)
+    idx, scores = _routes(w)
+    assert _tile_kinds(idx, w.experts)[0]
+    dy = wl.upstream_grad(w)
+    m = build_module(w, dense, lora)
+    _, g = _gpu_grads(m, x, scores, idx, dy)
+    rows = torch.arange(0, w.tokens, 64)
+    weights = oracle_weights(w, dense, dtype=torch.bfloat16)
+    _, ref = _oracle_grads(w, dense, lora, x, scores, idx, dy, rows, weights)
+    _close("tokens", g["tokens"][rows.cuda()], ref["tokens"])
+    _close("scores", g["scores"][rows.cuda()], ref["scores"])
+    for e in (0, 17, 63):
+        tok, slot = torch.nonzero(idx == e, as_tuple=True)
+        # Expert e alone: its routes as k = 1 problems over its own tokens.
+        we = wl.Workload(w.name, w.index, int(tok.numel()), w.hidden, w.ffn, w.experts, 1,
+                         w.rank, w.alpha, w.fmt, w.dtype)
+        sub = torch.arange(int(tok.numel()))
+        _, ref_e = _oracle_grads(we, dense, lora, x[tok], scores[tok, slot].unsqueeze(1),
+                                 idx[tok, slot].unsqueeze(1), dy[tok], sub, weights)
+        for key in lora:
+            for part in ("a", "b"):
+                name = f"{key}.{part}"
+                _close(f"{name}[{e}]", g[name][e], ref_e[name][e])
 
 
 def test_c5_backward_on_token_subset():

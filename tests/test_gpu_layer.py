@@ -91,6 +91,13 @@ def test_c2_full_size_on_token_subset():
     _run_case(w, token_subset=subset)
 
 
+def test_target_shape_full_size_on_token_subset():
+    # The headline shape (C2 geometry at T = 32768, R = 131072): 256-row tiles
+    # and remainder tiles, as in the benchmark; compared on every 128th token.
+    w = wl.WORKLOADS["target"]
+    _run_case(w, token_subset=torch.arange(0, w.tokens, 128))
+
+
 def test_c3_zipf_full_size_on_token_subset():
     # E=128, top-8, Zipf-biased logits: at least 5 experts receive no token.
     w = wl.WORKLOADS["c3"]
@@ -144,3 +151,118 @@ def test_routed_layer_is_deterministic():
         b = m.run_direct_routed(x, scores, idx)
     assert torch.equal(a, b)
     np.testing.assert_array_equal(a.float().cpu().numpy(), b.float().cpu().numpy())
+
+
+def test_module_built_from_a_provider_base_with_a_foreign_spec():
+    """CompressedGroupedExperts(base) where the base carries its own spec class
+    and tensor names (as LingBot providers set mirai_expert_mlp_spec,
+    lingbot_video/pipeline.py:1678); the layer then matches the oracle."""
+    from dataclasses import dataclass
+
+    from mirai_amd import CompressedGroupedExperts
+
+    @dataclass(frozen=True)
+    class Role:
+        role: str
+        tensor_name: str
+
+    @dataclass(frozen=True)
+    class Spec:
+        projections: tuple
+        activation: str = "silu"
+        combiner: str = "gated_product"
+
+    w = small("nf4", T=200, E=6, k=2)
+    dense = wl.dense_weights(w)
+    spec = Spec((Role("gate", "gate_proj"), Role("up", "up_proj"), Role("down", "down_proj")))
+
+    class Base(torch.nn.Module):
+        num_experts = w.experts
+        mirai_expert_mlp_spec = spec
+
+        def __init__(self):
+            super().__init__()
+            self.gate_proj = dense["w1"].cuda()
+            self.up_proj = dense["w3"].cuda()
+            self.down_proj = dense["w2"].cuda()
+
+    m = CompressedGroupedExperts(Base(), quant_format="nf4", expert_weight_access="chunked_dequant",
+                                 expert_dequant_chunk_size=8)
+    assert m.expert_mlp_spec is spec and m.is_fully_loaded()
+    x = wl.tokens(w)
+    idx_np, scores_np = oroute.route_topk(wl.router_logits(w).numpy(), w.top_k)
+    idx, scores = torch.from_numpy(idx_np), torch.from_numpy(scores_np)
+    with torch.no_grad():
+        out = m.run_direct_routed(x.cuda(), scores.cuda(), idx.cuda())
+    ref = olayer.layer_forward(x, scores, idx, oracle_weights(w, dense), {}, w.experts)
+    assert_layer_close(out.cpu(), ref)
+
+
+def test_logical_aliases_coalesce_token_choice_routes():
+    """Routes over 10 logical experts aliased onto 6 physical ones
+    (experts.py:1767-1770): same output as the oracle on the coalesced
+    physical routes (duplicate physical slots summed into the first)."""
+    w = small("nf4", T=240, E=6, k=3)
+    dense = wl.dense_weights(w)
+    lora = wl.lora_factors(w)
+    m = build_module(w, dense, lora)
+    aliases = (0, 1, 2, 3, 4, 5, 2, 0, 5, 1)
+    m.configure_logical_expert_aliases(aliases)
+    g = torch.Generator().manual_seed(8)
+    idx = torch.stack([torch.randperm(10, generator=g)[:3] for _ in range(w.tokens)])
+    scores = torch.rand(w.tokens, 3, generator=g)
+    x = wl.tokens(w)
+    with torch.no_grad():
+        out = m.run_direct_routed(x.cuda(), scores.cuda(), idx.cuda())
+    phys = torch.tensor(aliases)[idx]
+    coalesced = torch.zeros_like(scores)
+    for t in range(w.tokens):
+        for j in range(3):
+            first = min(i for i in range(3) if phys[t, i] == phys[t, j])
+            coalesced[t, first] += scores[t, j]
+    assert bool((coalesced == 0).any())
+    ref = olayer.layer_forward(x, coalesced, phys, oracle_weights(w, dense),
+                               oracle_loras(w, lora), w.experts)
+    assert_layer_close(out.cpu(), ref)
+
+
+def test_out_of_range_route_ids_are_reported():
+    """Expert ids outside [0, E) are left out of the computation and reported
+    as RouteIndexError (a ValueError, as the reference's bincount refuses
+    negative ids, dispatch_preprocess.py:155-157): after the fact by default,
+    at the call in "sync" mode."""
+    import mirai_amd
+    from mirai_amd import _native as nat
+
+    w = small("bf16", T=64, E=8, k=2)
+    dense = wl.dense_weights(w)
+    m = build_module(w, dense, None)
+    x = wl.tokens(w)
+    idx_np, scores_np = oroute.route_topk(wl.router_logits(w).numpy(), w.top_k)
+    idx, scores = torch.from_numpy(idx_np), torch.from_numpy(scores_np)
+    bad = idx.clone()
+    bad[3, 1] = 8
+    bad[10, 0] = -1
+    mirai_amd.check_route_errors()
+    with torch.no_grad():
+        out = m.run_direct_routed(x.cuda(), scores.cuda(), bad.cuda())
+    with pytest.raises(mirai_amd.RouteIndexError, match="2 route slot"):
+        mirai_amd.check_route_errors()
+    # The valid slots are computed as usual.
+    kept = scores.clone()
+    kept[3, 1] = 0.0
+    kept[10, 0] = 0.0
+    ref = olayer.layer_forward(x, kept, bad.clamp(0, w.experts - 1), oracle_weights(w, dense),
+                               {}, w.experts)
+    assert_layer_close(out.cpu(), ref)
+    # Valid routes leave nothing behind.
+    with torch.no_grad():
+        m.run_direct_routed(x.cuda(), scores.cuda(), idx.cuda())
+    mirai_amd.check_route_errors()
+    previous = nat.route_check_mode()
+    mirai_amd.set_route_check("sync")
+    try:
+        with pytest.raises(ValueError, match="expert id outside"), torch.no_grad():
+            m.run_direct_routed(x.cuda(), scores.cuda(), bad.cuda())
+    finally:
+        mirai_amd.set_route_check(previous)

@@ -25,7 +25,8 @@ def test_route_matches_oracle_on_benchmark_logits(name):
 
 @pytest.mark.parametrize("renorm", ["clamp", "eps", "none"])
 @pytest.mark.parametrize("experts,k", [(8, 2), (100, 3), (128, 8), (1024, 16), (5, 5), (64, 4),
-                                        (40, 6), (36, 16), (48, 1)])
+                                        (40, 6), (36, 16), (48, 1), (16, 4), (12, 3), (24, 6),
+                                        (32, 8), (50, 5), (63, 16), (2, 1)])
 def test_route_modes_and_shapes(renorm, experts, k):
     g = torch.Generator().manual_seed(experts * 31 + k)
     logits = torch.randn(333, experts, generator=g)
@@ -52,3 +53,18 @@ def test_route_bf16_scores_and_backward():
     ref_grad = oroute.route_topk_backward(logits.numpy(), idx.cpu().numpy(), gs.numpy(),
                                           renorm=oroute.RENORM_CLAMP, route_scale=1.5)
     np.testing.assert_allclose(lg.grad.cpu().numpy(), ref_grad, rtol=1e-4, atol=2e-6)
+
+
+@pytest.mark.parametrize("experts,k", [(64, 4), (40, 6), (16, 4), (32, 8)])
+def test_route_misaligned_logits_view(experts, k):
+    # A contiguous view one float into its storage: the base is 4-byte but not
+    # 16-byte aligned, so the float4 row paths must not be taken.
+    g = torch.Generator().manual_seed(experts + k)
+    storage = torch.randn(257 * experts + 1, generator=g)
+    logits = storage[1:].view(257, experts)
+    dev = storage.cuda()[1:].view(257, experts)
+    assert dev.data_ptr() % 16 != 0
+    idx, scores = route_topk(dev, k, renorm="clamp", score_dtype=torch.float32)
+    ref_idx, ref_scores = oroute.route_topk(logits.numpy(), k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ref_idx)
+    np.testing.assert_allclose(scores.cpu().numpy(), ref_scores, rtol=3e-6, atol=1e-7)

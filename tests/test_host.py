@@ -127,6 +127,74 @@ def test_execution_spec_surface():
     assert spec.tensor_for_role("down") == "w2"
 
 
+# A spec class that is not this package's: the reference's own
+# ExpertMLPExecutionSpec (mirai/core/moe/runtime/specs.py:111-231) reaches the
+# module this way from provider code (prepare.py:137-151,
+# lingbot_video/pipeline.py:1678).
+from dataclasses import dataclass as _dataclass
+
+
+@_dataclass(frozen=True)
+class _ForeignRole:
+    role: str
+    tensor_name: str
+
+
+@_dataclass(frozen=True)
+class _ForeignSpec:
+    projections: tuple
+    activation: str = "silu"
+    combiner: str = "gated_product"
+
+
+_FOREIGN = _ForeignSpec((_ForeignRole("gate", "gate_proj"), _ForeignRole("up", "up_proj"),
+                         _ForeignRole("down", "down_proj")))
+
+
+def test_foreign_spec_objects_are_accepted_by_fields():
+    m = _module(execution_spec=_FOREIGN)
+    # The provider's object is kept as given; the module works from its fields.
+    assert m.mirai_expert_mlp_spec is _FOREIGN and m.expert_mlp_spec is _FOREIGN
+    assert m.projection_for_role("gate") == "gate_proj"
+    assert m.projection_for_role("down") == "down_proj"
+    with pytest.raises(ValueError, match="Unknown compressed_weights grouped expert tensor"):
+        m.load_dense_weight("w1", torch.zeros(4, 64, 64))
+    assert not m.is_fully_loaded()
+    # Field validation still applies to foreign specs.
+    with pytest.raises(ValueError):
+        _module(execution_spec=_ForeignSpec(_FOREIGN.projections, activation="tanh"))
+    with pytest.raises(ValueError):
+        _module(execution_spec=_ForeignSpec(_FOREIGN.projections[:2]))
+    with pytest.raises(TypeError):
+        _module(execution_spec=_ForeignSpec(projections=(object(),)))
+
+
+def test_foreign_spec_through_the_base_module_constructor():
+    class Base(torch.nn.Module):
+        num_experts = 4
+        mirai_expert_mlp_spec = _FOREIGN
+
+        def __init__(self):
+            super().__init__()
+            self.gate_proj = torch.zeros(4, 64, 64)
+            self.up_proj = torch.zeros(4, 64, 64)
+            self.down_proj = torch.zeros(4, 64, 64)
+
+    # Construction reads the foreign spec and goes on to quantise its tensors,
+    # which needs the GPU library: without a GPU the error is the library's,
+    # not a TypeError about the spec class.
+    if torch.cuda.is_available():
+        m = CompressedGroupedExperts(Base(), quant_format="nf4",
+                                     expert_weight_access="chunked_dequant",
+                                     expert_dequant_chunk_size=2)
+        assert m.is_fully_loaded() and m.expert_mlp_spec is _FOREIGN
+    else:
+        with pytest.raises(nat.NativeLibraryError):
+            CompressedGroupedExperts(Base(), quant_format="nf4",
+                                     expert_weight_access="chunked_dequant",
+                                     expert_dequant_chunk_size=2)
+
+
 def test_token_chunk_policy_surface():
     from mirai_amd.chunking import MoETokenChunkPolicy
 
@@ -177,3 +245,64 @@ def test_lora_scale_follows_alpha_buffer_updates():
     assert ad.scale() == pytest.approx(4.0)
     ad.load_state_dict({**ad.state_dict(), "lora_alpha": torch.tensor(8.0)})
     assert ad.scale() == pytest.approx(1.0)
+
+
+def _coalesce_brute(scores, idx, aliases):
+    """coalesce_alias_routes (storage/aliases.py:156-199) one slot at a time."""
+    T, k = idx.shape
+    phys = torch.tensor([[aliases[int(idx[t, j])] for j in range(k)] for t in range(T)])
+    out = torch.zeros_like(scores)
+    for t in range(T):
+        for j in range(k):
+            first = min(i for i in range(k) if phys[t, i] == phys[t, j])
+            out[t, first] += scores[t, j]
+    return out, phys
+
+
+def test_logical_alias_coalescing_matches_slot_by_slot_rule():
+    m = _module(num_experts=4)
+    aliases = (0, 1, 2, 3, 1, 2, 0, 3, 2)
+    m.configure_logical_expert_aliases(aliases)
+    assert m.has_logical_expert_aliases() and m.logical_num_experts == 9
+    assert m.prototype_logical_ids == (0, 1, 2, 3)
+    g = torch.Generator().manual_seed(4)
+    idx = torch.stack([torch.randperm(9, generator=g)[:4] for _ in range(200)])
+    scores = torch.rand(200, 4, generator=g, dtype=torch.float64).float()
+    got_s, got_p = m._coalesce_logical_routes(scores, idx)
+    want_s, want_p = _coalesce_brute(scores, idx, aliases)
+    assert torch.equal(got_p, want_p)
+    torch.testing.assert_close(got_s, want_s, rtol=0, atol=1e-7)
+    # At least one token must have had two slots on one physical expert.
+    assert bool((got_s == 0).any())
+    # Out-of-range logical ids become invalid physical ids (reported by the plan).
+    bad = idx.clone()
+    bad[5, 1] = 9
+    bad[7, 0] = -2
+    _, p = m._coalesce_logical_routes(scores, bad)
+    assert int(p[5, 1]) == -1 and int(p[7, 0]) == -1
+    # Gradients reach the scores through the coalescing.
+    sg = scores.clone().requires_grad_(True)
+    out, _ = m._coalesce_logical_routes(sg, idx)
+    out.sum().backward()
+    assert torch.equal(sg.grad, torch.ones_like(scores))
+
+
+def test_configure_logical_expert_aliases_validation():
+    m = _module(num_experts=4)
+    with pytest.raises(ValueError, match="more logical than physical"):
+        m.configure_logical_expert_aliases((0, 1, 2, 3))
+    with pytest.raises(ValueError, match="invalid ids"):
+        m.configure_logical_expert_aliases((0, 1, 2, 3, 4))
+    with pytest.raises(ValueError, match="does not reference"):
+        m.configure_logical_expert_aliases((0, 1, 2, 2, 1))
+    with pytest.raises(ValueError, match="corresponding physical id"):
+        m.configure_logical_expert_aliases((0, 1, 2, 3, 1), prototype_logical_ids=(0, 4, 2, 1))
+    assert not m.has_logical_expert_aliases()
+
+
+def test_route_check_modes():
+    assert nat.route_check_mode() in nat.ROUTE_CHECK_MODES
+    with pytest.raises(ValueError):
+        nat.set_route_check("loud")
+    assert issubclass(nat.RouteIndexError, ValueError)
+    nat.check_route_errors()  # nothing pending: returns
