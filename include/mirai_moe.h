@@ -358,6 +358,28 @@ size_t mx_moe_workspace_size(int64_t num_tokens, int top_k, int num_experts,
 size_t mx_moe_f32x3_workspace_size(int64_t num_tokens, int top_k, int num_experts,
                                    int64_t hidden, int64_t ffn);
 
+/* Size of the static device scratch of mx_moe_forward_static (64 MiB per GPU). */
+#define MX_STATIC_SCRATCH_BYTES (64u << 20)
+
+/*
+ * mx_moe_forward_act without a workspace argument and without saved
+ * activations (inference): the scratch is a static device array of
+ * MX_STATIC_SCRATCH_BYTES that each GPU holds until the process ends, so the
+ * call allocates nothing (no hipMalloc / hipFree, no allocating library call).
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops). Calls whose
+ * mx_moe_workspace_size (mx_moe_f32x3_workspace_size for MX_FMT_F32X3
+ * weights) exceeds MX_STATIC_SCRATCH_BYTES fail with MX_ERR_INVALID. Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU (on
+ * different streams or threads) race.
+ */
+int mx_moe_forward_static(const void *tokens, const int64_t *top_idx, const void *top_scores,
+                          int score_dtype, int64_t num_tokens, int top_k, int num_experts,
+                          int64_t hidden, int64_t ffn, int act, const mx_weight *w1,
+                          const mx_weight *w3, const mx_weight *w2, const mx_lora *l1,
+                          const mx_lora *l3, const mx_lora *l2, void *out, int out_dtype,
+                          void *stream);
+
 /*
  * fp32 -> bf16 planes for the fp32 path on bf16 MFMA. Row i of x (cols fp32)
  * becomes 3*cols bf16 values with hi = bf16(x), lo = bf16(x - hi), in the

@@ -46,6 +46,7 @@ ROUTE_LAYOUT_HEADS = 0
 ROUTE_LAYOUT_ROWS = 1
 
 PLAN_MAX_EXPERTS = 8192
+STATIC_SCRATCH_BYTES = 64 << 20  # MX_STATIC_SCRATCH_BYTES
 ROUTER_MAX_EXPERTS = 256  # mx_router_forward
 
 
@@ -132,6 +133,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         c_int,
         [_P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, c_int64, c_int, _W, _W, _W, _L, _L,
          _L, _P, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "mx_moe_forward_static": (
+        c_int,
+        [_P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, c_int64, c_int, _W, _W, _W, _L, _L,
+         _L, _P, c_int, _P]),
     "mx_moe_for_loop": (
         c_int, [_P, _P, c_int64, c_int, c_int64, c_int64, _W, _W, _W, _L, _L, _L, _P, _P, _P]),
     "mx_grouped_linear": (c_int, [_P, _P, c_int64, c_int, _W, _L, _P, _P, _P]),

@@ -18,6 +18,7 @@
 // expert's weights, run on the same XCD and hit its L2.
 #include <stdlib.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1500,6 +1501,93 @@ extern "C" int mx_moe_forward(const void *tokens, const int64_t *top_idx, const 
                             num_experts, hidden, ffn, MX_ACT_SILU, w1, w3, w2, l1, l3, l2, out,
                             out_dtype, save_gate, save_up, save_h, save_y, save_lora, workspace,
                             stream);
+}
+
+// ------------------------------------------------- allocation-free forward
+// mx_moe_forward_static runs mx_moe_forward_act on a file-scope device array
+// instead of a caller workspace, for callers that cannot allocate. Each GPU
+// holds its own copy of the array (loaded with the code object, freed at
+// process exit); its address on a device is looked up once, with that device
+// current, and kept. Calls that overlap on one GPU share the array and race.
+namespace {
+
+constexpr size_t kStaticScratchBytes = size_t(MX_STATIC_SCRATCH_BYTES);
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the stream's device (the current device for
+// the null stream). The array's name is only a host-side stand-in: kernels
+// and copies get this pointer.
+int static_scratch(const char *name, hipStream_t s, void **out) {
+  int dev = -1;
+  hipError_t err = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+  if (err != hipSuccess) {
+    set_error("%s: cannot resolve the stream's device: %s", name, hipGetErrorString(err));
+    return MX_ERR_HIP;
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) {
+    set_error("%s: device %d is beyond the %d devices the static scratch tracks", name, dev,
+              kMaxScratchDevices);
+    return MX_ERR_INVALID;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if ((err = hipGetDevice(&cur)) != hipSuccess) {
+      set_error("%s: hipGetDevice: %s", name, hipGetErrorString(err));
+      return MX_ERR_HIP;
+    }
+    if (cur != dev && (err = hipSetDevice(dev)) != hipSuccess) {
+      set_error("%s: hipSetDevice(%d): %s", name, dev, hipGetErrorString(err));
+      return MX_ERR_HIP;
+    }
+    void *ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (err != hipSuccess || !ptr) {
+      set_error("%s: hipGetSymbolAddress(scratch) on device %d: %s", name, dev,
+                hipGetErrorString(err));
+      return MX_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MX_OK;
+}
+
+}  // namespace
+
+extern "C" int mx_moe_forward_static(const void *tokens, const int64_t *top_idx,
+                                     const void *top_scores, int score_dtype, int64_t num_tokens,
+                                     int top_k, int num_experts, int64_t hidden, int64_t ffn,
+                                     int act, const mx_weight *w1, const mx_weight *w3,
+                                     const mx_weight *w2, const mx_lora *l1, const mx_lora *l3,
+                                     const mx_lora *l2, void *out, int out_dtype, void *stream) {
+  clear_error();
+  const char *name = "mx_moe_forward_static";
+  int rc = validate_plan_args(name, num_tokens, top_k, num_experts);
+  if (rc) return rc;
+  if ((rc = check_layer(name, hidden, ffn, w1, w3, w2, l1, l3, l2))) return rc;
+  if (num_tokens == 0) return MX_OK;
+  const bool split = w1->format == MX_FMT_F32X3;
+  const size_t need = layer_layout(num_tokens * top_k, num_experts, hidden, ffn, split,
+                                   num_tokens).bytes;
+  if (need > kStaticScratchBytes) {
+    set_error("%s: this layer call needs %zu bytes of scratch, more than the %zu of the static "
+              "array; use mx_moe_forward with a workspace", name, need, kStaticScratchBytes);
+    return MX_ERR_INVALID;
+  }
+  void *ws = nullptr;
+  if ((rc = static_scratch(name, as_stream(stream), &ws))) return rc;
+  // Every buffer of the layout is written before it is read in this call;
+  // the plan clears its own counters with a kernel.
+  return mx_moe_forward_ex(tokens, top_idx, top_scores, score_dtype, num_tokens, top_k,
+                           num_experts, hidden, ffn, act, w1, w3, w2, l1, l3, l2, out, out_dtype,
+                           nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, ws,
+                           stream);
 }
 
 extern "C" int mx_set_stage_events(void **events, int count) {
