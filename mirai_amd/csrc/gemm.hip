@@ -610,10 +610,132 @@ void grouped_gemm_kernel(Params p) {
       __attribute__((always_inline)) {
     __builtin_amdgcn_raw_buffer_store_b64(u32x2{w0, w1}, rs, off, 0, 0);
   };
-  if (EPI == EPI_SWIGLU) {
+  // Gate / up run of 4 columns (values 4g..4g+3 of blocks (mb, nbp) and
+  // (mb, nbp + NB/2)) -> the packed bf16 h run; gv / uv end rounded as the
+  // reference's bf16 gate / up (with the bf16 LoRA deltas added).
+  auto swiglu_run = [&](float (&gv)[4], float (&uv)[4], const f32x16 &lg, const f32x16 &lu, int g,
+                        uint32_t &h0, uint32_t &h1) __attribute__((always_inline)) {
+    round2(gv[0], gv[1]);
+    round2(gv[2], gv[3]);
+    round2(uv[0], uv[1]);
+    round2(uv[2], uv[3]);
+    if (LORA) {
+      float a[4], b[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        a[q] = lg[4 * g + q];
+        b[q] = lu[4 * g + q];
+      }
+      round2(a[0], a[1]);
+      round2(a[2], a[3]);
+      round2(b[0], b[1]);
+      round2(b[2], b[3]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        gv[q] += a[q];
+        uv[q] += b[q];
+      }
+      round2(gv[0], gv[1]);
+      round2(gv[2], gv[3]);
+      round2(uv[0], uv[1]);
+      round2(uv[2], uv[3]);
+    }
+    if (p.act == MX_ACT_SWIGLU7) {
+      // bf16 gate / up in, fp32 swiglu7, one rounding (grouped_moe.py:287-306).
+      float hq[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) hq[q] = swiglu7(gv[q], uv[q]);
+      h0 = pack_bf16x2(hq[0], hq[1]);
+      h1 = pack_bf16x2(hq[2], hq[3]);
+    } else {
+      // silu(g) rounded to bf16, then the bf16 product (experts.py:289-317).
+      float sv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sv[q] = gv[q] * __builtin_amdgcn_rcpf(1.0f + __expf(-gv[q]));
+      round2(sv[0], sv[1]);
+      round2(sv[2], sv[3]);
+      h0 = pack_bf16x2(sv[0] * uv[0], sv[1] * uv[1]);
+      h1 = pack_bf16x2(sv[2] * uv[2], sv[3] * uv[3]);
+    }
+  };
+  // Down / backward run of 4 columns of block (mb, nb): the bf16 projection
+  // plus the bf16 LoRA delta, rounded again (experts.py:3370-3374).
+  auto store_run = [&](float (&v)[4], const f32x16 &l2, int g, uint32_t &w0, uint32_t &w1)
+      __attribute__((always_inline)) {
+    round2(v[0], v[1]);
+    round2(v[2], v[3]);
+    if (LORA) {
+      float a[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[q] = l2[4 * g + q];
+      round2(a[0], a[1]);
+      round2(a[2], a[3]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] += a[q];
+    }
+    w0 = pack_bf16x2(v[0], v[1]);
+    w1 = pack_bf16x2(v[2], v[3]);
+  };
+  // Staged stores: a lane's runs are 8 bytes of one row, 32 rows per store
+  // instruction, which the memory system takes as partial-line writes. The
+  // rounded tile goes to LDS first (the B stages are free after the K loop)
+  // and leaves in 16-byte pieces of whole row runs. Staged rows are 16-byte
+  // chunks XOR-swizzled by the row, so the 32 rows a wave writes at once
+  // spread over the banks.
+  const bool saves = EPI == EPI_SWIGLU && p.save_gate != nullptr;
+  if (EPI == EPI_SWIGLU && !kSplit && !saves) {
+    // Inference h: the whole [BM][BN/2] tile is staged (BM/2 rows per B
+    // stage), then every wave stores BM/8 rows, 16 lanes per 256-byte row.
+    constexpr int HC = T::BN / 2;
+    constexpr int RSB = HC * 2;
+    constexpr int CPRH = RSB / 16;
+    static_assert(EPI != EPI_SWIGLU || (CPRH == 16 && (T::BM / 2) * RSB <= T::STAGE_B),
+                  "h tile must fit the B stages");
+    auto h_stage = [&](int r) -> uint8_t * {
+      return (r < T::BM / 2 ? sB0 : sB1) + (r & (T::BM / 2 - 1)) * RSB;
+    };
+#pragma unroll
+    for (int mb = 0; mb < T::MB; ++mb) {
+      const int r = wm * T::WM + mb * 32 + lrow;
+      uint8_t *srow = h_stage(r);
+#pragma unroll
+      for (int nbp = 0; nbp < T::NB / 2; ++nbp) {
+        f32x16 lg, lu;
+        if (LORA) {
+          lg = lora_block(mb, nbp);
+          lu = lora_block(mb, nbp + T::NB / 2);
+        }
+        const int hc0 = wn * (T::WN / 2) + nbp * 32 + lcol;  // h column of the run, g = 0
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float gv[4], uv[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            gv[q] = acc[mb][nbp][4 * g + q];
+            uv[q] = acc[mb][nbp + T::NB / 2][4 * g + q];
+          }
+          uint32_t h0, h1;
+          swiglu_run(gv, uv, lg, lu, g, h0, h1);
+          const int hc = hc0 + 8 * g;
+          *reinterpret_cast<u32x2 *>(srow + (((hc >> 3) ^ (r & 15)) << 4) + ((hc & 7) << 1)) =
+              u32x2{h0, h1};
+        }
+      }
+    }
+    __syncthreads();
+    constexpr int RPW = T::BM / 8;  // rows stored per wave
+    const int c = lane & 15;
+    const int64_t col = static_cast<int64_t>(nt) * HC + c * 8;
+#pragma unroll
+    for (int it = 0; it < RPW / 4; ++it) {
+      const int r = wid * RPW + it * 4 + (lane >> 4);
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(h_stage(r) + ((c ^ (r & 15)) << 4));
+      if (row0 + r < row_end && col < p.N)
+        *reinterpret_cast<u32x4 *>(p.out + (row0 + r) * p.ldo + col) = v;
+    }
+  } else if (EPI == EPI_SWIGLU) {
     const uint32_t ld2 = static_cast<uint32_t>(p.ldo) * 2u, n2 = static_cast<uint32_t>(p.N) * 2u;
     const auto rs_h = tile_rsrc(p.out + row0 * p.ldo, tile_rows * p.ldo * 2);
-    const bool saves = p.save_gate != nullptr;
     const auto rs_g = tile_rsrc(saves ? p.save_gate + row0 * p.N : p.out, saves ? tile_rows * p.N * 2 : 0);
     const auto rs_u = tile_rsrc(saves ? p.save_up + row0 * p.N : p.out, saves ? tile_rows * p.N * 2 : 0);
 #pragma unroll
@@ -661,46 +783,9 @@ void grouped_gemm_kernel(Params p) {
             st8(rs_h, off_h + 2 * n2, lo0, lo1);
             continue;
           }
-          round2(gv[0], gv[1]);
-          round2(gv[2], gv[3]);
-          round2(uv[0], uv[1]);
-          round2(uv[2], uv[3]);
-          if (LORA) {
-            float a[4], b[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              a[q] = lg[4 * g + q];
-              b[q] = lu[4 * g + q];
-            }
-            round2(a[0], a[1]);
-            round2(a[2], a[3]);
-            round2(b[0], b[1]);
-            round2(b[2], b[3]);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              gv[q] += a[q];
-              uv[q] += b[q];
-            }
-            round2(gv[0], gv[1]);
-            round2(gv[2], gv[3]);
-            round2(uv[0], uv[1]);
-            round2(uv[2], uv[3]);
-          }
-          if (p.act == MX_ACT_SWIGLU7) {
-            // bf16 gate / up in, fp32 swiglu7, one rounding (grouped_moe.py:287-306).
-            float hq[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) hq[q] = swiglu7(gv[q], uv[q]);
-            st8(rs_h, off_h, pack_bf16x2(hq[0], hq[1]), pack_bf16x2(hq[2], hq[3]));
-          } else {
-            // silu(g) rounded to bf16, then the bf16 product (experts.py:289-317).
-            float sv[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) sv[q] = gv[q] * __builtin_amdgcn_rcpf(1.0f + __expf(-gv[q]));
-            round2(sv[0], sv[1]);
-            round2(sv[2], sv[3]);
-            st8(rs_h, off_h, pack_bf16x2(sv[0] * uv[0], sv[1] * uv[1]), pack_bf16x2(sv[2] * uv[2], sv[3] * uv[3]));
-          }
+          uint32_t h0, h1;
+          swiglu_run(gv, uv, lg, lu, g, h0, h1);
+          st8(rs_h, off_h, h0, h1);
           if (saves) {
             st8(rs_g, off_s, pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3]));
             st8(rs_u, off_s, pack_bf16x2(uv[0], uv[1]), pack_bf16x2(uv[2], uv[3]));
@@ -708,9 +793,58 @@ void grouped_gemm_kernel(Params p) {
         }
       }
     }
+  } else if ((EPI == EPI_STORE || EPI == EPI_STORE2) && !kSplit) {
+    // Each wave stages its own [32][WN] rows of one row block at a time in a
+    // private slice of the B stages, then stores them 16 bytes per lane,
+    // WN / 8 lanes per row, through the row map.
+    constexpr int CH = T::WN / 8;       // 16-byte chunks per staged row
+    constexpr int RPI = 64 / CH;        // rows per store instruction
+    constexpr int WSB = 32 * T::WN * 2; // staged bytes per wave
+    static_assert((EPI != EPI_STORE && EPI != EPI_STORE2) || (4 * WSB <= T::STAGE_B && (CH == 8 || CH == 16)),
+                  "wave slices must fit a B stage");
+    uint8_t *stg = (wid < 4 ? sB0 : sB1) + (wid & 3) * WSB;
+    const int c = lane % CH;
+    const int64_t col = static_cast<int64_t>(nt) * T::BN + wn * T::WN + c * 8;
+#pragma unroll
+    for (int mb = 0; mb < T::MB; ++mb) {
+#pragma unroll
+      for (int nb = 0; nb < T::NB; ++nb) {
+        f32x16 l2;
+        if (LORA) l2 = lora_block(mb, nb);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = acc[mb][nb][4 * g + q];
+          uint32_t w0, w1;
+          store_run(v, l2, g, w0, w1);
+          const int wc = nb * 32 + 8 * g + lcol;  // column inside the wave's slice
+          *reinterpret_cast<u32x2 *>(stg + lrow * (T::WN * 2) + (((wc >> 3) ^ (lrow & (CH - 1))) << 4) +
+                                     ((wc & 7) << 1)) = u32x2{w0, w1};
+        }
+      }
+      // The slice is private to the wave: its own LDS writes are ordered
+      // before these reads.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int it = 0; it < 32 / RPI; ++it) {
+        const int r = it * RPI + lane / CH;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + r * (T::WN * 2) + ((c ^ (r & (CH - 1))) << 4));
+        const int64_t rr = row0 + wm * T::WM + mb * 32 + r;
+        if (rr < row_end && col < p.N) {
+          const int64_t o = p.out_row ? static_cast<int64_t>(p.out_row[rr]) : rr;
+          *reinterpret_cast<u32x4 *>(p.out + o * p.ldo + col) = v;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
   } else if (EPI == EPI_STORE || EPI == EPI_STORE2) {
-    // Rows go to out_row[r] (slot order): one row pointer per lane and row
-    // block, shared by the column blocks.
+    // fp32 layer: y leaves as planes [hi | lo] (row stride 2N), straight from
+    // the accumulators.
 #pragma unroll
     for (int mb = 0; mb < T::MB; ++mb) {
       const int64_t rr = row0 + wm * T::WM + mb * 32 + lrow;
@@ -730,31 +864,17 @@ void grouped_gemm_kernel(Params p) {
           float v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) v[q] = acc[mb][nb][4 * g + q];
-          if constexpr (kSplit) {
-            if (LORA) {  // fp32 layer: one rounding of the sum
+          if (LORA) {  // one rounding of the sum
 #pragma unroll
-              for (int q = 0; q < 4; ++q) v[q] += l2[4 * g + q];
-            }
-          } else {
-            round2(v[0], v[1]);
-            round2(v[2], v[3]);
-            if (LORA) {
-              float a[4];
-#pragma unroll
-              for (int q = 0; q < 4; ++q) a[q] = l2[4 * g + q];
-              round2(a[0], a[1]);
-              round2(a[2], a[3]);
-#pragma unroll
-              for (int q = 0; q < 4; ++q) v[q] += a[q];
-            }
+            for (int q = 0; q < 4; ++q) v[q] += l2[4 * g + q];
           }
           const uint32_t w0 = pack_bf16x2(v[0], v[1]), w1 = pack_bf16x2(v[2], v[3]);
           uint16_t *dst = orow + n0 + 8 * g;
-          if (ok) *reinterpret_cast<u32x2 *>(dst) = u32x2{w0, w1};
-          if constexpr (kSplit) {  // fp32 layer: y leaves as planes [hi | lo] (row stride 2N)
-            const uint32_t l0 = pack_bf16x2(v[0] - bf16_bits_to_f32(w0 & 0xffffu), v[1] - bf16_bits_to_f32(w0 >> 16));
-            const uint32_t l1 = pack_bf16x2(v[2] - bf16_bits_to_f32(w1 & 0xffffu), v[3] - bf16_bits_to_f32(w1 >> 16));
-            if (ok) *reinterpret_cast<u32x2 *>(dst + p.N) = u32x2{l0, l1};
+          const uint32_t l0 = pack_bf16x2(v[0] - bf16_bits_to_f32(w0 & 0xffffu), v[1] - bf16_bits_to_f32(w0 >> 16));
+          const uint32_t l1 = pack_bf16x2(v[2] - bf16_bits_to_f32(w1 & 0xffffu), v[3] - bf16_bits_to_f32(w1 >> 16));
+          if (ok) {
+            *reinterpret_cast<u32x2 *>(dst) = u32x2{w0, w1};
+            *reinterpret_cast<u32x2 *>(dst + p.N) = u32x2{l0, l1};
           }
         }
       }
