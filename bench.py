@@ -14,6 +14,14 @@ events recorded on the library's stream around that kernel; ``cpu_baseline``
 times the oracle's restatement of the reference CPU expert path on a bounded
 token sample on the host cores.
 
+The headline's step time is the mean of exactly ``--steps`` back-to-back
+steps (synchronised before and after); ``median_ms`` / ``p95_ms`` / ``min_ms``
+come from events recorded between those steps on the same stream. The line
+also nests one record per benchmark configuration (``configs``: C1-C5 at their
+own shapes; ``--no-configs`` skips them) with the same timing summary, TFLOP/s,
+the fraction of the bf16 MFMA peak and of the roofline bound
+min(P_mfma, AI * BW_hbm) on algorithmic bytes, and the HBM rate of those bytes.
+
 ``--config c5`` (adapter training) times forward + backward per step: the
 forward keeps its activations, the backward produces d tokens, d scores and the
 LoRA factor gradients from dY ~ N(0, 1); forward and backward are also timed
@@ -53,8 +61,8 @@ BACK_STAGES = ("plan_and_combine_bwd", "lora_dz_down", "dh_gemm", "lora_grads_do
 def _parse():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="target",
                     help="workload key: target (default), c2, c3, c4")
     ap.add_argument("--weights", choices=("nf4", "int8", "bf16"), default=None,
@@ -68,6 +76,11 @@ def _parse():
                          "that time (the graph's output is checked against the eager step)")
     ap.add_argument("--path", choices=("layer", "router", "block", "expert_choice"),
                     default="layer", help="the path to time (layer: the headline)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the nested per-configuration records (C1-C5)")
+    ap.add_argument("--config-steps", type=int, default=30,
+                    help="timed steps of each nested configuration record")
+    ap.add_argument("--config-warmup", type=int, default=5)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the run, copy this many MiB device-to-device once: a kernel "
                          "of known traffic that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -342,6 +355,129 @@ def _bench_path(args, w, device) -> dict:
             "pct_bf16_peak": 100.0 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
 
 
+def _step_times(fn, steps, warmup):
+    """Mean ms per step over exactly `steps` back-to-back steps (synchronised on
+    both sides), plus each step's own duration from an event recorded between
+    steps on the same stream (no synchronisation inside the timed region)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    events[0].record()
+    for i in range(steps):
+        fn()
+        events[i + 1].record()
+    torch.cuda.synchronize()
+    per = [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
+    return events[0].elapsed_time(events[-1]) / steps, per
+
+
+def _summary(per):
+    s = sorted(per)
+    p95 = s[min(len(s) - 1, max(0, int(round(0.95 * (len(s) - 1)))))]
+    return {"median_ms": statistics.median(s), "p95_ms": p95, "min_ms": s[0]}
+
+
+def _flops(w):
+    """Algorithmic FLOPs of one step: the forward (base 2*R*3*d*f plus LoRA
+    2*R*r*3*(d+f)); with the backward, dX through the re-decoded base
+    (2*R*3*d*f) plus about twice the forward's LoRA FLOPs (dz, dA, dB and the
+    LoRA part of dX)."""
+    R = w.routed_rows
+    flops = w.flops()
+    if w.backward:
+        flops += 2 * R * 3 * w.hidden * w.ffn + 2 * (2 * R * w.rank * 3 * (w.hidden + w.ffn))
+    return flops
+
+
+class _Layer:
+    """One workload's module, inputs and step functions on the GPU."""
+
+    def __init__(self, w, device):
+        import torch
+
+        from mirai_amd import route_topk
+        from mirai_amd import workloads as wl
+
+        self.w = w
+        self.logits_cpu = wl.router_logits(w)
+        self.tokens_cpu = wl.tokens(w)
+        self.logits = self.logits_cpu.to(device)
+        self.x = self.tokens_cpu.to(device)
+        self.module = _build_module(w, device)
+        self.dy = wl.upstream_grad(w, device=device) if w.backward else None
+        self.lora_params = [p for ad in self.module.expert_lora.values()
+                            for p in (ad.lora_a, ad.lora_b)]
+        self.state = {}
+        self._route = route_topk
+
+    def routes(self):
+        import torch
+
+        with torch.no_grad():
+            return self._route(self.logits, self.w.top_k, renorm="clamp", score_dtype=self.w.dtype)
+
+    def forward_only(self):
+        import torch
+
+        with torch.no_grad():
+            idx, scores = self.routes()
+            self.state["out"] = self.module.run_direct_routed(self.x, scores, idx)
+            self.state["idx"] = idx
+
+    def forward_train(self):
+        # Routing stays outside the graph here: its backward (d logits) is a
+        # separate, tiny kernel; d scores is what the expert op produces.
+        idx, scores = self.routes()
+        xg = self.x.detach().requires_grad_(True)
+        sg = scores.detach().requires_grad_(True)
+        for p in self.lora_params:
+            p.grad = None
+        out = self.module.run_direct_routed(xg, sg, idx)
+        self.state["idx"] = idx
+        return out
+
+    def step(self):
+        if not self.w.backward:
+            self.forward_only()
+            return
+        self.forward_train().backward(self.dy)
+
+    def counts(self):
+        import torch
+
+        return torch.bincount(self.state["idx"].reshape(-1), minlength=self.w.experts).cpu()
+
+
+def _config_record(w, device, steps, warmup):
+    """Nested per-configuration record: step time (mean, median, p95), routed
+    tokens/s, TFLOP/s, the fraction of the bf16 MFMA peak and of the roofline
+    attainable = min(P_mfma, AI * BW_hbm) on algorithmic bytes, and the HBM rate
+    of those bytes (the weight-streaming view of light experts)."""
+    from mirai_amd import workloads as wl
+
+    layer = _Layer(w, device)
+    ms, per = _step_times(layer.step, steps, warmup)
+    counts = layer.counts()
+    flops = _flops(w)
+    nbytes = wl.algorithmic_bytes(w, counts)
+    attainable = min(PEAK_BF16_TFLOPS * 1e12, flops / nbytes * PEAK_HBM_GBS * 1e9)
+    rate = flops / (ms * 1e-3)
+    rec = {"workload": w.name, **{k: v for k, v in wl.describe(w).items() if k != "workload"},
+           "backward": w.backward, "steps": steps, "warmup": warmup, "ms_per_step": ms,
+           **_summary(per), "routed_tokens_per_s": w.routed_rows / (ms * 1e-3),
+           "tflops": rate / 1e12, "pct_bf16_peak": 100.0 * rate / 1e12 / PEAK_BF16_TFLOPS,
+           "algorithmic_bytes": nbytes, "hbm_gbs_of_algorithmic_bytes": nbytes / (ms * 1e-3) / 1e9,
+           "roofline_attainable_tflops": attainable / 1e12, "roofline_frac": rate / attainable,
+           "empty_experts": int((counts == 0).sum()),
+           "rows_per_expert": {"min": int(counts.min()), "median": int(counts.median()),
+                               "max": int(counts.max())}}
+    del layer
+    return rec
+
+
 def main() -> int:
     args = _parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -353,7 +489,6 @@ def main() -> int:
 
     import torch
 
-    from mirai_amd import route_topk
     from mirai_amd import workloads as wl
 
     if args.config not in wl.WORKLOADS:
@@ -371,111 +506,49 @@ def main() -> int:
         print(json.dumps(_bench_path(args, w, device)))
         return 0
 
-    logits_cpu = wl.router_logits(w)
-    tokens_cpu = wl.tokens(w)
-    logits = logits_cpu.to(device)
-    x = tokens_cpu.to(device)
-    module = _build_module(w, device)
-
-    state = {}
-    dy = wl.upstream_grad(w, device=device) if w.backward else None
-    lora_params = [p for ad in module.expert_lora.values() for p in (ad.lora_a, ad.lora_b)]
-
-    def forward_only():
-        with torch.no_grad():
-            idx, scores = route_topk(logits, w.top_k, renorm="clamp", score_dtype=w.dtype)
-            state["out"] = module.run_direct_routed(x, scores, idx)
-            state["idx"] = idx
-
-    def forward_train():
-        # Routing stays outside the graph here: its backward (d logits) is a
-        # separate, tiny kernel; d scores is what the expert op produces.
-        with torch.no_grad():
-            idx, scores = route_topk(logits, w.top_k, renorm="clamp", score_dtype=w.dtype)
-        xg = x.detach().requires_grad_(True)
-        sg = scores.detach().requires_grad_(True)
-        for p in lora_params:
-            p.grad = None
-        out = module.run_direct_routed(xg, sg, idx)
-        state["idx"] = idx
-        return out
-
-    def step():
-        if not w.backward:
-            forward_only()
-            return
-        forward_train().backward(dy)
-
-    def timed(fn):
-        for _ in range(args.warmup):
-            fn()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(args.steps):
-            fn()
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / args.steps
-
-    eager_ms = timed(step)
+    layer = _Layer(w, device)
+    eager_ms, per_step = _step_times(layer.step, args.steps, args.warmup)
     ms = eager_ms
     execution = "eager"
     if not w.backward and args.graph:
         # The inference step (route + layer: about a dozen kernels) replayed as
         # one HIP graph: the same kernels on the same inputs, without the
         # per-launch gaps. Nothing on this path records a memset.
-        forward_only()
+        layer.forward_only()
         torch.cuda.synchronize()
-        eager_out = state["out"].clone()
+        eager_out = layer.state["out"].clone()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             for _ in range(2):
-                forward_only()
+                layer.forward_only()
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            forward_only()
-        ms = timed(graph.replay)
-        if not torch.equal(state["out"], eager_out):
+            layer.forward_only()
+        ms, per_step = _step_times(graph.replay, args.steps, args.warmup)
+        if not torch.equal(layer.state["out"], eager_out):
             print("graph replay differs from the eager step", file=sys.stderr)
             return 1
         execution = "hip_graph"
 
     # Routing kernel alone, then the library stages (separate, synchronised passes).
-    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    r0.record()
-    for _ in range(args.steps):
-        route_topk(logits, w.top_k, renorm="clamp", score_dtype=w.dtype)
-    r1.record()
-    torch.cuda.synchronize()
-    route_ms = r0.elapsed_time(r1) / args.steps
-    stages = _stage_times(forward_only if not w.backward else forward_train,
+    route_ms, _ = _step_times(layer.routes, args.steps, 1)
+    stages = _stage_times(layer.forward_only if not w.backward else layer.forward_train,
                           max(3, args.steps // 2), device)
     back = {}
     if w.backward:
-        f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        f0.record()
-        for _ in range(args.steps):
-            out_f = forward_train()
-        f1.record()
-        torch.cuda.synchronize()
-        del out_f
-        fwd_ms = f0.elapsed_time(f1) / args.steps
+        fwd_ms, _ = _step_times(layer.forward_train, args.steps, 1)
         back = {
             "forward_ms": fwd_ms,
             "backward_ms": ms - fwd_ms,
-            "backward_stage_ms": _stage_times(step, max(3, args.steps // 2), device, BACK_STAGES),
+            "backward_stage_ms": _stage_times(layer.step, max(3, args.steps // 2), device,
+                                              BACK_STAGES),
         }
 
-    counts = torch.bincount(state["idx"].reshape(-1), minlength=w.experts).cpu()
+    counts = layer.counts()
     R = w.routed_rows
-    flops = w.flops()
-    if w.backward:
-        # dX through the re-decoded base (2*R*3*d*f) plus about twice the
-        # forward's LoRA FLOPs (dz, dA, dB and the LoRA part of dX).
-        flops += 2 * R * 3 * w.hidden * w.ffn + 2 * (2 * R * w.rank * 3 * (w.hidden + w.ffn))
+    flops = _flops(w)
     tflops = flops / (ms * 1e-3) / 1e12
     gate_up_flops = 2 * R * 2 * w.hidden * w.ffn + 2 * R * 2 * w.ffn * w.rank
     gu_ms = stages["gate_up_gemm"]
@@ -501,6 +574,7 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) tokens and logits, N(0,0.02) weights and LoRA)",
         "config": {**wl.describe(w), "lora_alpha": w.alpha, "parallelism": "single_gpu"},
+        **_summary(per_step),
         "tflops": tflops,
         "pct_bf16_peak": 100.0 * tflops / PEAK_BF16_TFLOPS,
         "tokens_per_s": w.tokens / (ms * 1e-3),
@@ -531,8 +605,18 @@ def main() -> int:
         result["copy_probe_bytes"] = {"read": n * 4, "write": n * 4}
         del src, dst
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = _cpu_baseline(w, module, logits_cpu, tokens_cpu,
-                                               args.cpu_seconds)
+        result["cpu_baseline"] = _cpu_baseline(w, layer.module, layer.logits_cpu,
+                                               layer.tokens_cpu, args.cpu_seconds)
+    del layer
+    if not args.no_configs:
+        # The benchmark definition's other configurations, as nested records
+        # (not the headline): C1 fp32, C2 at its own T = 4096, C3 Zipf-skewed,
+        # C4 INT8, C5 forward + backward.
+        result["configs"] = {}
+        for key in ("c1", "c2", "c3", "c4", "c5"):
+            torch.cuda.empty_cache()
+            result["configs"][key] = _config_record(wl.WORKLOADS[key], device,
+                                                    args.config_steps, args.config_warmup)
     print(json.dumps(result))
     return 0
 
