@@ -55,6 +55,13 @@ def build(verbose: bool = False) -> Path:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
+    # A kernel whose host-side instantiation fails is dropped silently and
+    # leaves its launch stub undefined: refuse such a library here rather
+    # than at load time.
+    nm = subprocess.run(["nm", "-u", str(tmp)], capture_output=True, text=True)
+    missing = [ln.split()[-1] for ln in nm.stdout.splitlines() if "__device_stub__" in ln]
+    if nm.returncode == 0 and missing:
+        raise RuntimeError(f"undefined kernel launch stubs in {tmp.name}: {missing[:4]}")
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")

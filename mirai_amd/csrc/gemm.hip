@@ -137,13 +137,17 @@ __device__ __forceinline__ void b_row(int j, int nt, int &which, int64_t &n) {
   }
 }
 
-// Tile rows of BK bf16 = 8 (BK 64) or 4 (BK 32) 16-byte chunks. The chunk is
-// XOR-ed with a row-dependent value so that any 16 consecutive rows at one
-// logical chunk hit 16 distinct 16-byte bank groups: both the MFMA fragment
-// reads and the row-owner writes are conflict free.
+// Row key of the 128-byte-row stage swizzle: any 16 consecutive rows at one
+// logical chunk land on 16 distinct 16-byte slots of a 256-byte bank line (the
+// MFMA fragment reads run conflict free), and any 8 consecutive rows on 8
+// distinct slots of a 128-byte half.
+__device__ __forceinline__ int swz_key64(int row) { return ((row >> 1) ^ (row << 2)) & 7; }
+
+// Tile rows of BK bf16 = 8 (BK 64) or 4 (BK 32) 16-byte chunks, the chunk
+// XOR-ed with a row key (above for BK 64).
 template <int BK>
 __device__ __forceinline__ int swz(int row, int chunk) {
-  if (BK == 64) return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);
+  if (BK == 64) return row * 128 + ((chunk ^ swz_key64(row)) << 4);
   return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 __device__ __forceinline__ int swz64(int row, int chunk) {  // 64-byte rows (LoRA tiles)
@@ -165,6 +169,12 @@ __device__ __forceinline__ void round2(float &a, float &b) {
   const uint32_t t = pack_bf16x2(a, b);
   a = __uint_as_float(t << 16);
   b = __uint_as_float(t & 0xffff0000u);
+}
+
+// The calling wave's index in its workgroup, as a value the compiler keeps in
+// a scalar register.
+__device__ __forceinline__ int uniform_wave_index() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
 }
 
 // Raw buffer over [base, base + bytes): accesses at offsets >= bytes are
@@ -269,7 +279,8 @@ void grouped_gemm_kernel(Params p) {
   // instruction fills 1 KB of the stage, lane l landing at byte 16*l. The lane
   // that lands on (row, physical chunk) loads the logical chunk the swizzle
   // maps there, so the stage ends up in the same swizzled layout.
-  const int wave = tid >> 6, lane_id = tid & 63;
+  // The wave index is uniform: kept in scalar registers (LDS DMA bases, M0).
+  const int wave = uniform_wave_index(), lane_id = tid & 63;
   constexpr int kRowsPerDma = 1024 / (BK * 2);
   const uint16_t *a_ptr[T::A_CHUNKS];
   int a_lds[T::A_CHUNKS];  // wave-uniform LDS byte offset of each DMA inside a stage
@@ -278,7 +289,7 @@ void grouped_gemm_kernel(Params p) {
     const int region = wave * T::A_CHUNKS + i;
     const int row = region * kRowsPerDma + lane_id / T::CPR;
     const int phys = lane_id % T::CPR;
-    const int logical = BK == 64 ? (phys ^ ((row >> 1) & 7)) : (phys ^ ((row >> 2) & 3));
+    const int logical = BK == 64 ? (phys ^ swz_key64(row)) : (phys ^ ((row >> 2) & 3));
     const int64_t grow = min(row0 + row, row_end - 1);
     const int64_t src = p.row_token ? static_cast<int64_t>(p.row_token[grow]) : grow;
     a_ptr[i] = p.x + src * p.ldx + logical * 8;
@@ -422,7 +433,7 @@ void grouped_gemm_kernel(Params p) {
   };
 
   // -------------------------------------------------------------- MFMA
-  const int lane = tid & 63, wid = tid >> 6;
+  const int lane = tid & 63, wid = wave;
   const int wm = wid / T::WAVES_N_, wn = wid % T::WAVES_N_;
   f32x16 acc[T::MB][T::NB];
 #pragma unroll
