@@ -76,6 +76,9 @@ def _parse():
                          "that time (the graph's output is checked against the eager step)")
     ap.add_argument("--path", choices=("layer", "router", "block", "expert_choice"),
                     default="layer", help="the path to time (layer: the headline)")
+    ap.add_argument("--settle-seconds", type=float, default=1.0,
+                    help="untimed steps for about this long after setup, before the warmup "
+                         "steps (clocks and power state settle)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the nested per-configuration records (C1-C5)")
     ap.add_argument("--config-steps", type=int, default=30,
@@ -355,21 +358,43 @@ def _bench_path(args, w, device) -> dict:
             "pct_bf16_peak": 100.0 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
 
 
+def _settle(fn, seconds):
+    """Untimed steps for about `seconds` before a measurement: the GPU's clocks
+    and power state take a few hundred steps to settle after setup (a run
+    without this showed a 24 ms step and some 15 slow steps after it)."""
+    import torch
+
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+
+
 def _step_times(fn, steps, warmup):
     """Mean ms per step over exactly `steps` back-to-back steps (synchronised on
     both sides), plus each step's own duration from an event recorded between
-    steps on the same stream (no synchronisation inside the timed region)."""
+    steps on the same stream (no synchronisation inside the timed region).
+    Python's garbage collector is off while the steps are issued."""
+    import gc
+
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    events[0].record()
-    for i in range(steps):
-        fn()
-        events[i + 1].record()
-    torch.cuda.synchronize()
+    gc_was_on = gc.isenabled()
+    gc.disable()
+    try:
+        events[0].record()
+        for i in range(steps):
+            fn()
+            events[i + 1].record()
+        torch.cuda.synchronize()
+    finally:
+        if gc_was_on:
+            gc.enable()
     per = [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
     return events[0].elapsed_time(events[-1]) / steps, per
 
@@ -451,7 +476,7 @@ class _Layer:
         return torch.bincount(self.state["idx"].reshape(-1), minlength=self.w.experts).cpu()
 
 
-def _config_record(w, device, steps, warmup):
+def _config_record(w, device, steps, warmup, args_settle=0.5):
     """Nested per-configuration record: step time (mean, median, p95), routed
     tokens/s, TFLOP/s, the fraction of the bf16 MFMA peak and of the roofline
     attainable = min(P_mfma, AI * BW_hbm) on algorithmic bytes, and the HBM rate
@@ -459,6 +484,7 @@ def _config_record(w, device, steps, warmup):
     from mirai_amd import workloads as wl
 
     layer = _Layer(w, device)
+    _settle(layer.step, args_settle)
     ms, per = _step_times(layer.step, steps, warmup)
     counts = layer.counts()
     flops = _flops(w)
@@ -507,6 +533,7 @@ def main() -> int:
         return 0
 
     layer = _Layer(w, device)
+    _settle(layer.step, args.settle_seconds)
     eager_ms, per_step = _step_times(layer.step, args.steps, args.warmup)
     ms = eager_ms
     execution = "eager"

@@ -13,6 +13,7 @@ from .dispatch import (
     permute_routed_tokens,
 )
 from ._native import RouteIndexError, check_route_errors, set_route_check
+from .chunking import MoETokenChunkPolicy, fused_chunk_runner
 from .experts import CompressedGroupedExperts
 from .lora import ActiveExpertLoRA, lora_scale
 from .magi2 import Magi2FusedMoEBackend, Magi2GroupedExperts, route_topk_heads
@@ -36,11 +37,13 @@ __all__ = [
     "ExpertProjectionRole",
     "Magi2FusedMoEBackend",
     "Magi2GroupedExperts",
+    "MoETokenChunkPolicy",
     "as_execution_spec",
     "build_dispatch_plan",
     "build_expert_choice_dispatch_plan",
     "check_route_errors",
     "combine_routed_tokens",
+    "fused_chunk_runner",
     "fused_router_forward",
     "lora_scale",
     "permute_routed_tokens",

@@ -14,11 +14,17 @@ import torch
 from . import _native as nat
 
 
-def routed_experts_backward(ctx, grad_out):
+def native_backward(module, saved, grad_out, token_dtype, *, need_tokens=True, need_scores=True,
+                    lora_needs=None):
+    """One mx_moe_backward_act call over the activations ``saved`` by a forward
+    of the routed layer (x, scores, idx, gate, up, h, y, low-rank rows).
+
+    Returns (grad_tokens, fp32 for fp32 tokens else bf16; fp32 grad_scores; raw fp32
+    LoRA factor gradients at the padded rank: [dA, dB] per adapter, None where
+    not wanted or absent)."""
     from .fused import _lora_descriptors, _weight_descriptors, kernel_activation
 
-    x, scores, idx, gate, up, h, y, lora_rows = ctx.saved_tensors
-    module = ctx.module
+    x, scores, idx, gate, up, h, y, lora_rows = saved
     device = x.device
     T, d = (int(v) for v in x.shape)
     k = int(idx.shape[1])
@@ -29,21 +35,21 @@ def routed_experts_backward(ctx, grad_out):
     g = grad_out.contiguous()
     if g.dtype not in (torch.float32, torch.bfloat16):
         g = g.float()
-    tok_dtype = torch.float32 if ctx.token_dtype == torch.float32 else torch.bfloat16
-    grad_tokens = torch.empty((T, d), dtype=tok_dtype, device=device)
+    grad_tokens = torch.empty((T, d), dtype=torch.float32 if token_dtype == torch.float32
+                              else torch.bfloat16, device=device)
     grad_scores = torch.empty((T, k), dtype=torch.float32, device=device)
-    lora_needs = ctx.needs_input_grad[4:]
     raw = []
     for i, adapter in enumerate(module._adapters()):
         if adapter is None:
             raw += [None, None]
             continue
+        want_a = lora_needs is None or lora_needs[2 * i]
+        want_b = lora_needs is None or lora_needs[2 * i + 1]
         r8 = adapter.padded_rank()
-        ga = (torch.empty((E, r8, adapter.in_features), dtype=torch.float32, device=device)
-              if lora_needs[2 * i] else None)
-        gb = (torch.empty((E, adapter.out_features, r8), dtype=torch.float32, device=device)
-              if lora_needs[2 * i + 1] else None)
-        raw += [ga, gb]
+        raw.append(torch.empty((E, r8, adapter.in_features), dtype=torch.float32, device=device)
+                   if want_a else None)
+        raw.append(torch.empty((E, adapter.out_features, r8), dtype=torch.float32, device=device)
+                   if want_b else None)
     lib = nat.load_library()
     ws = nat.workspace(lib.mx_moe_backward_workspace_size(T, k, E, d, f), device)
     nat.call("mx_moe_backward_act", g.data_ptr(), nat.dtype_code(g.dtype), x.data_ptr(),
@@ -54,18 +60,32 @@ def routed_experts_backward(ctx, grad_out):
              nat.dtype_code(grad_tokens.dtype), grad_scores.data_ptr(),
              *[nat.ptr(t) for t in raw], ws.data_ptr(), nat.stream(device))
     del keep
-    lora_grads = []
+    return (grad_tokens if need_tokens else None, grad_scores if need_scores else None, raw)
+
+
+def lora_param_grads(module, raw):
+    """Raw padded-rank fp32 LoRA gradients -> gradients shaped and typed like
+    each adapter's lora_a / lora_b (None where absent)."""
+    grads = []
     for i, adapter in enumerate(module._adapters()):
         ga, gb = raw[2 * i], raw[2 * i + 1]
         if adapter is None:
-            lora_grads += [None, None]
+            grads += [None, None]
             continue
         r = adapter.rank
-        lora_grads.append(None if ga is None else ga[:, :r, :].to(adapter.lora_a.dtype))
-        lora_grads.append(None if gb is None else gb[:, :, :r].contiguous().to(adapter.lora_b.dtype))
-    grad_t = grad_tokens.to(ctx.token_dtype) if ctx.needs_input_grad[1] else None
-    grad_s = grad_scores.to(ctx.score_dtype) if ctx.needs_input_grad[2] else None
-    return (None, grad_t, grad_s, None, *lora_grads)
+        grads.append(None if ga is None else ga[:, :r, :].to(adapter.lora_a.dtype))
+        grads.append(None if gb is None else gb[:, :, :r].contiguous().to(adapter.lora_b.dtype))
+    return grads
+
+
+def routed_experts_backward(ctx, grad_out):
+    gt, gs, raw = native_backward(ctx.module, ctx.saved_tensors, grad_out, ctx.token_dtype,
+                                  need_tokens=ctx.needs_input_grad[1],
+                                  need_scores=ctx.needs_input_grad[2],
+                                  lora_needs=ctx.needs_input_grad[4:])
+    grad_t = gt.to(ctx.token_dtype) if gt is not None else None
+    grad_s = gs.to(ctx.score_dtype) if gs is not None else None
+    return (None, grad_t, grad_s, None, *lora_param_grads(ctx.module, raw))
 
 
 def sorted_experts_autograd(module, tokens, counts):

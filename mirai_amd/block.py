@@ -23,7 +23,7 @@ import torch
 import torch.nn as nn
 
 from . import _native as nat
-from .chunking import MoETokenChunkPolicy
+from .chunking import MoETokenChunkPolicy, fused_chunk_runner
 from .experts import CompressedGroupedExperts
 from .fused import routed_experts, routed_experts_plus, sorted_experts
 from .router import FusedRouter
@@ -133,10 +133,8 @@ class FusedSparseMoeBlock(nn.Module):
         top_indices, top_scores = self._routes(tokens, padding_mask, router_logit_delta)
         policy = self._mirai_token_chunk_policy
         if policy is not None and policy.enabled and grad:
-            out = policy.execute(
-                tokens, top_scores, top_indices,
-                runner=lambda t, s, i, off: routed_experts(self.experts, t, s, i),
-                training=self.training)
+            out = policy.execute(tokens, top_scores, top_indices,
+                                 runner=fused_chunk_runner(self.experts), training=self.training)
             if shared is not None:
                 torch.cuda.current_stream(device).wait_event(ready)
                 out = out + shared

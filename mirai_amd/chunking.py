@@ -1,21 +1,24 @@
-"""Token-chunked routed expert execution for adapter training.
+"""Token-chunked routed expert execution (drop-in for MoETokenChunkPolicy,
+mirai/core/moe/runtime/token_chunking.py:26-118).
 
-Drop-in for MoETokenChunkPolicy (mirai/core/moe/runtime/token_chunking.py:26-118):
-routing is computed once for all tokens; in training with gradients the
-routed layer then runs one contiguous token chunk at a time under activation
-checkpointing, so the saved activations of only one chunk are alive at once
-(the fused layer saves gate / up / h / y / low-rank rows per routed slot, about
-(3f + d + 96) * 2 bytes per slot).
+Routing happens once, over all tokens; in training the routed layer then runs
+over contiguous token chunks so that only one chunk's per-slot activations are
+alive at a time. The policy's surface (``token_chunk_size``, ``enabled``,
+``chunk_count``, ``execute(tokens, top_scores, top_indices, *, runner,
+training)``, the ValueError messages) is the reference's.
 
-Each chunk is one call of the fused layer. Routed rows are computed
-independently of the other rows of their GEMM tile and the combine sums each
-token's own slots, so the chunked forward output is bit-identical to the
-unchunked one; only the LoRA weight gradients, summed over chunks, differ by
-fp32 summation order.
+Execution is this build's own. A runner made by :func:`fused_chunk_runner`
+(the fused routed layer of one ``CompressedGroupedExperts``) goes to a single
+autograd function that checkpoints at the native call boundary: the forward
+writes each chunk's output rows in place and keeps nothing but the inputs, the
+backward recomputes and differentiates one chunk at a time and sums the LoRA
+factor gradients in fp32 (``fused.routed_experts_chunked``). Any other runner
+falls back to torch's non-reentrant checkpoint per chunk.
 """
 
 from __future__ import annotations
 
+import functools
 from dataclasses import dataclass
 from typing import Any, Callable
 
@@ -24,57 +27,84 @@ import torch
 ChunkRunner = Callable[[Any, Any, Any, int], Any]
 
 
+class FusedChunkRunner:
+    """Runner ``(tokens, top_scores, top_indices, token_offset) -> out`` of the
+    fused routed layer of ``experts``; the policy recognises it and chunks at
+    the native call boundary."""
+
+    def __init__(self, experts) -> None:
+        self.experts = experts
+
+    def __call__(self, tokens, top_scores, top_indices, token_offset: int = 0):
+        from .fused import routed_experts
+
+        return routed_experts(self.experts, tokens, top_scores, top_indices)
+
+
+def fused_chunk_runner(experts) -> FusedChunkRunner:
+    return FusedChunkRunner(experts)
+
+
+def _checkpointed(runner: ChunkRunner, offset: int, tokens, top_scores, top_indices):
+    return runner(tokens, top_scores, top_indices, offset)
+
+
 @dataclass(frozen=True)
 class MoETokenChunkPolicy:
-    """Checkpoint local expert work in bounded contiguous token chunks."""
+    """Contiguous token chunks of at most ``token_chunk_size`` tokens (0: off)."""
 
     token_chunk_size: int = 0
 
     def __post_init__(self) -> None:
-        if int(self.token_chunk_size) < 0:
+        size = int(self.token_chunk_size)
+        if size < 0:
             raise ValueError("training.moe_token_chunk_size must be >= 0.")
-        object.__setattr__(self, "token_chunk_size", int(self.token_chunk_size))
+        object.__setattr__(self, "token_chunk_size", size)
 
     @property
     def enabled(self) -> bool:
         return self.token_chunk_size > 0
 
     def chunk_count(self, token_count: int) -> int:
-        count = int(token_count)
-        if count < 0:
+        n = int(token_count)
+        if n < 0:
             raise ValueError("MoE token count must be >= 0.")
-        if not self.enabled or count == 0:
-            return 1
-        return -(-count // self.token_chunk_size)
+        return len(self.chunk_bounds(n)) if self.enabled and n > 0 else 1
 
-    def execute(self, tokens: torch.Tensor, top_scores: torch.Tensor, top_indices: torch.Tensor,
-                *, runner: ChunkRunner, training: bool) -> torch.Tensor:
-        """Run one route plan through chunk-local expert execution (token_chunking.py:48-118)."""
-        if top_scores.shape != top_indices.shape or int(top_indices.ndim) != 2:
+    def chunk_bounds(self, token_count: int) -> list[tuple[int, int]]:
+        """[(start, end), ...] covering range(token_count) in order."""
+        n, c = int(token_count), self.token_chunk_size
+        return [(a, min(a + c, n)) for a in range(0, n, c)] if c > 0 else [(0, n)]
+
+    def execute(self, tokens: torch.Tensor, top_scores: torch.Tensor,
+                top_indices: torch.Tensor, *, runner: ChunkRunner,
+                training: bool) -> torch.Tensor:
+        if int(top_indices.ndim) != 2 or top_scores.shape != top_indices.shape:
             raise ValueError("MoE token chunking requires matching [tokens, top_k] routes.")
         if int(tokens.ndim) != 2:
             raise ValueError("MoE token chunking requires a [tokens, hidden] tensor.")
-        count = int(tokens.shape[0])
-        if int(top_indices.shape[0]) != count:
+        n = int(tokens.shape[0])
+        if int(top_indices.shape[0]) != n:
             raise ValueError("MoE token chunk routes do not match the token count.")
-        if not self.enabled or count <= self.token_chunk_size or not bool(training):
+        # One pass when chunking is off, when the tokens fit one chunk, and in
+        # inference (nothing is saved for a backward there).
+        if not (self.enabled and bool(training)) or n <= self.token_chunk_size:
             return runner(tokens, top_scores, top_indices, 0)
-        use_checkpoint = torch.is_grad_enabled()
-        outputs = []
-        for start in range(0, count, self.token_chunk_size):
-            end = min(start + self.token_chunk_size, count)
-            args = (tokens[start:end], top_scores[start:end], top_indices[start:end])
-            if use_checkpoint:
-                from torch.utils.checkpoint import checkpoint
+        bounds = self.chunk_bounds(n)
+        if isinstance(runner, FusedChunkRunner):
+            from .fused import routed_experts_chunked
 
-                def run_chunk(t, s, i, *, token_offset=start):
-                    return runner(t, s, i, token_offset)
+            return routed_experts_chunked(runner.experts, tokens, top_scores, top_indices,
+                                          bounds)
+        if not torch.is_grad_enabled():
+            return torch.cat([runner(tokens[a:b], top_scores[a:b], top_indices[a:b], a)
+                              for a, b in bounds], dim=0)
+        from torch.utils.checkpoint import checkpoint
 
-                outputs.append(checkpoint(run_chunk, *args, use_reentrant=False,
-                                          preserve_rng_state=True))
-            else:
-                outputs.append(runner(*args, start))
-        return torch.cat(outputs, dim=0)
+        parts = [checkpoint(functools.partial(_checkpointed, runner, a), tokens[a:b],
+                            top_scores[a:b], top_indices[a:b], use_reentrant=False)
+                 for a, b in bounds]
+        return torch.cat(parts, dim=0)
 
 
-__all__ = ["MoETokenChunkPolicy"]
+__all__ = ["ChunkRunner", "FusedChunkRunner", "MoETokenChunkPolicy", "fused_chunk_runner"]

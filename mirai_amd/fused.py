@@ -54,10 +54,12 @@ def _lora_params(module):
     return params
 
 
-def _forward(module, tokens, top_scores, top_indices, need_grad, addend=None, addend_ready=None):
+def _forward(module, tokens, top_scores, top_indices, need_grad, addend=None, addend_ready=None,
+             out=None):
     """One mx_moe_forward call; returns (out, saved tensors or None). With an
     addend [T, d] (bf16) the combine adds it to the rounded routed sum, after
-    waiting for the event ``addend_ready`` (torch.cuda.Event or None)."""
+    waiting for the event ``addend_ready`` (torch.cuda.Event or None). ``out``
+    (contiguous, the kernel's output dtype) receives the result in place."""
     device = nat.require_gpu(tokens, top_scores, top_indices)
     nat.poll_route_errors()
     # fp32 weights (quant_format "fp32") run the split-precision layer on
@@ -75,8 +77,11 @@ def _forward(module, tokens, top_scores, top_indices, need_grad, addend=None, ad
     (w1, w3, w2), packed = _weight_descriptors(module, device)
     f = int(packed[0].shape[1])
     lora, keep = _lora_descriptors(module, device, split)
-    out = torch.empty((T, d), dtype=tokens.dtype if tokens.dtype == torch.float32
-                      else torch.bfloat16, device=device)
+    out_dtype = tokens.dtype if tokens.dtype == torch.float32 else torch.bfloat16
+    if out is None:
+        out = torch.empty((T, d), dtype=out_dtype, device=device)
+    elif out.dtype != out_dtype or tuple(out.shape) != (T, d) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [tokens, hidden] tensor of the kernel's dtype.")
     if need_grad and split:
         raise NotImplementedError(
             "the fp32 (quant_format='fp32') expert layer is inference-only; train adapters "
@@ -132,6 +137,76 @@ def routed_experts(module, tokens, top_scores, top_indices):
             t is not None and t.requires_grad for t in (tokens, top_scores, *params)):
         return _RoutedExperts.apply(module, tokens, top_scores, top_indices, *params)
     return _forward(module, tokens, top_scores, top_indices, False)[0]
+
+
+class _ChunkedRoutedExperts(torch.autograd.Function):
+    """The routed layer over contiguous token chunks, checkpointed at the native
+    call boundary.
+
+    The forward runs each chunk through the inference kernels (no activation
+    is kept) straight into its rows of the output. The backward walks the
+    chunks in order: it reruns a chunk's forward with its per-slot activations
+    saved ((3f + d + 96) * 2 bytes per routed slot), runs that chunk's native
+    backward, writes the chunk's token and score gradients into their rows and
+    adds its fp32 LoRA factor gradients to running sums, then frees the chunk's
+    activations. At most one chunk's activations are alive at a time; the
+    layer is deterministic, so the recomputation reproduces the forward
+    exactly (there is no RNG state to carry)."""
+
+    @staticmethod
+    def forward(ctx, module, bounds, tokens, top_scores, top_indices, *lora_params):
+        T, d = (int(v) for v in tokens.shape)
+        out_dtype = tokens.dtype if tokens.dtype == torch.float32 else torch.bfloat16
+        out = torch.empty((T, d), dtype=out_dtype, device=tokens.device)
+        for a, b in bounds:
+            _forward(module, tokens[a:b], top_scores[a:b], top_indices[a:b], False, out=out[a:b])
+        ctx.module = module
+        ctx.bounds = bounds
+        ctx.token_dtype = tokens.dtype
+        ctx.score_dtype = top_scores.dtype
+        ctx.save_for_backward(tokens, top_scores, top_indices)
+        return out.to(tokens.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        from .backward import lora_param_grads, native_backward
+
+        tokens, scores, idx = ctx.saved_tensors
+        need_t, need_s = ctx.needs_input_grad[2], ctx.needs_input_grad[3]
+        lora_needs = ctx.needs_input_grad[5:]
+        grad_t = torch.empty(tokens.shape, dtype=ctx.token_dtype, device=tokens.device) if need_t else None
+        grad_s = torch.empty(scores.shape, dtype=ctx.score_dtype, device=scores.device) if need_s else None
+        lora_sum = None
+        for a, b in ctx.bounds:
+            _, saved = _forward(ctx.module, tokens[a:b], scores[a:b], idx[a:b], True)
+            gt, gs, raw = native_backward(ctx.module, saved, grad_out[a:b], ctx.token_dtype,
+                                          need_tokens=need_t, need_scores=need_s,
+                                          lora_needs=lora_needs)
+            del saved
+            if need_t:
+                grad_t[a:b] = gt
+            if need_s:
+                grad_s[a:b] = gs
+            lora_sum = raw if lora_sum is None else [
+                None if x is None else x.add_(y) for x, y in zip(lora_sum, raw)]
+        return (None, None, grad_t, grad_s, None, *lora_param_grads(ctx.module, lora_sum))
+
+
+def routed_experts_chunked(module, tokens, top_scores, top_indices, bounds):
+    """routed_experts(...) computed chunk by chunk over the token ranges
+    ``bounds`` ([(start, end), ...] covering the tokens in order); with autograd
+    through the chunk-checkpointed function above."""
+    bounds = [(int(a), int(b)) for a, b in bounds if int(b) > int(a)]
+    if not bounds:
+        return routed_experts(module, tokens, top_scores, top_indices)
+    params = _lora_params(module)
+    if torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (tokens, top_scores, *params)):
+        return _ChunkedRoutedExperts.apply(module, tuple(bounds), tokens, top_scores, top_indices,
+                                           *params)
+    with torch.no_grad():
+        return torch.cat([routed_experts(module, tokens[a:b], top_scores[a:b], top_indices[a:b])
+                          for a, b in bounds], dim=0)
 
 
 def routed_experts_plus(module, tokens, top_scores, top_indices, addend, addend_ready=None):
