@@ -489,7 +489,11 @@ int mx_build_expert_choice_plan(const int64_t *expert_token_indices,
  * 0..L-1, right when logical_to_physical is NULL or monotone). Tokens no
  * expert picked get 0. Preconditions: a token appears at most once per
  * (sample, logical expert); token ids outside [0, tokens_per_sample) are
- * skipped. L <= 1024. Inference (no saved activations).
+ * skipped. L <= 1024. mx_moe_forward_expert_choice_ex also keeps, when the
+ * save pointers are non-NULL, the activations the backward needs (as
+ * mx_moe_forward_ex does, with the S = B * L * C slots as the rows: gate / up /
+ * h [S, ffn] in expert-sorted order, y [S, hidden] in slot order, low-rank
+ * rows [S, 96]).
  */
 size_t mx_moe_expert_choice_workspace_size(int batch, int logical_experts, int capacity,
                                            int64_t tokens_per_sample, int num_experts,
@@ -503,6 +507,41 @@ int mx_moe_forward_expert_choice(const void *tokens, const int64_t *expert_token
                                  const mx_weight *w2, const mx_lora *l1, const mx_lora *l3,
                                  const mx_lora *l2, void *out, int out_dtype, void *workspace,
                                  void *stream);
+int mx_moe_forward_expert_choice_ex(
+    const void *tokens, const int64_t *expert_token_indices, const void *expert_token_scores,
+    int score_dtype, int batch, int logical_experts, int capacity, int64_t tokens_per_sample,
+    const int32_t *logical_to_physical, const int32_t *combine_order, int num_experts,
+    int64_t hidden, int64_t ffn, int act, const mx_weight *w1, const mx_weight *w3,
+    const mx_weight *w2, const mx_lora *l1, const mx_lora *l3, const mx_lora *l2, void *out,
+    int out_dtype, void *save_gate, void *save_up, void *save_h, void *save_y, void *save_lora,
+    void *workspace, void *stream);
+
+/*
+ * Backward of the expert-choice layer: the autograd of
+ * run_compressed_expert_choice (execution/expert_choice.py:16-152; its
+ * gather of token rows, per-expert MLP and index_add_ of y.float() * score),
+ * with frozen weights re-decoded as in mx_moe_backward. From grad_out [T,
+ * hidden] and the activations saved by mx_moe_forward_expert_choice_ex:
+ * grad_scores [B, L, C] fp32 (grad_out[token] . y of the slot, 0 for skipped
+ * slots), grad_tokens [T, hidden] (the sum over a token's slots of their dx
+ * rows, fp32 in the forward's combine order; 0 for tokens no expert picked)
+ * and the fp32 LoRA factor gradients (layout as mx_moe_backward; NULL: not
+ * wanted). Workspace: mx_moe_backward_expert_choice_workspace_size bytes.
+ */
+size_t mx_moe_backward_expert_choice_workspace_size(int batch, int logical_experts,
+                                                    int capacity, int64_t tokens_per_sample,
+                                                    int num_experts, int64_t hidden,
+                                                    int64_t ffn);
+int mx_moe_backward_expert_choice(
+    const void *grad_out, int grad_dtype, const void *tokens, const int64_t *expert_token_indices,
+    const void *expert_token_scores, int score_dtype, int batch, int logical_experts,
+    int capacity, int64_t tokens_per_sample, const int32_t *logical_to_physical,
+    const int32_t *combine_order, int num_experts, int64_t hidden, int64_t ffn, int act,
+    const mx_weight *w1, const mx_weight *w3, const mx_weight *w2, const mx_lora *l1,
+    const mx_lora *l3, const mx_lora *l2, const void *save_gate, const void *save_up,
+    const void *save_h, const void *save_y, const void *save_lora, void *grad_tokens,
+    int grad_tokens_dtype, float *grad_scores, float *grad_a1, float *grad_b1, float *grad_a3,
+    float *grad_b3, float *grad_a2, float *grad_b2, void *workspace, void *stream);
 
 /*
  * Expert MLP over rows already sorted by expert (no gate weighting):

@@ -100,6 +100,17 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         c_int,
         [_P, _P, _P, c_int, c_int, c_int, c_int, c_int64, _P, _P, c_int, c_int64, c_int64, c_int,
          _W, _W, _W, _L, _L, _L, _P, c_int, _P, _P]),
+    "mx_moe_forward_expert_choice_ex": (
+        c_int,
+        [_P, _P, _P, c_int, c_int, c_int, c_int, c_int64, _P, _P, c_int, c_int64, c_int64, c_int,
+         _W, _W, _W, _L, _L, _L, _P, c_int, _P, _P, _P, _P, _P, _P, _P]),
+    "mx_moe_backward_expert_choice_workspace_size": (
+        c_size_t, [c_int, c_int, c_int, c_int64, c_int, c_int64, c_int64]),
+    "mx_moe_backward_expert_choice": (
+        c_int,
+        [_P, c_int, _P, _P, _P, c_int, c_int, c_int, c_int, c_int64, _P, _P, c_int, c_int64,
+         c_int64, c_int, _W, _W, _W, _L, _L, _L, _P, _P, _P, _P, _P, _P, c_int, _P, _P, _P, _P,
+         _P, _P, _P, _P, _P]),
     "mx_plan_workspace_size": (c_size_t, [c_int64, c_int, c_int]),
     "mx_build_plan": (
         c_int, [_P, _P, c_int, c_int64, c_int, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P]),

@@ -1297,6 +1297,133 @@ int run_lora_grad(const LoraGradJob &j, int rank, const PlanView &v, int experts
                           experts, j.out, se, j.a_layout ? 1 : rank, j.a_layout ? j.cols : 1, s);
 }
 
+// The layer backward after the combine backward, shared by token-choice and
+// expert-choice routes: from dy (per-slot grad of the expert outputs, slot
+// order) and the forward's saved activations to the per-slot dx rows (written
+// over dy, slot order) and the fp32 LoRA factor gradients. The plan view v
+// maps sorted rows to token rows (row_token) and to slots (row_slot).
+int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64_t R,
+                  int64_t hidden, int64_t ffn, int act, const mx_weight *w1, const mx_weight *w3,
+                  const mx_weight *w2, const mx_lora *l1, const mx_lora *l3, const mx_lora *l2,
+                  const uint16_t *x, const uint16_t *g_in, const uint16_t *u_in,
+                  const uint16_t *h_in, const uint16_t *lsave, uint16_t *dy, uint16_t *dgu,
+                  uint16_t *dz, uint16_t *const *fact, float *grad_a1, float *grad_b1,
+                  float *grad_a3, float *grad_b3, float *grad_a2, float *grad_b2, hipStream_t s) {
+  const bool lora1 = has_lora(l1), lora3 = has_lora(l3), lora2 = has_lora(l2);
+  int rc;
+  // The six LoRA factor transposes (B2^T, A2^T, B1^T, A1^T, B3^T, A3^T) in one launch.
+  {
+    FactorTransposes jobs = {};
+    auto add = [&](const void *src, int64_t rows, int64_t cols, uint16_t *dst) {
+      jobs.job[jobs.n++] = {static_cast<const uint16_t *>(src), dst, rows, cols,
+                            static_cast<int64_t>(num_experts) * rows * cols};
+    };
+    if (lora2) {
+      add(l2->b, hidden, l2->rank, fact[0]);
+      add(l2->a, l2->rank, ffn, fact[1]);
+    }
+    const mx_lora *l13t[2] = {l1, l3};
+    for (int i = 0; i < 2; ++i)
+      if (has_lora(l13t[i])) {
+        add(l13t[i]->b, ffn, l13t[i]->rank, fact[2 + 2 * i]);
+        add(l13t[i]->a, l13t[i]->rank, hidden, fact[3 + 2 * i]);
+      }
+    if ((rc = transpose_factors_multi(jobs, s))) return rc;
+  }
+
+  // Down projection: dz2 = s2 * dy B2, then dh = dy W2 + dz2 A2 into the dG
+  // half of [dG | dU], and the SwiGLU backward turns it into [dG | dU].
+  if (lora2) {
+    const int r = l2->rank;
+    const mx_lora t = {fact[0], nullptr, r, l2->scale};
+    const mx_lora *ad[1] = {&t};
+    if ((rc = lora_down(v, num_experts, L.plan.max_tiles, dy, hidden, v.row_slot, hidden, ad, 1,
+                        dz + 64, kLoraLd, s)))
+      return rc;
+  }
+  mark_stage(2, s);
+  {
+    Params p = base_params(v);
+    p.x = dy;
+    p.ldx = hidden;
+    p.row_token = v.row_slot;
+    p.K = hidden;
+    p.w[0] = w2->data;
+    p.wscale[0] = w2->scale;
+    p.wn[0] = hidden;
+    p.k_split = hidden;
+    p.N = ffn;
+    p.lora_p = dz + 64;
+    p.ldp = kLoraLd;
+    p.lora_b[0] = lora2 ? fact[1] : nullptr;
+    p.lora_r[0] = lora2 ? l2->rank : 0;
+    p.seg_end = v.seg + num_experts;
+    p.out = dgu;
+    p.ldo = 2 * ffn;
+    if ((rc = launch_any<EPI_STORE2>(w2->format, lora2, p, L.plan, v, s))) return rc;
+    if ((rc = swiglu_backward(dgu, g_in, u_in, R, ffn, act, s))) return rc;
+  }
+  mark_stage(3, s);
+  if (lora2) {
+    const LoraGradJob jb = {dy, hidden, v.row_slot, lsave + 64, hidden, grad_b2, false};
+    const LoraGradJob ja = {h_in, ffn, nullptr, dz + 64, ffn, grad_a2, true};
+    if ((rc = run_lora_grad(jb, l2->rank, v, num_experts, s))) return rc;
+    if ((rc = run_lora_grad(ja, l2->rank, v, num_experts, s))) return rc;
+  }
+
+  // Gate / up projections: dz1 = s1 * dG B1, dz3 = s3 * dU B3, then per-slot
+  // dx = dG W1 + dU W3 + dz1 A1 + dz3 A3 (written over dy, slot order).
+  const mx_lora *l13[2] = {l1, l3};
+  for (int i = 0; i < 2; ++i) {
+    const mx_lora *l = l13[i];
+    if (!has_lora(l)) continue;
+    const int r = l->rank;
+    uint16_t *bt = fact[2 + 2 * i];
+    const mx_lora t = {bt, nullptr, r, l->scale};
+    const mx_lora *ad[1] = {&t};
+    if ((rc = lora_down(v, num_experts, L.plan.max_tiles, dgu + i * ffn, 2 * ffn, nullptr, ffn, ad,
+                        1, dz + 32 * i, kLoraLd, s)))
+      return rc;
+  }
+  mark_stage(4, s);
+  {
+    Params p = base_params(v);
+    p.x = dgu;
+    p.ldx = 2 * ffn;
+    p.row_token = nullptr;
+    p.K = 2 * ffn;
+    p.w[0] = w1->data;
+    p.w[1] = w3->data;
+    p.wscale[0] = w1->scale;
+    p.wscale[1] = w3->scale;
+    p.wn[0] = p.wn[1] = ffn;
+    p.k_split = ffn;
+    p.N = hidden;
+    p.lora_p = dz;
+    p.ldp = kLoraLd;
+    p.lora_b[0] = lora1 ? fact[3] : nullptr;
+    p.lora_b[1] = lora3 ? fact[5] : nullptr;
+    p.lora_r[0] = lora1 ? l1->rank : 0;
+    p.lora_r[1] = lora3 ? l3->rank : 0;
+    p.seg_end = v.seg + num_experts;
+    p.out = dy;
+    p.ldo = hidden;
+    p.out_row = v.row_slot;
+    if ((rc = launch_any<EPI_STORE2>(w1->format, lora1 || lora3, p, L.plan, v, s))) return rc;
+  }
+  mark_stage(5, s);
+  for (int i = 0; i < 2; ++i) {
+    const mx_lora *l = l13[i];
+    if (!has_lora(l)) continue;
+    const LoraGradJob jb = {dgu + i * ffn, 2 * ffn, nullptr, lsave + 32 * i, ffn,
+                            i ? grad_b3 : grad_b1, false};
+    const LoraGradJob ja = {x, hidden, v.row_token, dz + 32 * i, hidden, i ? grad_a3 : grad_a1, true};
+    if ((rc = run_lora_grad(jb, l->rank, v, num_experts, s))) return rc;
+    if ((rc = run_lora_grad(ja, l->rank, v, num_experts, s))) return rc;
+  }
+  return MX_OK;
+}
+
 }  // namespace gemm
 }  // namespace mx
 
@@ -1372,116 +1499,10 @@ extern "C" int mx_moe_backward_act(const void *grad_out, int grad_dtype, const v
   if (rc) return rc;
   mark_stage(1, s);
 
-  // The six LoRA factor transposes (B2^T, A2^T, B1^T, A1^T, B3^T, A3^T) in one launch.
-  {
-    FactorTransposes jobs = {};
-    auto add = [&](const void *src, int64_t rows, int64_t cols, uint16_t *dst) {
-      jobs.job[jobs.n++] = {static_cast<const uint16_t *>(src), dst, rows, cols,
-                            static_cast<int64_t>(num_experts) * rows * cols};
-    };
-    if (lora2) {
-      add(l2->b, hidden, l2->rank, fact[0]);
-      add(l2->a, l2->rank, ffn, fact[1]);
-    }
-    const mx_lora *l13t[2] = {l1, l3};
-    for (int i = 0; i < 2; ++i)
-      if (has_lora(l13t[i])) {
-        add(l13t[i]->b, ffn, l13t[i]->rank, fact[2 + 2 * i]);
-        add(l13t[i]->a, l13t[i]->rank, hidden, fact[3 + 2 * i]);
-      }
-    if ((rc = transpose_factors_multi(jobs, s))) return rc;
-  }
-
-  // Down projection: dz2 = s2 * dy B2, then dh = dy W2 + dz2 A2 into the dG
-  // half of [dG | dU], and the SwiGLU backward turns it into [dG | dU].
-  if (lora2) {
-    const int r = l2->rank;
-    const mx_lora t = {fact[0], nullptr, r, l2->scale};
-    const mx_lora *ad[1] = {&t};
-    if ((rc = lora_down(v, num_experts, L.plan.max_tiles, dy, hidden, v.row_slot, hidden, ad, 1,
-                        dz + 64, kLoraLd, s)))
-      return rc;
-  }
-  mark_stage(2, s);
-  {
-    Params p = base_params(v);
-    p.x = dy;
-    p.ldx = hidden;
-    p.row_token = v.row_slot;
-    p.K = hidden;
-    p.w[0] = w2->data;
-    p.wscale[0] = w2->scale;
-    p.wn[0] = hidden;
-    p.k_split = hidden;
-    p.N = ffn;
-    p.lora_p = dz + 64;
-    p.ldp = kLoraLd;
-    p.lora_b[0] = lora2 ? fact[1] : nullptr;
-    p.lora_r[0] = lora2 ? l2->rank : 0;
-    p.seg_end = v.seg + num_experts;
-    p.out = dgu;
-    p.ldo = 2 * ffn;
-    if ((rc = launch_any<EPI_STORE2>(w2->format, lora2, p, L.plan, v, s))) return rc;
-    if ((rc = swiglu_backward(dgu, g_in, u_in, R, ffn, act, s))) return rc;
-  }
-  mark_stage(3, s);
-  if (lora2) {
-    const LoraGradJob jb = {dy, hidden, v.row_slot, lsave + 64, hidden, grad_b2, false};
-    const LoraGradJob ja = {h_in, ffn, nullptr, dz + 64, ffn, grad_a2, true};
-    if ((rc = run_lora_grad(jb, l2->rank, v, num_experts, s))) return rc;
-    if ((rc = run_lora_grad(ja, l2->rank, v, num_experts, s))) return rc;
-  }
-
-  // Gate / up projections: dz1 = s1 * dG B1, dz3 = s3 * dU B3, then per-slot
-  // dx = dG W1 + dU W3 + dz1 A1 + dz3 A3 (written over dy, slot order).
-  const mx_lora *l13[2] = {l1, l3};
-  for (int i = 0; i < 2; ++i) {
-    const mx_lora *l = l13[i];
-    if (!has_lora(l)) continue;
-    const int r = l->rank;
-    uint16_t *bt = fact[2 + 2 * i], *at = fact[3 + 2 * i];
-    const mx_lora t = {bt, nullptr, r, l->scale};
-    const mx_lora *ad[1] = {&t};
-    if ((rc = lora_down(v, num_experts, L.plan.max_tiles, dgu + i * ffn, 2 * ffn, nullptr, ffn, ad,
-                        1, dz + 32 * i, kLoraLd, s)))
-      return rc;
-  }
-  mark_stage(4, s);
-  {
-    Params p = base_params(v);
-    p.x = dgu;
-    p.ldx = 2 * ffn;
-    p.row_token = nullptr;
-    p.K = 2 * ffn;
-    p.w[0] = w1->data;
-    p.w[1] = w3->data;
-    p.wscale[0] = w1->scale;
-    p.wscale[1] = w3->scale;
-    p.wn[0] = p.wn[1] = ffn;
-    p.k_split = ffn;
-    p.N = hidden;
-    p.lora_p = dz;
-    p.ldp = kLoraLd;
-    p.lora_b[0] = lora1 ? fact[3] : nullptr;
-    p.lora_b[1] = lora3 ? fact[5] : nullptr;
-    p.lora_r[0] = lora1 ? l1->rank : 0;
-    p.lora_r[1] = lora3 ? l3->rank : 0;
-    p.seg_end = v.seg + num_experts;
-    p.out = dy;
-    p.ldo = hidden;
-    p.out_row = v.row_slot;
-    if ((rc = launch_any<EPI_STORE2>(w1->format, lora1 || lora3, p, L.plan, v, s))) return rc;
-  }
-  mark_stage(5, s);
-  for (int i = 0; i < 2; ++i) {
-    const mx_lora *l = l13[i];
-    if (!has_lora(l)) continue;
-    const LoraGradJob jb = {dgu + i * ffn, 2 * ffn, nullptr, lsave + 32 * i, ffn,
-                            i ? grad_b3 : grad_b1, false};
-    const LoraGradJob ja = {x, hidden, v.row_token, dz + 32 * i, hidden, i ? grad_a3 : grad_a1, true};
-    if ((rc = run_lora_grad(jb, l->rank, v, num_experts, s))) return rc;
-    if ((rc = run_lora_grad(ja, l->rank, v, num_experts, s))) return rc;
-  }
+  rc = backward_core(L, v, num_experts, R, hidden, ffn, act, w1, w3, w2, l1, l3, l2, x, g_in,
+                     u_in, h_in, lsave, dy, dgu, dz, fact, grad_a1, grad_b1, grad_a3, grad_b3,
+                     grad_a2, grad_b2, s);
+  if (rc) return rc;
   // grad_tokens[t] = sum of its slots' dx rows (fp32, ascending expert order).
   rc = mx_combine(dy, top_idx, nullptr, score_dtype, num_tokens, top_k, num_experts, hidden,
                   grad_tokens, grad_tokens_dtype, stream);
@@ -1893,7 +1914,8 @@ __global__ __launch_bounds__(256) void ec_fill_kernel(int32_t *p, int64_t n, int
 
 // One wave per token: the token's slots are collected in the given logical
 // order into LDS, then each 512-column span sums score * y over them in fp32
-// (product and sum each rounded once, as index_add_(y.float() * score)).
+// (product and sum each rounded once, as index_add_(y.float() * score)); with
+// no scores the rows are summed as they are (the backward's dx rows).
 __global__ __launch_bounds__(256) void ec_combine_kernel(const uint16_t *y, const void *scores,
                                                          int score_dtype, const int32_t *map,
                                                          const int32_t *order, int64_t T, int L,
@@ -1920,7 +1942,7 @@ __global__ __launch_bounds__(256) void ec_combine_kernel(const uint16_t *y, cons
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
     for (int j = 0; j < n; ++j) {
       const int32_t s = s_slot[w][j];
-      const float sc = load_score(scores, s, score_dtype);
+      const float sc = scores ? load_score(scores, s, score_dtype) : 1.0f;
       const uint4 v = *reinterpret_cast<const uint4 *>(y + static_cast<int64_t>(s) * cols + c0);
       const uint32_t q[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -1942,6 +1964,77 @@ __global__ __launch_bounds__(256) void ec_combine_kernel(const uint16_t *y, cons
       o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
     }
   }
+}
+
+// One wave per slot s of token t = tok[s]: grad_y[s] = bf16(score[s] *
+// grad_out[t]) and grad_scores[s] = sum_c grad_out[t, c] * y[s, c] in fp32, as
+// the token-choice combine backward does per route; slots whose token lies
+// outside [0, T) (they were not combined) get zero gradients.
+__global__ __launch_bounds__(256) void ec_combine_backward_kernel(
+    const void *grad_out, int grad_dtype, const uint16_t *y, const int64_t *tok,
+    const void *scores, int score_dtype, int64_t slots, int64_t T, int64_t cols,
+    uint16_t *grad_y, float *grad_scores) {
+  const int64_t sl = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (sl >= slots) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = tok[sl];
+  const bool ok = t >= 0 && t < T;
+  const float sc = ok ? load_score(scores, sl, score_dtype) : 0.0f;
+  float part = 0.0f;
+  for (int64_t c0 = static_cast<int64_t>(lane) * 8; c0 < cols; c0 += 512) {
+    float g[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    uint4 yv = make_uint4(0, 0, 0, 0);
+    if (ok) {
+      if (grad_dtype == MX_DTYPE_BF16) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(grad_out) + t * cols + c0);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          g[2 * i] = bf16_bits_to_f32(w[i] & 0xffffu);
+          g[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
+        }
+      } else {
+        const float4 *gp = reinterpret_cast<const float4 *>(static_cast<const float *>(grad_out) + t * cols + c0);
+        const float4 a = gp[0], b = gp[1];
+        g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w;
+        g[4] = b.x; g[5] = b.y; g[6] = b.z; g[7] = b.w;
+      }
+      yv = *reinterpret_cast<const uint4 *>(y + sl * cols + c0);
+    }
+    const uint32_t w[4] = {yv.x, yv.y, yv.z, yv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      part += g[2 * i] * bf16_bits_to_f32(w[i] & 0xffffu) + g[2 * i + 1] * bf16_bits_to_f32(w[i] >> 16);
+      o[i] = pack_bf16x2(g[2 * i] * sc, g[2 * i + 1] * sc);
+    }
+    *reinterpret_cast<uint4 *>(grad_y + sl * cols + c0) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
+  if (lane == 0) grad_scores[sl] = ok ? part : 0.0f;
+}
+
+// Scratch of the expert-choice backward: the layer backward's over the slots,
+// then the slot -> physical expert / token arrays and the token -> slot map.
+struct EcBackLayout {
+  BackLayout back;
+  size_t off_phys = 0, off_tok = 0, off_map = 0, bytes = 0;
+};
+
+EcBackLayout ec_back_layout(int64_t slots, int num_experts, int64_t hidden, int64_t ffn,
+                            int64_t tokens, int logical) {
+  EcBackLayout L;
+  L.back = back_layout(slots, num_experts, hidden, ffn);
+  size_t off = align_up(L.back.bytes, 256);
+  L.off_phys = off;
+  off = align_up(off + sizeof(int64_t) * slots, 256);
+  L.off_tok = off;
+  off = align_up(off + sizeof(int64_t) * slots, 256);
+  L.off_map = off;
+  off = align_up(off + sizeof(int32_t) * tokens * logical, 256);
+  L.bytes = off;
+  return L;
 }
 
 int validate_ec(const char *name, int batch, int logical, int capacity, int64_t tps,
@@ -2025,13 +2118,14 @@ extern "C" size_t mx_moe_expert_choice_workspace_size(int batch, int logical_exp
       .bytes;
 }
 
-extern "C" int mx_moe_forward_expert_choice(
+extern "C" int mx_moe_forward_expert_choice_ex(
     const void *tokens, const int64_t *expert_token_indices, const void *expert_token_scores,
     int score_dtype, int batch, int logical_experts, int capacity, int64_t tokens_per_sample,
     const int32_t *logical_to_physical, const int32_t *combine_order, int num_experts,
     int64_t hidden, int64_t ffn, int act, const mx_weight *w1, const mx_weight *w3,
     const mx_weight *w2, const mx_lora *l1, const mx_lora *l3, const mx_lora *l2, void *out,
-    int out_dtype, void *workspace, void *stream) {
+    int out_dtype, void *save_gate, void *save_up, void *save_h, void *save_y, void *save_lora,
+    void *workspace, void *stream) {
   clear_error();
   const char *name = "mx_moe_forward_expert_choice";
   int rc = validate_ec(name, batch, logical_experts, capacity, tokens_per_sample, num_experts,
@@ -2078,16 +2172,138 @@ extern "C" int mx_moe_forward_expert_choice(
     hipLaunchKernelGGL((ec_gather_tok_kernel<int32_t, int32_t>), sgrid, dim3(256), 0, s,
                        v.row_token, tok, slots, T, true, v.row_token);
     if ((rc = check_launch(name))) return rc;
-    uint16_t *y = reinterpret_cast<uint16_t *>(ws + L.layer.off_y);
+    uint16_t *y = save_y ? static_cast<uint16_t *>(save_y)
+                         : reinterpret_cast<uint16_t *>(ws + L.layer.off_y);
+    uint16_t *lora_buf = save_lora ? static_cast<uint16_t *>(save_lora)
+                                   : reinterpret_cast<uint16_t *>(ws + L.layer.off_lora);
+    uint16_t *h = save_h ? static_cast<uint16_t *>(save_h)
+                         : reinterpret_cast<uint16_t *>(ws + L.layer.off_h);
     rc = expert_mlp(L.layer.plan, v, num_experts, static_cast<const uint16_t *>(tokens), hidden,
-                    v.row_token, hidden, ffn, act, w1, w3, w2, l1, l3, l2,
-                    reinterpret_cast<uint16_t *>(ws + L.layer.off_lora),
-                    reinterpret_cast<uint16_t *>(ws + L.layer.off_h), nullptr, nullptr, y, hidden,
-                    v.row_slot, s);
+                    v.row_token, hidden, ffn, act, w1, w3, w2, l1, l3, l2, lora_buf, h,
+                    static_cast<uint16_t *>(save_gate), static_cast<uint16_t *>(save_up), y,
+                    hidden, v.row_slot, s);
     if (rc) return rc;
   }
   hipLaunchKernelGGL(ec_combine_kernel, dim3(static_cast<unsigned>(ceil_div(T, 4))), dim3(256), 0,
-                     s, reinterpret_cast<const uint16_t *>(ws + L.layer.off_y), expert_token_scores,
-                     score_dtype, map, combine_order, T, logical_experts, hidden, out, out_dtype);
+                     s, save_y ? static_cast<const uint16_t *>(save_y)
+                               : reinterpret_cast<const uint16_t *>(ws + L.layer.off_y),
+                     expert_token_scores, score_dtype, map, combine_order, T, logical_experts,
+                     hidden, out, out_dtype);
+  return check_launch(name);
+}
+
+extern "C" int mx_moe_forward_expert_choice(
+    const void *tokens, const int64_t *expert_token_indices, const void *expert_token_scores,
+    int score_dtype, int batch, int logical_experts, int capacity, int64_t tokens_per_sample,
+    const int32_t *logical_to_physical, const int32_t *combine_order, int num_experts,
+    int64_t hidden, int64_t ffn, int act, const mx_weight *w1, const mx_weight *w3,
+    const mx_weight *w2, const mx_lora *l1, const mx_lora *l3, const mx_lora *l2, void *out,
+    int out_dtype, void *workspace, void *stream) {
+  return mx_moe_forward_expert_choice_ex(
+      tokens, expert_token_indices, expert_token_scores, score_dtype, batch, logical_experts,
+      capacity, tokens_per_sample, logical_to_physical, combine_order, num_experts, hidden, ffn,
+      act, w1, w3, w2, l1, l3, l2, out, out_dtype, nullptr, nullptr, nullptr, nullptr, nullptr,
+      workspace, stream);
+}
+
+extern "C" size_t mx_moe_backward_expert_choice_workspace_size(int batch, int logical_experts,
+                                                               int capacity,
+                                                               int64_t tokens_per_sample,
+                                                               int num_experts, int64_t hidden,
+                                                               int64_t ffn) {
+  if (batch < 0 || logical_experts <= 0 || capacity <= 0 || tokens_per_sample <= 0 ||
+      num_experts <= 0 || hidden <= 0 || ffn <= 0)
+    return 0;
+  const int64_t slots = static_cast<int64_t>(batch) * logical_experts * capacity;
+  return ec_back_layout(slots, num_experts, hidden, ffn, batch * tokens_per_sample,
+                        logical_experts).bytes;
+}
+
+extern "C" int mx_moe_backward_expert_choice(
+    const void *grad_out, int grad_dtype, const void *tokens, const int64_t *expert_token_indices,
+    const void *expert_token_scores, int score_dtype, int batch, int logical_experts,
+    int capacity, int64_t tokens_per_sample, const int32_t *logical_to_physical,
+    const int32_t *combine_order, int num_experts, int64_t hidden, int64_t ffn, int act,
+    const mx_weight *w1, const mx_weight *w3, const mx_weight *w2, const mx_lora *l1,
+    const mx_lora *l3, const mx_lora *l2, const void *save_gate, const void *save_up,
+    const void *save_h, const void *save_y, const void *save_lora, void *grad_tokens,
+    int grad_tokens_dtype, float *grad_scores, float *grad_a1, float *grad_b1, float *grad_a3,
+    float *grad_b3, float *grad_a2, float *grad_b2, void *workspace, void *stream) {
+  clear_error();
+  const char *name = "mx_moe_backward_expert_choice";
+  int rc = validate_ec(name, batch, logical_experts, capacity, tokens_per_sample, num_experts,
+                       logical_to_physical);
+  if (rc) return rc;
+  if (act != MX_ACT_SILU && act != MX_ACT_SWIGLU7) {
+    set_error("%s: unknown activation %d", name, act);
+    return MX_ERR_INVALID;
+  }
+  if ((rc = check_layer(name, hidden, ffn, w1, w3, w2, l1, l3, l2))) return rc;
+  if (w1->format == MX_FMT_F32X3) {
+    set_error("%s: MX_FMT_F32X3 (fp32) weights are inference-only", name);
+    return MX_ERR_INVALID;
+  }
+  const int64_t T = static_cast<int64_t>(batch) * tokens_per_sample;
+  const int64_t slots = static_cast<int64_t>(batch) * logical_experts * capacity;
+  if (T == 0) return MX_OK;
+  const bool lora = has_lora(l1) || has_lora(l3) || has_lora(l2);
+  if (!grad_out || !tokens || !grad_tokens || !workspace ||
+      (slots > 0 && (!expert_token_indices || !expert_token_scores || !grad_scores ||
+                     !save_gate || !save_up || !save_h || !save_y || (lora && !save_lora)))) {
+    set_error("%s: gradients, routes, saved activations and workspace must be non-null", name);
+    return MX_ERR_INVALID;
+  }
+  if ((grad_dtype != MX_DTYPE_BF16 && grad_dtype != MX_DTYPE_F32) ||
+      (grad_tokens_dtype != MX_DTYPE_BF16 && grad_tokens_dtype != MX_DTYPE_F32)) {
+    set_error("%s: gradients must be bf16 or fp32", name);
+    return MX_ERR_INVALID;
+  }
+  hipStream_t s = as_stream(stream);
+  const EcBackLayout L = ec_back_layout(slots, num_experts, hidden, ffn, T, logical_experts);
+  char *ws = static_cast<char *>(workspace);
+  int64_t *phys = reinterpret_cast<int64_t *>(ws + L.off_phys);
+  int64_t *tok = reinterpret_cast<int64_t *>(ws + L.off_tok);
+  int32_t *map = reinterpret_cast<int32_t *>(ws + L.off_map);
+  uint16_t *dy = reinterpret_cast<uint16_t *>(ws + L.back.off_dy);
+  hipLaunchKernelGGL(ec_fill_kernel, dim3(static_cast<unsigned>(ceil_div(T * logical_experts, 256))),
+                     dim3(256), 0, s, map, T * logical_experts, -1);
+  if (slots > 0) {
+    const dim3 sgrid(static_cast<unsigned>(ceil_div(slots, 256)));
+    hipLaunchKernelGGL(ec_slots_kernel, sgrid, dim3(256), 0, s, expert_token_indices, slots,
+                       logical_experts, capacity, tokens_per_sample, logical_to_physical, phys,
+                       tok);
+    hipLaunchKernelGGL(ec_map_kernel, sgrid, dim3(256), 0, s, tok, slots, logical_experts,
+                       capacity, T, map);
+    if ((rc = check_launch(name))) return rc;
+    // The forward's plan over the slots (k = 1), rebuilt.
+    rc = build_plan(phys, nullptr, score_dtype, slots, 1, num_experts, nullptr, nullptr, nullptr,
+                    nullptr, nullptr, nullptr, nullptr, ws, s);
+    if (rc) return rc;
+    const PlanView v = plan_view(ws, L.back.plan);
+    hipLaunchKernelGGL((ec_gather_tok_kernel<int32_t, int32_t>), sgrid, dim3(256), 0, s,
+                       v.row_token, tok, slots, T, true, v.row_token);
+    hipLaunchKernelGGL(ec_combine_backward_kernel, dim3(static_cast<unsigned>(ceil_div(slots, 4))),
+                       dim3(256), 0, s, grad_out, grad_dtype,
+                       static_cast<const uint16_t *>(save_y), tok, expert_token_scores,
+                       score_dtype, slots, T, hidden, dy, grad_scores);
+    if ((rc = check_launch(name))) return rc;
+    uint16_t *fact[6];
+    for (int i = 0; i < 6; ++i) fact[i] = reinterpret_cast<uint16_t *>(ws + L.back.off_fact[i]);
+    rc = backward_core(L.back, v, num_experts, slots, hidden, ffn, act, w1, w3, w2, l1, l3, l2,
+                       static_cast<const uint16_t *>(tokens),
+                       static_cast<const uint16_t *>(save_gate),
+                       static_cast<const uint16_t *>(save_up),
+                       static_cast<const uint16_t *>(save_h),
+                       static_cast<const uint16_t *>(save_lora), dy,
+                       reinterpret_cast<uint16_t *>(ws + L.back.off_dgu),
+                       reinterpret_cast<uint16_t *>(ws + L.back.off_dz), fact, grad_a1, grad_b1,
+                       grad_a3, grad_b3, grad_a2, grad_b2, s);
+    if (rc) return rc;
+  }
+  // grad_tokens[t] = sum of its slots' dx rows (fp32, ascending (physical,
+  // logical) order; zero for tokens no expert picked).
+  hipLaunchKernelGGL(ec_combine_kernel, dim3(static_cast<unsigned>(ceil_div(T, 4))), dim3(256), 0,
+                     s, dy, nullptr, MX_DTYPE_F32, map, combine_order, T, logical_experts,
+                     hidden, grad_tokens, grad_tokens_dtype);
   return check_launch(name);
 }

@@ -245,15 +245,8 @@ def _expert_choice_meta(aliases, logical, num_experts, device):
     return _EC_META[key]
 
 
-def expert_choice_experts(module, tokens, expert_token_scores, expert_token_indices,
-                          tokens_per_sample, aliases=()):
-    """Expert-choice routed layer (inference) through mx_moe_forward_expert_choice."""
-    params = _lora_params(module)
-    if torch.is_grad_enabled() and any(
-            t is not None and t.requires_grad
-            for t in (tokens, expert_token_scores, *params)):
-        raise NotImplementedError(
-            "the fused expert-choice layer is inference-only; call it under torch.no_grad()")
+def _ec_inputs(module, tokens, expert_token_scores, expert_token_indices, tokens_per_sample,
+               aliases):
     if expert_token_indices.shape != expert_token_scores.shape:
         raise ValueError("Expert-choice indices and scores must have matching shapes.")
     if expert_token_indices.ndim != 3:
@@ -266,12 +259,20 @@ def expert_choice_experts(module, tokens, expert_token_scores, expert_token_indi
     B, L, C = (int(v) for v in expert_token_indices.shape)
     l2p, order = _expert_choice_meta(tuple(aliases), L, module.num_experts, device)
     x = tokens.detach().to(torch.bfloat16).contiguous()
-    T, d = (int(v) for v in x.shape)
     idx = expert_token_indices.detach().to(torch.int64).contiguous()
     scores = expert_token_scores.detach()
     if scores.dtype not in (torch.float32, torch.bfloat16):
         scores = scores.float()
-    scores = scores.contiguous()
+    return device, (B, L, C), l2p, order, x, idx, scores.contiguous()
+
+
+def _ec_forward(module, tokens, expert_token_scores, expert_token_indices, tokens_per_sample,
+                aliases, need_grad):
+    """One mx_moe_forward_expert_choice_ex call; returns (out, saved or None)."""
+    device, (B, L, C), l2p, order, x, idx, scores = _ec_inputs(
+        module, tokens, expert_token_scores, expert_token_indices, tokens_per_sample, aliases)
+    T, d = (int(v) for v in x.shape)
+    S = B * L * C
     (w1, w3, w2), packed = _weight_descriptors(module, device)
     f = int(packed[0].shape[1])
     lora, keep = _lora_descriptors(module, device)
@@ -279,16 +280,103 @@ def expert_choice_experts(module, tokens, expert_token_scores, expert_token_indi
     # to the token dtype).
     out = torch.empty((T, d), dtype=torch.float32 if tokens.dtype == torch.float32
                       else torch.bfloat16, device=device)
+    saves = [None] * 5
+    if need_grad:
+        saves = [torch.empty((S, f), dtype=torch.bfloat16, device=device),
+                 torch.empty((S, f), dtype=torch.bfloat16, device=device),
+                 torch.empty((S, f), dtype=torch.bfloat16, device=device),
+                 torch.empty((S, d), dtype=torch.bfloat16, device=device),
+                 torch.zeros((S, LORA_ROW), dtype=torch.bfloat16, device=device)]
     lib = nat.load_library()
     ws = nat.workspace(lib.mx_moe_expert_choice_workspace_size(B, L, C, tokens_per_sample,
                                                                module.num_experts, d, f), device)
-    nat.call("mx_moe_forward_expert_choice", x.data_ptr(), idx.data_ptr(), scores.data_ptr(),
+    nat.call("mx_moe_forward_expert_choice_ex", x.data_ptr(), idx.data_ptr(), scores.data_ptr(),
              nat.dtype_code(scores.dtype), B, L, C, int(tokens_per_sample), nat.ptr(l2p),
              nat.ptr(order), module.num_experts, d, f, kernel_activation(module), w1, w3, w2,
-             lora[0], lora[1], lora[2], out.data_ptr(), nat.dtype_code(out.dtype), ws.data_ptr(),
-             nat.stream(device))
+             lora[0], lora[1], lora[2], out.data_ptr(), nat.dtype_code(out.dtype),
+             *[nat.ptr(t) for t in saves], ws.data_ptr(), nat.stream(device))
     del keep
-    return out.to(tokens.dtype)
+    return out.to(tokens.dtype), ((x, scores, idx, *saves) if need_grad else None)
+
+
+class _ExpertChoiceExperts(torch.autograd.Function):
+    """Expert-choice layer with gradients to tokens, scores and the LoRA
+    factors (the autograd of run_compressed_expert_choice,
+    execution/expert_choice.py:16-152): one mx_moe_backward_expert_choice call."""
+
+    @staticmethod
+    def forward(ctx, module, tokens_per_sample, aliases, tokens, expert_token_scores,
+                expert_token_indices, *lora_params):
+        out, saved = _ec_forward(module, tokens, expert_token_scores, expert_token_indices,
+                                 tokens_per_sample, aliases, True)
+        ctx.module, ctx.tps, ctx.aliases = module, tokens_per_sample, aliases
+        ctx.token_dtype, ctx.score_dtype = tokens.dtype, expert_token_scores.dtype
+        ctx.save_for_backward(*saved)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        from .backward import lora_param_grads
+
+        x, scores, idx, gate, up, h, y, lora_rows = ctx.saved_tensors
+        module = ctx.module
+        device = x.device
+        B, L, C = (int(v) for v in idx.shape)
+        T, d = (int(v) for v in x.shape)
+        E = module.num_experts
+        l2p, order = _expert_choice_meta(tuple(ctx.aliases), L, E, device)
+        (w1, w3, w2), packed = _weight_descriptors(module, device)
+        f = int(packed[0].shape[1])
+        lora, keep = _lora_descriptors(module, device)
+        g = grad_out.contiguous()
+        if g.dtype not in (torch.float32, torch.bfloat16):
+            g = g.float()
+        grad_tokens = torch.empty((T, d), dtype=torch.float32 if ctx.token_dtype == torch.float32
+                                  else torch.bfloat16, device=device)
+        grad_scores = torch.empty((B, L, C), dtype=torch.float32, device=device)
+        lora_needs = ctx.needs_input_grad[6:]
+        raw = []
+        for i, adapter in enumerate(module._adapters()):
+            if adapter is None:
+                raw += [None, None]
+                continue
+            r8 = adapter.padded_rank()
+            raw.append(torch.empty((E, r8, adapter.in_features), dtype=torch.float32,
+                                   device=device) if lora_needs[2 * i] else None)
+            raw.append(torch.empty((E, adapter.out_features, r8), dtype=torch.float32,
+                                   device=device) if lora_needs[2 * i + 1] else None)
+        lib = nat.load_library()
+        ws = nat.workspace(lib.mx_moe_backward_expert_choice_workspace_size(
+            B, L, C, ctx.tps, E, d, f), device)
+        nat.call("mx_moe_backward_expert_choice", g.data_ptr(), nat.dtype_code(g.dtype),
+                 x.data_ptr(), idx.data_ptr(), scores.data_ptr(), nat.dtype_code(scores.dtype),
+                 B, L, C, int(ctx.tps), nat.ptr(l2p), nat.ptr(order), E, d, f,
+                 kernel_activation(module), w1, w3, w2, lora[0], lora[1], lora[2],
+                 gate.data_ptr(), up.data_ptr(), h.data_ptr(), y.data_ptr(), lora_rows.data_ptr(),
+                 grad_tokens.data_ptr(), nat.dtype_code(grad_tokens.dtype),
+                 grad_scores.data_ptr(), *[nat.ptr(t) for t in raw], ws.data_ptr(),
+                 nat.stream(device))
+        del keep
+        grad_t = grad_tokens.to(ctx.token_dtype) if ctx.needs_input_grad[3] else None
+        grad_s = grad_scores.to(ctx.score_dtype) if ctx.needs_input_grad[4] else None
+        return (None, None, None, grad_t, grad_s, None, *lora_param_grads(module, raw))
+
+
+def expert_choice_experts(module, tokens, expert_token_scores, expert_token_indices,
+                          tokens_per_sample, aliases=()):
+    """Expert-choice routed layer through mx_moe_forward_expert_choice_ex; with
+    autograd (gradients to tokens, scores and the LoRA factors) when one of
+    them requires a gradient."""
+    params = _lora_params(module)
+    if torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad
+            for t in (tokens, expert_token_scores, *params)):
+        _ec_inputs(module, tokens, expert_token_scores, expert_token_indices, tokens_per_sample,
+                   aliases)  # validates before autograd records anything
+        return _ExpertChoiceExperts.apply(module, int(tokens_per_sample), tuple(aliases), tokens,
+                                          expert_token_scores, expert_token_indices, *params)
+    return _ec_forward(module, tokens, expert_token_scores, expert_token_indices,
+                       int(tokens_per_sample), aliases, False)[0]
 
 
 def sorted_experts(module, tokens, counts):

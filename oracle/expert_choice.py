@@ -46,11 +46,13 @@ def expert_choice_forward(tokens: torch.Tensor, scores: torch.Tensor, idx: torch
                           tokens_per_sample: int, weights: dict, loras: dict, num_physical: int,
                           alias=()) -> torch.Tensor:
     """[B * tokens_per_sample, d] output in the token dtype."""
-    plan = build_expert_choice_plan(idx.numpy(), scores.float().numpy(), tokens_per_sample,
-                                    num_physical, alias)
+    plan = build_expert_choice_plan(idx.numpy(), scores.detach().float().numpy(),
+                                    tokens_per_sample, num_physical, alias)
     output = torch.zeros(tokens.shape, dtype=torch.float32)
     sorted_tokens = torch.from_numpy(plan["sorted_token_indices"])
-    sorted_scores = torch.from_numpy(plan["sorted_scores"]).float()
+    # The plan's sorted scores, gathered with torch so that autograd reaches
+    # the [B, L, C] scores (the reference's plan index_selects them).
+    sorted_scores = scores.reshape(-1).float()[torch.from_numpy(plan["sort_positions"])]
     for e in range(num_physical):
         a, n = int(plan["starts"][e]), int(plan["counts"][e])
         if n == 0:
