@@ -23,9 +23,13 @@
  *   BF16 weight     w [E, out, in] bf16
  *   F32X3 weight    w [E, out, 3*in] bf16: an fp32 weight split into bf16
  *                   planes [hi | lo | hi] along in (see mx_split_f32)
- *   LoRA factors    A [E, r, in], B [E, out, r] bf16 (rank r <= 32); with
- *                   F32X3 weights A [E, r, 3*in] and B [E, out, 3*r] in
- *                   [hi | lo | hi] planes, r = 8
+ *   LoRA factors    A [E, r, in], B [E, out, r] bf16 (r a multiple of 8,
+ *                   at most 256); with F32X3 weights A [E, r, 3*in] and
+ *                   B [E, out, 3*r] in [hi | lo | hi] planes, r = 8
+ *   lora_rank       argument of the *_workspace_size queries: the largest
+ *                   rank of the adapters the calls will carry (0 without
+ *                   LoRA). The low-rank rows hold 3 planes of
+ *                   rc = max(32, lora_rank rounded up to 32) columns.
  *
  * Each declaration cites the reference interface (seruva19/mirai, path:line)
  * whose semantics it implements.
@@ -336,7 +340,7 @@ typedef struct mx_weight {
 typedef struct mx_lora {
   const void *a;        /* bf16 [E, r, in]  */
   const void *b;        /* bf16 [E, out, r] */
-  int rank;             /* 0 (no adapter) .. 32 */
+  int rank;             /* 0 (no adapter), or a multiple of 8 up to 256 */
   float scale;          /* alpha / r (or alpha / sqrt(r)) times extra scales */
 } mx_lora;
 
@@ -350,9 +354,10 @@ typedef struct mx_lora {
  */
 int mx_set_stage_events(void **events, int count);
 
-/* Bytes of scratch for mx_moe_forward / mx_moe_for_loop (BF16, NF4, INT8 weights). */
+/* Bytes of scratch for mx_moe_forward / mx_moe_for_loop / mx_grouped_linear
+ * (BF16, NF4, INT8 weights) with adapters of rank <= lora_rank. */
 size_t mx_moe_workspace_size(int64_t num_tokens, int top_k, int num_experts,
-                             int64_t hidden, int64_t ffn);
+                             int64_t hidden, int64_t ffn, int lora_rank);
 
 /* Bytes of scratch for mx_moe_forward with MX_FMT_F32X3 weights (fp32 tokens). */
 size_t mx_moe_f32x3_workspace_size(int64_t num_tokens, int top_k, int num_experts,
@@ -404,7 +409,8 @@ int mx_split_f32(const float *x, int64_t rows, int64_t cols, int pattern, void *
  * Optional saved activations for backward (any may be NULL):
  *   save_gate/save_up [R, ffn] bf16 pre-activation projections (sorted order),
  *   save_h [R, ffn] bf16, save_y [R, hidden] bf16 (flat slot order t*k+j),
- *   save_lora [R, 3, 32] bf16 scaled low-rank activations.
+ *   save_lora [R, 3, rc] bf16 scaled low-rank activations (rc as above,
+ *   from the largest attached rank).
  * With MX_FMT_F32X3 weights (all three) the layer runs at fp32 precision:
  * tokens are fp32 [T, hidden], the workspace comes from
  * mx_moe_f32x3_workspace_size, no activations are saved (inference only),
@@ -493,11 +499,11 @@ int mx_build_expert_choice_plan(const int64_t *expert_token_indices,
  * save pointers are non-NULL, the activations the backward needs (as
  * mx_moe_forward_ex does, with the S = B * L * C slots as the rows: gate / up /
  * h [S, ffn] in expert-sorted order, y [S, hidden] in slot order, low-rank
- * rows [S, 96]).
+ * rows [S, 3, rc]).
  */
 size_t mx_moe_expert_choice_workspace_size(int batch, int logical_experts, int capacity,
                                            int64_t tokens_per_sample, int num_experts,
-                                           int64_t hidden, int64_t ffn);
+                                           int64_t hidden, int64_t ffn, int lora_rank);
 int mx_moe_forward_expert_choice(const void *tokens, const int64_t *expert_token_indices,
                                  const void *expert_token_scores, int score_dtype, int batch,
                                  int logical_experts, int capacity, int64_t tokens_per_sample,
@@ -531,7 +537,7 @@ int mx_moe_forward_expert_choice_ex(
 size_t mx_moe_backward_expert_choice_workspace_size(int batch, int logical_experts,
                                                     int capacity, int64_t tokens_per_sample,
                                                     int num_experts, int64_t hidden,
-                                                    int64_t ffn);
+                                                    int64_t ffn, int lora_rank);
 int mx_moe_backward_expert_choice(
     const void *grad_out, int grad_dtype, const void *tokens, const int64_t *expert_token_indices,
     const void *expert_token_scores, int score_dtype, int batch, int logical_experts,
@@ -605,7 +611,7 @@ int mx_moe_backward_act(const void *grad_out, int grad_dtype, const void *tokens
 
 /* Bytes of scratch for mx_moe_backward (and mx_moe_backward_act). */
 size_t mx_moe_backward_workspace_size(int64_t num_tokens, int top_k, int num_experts,
-                                      int64_t hidden, int64_t ffn);
+                                      int64_t hidden, int64_t ffn, int lora_rank);
 
 #ifdef __cplusplus
 }

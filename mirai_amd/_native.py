@@ -95,7 +95,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         c_int, [_P, _P, c_int, c_int, c_int, c_int, c_int64, _P, c_int, _P, _P, _P, _P, _P, _P,
                 _P, _P, _P]),
     "mx_moe_expert_choice_workspace_size": (
-        c_size_t, [c_int, c_int, c_int, c_int64, c_int, c_int64, c_int64]),
+        c_size_t, [c_int, c_int, c_int, c_int64, c_int, c_int64, c_int64, c_int]),
     "mx_moe_forward_expert_choice": (
         c_int,
         [_P, _P, _P, c_int, c_int, c_int, c_int, c_int64, _P, _P, c_int, c_int64, c_int64, c_int,
@@ -105,7 +105,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_P, _P, _P, c_int, c_int, c_int, c_int, c_int64, _P, _P, c_int, c_int64, c_int64, c_int,
          _W, _W, _W, _L, _L, _L, _P, c_int, _P, _P, _P, _P, _P, _P, _P]),
     "mx_moe_backward_expert_choice_workspace_size": (
-        c_size_t, [c_int, c_int, c_int, c_int64, c_int, c_int64, c_int64]),
+        c_size_t, [c_int, c_int, c_int, c_int64, c_int, c_int64, c_int64, c_int]),
     "mx_moe_backward_expert_choice": (
         c_int,
         [_P, c_int, _P, _P, _P, c_int, c_int, c_int, c_int, c_int64, _P, _P, c_int, c_int64,
@@ -129,7 +129,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "mx_int8_quantize": (c_int, [_P, c_int, c_int64, c_int64, _P, _P, _P]),
     "mx_int8_dequantize": (c_int, [_P, _P, c_int64, c_int64, _P, c_int, _P]),
     "mx_set_stage_events": (c_int, [POINTER(c_void_p), c_int]),
-    "mx_moe_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int64]),
+    "mx_moe_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int64, c_int]),
     "mx_moe_f32x3_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int64]),
     "mx_split_f32": (c_int, [_P, c_int64, c_int64, c_int, _P, _P]),
     "mx_moe_forward": (
@@ -151,7 +151,8 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "mx_moe_for_loop": (
         c_int, [_P, _P, c_int64, c_int, c_int64, c_int64, _W, _W, _W, _L, _L, _L, _P, _P, _P]),
     "mx_grouped_linear": (c_int, [_P, _P, c_int64, c_int, _W, _L, _P, _P, _P]),
-    "mx_moe_backward_workspace_size": (c_size_t, [c_int64, c_int, c_int, c_int64, c_int64]),
+    "mx_moe_backward_workspace_size": (c_size_t,
+                                       [c_int64, c_int, c_int, c_int64, c_int64, c_int]),
     "mx_moe_backward": (
         c_int,
         [_P, c_int, _P, _P, _P, c_int, c_int64, c_int, c_int, c_int64, c_int64, _W, _W, _W,

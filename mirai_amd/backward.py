@@ -22,7 +22,7 @@ def native_backward(module, saved, grad_out, token_dtype, *, need_tokens=True, n
     Returns (grad_tokens, fp32 for fp32 tokens else bf16; fp32 grad_scores; raw fp32
     LoRA factor gradients at the padded rank: [dA, dB] per adapter, None where
     not wanted or absent)."""
-    from .fused import _lora_descriptors, _weight_descriptors, kernel_activation
+    from .fused import _lora_descriptors, _weight_descriptors, kernel_activation, lora_rank
 
     x, scores, idx, gate, up, h, y, lora_rows = saved
     device = x.device
@@ -51,7 +51,8 @@ def native_backward(module, saved, grad_out, token_dtype, *, need_tokens=True, n
         raw.append(torch.empty((E, adapter.out_features, r8), dtype=torch.float32, device=device)
                    if want_b else None)
     lib = nat.load_library()
-    ws = nat.workspace(lib.mx_moe_backward_workspace_size(T, k, E, d, f), device)
+    ws = nat.workspace(lib.mx_moe_backward_workspace_size(T, k, E, d, f, lora_rank(module)),
+                       device)
     nat.call("mx_moe_backward_act", g.data_ptr(), nat.dtype_code(g.dtype), x.data_ptr(),
              idx.data_ptr(), scores.data_ptr(), nat.dtype_code(scores.dtype), T, k, E, d, f,
              kernel_activation(module), w1, w3, w2, lora[0], lora[1], lora[2], gate.data_ptr(),

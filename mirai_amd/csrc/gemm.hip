@@ -18,6 +18,8 @@
 // expert's weights, run on the same XCD and hit its L2.
 #include <stdlib.h>
 
+#include <algorithm>
+#include <initializer_list>
 #include <mutex>
 #include <type_traits>
 
@@ -31,8 +33,8 @@ namespace mx {
 namespace gemm {
 
 constexpr int kNf4Block = 64;   // NF4 absmax block along K
-constexpr int kLoraK = 32;      // LoRA rank padded to two MFMA K steps
-constexpr int kLoraLd = 96;     // low-rank activation row: [gate 32 | up 32 | down 32]
+constexpr int kLoraK = 32;        // one LDS-staged LoRA K chunk: two MFMA K steps
+constexpr int kLoraMaxRank = 256; // largest LoRA rank the layer takes
 
 enum { EPI_SWIGLU = 0, EPI_STORE = 1, EPI_LORA_A = 2, EPI_STORE2 = 4 };
 
@@ -90,10 +92,12 @@ struct Params {
   int64_t k_split;           // transposed B: K rows taken from w[0], the rest from w[1]
   int64_t N;                 // output columns
   int n_tiles_n;
-  const uint16_t *lora_p;    // [R, ldp] scaled low-rank activations
+  const uint16_t *lora_p;    // [R, ldp] scaled low-rank activations, adapter i at column i * lora_rc
   int64_t ldp;
+  int lora_rc;               // width of one adapter's low-rank columns (a multiple of 32)
   const uint16_t *lora_b[2]; // [E, N, r]
   int lora_r[2];
+  int64_t lora_stride[4];    // EPI_LORA_A: factor rows per expert of each sub-adapter's factor
   const int2 *tiles;
   const int32_t *num_tiles;
   const int64_t *seg_end;
@@ -314,7 +318,8 @@ void grouped_gemm_kernel(Params p) {
   const int64_t wn_rows = pick(p.wn, which);
   const bool b_valid = EPI == EPI_LORA_A ? bn < wn_rows : !TRANS;
   if (EPI != EPI_LORA_A) bn = min(bn, wn_rows - 1);
-  const int64_t wrow = static_cast<int64_t>(e) * wn_rows + bn;
+  const int64_t wrow =
+      static_cast<int64_t>(e) * (EPI == EPI_LORA_A ? pick(p.lora_stride, which) : wn_rows) + bn;
   const uint8_t *b_base = nullptr;
   const void *b_absmax = nullptr;  // the row's absmax entries
   float b_scale = 0.0f;
@@ -511,7 +516,7 @@ void grouped_gemm_kernel(Params p) {
       const int row = rem >> 6, c = ((rem >> 4) & 3) ^ ((row >> 1) & 3);
       // Rows past the segment end repeat its last row: they feed dropped outputs.
       const int64_t grow = min(row0 + row, row_end - 1);
-      dma16(p.lora_p + grow * p.ldp + ad * 32 + c * 8, dP + g * 1024);
+      dma16(p.lora_p + grow * p.ldp + ad * p.lora_rc + c * 8, dP + g * 1024);
     }
 #pragma unroll
     for (int i = 0; i < kLDma / kWaves; ++i) {
@@ -587,7 +592,8 @@ void grouped_gemm_kernel(Params p) {
 #pragma unroll
     for (int a2 = 0; a2 < n_lb; ++a2) {
       const int ad = EPI == EPI_SWIGLU ? (nb / (T::NB / 2)) : a2;
-      if (pick2(p.lora_r, ad) == 0) continue;  // absent adapter: its tiles are not staged
+      const int r = pick2(p.lora_r, ad);
+      if (r == 0) continue;  // absent adapter: its tiles are not staged
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         const int ch = kk * 2 + (lane >> 5);
@@ -596,6 +602,30 @@ void grouped_gemm_kernel(Params p) {
         const bf16x8 b = *reinterpret_cast<const bf16x8 *>(
             sL + a2 * T::BN * 64 + swz64(wn * T::WN + nb * 32 + (lane & 31), ch));
         t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, t, 0, 0, 0);
+      }
+      if (r <= kLoraK) continue;
+      // Ranks above 32: the further 32-wide K chunks read their fragments
+      // straight from global memory (the tile's low-rank rows and factor rows
+      // stay in L2) into the same fp32 sum, so the delta is still rounded
+      // once. The factor row is the one the staged tile holds for this lane.
+      const int j = wn * T::WN + nb * 32 + (lane & 31);
+      int lw = ad;
+      int64_t n = static_cast<int64_t>(nt) * T::BN + j;
+      if (EPI == EPI_SWIGLU) b_row<EPI, T>(j, nt, lw, n);
+      n = min(n, p.N - 1);
+      const uint16_t *frow = pick2(p.lora_b, ad) + (static_cast<int64_t>(e) * p.N + n) * r;
+      const int64_t prow = min(row0 + wm * T::WM + mb * 32 + (lane & 31), row_end - 1);
+      const uint16_t *arow = p.lora_p + prow * p.ldp + ad * p.lora_rc;
+      for (int c0 = kLoraK; c0 < r; c0 += kLoraK) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const int col = c0 + kk * 16 + (lane >> 5) * 8;
+          // Columns past the rank hold zero activations; their factor read
+          // stays inside the row.
+          const bf16x8 a = *reinterpret_cast<const bf16x8 *>(arow + col);
+          const bf16x8 b = *reinterpret_cast<const bf16x8 *>(frow + (col < r ? col : 0));
+          t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, t, 0, 0, 0);
+        }
       }
     }
     return t;
@@ -1032,22 +1062,29 @@ void mark_stage(int i, hipStream_t s) {
     (void)hipEventRecord(static_cast<hipEvent_t>(g_stage_events[i]), s);
 }
 
+// Columns of one adapter's low-rank plane: the rank rounded up to a whole
+// LoRA K chunk (32).
+int lora_width(int rank) {
+  return rank <= kLoraK ? kLoraK : (rank + kLoraK - 1) / kLoraK * kLoraK;
+}
+
 struct LayerLayout {
   PlanLayout plan;
   size_t off_lora = 0, off_h = 0, off_y = 0, off_x = 0, off_sum = 0, bytes = 0;
 };
 
-// Scratch of the layer: plan | low-rank activations [R, 96] | h [R, f] |
-// y [R, d]. The fp32 (MX_FMT_F32X3) layer holds h as planes [R, 3f] and y as
-// planes [R, 2d], and adds the split tokens [T, 3d] and the fp32 combine of
-// both y planes [T, 2d].
+// Scratch of the layer: plan | low-rank activations [R, 3 rc] (planes of rc
+// columns for gate, up and down, rc = lora_width of the largest rank) |
+// h [R, f] | y [R, d]. The fp32 (MX_FMT_F32X3) layer holds h as planes
+// [R, 3f] and y as planes [R, 2d], and adds the split tokens [T, 3d] and the
+// fp32 combine of both y planes [T, 2d].
 LayerLayout layer_layout(int64_t rows, int num_experts, int64_t hidden, int64_t ffn,
-                         bool split = false, int64_t tokens = 0) {
+                         bool split = false, int64_t tokens = 0, int rc = kLoraK) {
   LayerLayout L;
   L.plan = plan_layout(rows, num_experts);
   size_t off = align_up(L.plan.bytes, 256);
   L.off_lora = off;
-  off = align_up(off + sizeof(uint16_t) * rows * kLoraLd, 256);
+  off = align_up(off + sizeof(uint16_t) * rows * 3 * rc, 256);
   L.off_h = off;
   off = align_up(off + sizeof(uint16_t) * rows * ffn * (split ? 3 : 1), 256);
   L.off_y = off;
@@ -1063,6 +1100,13 @@ LayerLayout layer_layout(int64_t rows, int num_experts, int64_t hidden, int64_t 
 }
 
 bool has_lora(const mx_lora *l) { return l && l->rank > 0; }
+
+int lora_width(const mx_lora *a, const mx_lora *b, const mx_lora *c) {
+  int r = 0;
+  for (const mx_lora *l : {a, b, c})
+    if (has_lora(l) && l->rank > r) r = l->rank;
+  return lora_width(r);
+}
 
 int check_weight(const char *name, const char *key, const mx_weight *w, int64_t out_f,
                  int64_t in_f) {
@@ -1091,9 +1135,9 @@ int check_weight(const char *name, const char *key, const mx_weight *w, int64_t 
 
 int check_lora(const char *name, const char *key, const mx_lora *l) {
   if (!l || l->rank == 0) return MX_OK;
-  if (l->rank < 0 || l->rank > kLoraK || l->rank % 8 != 0 || !l->a || !l->b) {
-    set_error("%s: LoRA on %s needs rank in {8,16,24,32} and both factors (got rank %d)", name,
-              key, l->rank);
+  if (l->rank < 0 || l->rank > kLoraMaxRank || l->rank % 8 != 0 || !l->a || !l->b) {
+    set_error("%s: LoRA on %s needs a rank that is a multiple of 8 up to %d and both factors "
+              "(got rank %d)", name, key, kLoraMaxRank, l->rank);
     return MX_ERR_INVALID;
   }
   return MX_OK;
@@ -1106,37 +1150,73 @@ Params base_params(const PlanView &v) {
   return p;
 }
 
-// LoRA down-projection p = bf16(s * bf16(x a^T)) for up to 4 adapters that
-// share the same input rows; adapter i lands in columns [32i, 32i+32).
+// LoRA down-projection p = bf16(s * bf16(x a^T)) for adapters that share the
+// same input rows: adapter i lands in columns [i rc, (i + 1) rc) of `out`,
+// zero past its rank. A rank-r adapter runs as ceil(r / 32) sub-adapters of
+// at most 32 factor rows (rows [32c, 32c + 32) of every expert's [r, K]
+// factor), up to four sub-adapters per launch.
 int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t *x, int64_t ldx,
               const int32_t *row_token, int64_t K, const mx_lora *const *adapters, int n_adapt,
-              uint16_t *out, int64_t ldo, hipStream_t s, bool split = false) {
-  Params p = base_params(v);
-  p.x = x;
-  p.ldx = ldx;
-  p.row_token = row_token;
-  p.K = K;
-  for (int i = 0; i < 4; ++i) {
-    const mx_lora *l = i < n_adapt ? adapters[i] : nullptr;
-    p.w[i] = has_lora(l) ? l->a : nullptr;
-    p.wn[i] = has_lora(l) ? l->rank : 0;
-    p.scale[i] = has_lora(l) ? l->scale : 0.0f;
-    p.split_r[i] = has_lora(l) ? l->rank : 0;
+              int rc, uint16_t *out, int64_t ldo, hipStream_t s, bool split = false) {
+  struct Sub {
+    const uint16_t *a = nullptr;
+    int rows = 0, stride = 0;
+    float scale = 0.0f;
+  };
+  constexpr int kMaxSubs = 2 * kLoraMaxRank / kLoraK;
+  const int per = rc / kLoraK;
+  if (n_adapt < 1 || n_adapt * per > kMaxSubs) {
+    set_error("LoRA down-projection: %d adapters of width %d exceed %d sub-adapters", n_adapt, rc,
+              kMaxSubs);
+    return MX_ERR_INVALID;
   }
-  p.N = 32 * n_adapt;
-  p.n_tiles_n = 1;
-  p.seg_end = v.seg + experts;
-  p.out = out;
-  p.ldo = ldo;
-  // Up to two adapters fill a 64-column tile; the kernel is bound by the
-  // activation reads, so the narrower tile (more workgroups, half the MFMA
-  // and B traffic) is the faster one (K stages of 32, for more resident
-  // workgroups, measured slower: 112 vs 92 us at the target shape).
-  // The fp32 layer (split planes, K = 3 * in) writes split outputs.
-  if (split) return launch<MX_FMT_F32X3, EPI_LORA_A, false, Tile<128, 64, 4, 1, 64>>(p, max_tiles, s);
-  if (n_adapt <= 2)
-    return launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 64, 4, 1, 64>>(p, max_tiles, s);
-  return launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 128, 2, 2, 64>>(p, max_tiles, s);
+  Sub subs[kMaxSubs];
+  const int n_sub = n_adapt * per;
+  for (int i = 0; i < n_adapt; ++i) {
+    const mx_lora *l = adapters[i];
+    for (int c = 0; c < per && has_lora(l) && kLoraK * c < l->rank; ++c) {
+      Sub &u = subs[i * per + c];
+      u.a = static_cast<const uint16_t *>(l->a) + static_cast<int64_t>(kLoraK) * c * K;
+      u.rows = std::min(kLoraK, l->rank - kLoraK * c);
+      u.stride = l->rank;
+      u.scale = l->scale;
+    }
+  }
+  for (int first = 0; first < n_sub; first += 4) {
+    const int cnt = std::min(4, n_sub - first);
+    Params p = base_params(v);
+    p.x = x;
+    p.ldx = ldx;
+    p.row_token = row_token;
+    p.K = K;
+    for (int i = 0; i < cnt; ++i) {
+      const Sub &u = subs[first + i];
+      p.w[i] = u.a;
+      p.wn[i] = u.rows;
+      p.lora_stride[i] = u.stride;
+      p.scale[i] = u.scale;
+      p.split_r[i] = u.rows;
+    }
+    p.N = kLoraK * cnt;
+    p.n_tiles_n = 1;
+    p.seg_end = v.seg + experts;
+    p.out = out + kLoraK * first;
+    p.ldo = ldo;
+    // Up to two sub-adapters fill a 64-column tile; the kernel is bound by
+    // the activation reads, so the narrower tile (more workgroups, half the
+    // MFMA and B traffic) is the faster one (K stages of 32, for more
+    // resident workgroups, measured slower: 112 vs 92 us at the target
+    // shape). The fp32 layer (split planes, K = 3 * in) writes split outputs.
+    int rc2;
+    if (split)
+      rc2 = launch<MX_FMT_F32X3, EPI_LORA_A, false, Tile<128, 64, 4, 1, 64>>(p, max_tiles, s);
+    else if (cnt <= 2)
+      rc2 = launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 64, 4, 1, 64>>(p, max_tiles, s);
+    else
+      rc2 = launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 128, 2, 2, 64>>(p, max_tiles, s);
+    if (rc2) return rc2;
+  }
+  return MX_OK;
 }
 
 // gate/up grouped GEMM with SwiGLU epilogue, then the down grouped GEMM.
@@ -1144,7 +1224,7 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
                int64_t ldx, const int32_t *row_token, int64_t hidden, int64_t ffn, int act,
                const mx_weight *w1, const mx_weight *w3, const mx_weight *w2,
                const mx_lora *l1, const mx_lora *l3, const mx_lora *l2, uint16_t *lora_buf,
-               uint16_t *h, uint16_t *save_gate, uint16_t *save_up, uint16_t *y, int64_t ldy,
+               int lrc, uint16_t *h, uint16_t *save_gate, uint16_t *save_up, uint16_t *y, int64_t ldy,
                const int32_t *out_row, hipStream_t s) {
   const bool lora13 = has_lora(l1) || has_lora(l3);
   const bool lora2 = has_lora(l2);
@@ -1156,8 +1236,8 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
   int rc;
   if (lora13) {
     const mx_lora *ad[2] = {l1, l3};
-    rc = lora_down(v, experts, PL.max_tiles, x, ldx, row_token, kx * hidden, ad, 2, lora_buf,
-                   kLoraLd, s, split);
+    rc = lora_down(v, experts, PL.max_tiles, x, ldx, row_token, kx * hidden, ad, 2, lrc,
+                   lora_buf, 3 * lrc, s, split);
     if (rc) return rc;
   }
   mark_stage(2, s);
@@ -1174,7 +1254,8 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
     p.wn[0] = p.wn[1] = ffn;
     p.N = ffn;
     p.lora_p = lora_buf;
-    p.ldp = kLoraLd;
+    p.ldp = 3 * lrc;
+    p.lora_rc = lrc;
     p.lora_b[0] = has_lora(l1) ? static_cast<const uint16_t *>(l1->b) : nullptr;
     p.lora_b[1] = has_lora(l3) ? static_cast<const uint16_t *>(l3->b) : nullptr;
     p.lora_r[0] = has_lora(l1) ? rx * l1->rank : 0;
@@ -1191,8 +1272,8 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
   mark_stage(3, s);
   if (lora2) {
     const mx_lora *ad[1] = {l2};
-    rc = lora_down(v, experts, PL.max_tiles, h, kx * ffn, nullptr, kx * ffn, ad, 1, lora_buf + 64,
-                   kLoraLd, s, split);
+    rc = lora_down(v, experts, PL.max_tiles, h, kx * ffn, nullptr, kx * ffn, ad, 1, lrc,
+                   lora_buf + 2 * lrc, 3 * lrc, s, split);
     if (rc) return rc;
   }
   mark_stage(4, s);
@@ -1205,8 +1286,9 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
   p.wscale[0] = w2->scale;
   p.wn[0] = hidden;
   p.N = hidden;
-  p.lora_p = lora_buf + 64;
-  p.ldp = kLoraLd;
+  p.lora_p = lora_buf + 2 * lrc;
+  p.ldp = 3 * lrc;
+  p.lora_rc = lrc;
   p.lora_b[0] = lora2 ? static_cast<const uint16_t *>(l2->b) : nullptr;
   p.lora_r[0] = lora2 ? rx * l2->rank : 0;
   p.seg_end = v.seg + experts;
@@ -1256,13 +1338,17 @@ int check_layer(const char *name, int64_t hidden, int64_t ffn, const mx_weight *
 struct BackLayout {
   PlanLayout plan;
   size_t off_dy = 0, off_dgu = 0, off_dz = 0, off_fact[6] = {}, bytes = 0;
+  int rc = kLoraK;
 };
 
 // Scratch of the backward: plan, dy [R, d] (slot order; reused for the per-
-// slot dx rows), [dG | dU] [R, 2f] and dz [R, 96] (sorted order), and the six
-// transposed LoRA factors (B2^T, A2^T, B1^T, A1^T, B3^T, A3^T) at rank <= 32.
-BackLayout back_layout(int64_t rows, int num_experts, int64_t hidden, int64_t ffn) {
+// slot dx rows), [dG | dU] [R, 2f] and dz [R, 3 rc] (sorted order; planes of
+// rc columns as the forward's low-rank activations), and the six transposed
+// LoRA factors (B2^T, A2^T, B1^T, A1^T, B3^T, A3^T) at rank <= rc.
+BackLayout back_layout(int64_t rows, int num_experts, int64_t hidden, int64_t ffn,
+                       int rc = kLoraK) {
   BackLayout L;
+  L.rc = rc;
   L.plan = plan_layout(rows, num_experts);
   size_t off = align_up(L.plan.bytes, 256);
   L.off_dy = off;
@@ -1270,11 +1356,11 @@ BackLayout back_layout(int64_t rows, int num_experts, int64_t hidden, int64_t ff
   L.off_dgu = off;
   off = align_up(off + sizeof(uint16_t) * rows * 2 * ffn, 256);
   L.off_dz = off;
-  off = align_up(off + sizeof(uint16_t) * rows * kLoraLd, 256);
+  off = align_up(off + sizeof(uint16_t) * rows * 3 * rc, 256);
   const int64_t fact[6] = {hidden, ffn, ffn, hidden, ffn, hidden};
   for (int i = 0; i < 6; ++i) {
     L.off_fact[i] = off;
-    off = align_up(off + sizeof(uint16_t) * num_experts * kLoraK * fact[i], 256);
+    off = align_up(off + sizeof(uint16_t) * num_experts * rc * fact[i], 256);
   }
   L.bytes = off;
   return L;
@@ -1290,11 +1376,20 @@ struct LoraGradJob {
   bool a_layout;  // [E, r, cols] (dA) rather than [E, cols, r] (dB)
 };
 
-int run_lora_grad(const LoraGradJob &j, int rank, const PlanView &v, int experts, hipStream_t s) {
+// One launch per 32-wide slice of the rank: slice c reads low-rank columns
+// [32c, 32c + 32) and writes those ranks of the gradient.
+int run_lora_grad(const LoraGradJob &j, int rank, int64_t ldv, const PlanView &v, int experts,
+                  hipStream_t s) {
   if (!j.out) return MX_OK;
   const int64_t se = j.cols * rank;
-  return lora_weight_grad(j.m, j.ldm, j.map, j.v, kLoraLd, rank, j.cols, v.seg, v.seg + experts,
-                          experts, j.out, se, j.a_layout ? 1 : rank, j.a_layout ? j.cols : 1, s);
+  const int64_t sc = j.a_layout ? 1 : rank, sj = j.a_layout ? j.cols : 1;
+  for (int c0 = 0; c0 < rank; c0 += kLoraK) {
+    const int rc = lora_weight_grad(j.m, j.ldm, j.map, j.v + c0, ldv, std::min(kLoraK, rank - c0),
+                                    j.cols, v.seg, v.seg + experts, experts, j.out + c0 * sj, se,
+                                    sc, sj, s);
+    if (rc) return rc;
+  }
+  return MX_OK;
 }
 
 // The layer backward after the combine backward, shared by token-choice and
@@ -1310,6 +1405,8 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
                   uint16_t *dz, uint16_t *const *fact, float *grad_a1, float *grad_b1,
                   float *grad_a3, float *grad_b3, float *grad_a2, float *grad_b2, hipStream_t s) {
   const bool lora1 = has_lora(l1), lora3 = has_lora(l3), lora2 = has_lora(l2);
+  const int lrc = L.rc;
+  const int64_t ldz = 3 * lrc;
   int rc;
   // The six LoRA factor transposes (B2^T, A2^T, B1^T, A1^T, B3^T, A3^T) in one launch.
   {
@@ -1338,7 +1435,7 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
     const mx_lora t = {fact[0], nullptr, r, l2->scale};
     const mx_lora *ad[1] = {&t};
     if ((rc = lora_down(v, num_experts, L.plan.max_tiles, dy, hidden, v.row_slot, hidden, ad, 1,
-                        dz + 64, kLoraLd, s)))
+                        lrc, dz + 2 * lrc, ldz, s)))
       return rc;
   }
   mark_stage(2, s);
@@ -1353,8 +1450,9 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
     p.wn[0] = hidden;
     p.k_split = hidden;
     p.N = ffn;
-    p.lora_p = dz + 64;
-    p.ldp = kLoraLd;
+    p.lora_p = dz + 2 * lrc;
+    p.ldp = ldz;
+    p.lora_rc = lrc;
     p.lora_b[0] = lora2 ? fact[1] : nullptr;
     p.lora_r[0] = lora2 ? l2->rank : 0;
     p.seg_end = v.seg + num_experts;
@@ -1365,10 +1463,10 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
   }
   mark_stage(3, s);
   if (lora2) {
-    const LoraGradJob jb = {dy, hidden, v.row_slot, lsave + 64, hidden, grad_b2, false};
-    const LoraGradJob ja = {h_in, ffn, nullptr, dz + 64, ffn, grad_a2, true};
-    if ((rc = run_lora_grad(jb, l2->rank, v, num_experts, s))) return rc;
-    if ((rc = run_lora_grad(ja, l2->rank, v, num_experts, s))) return rc;
+    const LoraGradJob jb = {dy, hidden, v.row_slot, lsave + 2 * lrc, hidden, grad_b2, false};
+    const LoraGradJob ja = {h_in, ffn, nullptr, dz + 2 * lrc, ffn, grad_a2, true};
+    if ((rc = run_lora_grad(jb, l2->rank, ldz, v, num_experts, s))) return rc;
+    if ((rc = run_lora_grad(ja, l2->rank, ldz, v, num_experts, s))) return rc;
   }
 
   // Gate / up projections: dz1 = s1 * dG B1, dz3 = s3 * dU B3, then per-slot
@@ -1382,7 +1480,7 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
     const mx_lora t = {bt, nullptr, r, l->scale};
     const mx_lora *ad[1] = {&t};
     if ((rc = lora_down(v, num_experts, L.plan.max_tiles, dgu + i * ffn, 2 * ffn, nullptr, ffn, ad,
-                        1, dz + 32 * i, kLoraLd, s)))
+                        1, lrc, dz + lrc * i, ldz, s)))
       return rc;
   }
   mark_stage(4, s);
@@ -1400,7 +1498,8 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
     p.k_split = ffn;
     p.N = hidden;
     p.lora_p = dz;
-    p.ldp = kLoraLd;
+    p.ldp = ldz;
+    p.lora_rc = lrc;
     p.lora_b[0] = lora1 ? fact[3] : nullptr;
     p.lora_b[1] = lora3 ? fact[5] : nullptr;
     p.lora_r[0] = lora1 ? l1->rank : 0;
@@ -1415,11 +1514,12 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
   for (int i = 0; i < 2; ++i) {
     const mx_lora *l = l13[i];
     if (!has_lora(l)) continue;
-    const LoraGradJob jb = {dgu + i * ffn, 2 * ffn, nullptr, lsave + 32 * i, ffn,
+    const LoraGradJob jb = {dgu + i * ffn, 2 * ffn, nullptr, lsave + lrc * i, ffn,
                             i ? grad_b3 : grad_b1, false};
-    const LoraGradJob ja = {x, hidden, v.row_token, dz + 32 * i, hidden, i ? grad_a3 : grad_a1, true};
-    if ((rc = run_lora_grad(jb, l->rank, v, num_experts, s))) return rc;
-    if ((rc = run_lora_grad(ja, l->rank, v, num_experts, s))) return rc;
+    const LoraGradJob ja = {x, hidden, v.row_token, dz + lrc * i, hidden, i ? grad_a3 : grad_a1,
+                            true};
+    if ((rc = run_lora_grad(jb, l->rank, ldz, v, num_experts, s))) return rc;
+    if ((rc = run_lora_grad(ja, l->rank, ldz, v, num_experts, s))) return rc;
   }
   return MX_OK;
 }
@@ -1431,9 +1531,11 @@ using namespace mx;
 using namespace mx::gemm;
 
 extern "C" size_t mx_moe_backward_workspace_size(int64_t num_tokens, int top_k, int num_experts,
-                                                 int64_t hidden, int64_t ffn) {
-  if (num_tokens < 0 || top_k <= 0 || num_experts <= 0 || hidden <= 0 || ffn <= 0) return 0;
-  return back_layout(num_tokens * top_k, num_experts, hidden, ffn).bytes;
+                                                 int64_t hidden, int64_t ffn, int lora_rank) {
+  if (num_tokens < 0 || top_k <= 0 || num_experts <= 0 || hidden <= 0 || ffn <= 0 ||
+      lora_rank < 0 || lora_rank > kLoraMaxRank)
+    return 0;
+  return back_layout(num_tokens * top_k, num_experts, hidden, ffn, lora_width(lora_rank)).bytes;
 }
 
 extern "C" int mx_moe_backward_act(const void *grad_out, int grad_dtype, const void *tokens,
@@ -1474,7 +1576,7 @@ extern "C" int mx_moe_backward_act(const void *grad_out, int grad_dtype, const v
   }
   hipStream_t s = as_stream(stream);
   const int64_t R = num_tokens * top_k;
-  const BackLayout L = back_layout(R, num_experts, hidden, ffn);
+  const BackLayout L = back_layout(R, num_experts, hidden, ffn, lora_width(l1, l3, l2));
   char *ws = static_cast<char *>(workspace);
   const PlanView v = plan_view(ws, L.plan);
   uint16_t *dy = reinterpret_cast<uint16_t *>(ws + L.off_dy);
@@ -1528,9 +1630,12 @@ extern "C" int mx_moe_backward(const void *grad_out, int grad_dtype, const void 
 }
 
 extern "C" size_t mx_moe_workspace_size(int64_t num_tokens, int top_k, int num_experts,
-                                        int64_t hidden, int64_t ffn) {
-  if (num_tokens < 0 || top_k <= 0 || num_experts <= 0 || hidden <= 0 || ffn <= 0) return 0;
-  return layer_layout(num_tokens * top_k, num_experts, hidden, ffn).bytes;
+                                        int64_t hidden, int64_t ffn, int lora_rank) {
+  if (num_tokens < 0 || top_k <= 0 || num_experts <= 0 || hidden <= 0 || ffn <= 0 ||
+      lora_rank < 0 || lora_rank > kLoraMaxRank)
+    return 0;
+  return layer_layout(num_tokens * top_k, num_experts, hidden, ffn, false, 0,
+                      lora_width(lora_rank)).bytes;
 }
 
 extern "C" size_t mx_moe_f32x3_workspace_size(int64_t num_tokens, int top_k, int num_experts,
@@ -1578,7 +1683,8 @@ extern "C" int mx_moe_forward_ex(const void *tokens, const int64_t *top_idx,
     set_error("%s: addend_ready needs an addend", name);
     return MX_ERR_INVALID;
   }
-  const LayerLayout L = layer_layout(R, num_experts, hidden, ffn, split, num_tokens);
+  const int lrc = lora_width(l1, l3, l2);
+  const LayerLayout L = layer_layout(R, num_experts, hidden, ffn, split, num_tokens, lrc);
   char *ws = static_cast<char *>(workspace);
   const PlanView v = plan_view(ws, L.plan);
   mark_stage(0, s);
@@ -1600,7 +1706,7 @@ extern "C" int mx_moe_forward_ex(const void *tokens, const int64_t *top_idx,
   uint16_t *h = save_h ? static_cast<uint16_t *>(save_h) : reinterpret_cast<uint16_t *>(ws + L.off_h);
   uint16_t *y = save_y ? static_cast<uint16_t *>(save_y) : reinterpret_cast<uint16_t *>(ws + L.off_y);
   rc = expert_mlp(L.plan, v, num_experts, x, (split ? 3 : 1) * hidden,
-                  v.row_token, hidden, ffn, act, w1, w3, w2, l1, l3, l2, lora_buf, h,
+                  v.row_token, hidden, ffn, act, w1, w3, w2, l1, l3, l2, lora_buf, lrc, h,
                   static_cast<uint16_t *>(save_gate), static_cast<uint16_t *>(save_up), y,
                   (split ? 2 : 1) * hidden, v.row_slot, s);
   if (rc) return rc;
@@ -1726,7 +1832,7 @@ extern "C" int mx_moe_forward_static(const void *tokens, const int64_t *top_idx,
   if (num_tokens == 0) return MX_OK;
   const bool split = w1->format == MX_FMT_F32X3;
   const size_t need = layer_layout(num_tokens * top_k, num_experts, hidden, ffn, split,
-                                   num_tokens).bytes;
+                                   num_tokens, lora_width(l1, l3, l2)).bytes;
   if (need > kStaticScratchBytes) {
     set_error("%s: this layer call needs %zu bytes of scratch, more than the %zu of the static "
               "array; use mx_moe_forward with a workspace", name, need, kStaticScratchBytes);
@@ -1773,13 +1879,14 @@ extern "C" int mx_moe_for_loop(const void *tokens_sorted, const int64_t *counts,
     return MX_ERR_INVALID;
   }
   hipStream_t s = as_stream(stream);
-  const LayerLayout L = layer_layout(num_rows, num_experts, hidden, ffn);
+  const int lrc = lora_width(l1, l3, l2);
+  const LayerLayout L = layer_layout(num_rows, num_experts, hidden, ffn, false, 0, lrc);
   char *ws = static_cast<char *>(workspace);
   const PlanView v = plan_view(ws, L.plan);
   if ((rc = plan_from_counts(counts, num_rows, num_experts, ws, s))) return rc;
   return expert_mlp(L.plan, v, num_experts, static_cast<const uint16_t *>(tokens_sorted), hidden,
                     nullptr, hidden, ffn, MX_ACT_SILU, w1, w3, w2, l1, l3, l2,
-                    reinterpret_cast<uint16_t *>(ws + L.off_lora),
+                    reinterpret_cast<uint16_t *>(ws + L.off_lora), lrc,
                     reinterpret_cast<uint16_t *>(ws + L.off_h), nullptr, nullptr,
                     static_cast<uint16_t *>(out), hidden, nullptr, s);
 }
@@ -1812,7 +1919,8 @@ extern "C" int mx_grouped_linear(const void *x, const int64_t *counts, int64_t n
     return MX_ERR_INVALID;
   }
   hipStream_t s = as_stream(stream);
-  const LayerLayout L = layer_layout(num_rows, num_experts, in_f, out_f);
+  const int lrc = lora_width(lora, nullptr, nullptr);
+  const LayerLayout L = layer_layout(num_rows, num_experts, in_f, out_f, false, 0, lrc);
   char *ws = static_cast<char *>(workspace);
   const PlanView v = plan_view(ws, L.plan);
   if ((rc = plan_from_counts(counts, num_rows, num_experts, ws, s))) return rc;
@@ -1821,7 +1929,7 @@ extern "C" int mx_grouped_linear(const void *x, const int64_t *counts, int64_t n
   if (lr) {
     const mx_lora *ad[1] = {lora};
     rc = lora_down(v, num_experts, L.plan.max_tiles, static_cast<const uint16_t *>(x), in_f,
-                   nullptr, in_f, ad, 1, lora_buf, kLoraLd, s);
+                   nullptr, in_f, ad, 1, lrc, lora_buf, 3 * lrc, s);
     if (rc) return rc;
   }
   Params p = base_params(v);
@@ -1833,7 +1941,8 @@ extern "C" int mx_grouped_linear(const void *x, const int64_t *counts, int64_t n
   p.wn[0] = out_f;
   p.N = out_f;
   p.lora_p = lora_buf;
-  p.ldp = kLoraLd;
+  p.ldp = 3 * lrc;
+  p.lora_rc = lrc;
   p.lora_b[0] = lr ? static_cast<const uint16_t *>(lora->b) : nullptr;
   p.lora_r[0] = lr ? lora->rank : 0;
   p.seg_end = v.seg + num_experts;
@@ -1857,9 +1966,9 @@ struct EcLayout {
 };
 
 EcLayout ec_layout(int64_t slots, int num_experts, int64_t hidden, int64_t ffn, int64_t tokens,
-                   int logical) {
+                   int logical, int rc) {
   EcLayout L;
-  L.layer = layer_layout(slots, num_experts, hidden, ffn);
+  L.layer = layer_layout(slots, num_experts, hidden, ffn, false, 0, rc);
   size_t off = align_up(L.layer.bytes, 256);
   L.off_phys = off;
   off = align_up(off + sizeof(int64_t) * slots, 256);
@@ -2023,9 +2132,9 @@ struct EcBackLayout {
 };
 
 EcBackLayout ec_back_layout(int64_t slots, int num_experts, int64_t hidden, int64_t ffn,
-                            int64_t tokens, int logical) {
+                            int64_t tokens, int logical, int rc) {
   EcBackLayout L;
-  L.back = back_layout(slots, num_experts, hidden, ffn);
+  L.back = back_layout(slots, num_experts, hidden, ffn, rc);
   size_t off = align_up(L.back.bytes, 256);
   L.off_phys = off;
   off = align_up(off + sizeof(int64_t) * slots, 256);
@@ -2109,12 +2218,13 @@ extern "C" int mx_build_expert_choice_plan(
 extern "C" size_t mx_moe_expert_choice_workspace_size(int batch, int logical_experts,
                                                       int capacity, int64_t tokens_per_sample,
                                                       int num_experts, int64_t hidden,
-                                                      int64_t ffn) {
+                                                      int64_t ffn, int lora_rank) {
   if (batch < 0 || logical_experts <= 0 || capacity <= 0 || tokens_per_sample <= 0 ||
-      num_experts <= 0 || hidden <= 0 || ffn <= 0)
+      num_experts <= 0 || hidden <= 0 || ffn <= 0 || lora_rank < 0 || lora_rank > kLoraMaxRank)
     return 0;
   const int64_t slots = static_cast<int64_t>(batch) * logical_experts * capacity;
-  return ec_layout(slots, num_experts, hidden, ffn, batch * tokens_per_sample, logical_experts)
+  return ec_layout(slots, num_experts, hidden, ffn, batch * tokens_per_sample, logical_experts,
+                   lora_width(lora_rank))
       .bytes;
 }
 
@@ -2149,7 +2259,8 @@ extern "C" int mx_moe_forward_expert_choice_ex(
     return MX_ERR_INVALID;
   }
   hipStream_t s = as_stream(stream);
-  const EcLayout L = ec_layout(slots, num_experts, hidden, ffn, T, logical_experts);
+  const int lrc = lora_width(l1, l3, l2);
+  const EcLayout L = ec_layout(slots, num_experts, hidden, ffn, T, logical_experts, lrc);
   char *ws = static_cast<char *>(workspace);
   int64_t *phys = reinterpret_cast<int64_t *>(ws + L.off_phys);
   int64_t *tok = reinterpret_cast<int64_t *>(ws + L.off_tok);
@@ -2179,7 +2290,7 @@ extern "C" int mx_moe_forward_expert_choice_ex(
     uint16_t *h = save_h ? static_cast<uint16_t *>(save_h)
                          : reinterpret_cast<uint16_t *>(ws + L.layer.off_h);
     rc = expert_mlp(L.layer.plan, v, num_experts, static_cast<const uint16_t *>(tokens), hidden,
-                    v.row_token, hidden, ffn, act, w1, w3, w2, l1, l3, l2, lora_buf, h,
+                    v.row_token, hidden, ffn, act, w1, w3, w2, l1, l3, l2, lora_buf, lrc, h,
                     static_cast<uint16_t *>(save_gate), static_cast<uint16_t *>(save_up), y,
                     hidden, v.row_slot, s);
     if (rc) return rc;
@@ -2210,13 +2321,13 @@ extern "C" size_t mx_moe_backward_expert_choice_workspace_size(int batch, int lo
                                                                int capacity,
                                                                int64_t tokens_per_sample,
                                                                int num_experts, int64_t hidden,
-                                                               int64_t ffn) {
+                                                               int64_t ffn, int lora_rank) {
   if (batch < 0 || logical_experts <= 0 || capacity <= 0 || tokens_per_sample <= 0 ||
-      num_experts <= 0 || hidden <= 0 || ffn <= 0)
+      num_experts <= 0 || hidden <= 0 || ffn <= 0 || lora_rank < 0 || lora_rank > kLoraMaxRank)
     return 0;
   const int64_t slots = static_cast<int64_t>(batch) * logical_experts * capacity;
   return ec_back_layout(slots, num_experts, hidden, ffn, batch * tokens_per_sample,
-                        logical_experts).bytes;
+                        logical_experts, lora_width(lora_rank)).bytes;
 }
 
 extern "C" int mx_moe_backward_expert_choice(
@@ -2259,7 +2370,8 @@ extern "C" int mx_moe_backward_expert_choice(
     return MX_ERR_INVALID;
   }
   hipStream_t s = as_stream(stream);
-  const EcBackLayout L = ec_back_layout(slots, num_experts, hidden, ffn, T, logical_experts);
+  const EcBackLayout L = ec_back_layout(slots, num_experts, hidden, ffn, T, logical_experts,
+                                        lora_width(l1, l3, l2));
   char *ws = static_cast<char *>(workspace);
   int64_t *phys = reinterpret_cast<int64_t *>(ws + L.off_phys);
   int64_t *tok = reinterpret_cast<int64_t *>(ws + L.off_tok);

@@ -12,11 +12,12 @@ namespace mx {
 namespace {
 
 // Several [E, rows, cols] -> [E, cols, rows] transposes in one launch. One of
-// rows / cols is a LoRA rank (at most 32): a thread moves the rank-long run at
-// one position of the other (long) dimension, so the long dimension runs
-// across the lanes of a wave and both the loads and the stores are coalesced.
-// Runs are moved as 16-byte vectors when the rank is a multiple of 8 and both
-// buffers are 16-byte aligned. Workgroups [block0[j], block0[j + 1]) serve job j.
+// rows / cols is a LoRA rank (at most 256): a thread moves the rank-long run
+// at one position of the other (long) dimension, 32 ranks at a time, so the
+// long dimension runs across the lanes of a wave and both the loads and the
+// stores are coalesced. Runs are moved as 16-byte vectors when the rank is a
+// multiple of 8 and both buffers are 16-byte aligned. Workgroups
+// [block0[j], block0[j + 1]) serve job j.
 struct TransposeLaunch {
   FactorTranspose job[6];
   int64_t block0[7];
@@ -39,49 +40,52 @@ __global__ __launch_bounds__(256) void transpose_factors_multi_kernel(TransposeL
   const uint16_t *src = t.src + base;
   uint16_t *dst = t.dst + base;
   const bool vec = L.vec[j] != 0;
-  uint16_t v[32];
-  if (small_rows) {  // src [S][Lg] -> dst [Lg][S]: gather the column, store the run
+  for (uint32_t s0 = 0; s0 < S; s0 += 32) {
+    const int n = static_cast<int>(S - s0 < 32 ? S - s0 : 32);  // ranks of this pass
+    uint16_t v[32];
+    if (small_rows) {  // src [S][Lg] -> dst [Lg][S]: gather the column, store the run
 #pragma unroll
-    for (int s = 0; s < 32; ++s)
-      if (s < static_cast<int>(S)) v[s] = src[static_cast<int64_t>(s) * Lg + l];
-    uint16_t *run = dst + static_cast<int64_t>(l) * S;
-    if (vec) {
+      for (int q = 0; q < 32; ++q)
+        if (q < n) v[q] = src[static_cast<int64_t>(s0 + q) * Lg + l];
+      uint16_t *run = dst + static_cast<int64_t>(l) * S + s0;
+      if (vec) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (q * 8 < static_cast<int>(S)) {
-          u32x4 w;
+        for (int q = 0; q < 4; ++q)
+          if (q * 8 < n) {
+            u32x4 w;
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            w[i] = static_cast<uint32_t>(v[q * 8 + 2 * i]) |
-                   (static_cast<uint32_t>(v[q * 8 + 2 * i + 1]) << 16);
-          *reinterpret_cast<u32x4 *>(run + q * 8) = w;
-        }
-    } else {
-#pragma unroll
-      for (int s = 0; s < 32; ++s)
-        if (s < static_cast<int>(S)) run[s] = v[s];
-    }
-  } else {  // src [Lg][S] -> dst [S][Lg]: load the run, scatter it down the column
-    const uint16_t *run = src + static_cast<int64_t>(l) * S;
-    if (vec) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (q * 8 < static_cast<int>(S)) {
-          const u32x4 w = *reinterpret_cast<const u32x4 *>(run + q * 8);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            v[q * 8 + 2 * i] = static_cast<uint16_t>(w[i] & 0xFFFFu);
-            v[q * 8 + 2 * i + 1] = static_cast<uint16_t>(w[i] >> 16);
+            for (int i = 0; i < 4; ++i)
+              w[i] = static_cast<uint32_t>(v[q * 8 + 2 * i]) |
+                     (static_cast<uint32_t>(v[q * 8 + 2 * i + 1]) << 16);
+            *reinterpret_cast<u32x4 *>(run + q * 8) = w;
           }
-        }
-    } else {
+      } else {
 #pragma unroll
-      for (int s = 0; s < 32; ++s)
-        if (s < static_cast<int>(S)) v[s] = run[s];
+        for (int q = 0; q < 32; ++q)
+          if (q < n) run[q] = v[q];
+      }
+    } else {  // src [Lg][S] -> dst [S][Lg]: load the run, scatter it down the column
+      const uint16_t *run = src + static_cast<int64_t>(l) * S + s0;
+      if (vec) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (q * 8 < n) {
+            const u32x4 w = *reinterpret_cast<const u32x4 *>(run + q * 8);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              v[q * 8 + 2 * i] = static_cast<uint16_t>(w[i] & 0xFFFFu);
+              v[q * 8 + 2 * i + 1] = static_cast<uint16_t>(w[i] >> 16);
+            }
+          }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 32; ++q)
+          if (q < n) v[q] = run[q];
+      }
+#pragma unroll
+      for (int q = 0; q < 32; ++q)
+        if (q < n) dst[static_cast<int64_t>(s0 + q) * Lg + l] = v[q];
     }
-#pragma unroll
-    for (int s = 0; s < 32; ++s)
-      if (s < static_cast<int>(S)) dst[static_cast<int64_t>(s) * Lg + l] = v[s];
   }
 }
 
@@ -294,8 +298,8 @@ int transpose_factors_multi(const FactorTransposes &jobs, hipStream_t s) {
   for (int j = 0; j < jobs.n; ++j) {
     const FactorTranspose &t = jobs.job[j];
     const int64_t small = t.rows < t.cols ? t.rows : t.cols;
-    if (t.total < 0 || (t.total > 0 && (small < 1 || small > 32 || t.total / small >= (int64_t{1} << 31)))) {
-      set_error("LoRA factor transposes: one dimension must be a rank in [1, 32] and the other "
+    if (t.total < 0 || (t.total > 0 && (small < 1 || small > 256 || t.total / small >= (int64_t{1} << 31)))) {
+      set_error("LoRA factor transposes: one dimension must be a rank in [1, 256] and the other "
                 "times the experts below 2^31 (got %lld x %lld)",
                 static_cast<long long>(t.rows), static_cast<long long>(t.cols));
       return MX_ERR_INVALID;

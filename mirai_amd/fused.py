@@ -14,7 +14,18 @@ import torch
 
 from . import _native as nat
 
-LORA_ROW = 96  # [gate 32 | up 32 | down 32] scaled low-rank activations per sorted row
+
+
+def lora_rank(module) -> int:
+    """Largest padded rank of the attached adapters (0 without LoRA): the
+    ``lora_rank`` the native workspace queries are sized for."""
+    return max((a.padded_rank() for a in module._adapters() if a is not None), default=0)
+
+
+def lora_row(module) -> int:
+    """Columns of one saved low-rank row: [gate | up | down] planes of the
+    largest rank rounded up to 32 (at least 32 columns each)."""
+    return 3 * max(32, -(-lora_rank(module) // 32) * 32)
 
 
 def kernel_activation(module) -> int:
@@ -94,11 +105,13 @@ def _forward(module, tokens, top_scores, top_indices, need_grad, addend=None, ad
             torch.empty((R, f), dtype=torch.bfloat16, device=device),  # up
             torch.empty((R, f), dtype=torch.bfloat16, device=device),  # h
             torch.empty((R, d), dtype=torch.bfloat16, device=device),  # y (slot order)
-            torch.zeros((R, LORA_ROW), dtype=torch.bfloat16, device=device),
+            torch.zeros((R, lora_row(module)), dtype=torch.bfloat16, device=device),
         ]
     lib = nat.load_library()
-    size = lib.mx_moe_f32x3_workspace_size if split else lib.mx_moe_workspace_size
-    ws = nat.workspace(size(T, k, E, d, f), device)
+    if split:
+        ws = nat.workspace(lib.mx_moe_f32x3_workspace_size(T, k, E, d, f), device)
+    else:
+        ws = nat.workspace(lib.mx_moe_workspace_size(T, k, E, d, f, lora_rank(module)), device)
     if addend is not None:
         if need_grad or split or addend.dtype != out.dtype or tuple(addend.shape) != (T, d):
             raise ValueError("the fused addend is a bf16 [tokens, hidden] inference input.")
@@ -146,7 +159,7 @@ class _ChunkedRoutedExperts(torch.autograd.Function):
     The forward runs each chunk through the inference kernels (no activation
     is kept) straight into its rows of the output. The backward walks the
     chunks in order: it reruns a chunk's forward with its per-slot activations
-    saved ((3f + d + 96) * 2 bytes per routed slot), runs that chunk's native
+    saved ((3f + d + 3 rc) * 2 bytes per routed slot, rc the LoRA row plane), runs that chunk's native
     backward, writes the chunk's token and score gradients into their rows and
     adds its fp32 LoRA factor gradients to running sums, then frees the chunk's
     activations. At most one chunk's activations are alive at a time; the
@@ -286,10 +299,10 @@ def _ec_forward(module, tokens, expert_token_scores, expert_token_indices, token
                  torch.empty((S, f), dtype=torch.bfloat16, device=device),
                  torch.empty((S, f), dtype=torch.bfloat16, device=device),
                  torch.empty((S, d), dtype=torch.bfloat16, device=device),
-                 torch.zeros((S, LORA_ROW), dtype=torch.bfloat16, device=device)]
+                 torch.zeros((S, lora_row(module)), dtype=torch.bfloat16, device=device)]
     lib = nat.load_library()
-    ws = nat.workspace(lib.mx_moe_expert_choice_workspace_size(B, L, C, tokens_per_sample,
-                                                               module.num_experts, d, f), device)
+    ws = nat.workspace(lib.mx_moe_expert_choice_workspace_size(
+        B, L, C, tokens_per_sample, module.num_experts, d, f, lora_rank(module)), device)
     nat.call("mx_moe_forward_expert_choice_ex", x.data_ptr(), idx.data_ptr(), scores.data_ptr(),
              nat.dtype_code(scores.dtype), B, L, C, int(tokens_per_sample), nat.ptr(l2p),
              nat.ptr(order), module.num_experts, d, f, kernel_activation(module), w1, w3, w2,
@@ -347,7 +360,7 @@ class _ExpertChoiceExperts(torch.autograd.Function):
                                    device=device) if lora_needs[2 * i + 1] else None)
         lib = nat.load_library()
         ws = nat.workspace(lib.mx_moe_backward_expert_choice_workspace_size(
-            B, L, C, ctx.tps, E, d, f), device)
+            B, L, C, ctx.tps, E, d, f, lora_rank(module)), device)
         nat.call("mx_moe_backward_expert_choice", g.data_ptr(), nat.dtype_code(g.dtype),
                  x.data_ptr(), idx.data_ptr(), scores.data_ptr(), nat.dtype_code(scores.dtype),
                  B, L, C, int(ctx.tps), nat.ptr(l2p), nat.ptr(order), E, d, f,
@@ -398,7 +411,8 @@ def sorted_experts(module, tokens, counts):
     lora, keep = _lora_descriptors(module, device)
     out = torch.empty((S, d), dtype=torch.bfloat16, device=device)
     lib = nat.load_library()
-    ws = nat.workspace(lib.mx_moe_workspace_size(S, 1, module.num_experts, d, f), device)
+    ws = nat.workspace(lib.mx_moe_workspace_size(S, 1, module.num_experts, d, f,
+                                                 lora_rank(module)), device)
     nat.call("mx_moe_for_loop", x.data_ptr(), c.data_ptr(), S, module.num_experts, d, f, w1, w3,
              w2, lora[0], lora[1], lora[2], out.data_ptr(), ws.data_ptr(), nat.stream(device))
     del keep
@@ -429,7 +443,9 @@ def grouped_projection(module, key, x, offsets):
         lora = nat.MxLora(a.data_ptr(), b.data_ptr(), adapter.padded_rank(), float(adapter.scale()))
     out = torch.empty((S, out_f), dtype=torch.bfloat16, device=device)
     lib = nat.load_library()
-    ws = nat.workspace(lib.mx_moe_workspace_size(S, 1, module.num_experts, in_f, out_f), device)
+    rank = adapter.padded_rank() if adapter is not None else 0
+    ws = nat.workspace(lib.mx_moe_workspace_size(S, 1, module.num_experts, in_f, out_f, rank),
+                       device)
     nat.call("mx_grouped_linear", xb.data_ptr(), counts.data_ptr(), S, module.num_experts,
              packed.descriptor(), lora, out.data_ptr(), ws.data_ptr(), nat.stream(device))
     del keep

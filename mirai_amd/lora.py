@@ -17,7 +17,9 @@ import math
 import torch
 import torch.nn as nn
 
-MAX_FUSED_RANK = 32
+# Largest rank the fused kernels take: ranks up to 32 run as one LDS-staged
+# K chunk of the GEMM epilogues, larger ones add 32-wide chunks.
+MAX_FUSED_RANK = 256
 
 
 def lora_scale(alpha: float, rank: int, *, use_rslora: bool) -> float:

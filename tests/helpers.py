@@ -54,7 +54,7 @@ def build_module(w: wl.Workload, dense: dict, lora: dict | None, device="cuda",
         m.load_dense_weight(key, dense[key].to(device))
     if lora:
         for key, (a, b) in lora.items():
-            ad = m.attach_expert_lora(tensor_name=key, adapter_name="test", rank=w.rank,
+            ad = m.attach_expert_lora(tensor_name=key, adapter_name="test", rank=int(a.shape[1]),
                                       alpha=w.alpha)
             with torch.no_grad():
                 ad.lora_a.copy_(a.to(device))
@@ -73,5 +73,18 @@ def oracle_weights(w: wl.Workload, dense: dict, dtype=torch.bfloat16) -> dict:
 def oracle_loras(w: wl.Workload, lora: dict | None) -> dict:
     if not lora:
         return {}
-    s = wl.lora_scale(w)
-    return {k: (a.clone(), b.clone(), s) for k, (a, b) in lora.items()}
+    # alpha / r per adapter (the workload's rank unless a test mixes ranks)
+    return {k: (a.clone(), b.clone(), float(w.alpha) / int(a.shape[1]))
+            for k, (a, b) in lora.items()}
+
+
+def mixed_rank_factors(w: wl.Workload, ranks: dict, seed: int = 0) -> dict:
+    """fp32 LoRA factors {key: (A [E, r_key, in], B [E, out, r_key])} ~ N(0, 0.02)
+    with a rank of its own per projection."""
+    g = torch.Generator().manual_seed(4000 + w.index + seed)
+    E, d, f = w.experts, w.hidden, w.ffn
+    out = {}
+    for key, (o, i) in (("w1", (f, d)), ("w3", (f, d)), ("w2", (d, f))):
+        r = int(ranks[key])
+        out[key] = (torch.randn(E, r, i, generator=g) * 0.02, torch.randn(E, o, r, generator=g) * 0.02)
+    return out

@@ -43,19 +43,33 @@ def test_binding_covers_every_declared_symbol():
 
 
 def test_abi_version_and_error_text(lib):
-    assert lib.mx_abi_version() == 5
+    assert lib.mx_abi_version() == 6
     assert isinstance(nat.last_error(), str)
 
 
 def test_workspace_sizes(lib):
-    assert lib.mx_moe_workspace_size(4096, 4, 64, 2048, 1408) > 0
-    assert lib.mx_moe_backward_workspace_size(8192, 4, 64, 2048, 1408) > 0
+    assert lib.mx_moe_workspace_size(4096, 4, 64, 2048, 1408, 32) > 0
+    assert lib.mx_moe_backward_workspace_size(8192, 4, 64, 2048, 1408, 32) > 0
     assert lib.mx_plan_workspace_size(1000, 4, 64) > 0
-    assert lib.mx_moe_workspace_size(-1, 4, 64, 2048, 1408) == 0
-    assert lib.mx_moe_backward_workspace_size(16, 0, 64, 2048, 1408) == 0
+    assert lib.mx_moe_workspace_size(-1, 4, 64, 2048, 1408, 32) == 0
+    assert lib.mx_moe_backward_workspace_size(16, 0, 64, 2048, 1408, 32) == 0
     # Grows with the problem.
-    assert lib.mx_moe_workspace_size(8192, 4, 64, 2048, 1408) > lib.mx_moe_workspace_size(
-        4096, 4, 64, 2048, 1408)
+    assert lib.mx_moe_workspace_size(8192, 4, 64, 2048, 1408, 32) > lib.mx_moe_workspace_size(
+        4096, 4, 64, 2048, 1408, 32)
+    # The low-rank rows: 3 planes of max(32, rank rounded up to 32) bf16 columns.
+    R = 4096 * 4
+    base = lib.mx_moe_workspace_size(4096, 4, 64, 2048, 1408, 0)
+    assert lib.mx_moe_workspace_size(4096, 4, 64, 2048, 1408, 32) == base
+    assert lib.mx_moe_workspace_size(4096, 4, 64, 2048, 1408, 48) == base + R * 3 * 32 * 2
+    assert lib.mx_moe_workspace_size(4096, 4, 64, 2048, 1408, 256) == base + R * 3 * 224 * 2
+    assert lib.mx_moe_workspace_size(4096, 4, 64, 2048, 1408, 264) == 0
+    assert lib.mx_moe_backward_workspace_size(4096, 4, 64, 2048, 1408, -8) == 0
+    assert (lib.mx_moe_backward_workspace_size(4096, 4, 64, 2048, 1408, 64)
+            > lib.mx_moe_backward_workspace_size(4096, 4, 64, 2048, 1408, 32))
+    assert (lib.mx_moe_expert_choice_workspace_size(2, 8, 16, 64, 8, 256, 192, 128)
+            > lib.mx_moe_expert_choice_workspace_size(2, 8, 16, 64, 8, 256, 192, 0) > 0)
+    assert (lib.mx_moe_backward_expert_choice_workspace_size(2, 8, 16, 64, 8, 256, 192, 128)
+            > lib.mx_moe_backward_expert_choice_workspace_size(2, 8, 16, 64, 8, 256, 192, 8) > 0)
 
 
 def _rc(name, *args):

@@ -27,7 +27,7 @@ from mirai_amd import workloads as wl
 from oracle import layer as olayer
 from oracle import routing as oroute
 
-from helpers import build_module, oracle_weights
+from helpers import build_module, mixed_rank_factors, oracle_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -77,7 +77,7 @@ def _oracle_grads(w, dense, lora, x, scores, idx, dy, rows, weights=None):
         a = a.clone().float().requires_grad_(True)
         b = b.clone().float().requires_grad_(True)
         leaves[key] = (a, b)
-        loras[key] = (a, b, wl.lora_scale(w))
+        loras[key] = (a, b, float(w.alpha) / int(a.shape[1]))
     if weights is None:
         weights = oracle_weights(w, dense, dtype=torch.bfloat16)
     out = olayer.layer_forward(xo, so, idx[rows], weights, loras, w.experts)
@@ -89,9 +89,10 @@ def _oracle_grads(w, dense, lora, x, scores, idx, dy, rows, weights=None):
     return out, grads
 
 
-def _case(w, rows=None):
+def _case(w, rows=None, lora=None):
     dense = wl.dense_weights(w)
-    lora = wl.lora_factors(w)
+    if lora is None:
+        lora = wl.lora_factors(w)
     x = wl.tokens(w)
     idx_np, scores_np = oroute.route_topk(wl.router_logits(w).numpy(), w.top_k)
     idx, scores = torch.from_numpy(idx_np), torch.from_numpy(scores_np)
@@ -114,9 +115,15 @@ def test_small_backward_matches_oracle(fmt):
     _case(small(fmt))
 
 
-@pytest.mark.parametrize("r", [8, 32])
+@pytest.mark.parametrize("r", [8, 32, 48, 64, 128])
 def test_backward_lora_ranks(r):
+    # Ranks above 32: 32-wide slices of the weight gradients and of dz.
     _case(small("nf4", r=r, alpha=2.0 * r, E=5, k=3, T=300, f=320, d=192))
+
+
+def test_backward_mixed_lora_ranks_on_tall_tiles():
+    w = small("int8", E=4, k=2, T=1100, f=256, d=192, alpha=32.0)
+    _case(w, lora=mixed_rank_factors(w, {"w1": 96, "w3": 24, "w2": 64}))
 
 
 def test_backward_ragged_experts():

@@ -111,9 +111,10 @@ def _close_grad(name, actual, expected, mean_rel=1e-2, max_rel=3e-2):
     return stats
 
 
-@pytest.mark.parametrize("fmt,alias", [("nf4", ()), ("int8", ()),
-                                       ("nf4", (3, 0, 3, 1, 2, 0, 1, 2))])
-def test_backward_matches_oracle_autograd(fmt, alias):
+@pytest.mark.parametrize("fmt,alias,rank", [("nf4", (), 16), ("int8", (), 16),
+                                            ("nf4", (3, 0, 3, 1, 2, 0, 1, 2), 16),
+                                            ("int8", (), 64)])
+def test_backward_matches_oracle_autograd(fmt, alias, rank):
     # Gradients to tokens, [B, L, C] scores and every LoRA factor against torch
     # autograd through the oracle's gather / per-expert MLP / index_add
     # composition (bounds as the token-choice backward: mean-rel 1e-2, max
@@ -121,7 +122,8 @@ def test_backward_matches_oracle_autograd(fmt, alias):
     # slots' dx rows; tokens no expert picked get zero.
     B, L, C, tps = 2, 8, 24, 96
     E = max(alias) + 1 if alias else L
-    w = wl.Workload(f"ec_bwd_{fmt}", 21, B * tps, 256, 192, E, 1, 16, 16.0, fmt, torch.bfloat16)
+    w = wl.Workload(f"ec_bwd_{fmt}", 21, B * tps, 256, 192, E, 1, rank, float(rank), fmt,
+                    torch.bfloat16)
     dense, lora = wl.dense_weights(w), wl.lora_factors(w)
     m = build_module(w, dense, lora, access="active_dequant")
     if alias:

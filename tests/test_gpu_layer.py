@@ -13,7 +13,8 @@ from mirai_amd import workloads as wl
 from oracle import layer as olayer
 from oracle import routing as oroute
 
-from helpers import assert_layer_close, build_module, oracle_loras, oracle_weights
+from helpers import (assert_layer_close, build_module, mixed_rank_factors, oracle_loras,
+                     oracle_weights)
 
 pytestmark = pytest.mark.gpu
 
@@ -22,9 +23,10 @@ def small(fmt, *, T=256, d=256, f=192, E=8, k=2, r=16, alpha=16.0, dtype=torch.b
     return wl.Workload(f"small_{fmt}", 7, T, d, f, E, k, r, alpha, fmt, dtype)
 
 
-def _run_case(w: wl.Workload, *, with_lora=True, token_subset=None):
+def _run_case(w: wl.Workload, *, with_lora=True, token_subset=None, lora=None):
     dense = wl.dense_weights(w)
-    lora = wl.lora_factors(w) if with_lora else None
+    if lora is None:
+        lora = wl.lora_factors(w) if with_lora else None
     x = wl.tokens(w)
     logits = wl.router_logits(w)
     idx_np, scores_np = oroute.route_topk(logits.numpy(), w.top_k)
@@ -48,9 +50,23 @@ def test_small_layer_matches_oracle(fmt, with_lora):
     _run_case(small(fmt), with_lora=with_lora)
 
 
-@pytest.mark.parametrize("r", [8, 24, 32])
+@pytest.mark.parametrize("r", [8, 24, 32, 48, 64, 104, 128])
 def test_lora_ranks(r):
+    # Ranks above 32 add 32-wide K chunks to the epilogue's LoRA product (104:
+    # a partial last chunk) and split the down-projection into 32-row slices.
     _run_case(small("nf4", r=r, alpha=2.0 * r, E=5, k=3, T=300, f=320, d=192))
+
+
+@pytest.mark.parametrize("fmt,r", [("nf4", 64), ("int8", 256)])
+def test_wide_lora_on_tall_tiles(fmt, r):
+    # ~1024 rows per expert: 256-row tiles and 128-row remainders.
+    _run_case(small(fmt, r=r, alpha=float(r), E=4, k=2, T=2000, f=384, d=256))
+
+
+def test_mixed_lora_ranks():
+    # Each projection its own rank; the low-rank planes take the widest (128).
+    w = small("int8", E=6, k=2, T=400, f=256, d=192, alpha=32.0)
+    _run_case(w, lora=mixed_rank_factors(w, {"w1": 64, "w3": 8, "w2": 128}))
 
 
 def test_ragged_and_empty_experts():
@@ -112,8 +128,9 @@ def test_c4_int8_rank32_full_size_on_token_subset():
     _run_case(w, token_subset=torch.arange(0, w.tokens, 128))
 
 
-def test_run_for_loop_matches_oracle():
-    w = small("nf4", T=200, E=6, k=1)
+@pytest.mark.parametrize("r", [16, 72])
+def test_run_for_loop_matches_oracle(r):
+    w = small("nf4", T=200, E=6, k=1, r=r, alpha=float(r))
     dense = wl.dense_weights(w)
     lora = wl.lora_factors(w)
     m = build_module(w, dense, lora)
@@ -125,8 +142,9 @@ def test_run_for_loop_matches_oracle():
     assert_layer_close(out.cpu(), ref)
 
 
-def test_grouped_linear_matches_oracle():
-    w = small("int8", T=150, E=4, k=1, d=256, f=320)
+@pytest.mark.parametrize("r", [16, 160])
+def test_grouped_linear_matches_oracle(r):
+    w = small("int8", T=150, E=4, k=1, d=256, f=320, r=r, alpha=float(r))
     dense = wl.dense_weights(w)
     lora = wl.lora_factors(w)
     m = build_module(w, dense, lora, access="full_dequant")

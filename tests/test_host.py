@@ -112,9 +112,13 @@ def test_active_expert_lora_state():
     rs = ActiveExpertLoRA(adapter_name="r", num_experts=1, in_features=64, out_features=64,
                           rank=16, alpha=16.0, use_rslora=True)
     assert rs.scale() == pytest.approx(4.0)
+    wide = ActiveExpertLoRA(adapter_name="w", num_experts=2, in_features=64, out_features=32,
+                            rank=100, alpha=1.0)
+    assert wide.padded_rank() == 104  # ranks above 32 run as extra 32-wide K chunks
+    assert wide.kernel_factors(torch.device("cpu"))[0].shape == (2, 104, 64)
     with pytest.raises(ValueError):
         ActiveExpertLoRA(adapter_name="x", num_experts=1, in_features=64, out_features=64,
-                         rank=40, alpha=1.0)
+                         rank=260, alpha=1.0)
     with pytest.raises(ValueError):
         lora_scale(1.0, 0, use_rslora=False)
 

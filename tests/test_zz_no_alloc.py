@@ -9,7 +9,7 @@ import torch
 
 from mirai_amd import _native as nat
 from mirai_amd import workloads as wl
-from mirai_amd.fused import _lora_descriptors, _weight_descriptors
+from mirai_amd.fused import _lora_descriptors, _weight_descriptors, lora_rank
 from oracle import routing as oroute
 
 from helpers import build_module
@@ -26,7 +26,7 @@ def _args(m, x, idx, scores, out):
     common = (x.data_ptr(), idx.data_ptr(), scores.data_ptr(), nat.dtype_code(scores.dtype), T,
               int(idx.shape[1]), m.num_experts, d, f, nat.ACT_SILU, w1, w3, w2, lora[0], lora[1],
               lora[2], out.data_ptr(), nat.dtype_code(out.dtype))
-    return common, keep, (T, int(idx.shape[1]), m.num_experts, d, f)
+    return common, keep, (T, int(idx.shape[1]), m.num_experts, d, f, lora_rank(m))
 
 
 def _both(m, x, idx, scores):
@@ -59,7 +59,7 @@ def test_static_scratch_forward_matches_the_workspace_forward():
     # Too large for the static array: refused before any launch.
     big = nat.STATIC_SCRATCH_BYTES // (2 * (256 + 192 + 96)) + 1
     lib = nat.load_library()
-    assert lib.mx_moe_workspace_size(big, 1, 8, 256, 192) > nat.STATIC_SCRATCH_BYTES
+    assert lib.mx_moe_workspace_size(big, 1, 8, 256, 192, 16) > nat.STATIC_SCRATCH_BYTES
     xb = torch.empty((big, 256), dtype=torch.bfloat16, device="cuda")
     ib = torch.zeros((big, 1), dtype=torch.int64, device="cuda")
     sb = torch.ones((big, 1), dtype=torch.float32, device="cuda")
