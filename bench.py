@@ -68,6 +68,8 @@ def _parse():
     ap.add_argument("--weights", choices=("nf4", "int8", "bf16"), default=None,
                     help="override the workload's frozen-weight format")
     ap.add_argument("--tokens", type=int, default=None, help="override the token count")
+    ap.add_argument("--lora-rank", type=int, default=None,
+                    help="override the workload's LoRA rank (0: no adapters; alpha = 2 * rank)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget of the baseline sample")
@@ -103,7 +105,8 @@ def _build_module(w, device):
     for key in ("w1", "w3", "w2"):
         m.load_dense_weight(key, dense[key])
     del dense
-    for key, (a, b) in wl.lora_factors(w, device=device).items():
+    factors = wl.lora_factors(w, device=device) if w.rank > 0 else {}
+    for key, (a, b) in factors.items():
         ad = m.attach_expert_lora(tensor_name=key, adapter_name="bench", rank=w.rank,
                                   alpha=w.alpha)
         with torch.no_grad():
@@ -526,6 +529,10 @@ def main() -> int:
         w = dataclasses.replace(w, fmt=args.weights, name=f"{w.name}_{args.weights}")
     if args.tokens:
         w = dataclasses.replace(w.with_tokens(args.tokens), name=f"{w.name}_T{args.tokens}")
+    if args.lora_rank is not None:
+        r = int(args.lora_rank)
+        w = dataclasses.replace(w, rank=r, alpha=2.0 * r if r > 0 else w.alpha,
+                                name=f"{w.name}_r{r}")
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     if args.path != "layer":

@@ -1366,31 +1366,73 @@ BackLayout back_layout(int64_t rows, int num_experts, int64_t hidden, int64_t ff
   return L;
 }
 
-struct LoraGradJob {
+// The LoRA weight gradients that stream one M operand: M [rows, cols] (rows
+// through `map`, null: identity) against the low-rank columns of one or more
+// adapters, each gradient split into 32-wide rank slices. Slices that share
+// M run two to a job (M is read once for both), and a phase's jobs go out in
+// as few launches as the job table allows.
+struct GradSource {
   const uint16_t *m;
   int64_t ldm;
   const int32_t *map;
-  const uint16_t *v;
   int64_t cols;
-  float *out;
-  bool a_layout;  // [E, r, cols] (dA) rather than [E, cols, r] (dB)
 };
 
-// One launch per 32-wide slice of the rank: slice c reads low-rank columns
-// [32c, 32c + 32) and writes those ranks of the gradient.
-int run_lora_grad(const LoraGradJob &j, int rank, int64_t ldv, const PlanView &v, int experts,
-                  hipStream_t s) {
-  if (!j.out) return MX_OK;
-  const int64_t se = j.cols * rank;
-  const int64_t sc = j.a_layout ? 1 : rank, sj = j.a_layout ? j.cols : 1;
-  for (int c0 = 0; c0 < rank; c0 += kLoraK) {
-    const int rc = lora_weight_grad(j.m, j.ldm, j.map, j.v + c0, ldv, std::min(kLoraK, rank - c0),
-                                    j.cols, v.seg, v.seg + experts, experts, j.out + c0 * sj, se,
-                                    sc, sj, s);
-    if (rc) return rc;
+class GradPhase {
+ public:
+  // Gradient [E, cols, rank] (a_layout false: dB) or [E, rank, cols] (dA) of
+  // one adapter, from its low-rank columns v (leading dimension ldv).
+  void add(const GradSource &src, const uint16_t *v, int64_t ldv, int rank, float *out,
+           bool a_layout) {
+    if (!out || rank <= 0) return;
+    const int64_t se = src.cols * rank;
+    const int64_t sc = a_layout ? 1 : rank, sj = a_layout ? src.cols : 1;
+    for (int c0 = 0; c0 < rank; c0 += kLoraK) {
+      WeightGradJob *j = open_job(src, ldv);
+      const int b = j->nv++;
+      j->v[b] = v + c0;
+      j->rank[b] = std::min(kLoraK, rank - c0);
+      j->out[b] = out + c0 * sj;
+      j->stride_e[b] = se;
+      j->stride_c[b] = sc;
+      j->stride_j[b] = sj;
+    }
   }
-  return MX_OK;
-}
+  int run(const PlanView &v, int experts, hipStream_t s) {
+    for (int first = 0; first < n_; first += kMaxGradJobs) {
+      WeightGradJobs batch = {};
+      batch.n = std::min(kMaxGradJobs, n_ - first);
+      for (int i = 0; i < batch.n; ++i) batch.job[i] = jobs_[first + i];
+      const int rc = lora_weight_grads(batch, v.seg, v.seg + experts, experts, s);
+      if (rc) return rc;
+    }
+    n_ = 0;
+    return MX_OK;
+  }
+
+ private:
+  // The last job if it streams the same M and has a free V block, else a new one.
+  WeightGradJob *open_job(const GradSource &src, int64_t ldv) {
+    if (n_ > 0) {
+      WeightGradJob &j = jobs_[n_ - 1];
+      if (j.nv < 2 && j.m == src.m && j.ldm == src.ldm && j.map == src.map &&
+          j.cols == src.cols && j.ldv == ldv)
+        return &j;
+    }
+    WeightGradJob &j = jobs_[n_++];
+    j = WeightGradJob{};
+    j.m = src.m;
+    j.ldm = src.ldm;
+    j.map = src.map;
+    j.cols = src.cols;
+    j.ldv = ldv;
+    return &j;
+  }
+  // A phase holds at most four gradients of up to 256 / 32 slices each, and
+  // every slice adds at most one job.
+  WeightGradJob jobs_[4 * kLoraMaxRank / kLoraK];
+  int n_ = 0;
+};
 
 // The layer backward after the combine backward, shared by token-choice and
 // expert-choice routes: from dy (per-slot grad of the expert outputs, slot
@@ -1463,10 +1505,11 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
   }
   mark_stage(3, s);
   if (lora2) {
-    const LoraGradJob jb = {dy, hidden, v.row_slot, lsave + 2 * lrc, hidden, grad_b2, false};
-    const LoraGradJob ja = {h_in, ffn, nullptr, dz + 2 * lrc, ffn, grad_a2, true};
-    if ((rc = run_lora_grad(jb, l2->rank, ldz, v, num_experts, s))) return rc;
-    if ((rc = run_lora_grad(ja, l2->rank, ldz, v, num_experts, s))) return rc;
+    // dB2 = sum dy^T p2 and dA2 = sum dz2^T h, one launch.
+    GradPhase ph;
+    ph.add({dy, hidden, v.row_slot, hidden}, lsave + 2 * lrc, ldz, l2->rank, grad_b2, false);
+    ph.add({h_in, ffn, nullptr, ffn}, dz + 2 * lrc, ldz, l2->rank, grad_a2, true);
+    if ((rc = ph.run(v, num_experts, s))) return rc;
   }
 
   // Gate / up projections: dz1 = s1 * dG B1, dz3 = s3 * dU B3, then per-slot
@@ -1511,17 +1554,18 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
     if ((rc = launch_any<EPI_STORE2>(w1->format, lora1 || lora3, p, L.plan, v, s))) return rc;
   }
   mark_stage(5, s);
-  for (int i = 0; i < 2; ++i) {
-    const mx_lora *l = l13[i];
-    if (!has_lora(l)) continue;
-    const LoraGradJob jb = {dgu + i * ffn, 2 * ffn, nullptr, lsave + lrc * i, ffn,
-                            i ? grad_b3 : grad_b1, false};
-    const LoraGradJob ja = {x, hidden, v.row_token, dz + lrc * i, hidden, i ? grad_a3 : grad_a1,
-                            true};
-    if ((rc = run_lora_grad(jb, l->rank, ldz, v, num_experts, s))) return rc;
-    if ((rc = run_lora_grad(ja, l->rank, ldz, v, num_experts, s))) return rc;
-  }
-  return MX_OK;
+  // dB1 / dB3 = sum dG^T p1 / dU^T p3, and dA1 / dA3 = sum dz1^T x / dz3^T x
+  // from one pass over the gathered token rows, one launch.
+  GradPhase ph;
+  for (int i = 0; i < 2; ++i)
+    if (has_lora(l13[i]))
+      ph.add({dgu + i * ffn, 2 * ffn, nullptr, ffn}, lsave + lrc * i, ldz, l13[i]->rank,
+             i ? grad_b3 : grad_b1, false);
+  for (int i = 0; i < 2; ++i)
+    if (has_lora(l13[i]))
+      ph.add({x, hidden, v.row_token, hidden}, dz + lrc * i, ldz, l13[i]->rank,
+             i ? grad_a3 : grad_a1, true);
+  return ph.run(v, num_experts, s);
 }
 
 }  // namespace gemm

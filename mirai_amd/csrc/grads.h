@@ -19,17 +19,34 @@ struct FactorTransposes {
 // All jobs in one launch.
 int transpose_factors_multi(const FactorTransposes &jobs, hipStream_t s);
 
-// Per-expert outer-product sums over the expert's sorted rows:
-//   G[e, c, j] = sum_{r in [seg_start[e], seg_end[e])} M[map(r), c] * V[r, j]
-// for c < cols, j < rank (fp32 accumulation, fp32 output at
-// out + e*stride_e + c*stride_c + j*stride_j). M and V are bf16 with leading
-// dimensions ldm / ldv; map (null: identity) sends a sorted row to its M row.
-// V holds 32 columns (those past `rank`, up to 32, only feed unwritten
-// outputs); rank <= 32, cols a multiple of 8.
-int lora_weight_grad(const uint16_t *m, int64_t ldm, const int32_t *map, const uint16_t *v,
-                     int64_t ldv, int rank, int64_t cols, const int64_t *seg_start,
-                     const int64_t *seg_end, int experts, float *out, int64_t stride_e,
-                     int64_t stride_c, int64_t stride_j, hipStream_t s);
+// Per-expert outer-product sums over the expert's sorted rows, for one or
+// two V blocks that share M:
+//   G_b[e, c, j] = sum_{r in [seg_start[e], seg_end[e])} M[map(r), c] * V_b[r, j]
+// for c < cols, j < rank[b] (fp32 accumulation, fp32 output at
+// out[b] + e*stride_e[b] + c*stride_c[b] + j*stride_j[b]). M and V_b are bf16 with
+// leading dimensions ldm / ldv; map (null: identity) sends a sorted row to its
+// M row. Each V block holds 32 columns (those past its rank only feed
+// unwritten outputs); rank <= 32, cols a multiple of 8.
+struct WeightGradJob {
+  const uint16_t *m;
+  int64_t ldm;
+  const int32_t *map;
+  const uint16_t *v[2];
+  int64_t ldv;
+  int rank[2];
+  int nv;
+  int64_t cols;
+  float *out[2];
+  int64_t stride_e[2], stride_c[2], stride_j[2];
+};
+constexpr int kMaxGradJobs = 8;
+struct WeightGradJobs {
+  WeightGradJob job[kMaxGradJobs];
+  int n;
+};
+// All jobs in one launch.
+int lora_weight_grads(const WeightGradJobs &jobs, const int64_t *seg_start,
+                      const int64_t *seg_end, int experts, hipStream_t s);
 
 // Gated-activation backward in place over expert-sorted rows: row r of `dgu`
 // (stride 2f) holds dh in its first f columns on entry and [dG | dU] on exit,

@@ -108,78 +108,106 @@ __device__ __forceinline__ bf16x8 read_v_trans(const uint8_t *sV, int kk, int la
   return __builtin_bit_cast(bf16x8, v);
 }
 
-// One workgroup (4 waves) per (expert, 256-column slice): G[c, j] = sum over
-// the expert's rows of M[row, c] * V[row, j] on bf16 MFMA with fp32
-// accumulation. Both operands arrive row-major (the reduction runs along
-// rows), so 64-row chunks of M and V go to LDS as they are and the MFMA
-// fragments are read with ds_read_b64_tr_b16. Each wave owns 64 columns x 32
-// ranks (two 32 x 32 blocks). Rows past the segment and columns past `cols`
-// are zero-filled. The kernel streams M once, so it is bound by load latency:
-// each thread keeps two chunks of its loads in flight (register sets A and B,
-// alternating), the row map of the chunk after them is fetched one chunk ahead,
-// and two LDS stages alternate, so a chunk's loads are issued two chunks
-// before its MFMAs.
-__global__ __launch_bounds__(256) void lora_weight_grad_kernel(
-    const uint16_t *m, int64_t ldm, const int32_t *map, const uint16_t *v, int64_t ldv, int rank,
-    int64_t cols, const int64_t *seg_start, const int64_t *seg_end, float *out, int64_t se,
-    int64_t sc, int64_t sj) {
-  __shared__ __attribute__((aligned(16))) uint8_t sM0[64 * 512];
-  __shared__ __attribute__((aligned(16))) uint8_t sM1[64 * 512];
-  __shared__ __attribute__((aligned(16))) uint8_t sV0[64 * 64];
-  __shared__ __attribute__((aligned(16))) uint8_t sV1[64 * 64];
-  const int e = blockIdx.y;
-  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 256;
+// Jobs of one lora_weight_grads launch; workgroups [block0[j], block0[j + 1])
+// serve job j, expert-major (the column slices of one expert are adjacent, so
+// they meet the expert's V rows in L2).
+struct GradLaunch {
+  WeightGradJob job[kMaxGradJobs];
+  int64_t block0[kMaxGradJobs + 1];
+  int col_blocks[kMaxGradJobs];
+  int n;
+  const int64_t *seg_start, *seg_end;
+};
+
+// One workgroup (4 waves) per (job, expert, 128-column slice): G_b[c, j] = sum
+// over the expert's rows of M[row, c] * V_b[row, j] for the job's one or two V
+// blocks, on bf16 MFMA with fp32 accumulation. Both operands arrive row-major
+// (the reduction runs along rows), so 64-row chunks of M and V go to LDS as
+// they are and the MFMA fragments are read with ds_read_b64_tr_b16; the M
+// fragment of a K step feeds both V blocks. Each wave owns 32 columns x 32
+// ranks of each V block (one 32 x 32 block each). Rows past the segment and
+// columns past `cols` are zero-filled. The kernel streams M once, so it is
+// bound by load latency: each thread keeps two chunks of its loads in flight
+// (register sets A and B, alternating), the row map of the chunk after them
+// is fetched one chunk ahead, and two LDS stages alternate, so a chunk's
+// loads are issued two chunks before its MFMAs. The narrow slice keeps the
+// kernel within 256 registers (194) and 48 KB of LDS, so two workgroups share
+// a CU and their load chains overlap (a 256-column slice needs 288 registers
+// and runs one workgroup per CU).
+__global__ __launch_bounds__(256) void lora_weight_grad_kernel(GradLaunch L) {
+  __shared__ __attribute__((aligned(16))) uint8_t sM0[64 * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t sM1[64 * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t sV0[2 * 64 * 64];
+  __shared__ __attribute__((aligned(16))) uint8_t sV1[2 * 64 * 64];
+  int jn = 0;
+  while (jn + 1 < L.n && static_cast<int64_t>(blockIdx.x) >= L.block0[jn + 1]) ++jn;
+  const WeightGradJob &J = L.job[jn];
+  const int local = static_cast<int>(static_cast<int64_t>(blockIdx.x) - L.block0[jn]);
+  const int e = local / L.col_blocks[jn];
+  const int64_t c0 = static_cast<int64_t>(local - e * L.col_blocks[jn]) * 128;
+  const uint16_t *m = J.m;
+  const int32_t *map = J.map;
+  const int64_t ldm = J.ldm, ldv = J.ldv, cols = J.cols;
+  const int nv = J.nv;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t start = seg_start[e], end = seg_end[e];
+  const int64_t start = L.seg_start[e], end = L.seg_end[e];
   f32x16 acc[2];
 #pragma unroll
-  for (int b = 0; b < 2; ++b)
+  for (int vb = 0; vb < 2; ++vb)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc[b][j] = 0.0f;
+    for (int j = 0; j < 16; ++j) acc[vb][j] = 0.0f;
 
-  // This thread's share of a chunk: M pieces q = tid + 256*i (row q/32,
-  // 16-byte chunk q%32) and one 16-byte piece of V (row tid/4, chunk tid%4).
+  // This thread's share of a chunk: M pieces q = tid + 256*i (row q/16,
+  // 16-byte chunk q%16) and one 16-byte piece of each V block (row tid/4,
+  // chunk tid%4).
   struct Loads {
-    u32x4 mr[8];
-    u32x4 vr;
+    u32x4 mr[4];
+    u32x4 vr[2];
   };
   const int vrow = tid >> 2, vch = tid & 3;
   // M source rows of a chunk (-1 past the segment end).
   auto rows_of = [&](int64_t r0, int32_t *src) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t grow = r0 + ((tid + 256 * i) >> 5);
+    for (int i = 0; i < 4; ++i) {
+      const int64_t grow = r0 + ((tid + 256 * i) >> 4);
       src[i] = grow < end ? (map ? map[grow] : static_cast<int32_t>(grow)) : -1;
     }
   };
-  auto load = [&](int64_t r0, const int32_t *src, Loads &L) {
+  auto load = [&](int64_t r0, const int32_t *src, Loads &Ld) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t col = c0 + ((tid + 256 * i) & 31) * 8;
-      L.mr[i] = (src[i] >= 0 && col < cols)
-                    ? *reinterpret_cast<const u32x4 *>(m + static_cast<int64_t>(src[i]) * ldm + col)
-                    : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < 4; ++i) {
+      const int64_t col = c0 + ((tid + 256 * i) & 15) * 8;
+      Ld.mr[i] = (src[i] >= 0 && col < cols)
+                     ? *reinterpret_cast<const u32x4 *>(m + static_cast<int64_t>(src[i]) * ldm + col)
+                     : u32x4{0u, 0u, 0u, 0u};
     }
     const int64_t grow = r0 + vrow;
-    L.vr = grow < end ? *reinterpret_cast<const u32x4 *>(v + grow * ldv + vch * 8)
+#pragma unroll
+    for (int vb = 0; vb < 2; ++vb)
+      Ld.vr[vb] = (vb < nv && grow < end)
+                      ? *reinterpret_cast<const u32x4 *>(J.v[vb] + grow * ldv + vch * 8)
                       : u32x4{0u, 0u, 0u, 0u};
   };
-  auto store = [&](uint8_t *sM, uint8_t *sV, const Loads &L) {
+  auto store = [&](uint8_t *sM, uint8_t *sV, const Loads &Ld) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const int q = tid + 256 * i;
-      *reinterpret_cast<u32x4 *>(sM + swz_t(q >> 5, q & 31)) = L.mr[i];
+      *reinterpret_cast<u32x4 *>(sM + swz_t128(q >> 4, q & 15)) = Ld.mr[i];
     }
-    *reinterpret_cast<u32x4 *>(sV + vrow * 64 + vch * 16) = L.vr;
+#pragma unroll
+    for (int vb = 0; vb < 2; ++vb)
+      if (vb < nv) *reinterpret_cast<u32x4 *>(sV + vb * 4096 + vrow * 64 + vch * 16) = Ld.vr[vb];
   };
   auto compute = [&](const uint8_t *sM, const uint8_t *sV) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const bf16x8 bv = read_v_trans(sV, kk, lane);
+      const bf16x8 bm = read_b_trans<256>(sM, wave * 32, kk, lane);
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
-        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(read_b_trans(sM, wave * 64 + b * 32, kk, lane),
-                                                         bv, acc[b], 0, 0, 0);
+      for (int vb = 0; vb < 2; ++vb) {
+        if (vb >= nv) continue;
+        const bf16x8 bv = read_v_trans(sV + vb * 4096, kk, lane);
+        acc[vb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bm, bv, acc[vb], 0, 0, 0);
+      }
     }
   };
   // Chunk c (rows start + 64c) is loaded in step c-2 (set c % 2), stored to
@@ -194,7 +222,7 @@ __global__ __launch_bounds__(256) void lora_weight_grad_kernel(
   };
   if (start < end) {
     Loads la, lb;
-    int32_t src[8];
+    int32_t src[4];
     rows_of(start, src);
     load(start, src, la);
     if (start + 64 < end) {
@@ -213,15 +241,17 @@ __global__ __launch_bounds__(256) void lora_weight_grad_kernel(
   // Accumulator value jj of a lane: column c = 8*(jj/4) + 4*(lane/32) + jj%4 of
   // the block, rank j = lane % 32.
   const int j = lane & 31;
-  if (j >= rank) return;
-  float *o = out + e * se + j * sj;
 #pragma unroll
-  for (int b = 0; b < 2; ++b)
+  for (int vb = 0; vb < 2; ++vb) {
+    if (vb >= nv || j >= J.rank[vb]) continue;
+    float *o = J.out[vb] + e * J.stride_e[vb] + j * J.stride_j[vb];
+    const int64_t sc = J.stride_c[vb];
 #pragma unroll
     for (int jj = 0; jj < 16; ++jj) {
-      const int64_t c = c0 + wave * 64 + b * 32 + 8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3);
-      if (c < cols) o[c * sc] = acc[b][jj];
+      const int64_t c = c0 + wave * 32 + 8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3);
+      if (c < cols) o[c * sc] = acc[vb][jj];
     }
+  }
 }
 
 // One thread per 8 columns of one row.
@@ -318,18 +348,37 @@ int transpose_factors_multi(const FactorTransposes &jobs, hipStream_t s) {
   return check_launch("LoRA factor transposes");
 }
 
-int lora_weight_grad(const uint16_t *m, int64_t ldm, const int32_t *map, const uint16_t *v,
-                     int64_t ldv, int rank, int64_t cols, const int64_t *seg_start,
-                     const int64_t *seg_end, int experts, float *out, int64_t stride_e,
-                     int64_t stride_c, int64_t stride_j, hipStream_t s) {
-  if (cols % 8 != 0 || rank <= 0 || rank > 32) {
-    set_error("LoRA weight gradient: cols must be a multiple of 8 and rank in [1, 32]");
+int lora_weight_grads(const WeightGradJobs &jobs, const int64_t *seg_start,
+                      const int64_t *seg_end, int experts, hipStream_t s) {
+  if (jobs.n < 0 || jobs.n > kMaxGradJobs) {
+    set_error("LoRA weight gradients: %d jobs (at most %d per launch)", jobs.n, kMaxGradJobs);
     return MX_ERR_INVALID;
   }
-  const dim3 grid(static_cast<unsigned>(ceil_div(cols, 256)), static_cast<unsigned>(experts));
-  hipLaunchKernelGGL(lora_weight_grad_kernel, grid, dim3(256), 0, s, m, ldm, map, v, ldv, rank,
-                     cols, seg_start, seg_end, out, stride_e, stride_c, stride_j);
-  return check_launch("LoRA weight gradient");
+  GradLaunch L = {};
+  int64_t blocks = 0;
+  for (int i = 0; i < jobs.n; ++i) {
+    const WeightGradJob &j = jobs.job[i];
+    bool ok = j.m && j.cols > 0 && j.cols % 8 == 0 && j.nv >= 1 && j.nv <= 2;
+    for (int b = 0; ok && b < j.nv; ++b)
+      ok = j.v[b] && j.out[b] && j.rank[b] >= 1 && j.rank[b] <= 32;
+    if (!ok) {
+      set_error("LoRA weight gradients: job %d needs M, cols a multiple of 8, and 1-2 V blocks "
+                "with outputs and ranks in [1, 32]", i);
+      return MX_ERR_INVALID;
+    }
+    L.job[i] = j;
+    L.block0[i] = blocks;
+    L.col_blocks[i] = static_cast<int>(ceil_div(j.cols, 128));
+    blocks += static_cast<int64_t>(L.col_blocks[i]) * experts;
+  }
+  L.n = jobs.n;
+  L.block0[jobs.n] = blocks;
+  L.seg_start = seg_start;
+  L.seg_end = seg_end;
+  if (blocks <= 0) return MX_OK;
+  hipLaunchKernelGGL(lora_weight_grad_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     s, L);
+  return check_launch("LoRA weight gradients");
 }
 
 }  // namespace mx

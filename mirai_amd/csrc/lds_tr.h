@@ -16,6 +16,13 @@ __device__ __forceinline__ int swz_t(int row, int chunk) {
   return row * 512 + ((chunk ^ x) << 4);
 }
 
+// The same layout over [k rows][128 n] (256-byte rows, 16 chunks): the row
+// key only permutes chunks within the row, so the properties above hold.
+__device__ __forceinline__ int swz_t128(int row, int chunk) {
+  const int x = ((row & 3) << 2) | ((row >> 2) & 3);
+  return row * 256 + ((chunk ^ x) << 4);
+}
+
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 // B fragment of v_mfma_f32_32x32x16_bf16 (lane: column lane%32, k = 8*(lane/32)
@@ -23,16 +30,18 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 // 16-lane group the elements j, 16+j, 32+j, 48+j of the group's concatenated
 // 8-byte chunks; lane i of the group therefore fetches row k0 + i/4, columns
 // c0 + 4*(i%4) .. +3, and receives column c0 + j of rows k0 .. k0+3.
+template <int ROW_BYTES = 512>
 __device__ __forceinline__ bf16x8 read_b_trans(const uint8_t *sB, int ncol0, int kk, int lane) {
   const int g = lane >> 4, i = lane & 15;
   const int row = 16 * kk + 8 * (g >> 1) + (i >> 2);
   const int col = ncol0 + 16 * (g & 1) + 4 * (i & 3);
   const int chunk = col >> 3, half = ((col >> 2) & 1) * 8;
+  auto at = [](int r, int c) { return ROW_BYTES == 512 ? swz_t(r, c) : swz_t128(r, c); };
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
   const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4 *>(
-      reinterpret_cast<uintptr_t>(sB + swz_t(row, chunk) + half)));
+      reinterpret_cast<uintptr_t>(sB + at(row, chunk) + half)));
   const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4 *>(
-      reinterpret_cast<uintptr_t>(sB + swz_t(row + 4, chunk) + half)));
+      reinterpret_cast<uintptr_t>(sB + at(row + 4, chunk) + half)));
   typedef short i16x8 __attribute__((ext_vector_type(8)));
   const i16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   return __builtin_bit_cast(bf16x8, v);
