@@ -100,6 +100,9 @@ struct Params {
   int64_t lora_stride[4];    // EPI_LORA_A: factor rows per expert of each sub-adapter's factor
   const int2 *tiles;
   const int32_t *num_tiles;
+  const int2 *tiles_r;       // dual launch: the 128-row remainder tiles
+  const int32_t *num_tiles_r;
+  int slots_tall;            // dual launch: per-XCD slots of the 256-row tiles
   const int64_t *seg_end;
   uint16_t *out;
   int64_t ldo;
@@ -241,35 +244,27 @@ __device__ __forceinline__ void nf4_decode8(const Nf4Table &t, uint32_t c, uint3
   out[3] = __builtin_amdgcn_perm(ho, lo_, 0x07030602u);  // e6, e7
 }
 
+// LoRA factor tiles of the epilogue (one [BN][32] tile per adapter).
+template <int EPI, bool LORA, class T>
+constexpr int lora_tile_bytes() {
+  return LORA ? (EPI == EPI_STORE2 ? 2 : 1) * T::BN * 64 : 16;
+}
+
+// One (row tile, column tile) of the grouped GEMM: `tile` = (expert, first
+// sorted row), `nt` the column tile. The LDS stages are the caller's four
+// distinct __shared__ arrays (two stages of A and of B): once this is
+// inlined the compiler sees those objects and can prove that the A DMA into
+// one stage never aliases the LDS reads and B writes of the other, so it
+// inserts no wait between them.
 template <int FMT, int EPI, bool LORA, class T>
-__global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_SIMD)))
-void grouped_gemm_kernel(Params p) {
-  // Four distinct LDS objects (two stages of A and of B): the compiler can
-  // then prove that the A DMA into one stage never aliases the LDS reads and
-  // B writes of the other, and inserts no wait between them.
-  __shared__ __attribute__((aligned(16))) uint8_t sA0[T::STAGE_A];
-  __shared__ __attribute__((aligned(16))) uint8_t sA1[T::STAGE_A];
-  __shared__ __attribute__((aligned(16))) uint8_t sB0[T::STAGE_B];
-  __shared__ __attribute__((aligned(16))) uint8_t sB1[T::STAGE_B];
-  // LoRA factor tiles of the epilogue (one [BN][32] tile per adapter).
-  constexpr int kLTile = LORA ? (EPI == EPI_STORE2 ? 2 : 1) * T::BN * 64 : 16;
-  __shared__ __attribute__((aligned(16))) uint8_t sLt[kLTile];
+__device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *sA0,
+                                          uint8_t *sA1, uint8_t *sB0, uint8_t *sB1,
+                                          uint8_t *sLt) {
+  constexpr int kLTile = lora_tile_bytes<EPI, LORA, T>();
   const int tid = threadIdx.x;
   // MX_FMT_F32X3: bf16 planes with K = 3 * in (loaded as bf16); the
   // epilogues keep fp32 and write split outputs.
   constexpr bool kSplit = FMT == MX_FMT_F32X3;
-
-  // ---------------------------------------------------------------- tile
-  const int num_m = *p.num_tiles;
-  const int total = num_m * p.n_tiles_n;
-  const int per_xcd = (total + 7) >> 3;
-  const int slot = blockIdx.x >> 3;
-  if (slot >= per_xcd) return;
-  const int logical = (blockIdx.x & 7) * per_xcd + slot;
-  if (logical >= total) return;
-  const int mt = logical / p.n_tiles_n;
-  const int nt = logical - mt * p.n_tiles_n;
-  const int2 tile = p.tiles[mt];
   const int e = tile.x;
   const int64_t row0 = tile.y;
   const int64_t row_end = p.seg_end[e];
@@ -972,6 +967,69 @@ void grouped_gemm_kernel(Params p) {
   }
 }
 
+// One launch over one tile list (p.tiles, *p.num_tiles row tiles). The
+// blockIdx -> tile map gives each of the 8 XCDs (workgroups go to XCDs
+// round-robin) a contiguous run of tiles, row-tile major, so the column tiles
+// that share an activation tile, and the row tiles that share an expert's
+// weights, meet in one L2.
+template <int FMT, int EPI, bool LORA, class T>
+__global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_SIMD)))
+void grouped_gemm_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t sA0[T::STAGE_A];
+  __shared__ __attribute__((aligned(16))) uint8_t sA1[T::STAGE_A];
+  __shared__ __attribute__((aligned(16))) uint8_t sB0[T::STAGE_B];
+  __shared__ __attribute__((aligned(16))) uint8_t sB1[T::STAGE_B];
+  __shared__ __attribute__((aligned(16))) uint8_t sLt[lora_tile_bytes<EPI, LORA, T>()];
+  const int total = *p.num_tiles * p.n_tiles_n;
+  const int per_xcd = (total + 7) >> 3;
+  const int slot = blockIdx.x >> 3;
+  if (slot >= per_xcd) return;
+  const int logical = (blockIdx.x & 7) * per_xcd + slot;
+  if (logical >= total) return;
+  const int mt = logical / p.n_tiles_n;
+  gemm_tile<FMT, EPI, LORA, T>(p, p.tiles[mt], logical - mt * p.n_tiles_n, sA0, sA1, sB0, sB1,
+                               sLt);
+}
+
+// 256-row tiles (p.tiles) and the 128-row remainder tiles (p.tiles_r) in one
+// launch. Each XCD runs its share of the tall tiles first (slots below
+// p.slots_tall, in the map above) and then its share of the remainder tiles,
+// which so fill the tail of the tall ones instead of running as a launch of
+// their own after it.
+template <int FMT, int EPI, bool LORA, class Tall, class Short>
+__global__ __launch_bounds__(Tall::NT) __attribute__((amdgpu_waves_per_eu(Tall::WAVES_PER_SIMD)))
+void grouped_gemm_dual_kernel(Params p) {
+  static_assert(Tall::NT == Short::NT && Tall::BN == Short::BN && Tall::BK == Short::BK &&
+                    Short::STAGE_A <= Tall::STAGE_A && Short::STAGE_B == Tall::STAGE_B,
+                "both tile heights share one workgroup shape and its LDS");
+  __shared__ __attribute__((aligned(16))) uint8_t sA0[Tall::STAGE_A];
+  __shared__ __attribute__((aligned(16))) uint8_t sA1[Tall::STAGE_A];
+  __shared__ __attribute__((aligned(16))) uint8_t sB0[Tall::STAGE_B];
+  __shared__ __attribute__((aligned(16))) uint8_t sB1[Tall::STAGE_B];
+  __shared__ __attribute__((aligned(16))) uint8_t sLt[lora_tile_bytes<EPI, LORA, Tall>()];
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  if (slot < p.slots_tall) {
+    const int total = *p.num_tiles * p.n_tiles_n;
+    const int per_xcd = (total + 7) >> 3;
+    if (slot >= per_xcd) return;
+    const int logical = xcd * per_xcd + slot;
+    if (logical >= total) return;
+    const int mt = logical / p.n_tiles_n;
+    gemm_tile<FMT, EPI, LORA, Tall>(p, p.tiles[mt], logical - mt * p.n_tiles_n, sA0, sA1, sB0,
+                                    sB1, sLt);
+  } else {
+    const int total = *p.num_tiles_r * p.n_tiles_n;
+    const int per_xcd = (total + 7) >> 3;
+    const int s2 = slot - p.slots_tall;
+    if (s2 >= per_xcd) return;
+    const int logical = xcd * per_xcd + s2;
+    if (logical >= total) return;
+    const int mt = logical / p.n_tiles_n;
+    gemm_tile<FMT, EPI, LORA, Short>(p, p.tiles_r[mt], logical - mt * p.n_tiles_n, sA0, sA1, sB0,
+                                     sB1, sLt);
+  }
+}
+
 template <int FMT, int EPI, bool LORA, class T>
 int launch(const Params &p, int64_t max_row_tiles, hipStream_t s) {
   const int64_t total = max_row_tiles * p.n_tiles_n;
@@ -986,30 +1044,65 @@ int launch(const Params &p, int64_t max_row_tiles, hipStream_t s) {
   return check_launch("grouped GEMM launch");
 }
 
+// The dual launch: room for max_tall 256-row tiles and max_short remainder
+// tiles (upper bounds; the kernel reads the plan's counts).
+template <int FMT, int EPI, bool LORA, class Tall, class Short>
+int launch_dual(Params p, int64_t max_tall, int64_t max_short, hipStream_t s) {
+  const int64_t slots_tall = ceil_div(max_tall * p.n_tiles_n, 8);
+  const int64_t slots_short = ceil_div(max_short * p.n_tiles_n, 8);
+  const int64_t grid = 8 * (slots_tall + slots_short);
+  if (grid <= 0) return MX_OK;
+  if (grid > 0x7fffffff) {
+    set_error("grouped GEMM grid too large");
+    return MX_ERR_INVALID;
+  }
+  p.slots_tall = static_cast<int>(slots_tall);
+  hipLaunchKernelGGL((grouped_gemm_dual_kernel<FMT, EPI, LORA, Tall, Short>),
+                     dim3(static_cast<unsigned>(grid)), dim3(Tall::NT), 0, s, p);
+  return check_launch("grouped GEMM launch");
+}
+
 // Row-tile height: 256-row tiles when experts average at least 256 rows (the
 // taller tile's better MFMA / LDS ratio outweighs its tail waste from there
 // on, measured at C2, C3 and C5), else 128-row tiles.
 inline bool use_tall_tiles(int64_t rows, int experts) { return rows >= 256 * static_cast<int64_t>(experts); }
 
-template <int EPI, bool LORA, class Tall, class Short>
-int launch_tile(int fmt, bool tall, const Params &p, int64_t max_tiles, hipStream_t s) {
+// 128-row tiles only (experts averaging under 256 rows).
+template <int EPI, bool LORA, class Short>
+int launch_tile(int fmt, const Params &p, int64_t max_tiles, hipStream_t s) {
   switch (fmt) {
     case MX_FMT_BF16:
-      return tall ? launch<MX_FMT_BF16, EPI, LORA, Tall>(p, max_tiles, s)
-                  : launch<MX_FMT_BF16, EPI, LORA, Short>(p, max_tiles, s);
+      return launch<MX_FMT_BF16, EPI, LORA, Short>(p, max_tiles, s);
     case MX_FMT_NF4:
-      return tall ? launch<MX_FMT_NF4, EPI, LORA, Tall>(p, max_tiles, s)
-                  : launch<MX_FMT_NF4, EPI, LORA, Short>(p, max_tiles, s);
+      return launch<MX_FMT_NF4, EPI, LORA, Short>(p, max_tiles, s);
     case MX_FMT_NF4_F32:
-      return tall ? launch<MX_FMT_NF4_F32, EPI, LORA, Tall>(p, max_tiles, s)
-                  : launch<MX_FMT_NF4_F32, EPI, LORA, Short>(p, max_tiles, s);
+      return launch<MX_FMT_NF4_F32, EPI, LORA, Short>(p, max_tiles, s);
     case MX_FMT_INT8:
-      return tall ? launch<MX_FMT_INT8, EPI, LORA, Tall>(p, max_tiles, s)
-                  : launch<MX_FMT_INT8, EPI, LORA, Short>(p, max_tiles, s);
+      return launch<MX_FMT_INT8, EPI, LORA, Short>(p, max_tiles, s);
     case MX_FMT_F32X3:
       if constexpr (EPI == EPI_SWIGLU || EPI == EPI_STORE)
-        return tall ? launch<MX_FMT_F32X3, EPI, LORA, Tall>(p, max_tiles, s)
-                    : launch<MX_FMT_F32X3, EPI, LORA, Short>(p, max_tiles, s);
+        return launch<MX_FMT_F32X3, EPI, LORA, Short>(p, max_tiles, s);
+      break;
+  }
+  set_error("unknown weight format %d", fmt);
+  return MX_ERR_INVALID;
+}
+
+template <int EPI, bool LORA, class Tall, class Short>
+int launch_tile_dual(int fmt, const Params &p, int64_t max_tall, int64_t max_short,
+                     hipStream_t s) {
+  switch (fmt) {
+    case MX_FMT_BF16:
+      return launch_dual<MX_FMT_BF16, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
+    case MX_FMT_NF4:
+      return launch_dual<MX_FMT_NF4, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
+    case MX_FMT_NF4_F32:
+      return launch_dual<MX_FMT_NF4_F32, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
+    case MX_FMT_INT8:
+      return launch_dual<MX_FMT_INT8, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
+    case MX_FMT_F32X3:
+      if constexpr (EPI == EPI_SWIGLU || EPI == EPI_STORE)
+        return launch_dual<MX_FMT_F32X3, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
       break;
   }
   set_error("unknown weight format %d", fmt);
@@ -1028,18 +1121,16 @@ int launch_fmt(int fmt, Params p, const PlanLayout &PL, const PlanView &v, bool 
   if (!tall) {
     p.tiles = v.tiles;
     p.num_tiles = v.num_tiles;
-    return launch_tile<EPI, LORA, Tall, Short>(fmt, false, p, PL.max_tiles, s);
+    return launch_tile<EPI, LORA, Short>(fmt, p, PL.max_tiles, s);
   }
   // 256-row tiles over each expert's rows except a final remainder of at most
-  // 128 rows, then one launch of 128-row tiles for those remainders: a short
-  // remainder costs about half a tall tile instead of a whole one.
+  // 128 rows, which gets a 128-row tile (a short remainder costs about half a
+  // tall tile instead of a whole one); both kinds in one launch.
   p.tiles = v.tiles2m;
   p.num_tiles = v.num_tiles2m;
-  int rc = launch_tile<EPI, LORA, Tall, Short>(fmt, true, p, PL.max_tiles2, s);
-  if (rc) return rc;
-  p.tiles = v.tilesr;
-  p.num_tiles = v.num_tilesr;
-  return launch_tile<EPI, LORA, Tall, Short>(fmt, false, p, PL.experts, s);
+  p.tiles_r = v.tilesr;
+  p.num_tiles_r = v.num_tilesr;
+  return launch_tile_dual<EPI, LORA, Tall, Short>(fmt, p, PL.max_tiles2, PL.experts, s);
 }
 
 template <int EPI>
