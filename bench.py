@@ -620,7 +620,7 @@ def main() -> int:
         "down_gemm_tflops": down_flops / (stages["down_gemm"] * 1e-3) / 1e12,
         **back,
         "roofline": {
-            "kernel": "grouped_gemm_kernel<NF4, SWIGLU, LoRA> (gate/up)",
+            "kernel": "grouped_gemm_dual_kernel<NF4, SWIGLU, LoRA> (gate/up)",
             "bound": "mfma",
             "achieved": achieved,
             "peak": PEAK_BF16_TFLOPS,
