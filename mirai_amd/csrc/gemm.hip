@@ -305,7 +305,7 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   if (!TRANS) b_row<EPI, T>(bj, nt, which, bn);
   // Transposed B: lane = k row of the stage, wave = 32-column slice. Columns
   // past N re-read the last full 32-column slice (discarded by the epilogue).
-  const int tk = tid & 63, tc = tid >> 6;
+  const int tk = tid & 63, tc = wave;
   const int64_t t_col0 = TRANS ? min(static_cast<int64_t>(nt) * T::BN + 32 * tc, p.N - 32) : 0;
   // Weight rows past N (a partial column tile) re-read row N-1: they only
   // feed output columns the epilogue discards. The LoRA down-projection

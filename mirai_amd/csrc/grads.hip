@@ -100,9 +100,9 @@ __device__ __forceinline__ bf16x8 read_v_trans(const uint8_t *sV, int kk, int la
   const int col = 16 * (g & 1) + 4 * (i & 3);
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
   const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      reinterpret_cast<lds_i16x4 *>(reinterpret_cast<uintptr_t>(sV + row * 64 + col * 2)));
+      (lds_i16x4 *)(const_cast<uint8_t *>(sV) + row * 64 + col * 2));
   const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      reinterpret_cast<lds_i16x4 *>(reinterpret_cast<uintptr_t>(sV + (row + 4) * 64 + col * 2)));
+      (lds_i16x4 *)(const_cast<uint8_t *>(sV) + (row + 4) * 64 + col * 2));
   typedef short i16x8 __attribute__((ext_vector_type(8)));
   const i16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   return __builtin_bit_cast(bf16x8, v);

@@ -37,11 +37,14 @@ __device__ __forceinline__ bf16x8 read_b_trans(const uint8_t *sB, int ncol0, int
   const int col = ncol0 + 16 * (g & 1) + 4 * (i & 3);
   const int chunk = col >> 3, half = ((col >> 2) & 1) * 8;
   auto at = [](int r, int c) { return ROW_BYTES == 512 ? swz_t(r, c) : swz_t128(r, c); };
+  // An address-space cast of the stage pointer (not an integer round trip)
+  // keeps the LDS object the read comes from visible to the compiler, so a
+  // read of one stage does not wait for an LDS DMA into the other.
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4 *>(
-      reinterpret_cast<uintptr_t>(sB + at(row, chunk) + half)));
-  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4 *>(
-      reinterpret_cast<uintptr_t>(sB + at(row + 4, chunk) + half)));
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4 *)(const_cast<uint8_t *>(sB) + at(row, chunk) + half));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4 *)(const_cast<uint8_t *>(sB) + at(row + 4, chunk) + half));
   typedef short i16x8 __attribute__((ext_vector_type(8)));
   const i16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   return __builtin_bit_cast(bf16x8, v);
