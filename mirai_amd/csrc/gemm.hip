@@ -283,17 +283,25 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   constexpr int kRowsPerDma = 1024 / (BK * 2);
   const uint16_t *a_ptr[T::A_CHUNKS];
   int a_lds[T::A_CHUNKS];  // wave-uniform LDS byte offset of each DMA inside a stage
+  int64_t a_src[T::A_CHUNKS];
+  int a_col[T::A_CHUNKS];
 #pragma unroll
   for (int i = 0; i < T::A_CHUNKS; ++i) {
     const int region = wave * T::A_CHUNKS + i;
     const int row = region * kRowsPerDma + lane_id / T::CPR;
     const int phys = lane_id % T::CPR;
-    const int logical = BK == 64 ? (phys ^ swz_key64(row)) : (phys ^ ((row >> 2) & 3));
-    const int64_t grow = min(row0 + row, row_end - 1);
-    const int64_t src = p.row_token ? static_cast<int64_t>(p.row_token[grow]) : grow;
-    a_ptr[i] = p.x + src * p.ldx + logical * 8;
+    a_col[i] = 8 * (BK == 64 ? (phys ^ swz_key64(row)) : (phys ^ ((row >> 2) & 3)));
+    a_src[i] = min(row0 + row, row_end - 1);
     a_lds[i] = region * 1024;
   }
+  // The row map is read under one uniform branch, so the chunks' loads are
+  // in flight together (one wait, not one per chunk).
+  if (p.row_token) {
+#pragma unroll
+    for (int i = 0; i < T::A_CHUNKS; ++i) a_src[i] = p.row_token[a_src[i]];
+  }
+#pragma unroll
+  for (int i = 0; i < T::A_CHUNKS; ++i) a_ptr[i] = p.x + a_src[i] * p.ldx + a_col[i];
 
   // ------------------------------------------------------- B (weights)
   constexpr bool TRANS = trans_b(EPI);
