@@ -239,17 +239,44 @@ __global__ __launch_bounds__(256) void lora_weight_grad_kernel(GradLaunch L) {
     }
   }
   // Accumulator value jj of a lane: column c = 8*(jj/4) + 4*(lane/32) + jj%4 of
-  // the block, rank j = lane % 32.
+  // the wave's 32 columns, rank j = lane % 32.
   const int j = lane & 31;
 #pragma unroll
   for (int vb = 0; vb < 2; ++vb) {
-    if (vb >= nv || j >= J.rank[vb]) continue;
-    float *o = J.out[vb] + e * J.stride_e[vb] + j * J.stride_j[vb];
-    const int64_t sc = J.stride_c[vb];
+    if (vb >= nv) continue;
+    float *o = J.out[vb] + e * J.stride_e[vb];
+    const int rank = J.rank[vb];
+    if (J.stride_c[vb] == 1) {
+      // Rank-major rows of `cols` (dA): a store of the accumulators would
+      // scatter 4-byte writes over 32 rows. The [32 ranks][128 columns] block
+      // goes through LDS instead (16-byte chunks XOR-swizzled by the rank; the
+      // K loop's last barrier has retired every read of the stage) and leaves
+      // in 16-byte runs of whole rows.
+      uint8_t *st = vb ? sM1 : sM0;
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      const int64_t c = c0 + wave * 32 + 8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3);
-      if (c < cols) o[c * sc] = acc[vb][jj];
+      for (int g = 0; g < 4; ++g) {
+        const int q = wave * 8 + 2 * g + (lane >> 5);
+        *reinterpret_cast<u32x4 *>(st + j * 512 + ((q ^ j) << 4)) =
+            u32x4{__float_as_uint(acc[vb][4 * g]), __float_as_uint(acc[vb][4 * g + 1]),
+                  __float_as_uint(acc[vb][4 * g + 2]), __float_as_uint(acc[vb][4 * g + 3])};
+      }
+      __syncthreads();
+#pragma unroll
+      for (int pass = 0; pass < 4; ++pass) {
+        const int r = pass * 8 + (tid >> 5), q = tid & 31;
+        const int64_t c = c0 + 4 * q;
+        if (r < rank && c < cols)
+          *reinterpret_cast<u32x4 *>(o + r * J.stride_j[vb] + c) =
+              *reinterpret_cast<const u32x4 *>(st + r * 512 + ((q ^ r) << 4));
+      }
+    } else if (j < rank) {
+      float *oj = o + j * J.stride_j[vb];
+      const int64_t sc = J.stride_c[vb];
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int64_t c = c0 + wave * 32 + 8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3);
+        if (c < cols) oj[c * sc] = acc[vb][jj];
+      }
     }
   }
 }
