@@ -29,7 +29,7 @@ struct PlanLayout {
   int64_t max_tiles2 = 0;  // 256-row tiles
   size_t off_block_counts = 0, off_block_base = 0, off_seg = 0, off_tiles = 0, off_tiles2 = 0;
   size_t off_tiles2m = 0, off_tilesr = 0;
-  size_t off_row_token = 0, off_row_slot = 0;
+  size_t off_row_token = 0, off_row_slot = 0, off_block_err = 0;
   size_t bytes = 0;
 };
 
@@ -50,6 +50,7 @@ struct PlanView {
   int2 *tilesr;            // [experts]
   int32_t *row_token;      // [R]: sorted row -> token
   int32_t *row_slot;       // [R]: sorted row -> flat route slot t*k+j
+  int32_t *block_err;      // [blocks]: invalid expert ids per count block
 };
 
 int slots_per_plan_block(int num_experts, int64_t rows);

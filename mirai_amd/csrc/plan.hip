@@ -6,8 +6,10 @@
 // it (OR is order independent, so the masks are deterministic). A slot's rank
 // among the block's slots of the same expert is the popcount of the mask bits
 // below it, which is exactly the stable order of argsort(stable=True).
-// Pass 1 writes per-block expert counts, pass 2 (one workgroup) scans them into
-// per-(block, expert) bases, pass 3 rebuilds the masks and scatters.
+// Pass 1 writes per-block expert counts (and per-block counts of invalid ids),
+// pass 2 (one workgroup) scans them into per-(block, expert) bases and writes
+// the plan's error count, pass 3 rebuilds the masks and scatters. Every
+// counter is written, not accumulated, so a plan needs no clearing launch.
 #include "common.h"
 #include "plan.h"
 
@@ -16,15 +18,15 @@ namespace {
 
 __device__ __forceinline__ void build_masks(const int64_t *top_idx, int64_t slot0, int n_slots,
                                             int E, int words, uint32_t *mask,
-                                            int32_t *err_counter) {
+                                            int32_t *lds_err) {
   for (int i = threadIdx.x; i < E * words; i += blockDim.x) mask[i] = 0;
   __syncthreads();
   for (int p = threadIdx.x; p < n_slots; p += blockDim.x) {
     const int64_t e = top_idx[slot0 + p];
     if (e >= 0 && e < E) {
       atomicOr(&mask[e * words + (p >> 5)], 1u << (p & 31));
-    } else if (err_counter) {
-      atomicAdd(err_counter, 1);
+    } else if (lds_err) {
+      atomicAdd(lds_err, 1);
     }
   }
   __syncthreads();
@@ -32,12 +34,15 @@ __device__ __forceinline__ void build_masks(const int64_t *top_idx, int64_t slot
 
 __global__ __launch_bounds__(256) void plan_count_kernel(const int64_t *top_idx, int64_t R,
                                                          int E, int EB, int32_t *block_counts,
-                                                         int32_t *err_counter) {
+                                                         int32_t *block_err) {
   extern __shared__ uint32_t mask[];
+  __shared__ int32_t n_err;
+  if (threadIdx.x == 0) n_err = 0;
   const int words = EB >> 5;
   const int64_t slot0 = static_cast<int64_t>(blockIdx.x) * EB;
   const int n_slots = static_cast<int>(min<int64_t>(EB, R - slot0));
-  build_masks(top_idx, slot0, n_slots, E, words, mask, err_counter);
+  build_masks(top_idx, slot0, n_slots, E, words, mask, &n_err);  // syncs before and after
+  if (threadIdx.x == 0) block_err[blockIdx.x] = n_err;
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     int c = 0;
     for (int w = 0; w < words; ++w) c += __popc(mask[e * words + w]);
@@ -81,15 +86,23 @@ __device__ int64_t block_exclusive_scan(int64_t v, int64_t *shared, int64_t *tot
 // kEpt: experts per thread the kernel is compiled for (1 when E <= 1024).
 template <int kEpt>
 __global__ __launch_bounds__(1024) void plan_scan_kernel(
-    const int32_t *block_counts, int n_blocks, int E, int64_t n_rows, int tile_m,
-    const int64_t *counts_in, int32_t *block_base, int64_t *seg, int2 *tiles,
+    const int32_t *block_counts, const int32_t *block_err, int n_blocks, int E, int64_t n_rows,
+    int tile_m, const int64_t *counts_in, int32_t *block_base, int64_t *seg, int2 *tiles,
     int32_t *num_tiles, int2 *tiles2, int32_t *num_tiles2, int2 *tiles2m, int32_t *num_tiles2m,
     int2 *tilesr, int32_t *num_tilesr, int32_t *err_counter, int64_t *counts_out,
     int64_t *starts_out, int32_t *offsets_out) {
   __shared__ int64_t scan_tmp[32];
   __shared__ int32_t part[1024];     // [group][expert] block-range counts (E <= 1024)
   __shared__ int64_t start_s[1024];  // expert starts (E <= 1024)
+  __shared__ int32_t n_err;
   const int t = threadIdx.x;
+  if (t == 0) n_err = 0;
+  __syncthreads();
+  if (block_err) {
+    int32_t c = 0;
+    for (int b = t; b < n_blocks; b += blockDim.x) c += block_err[b];
+    if (c) atomicAdd(&n_err, c);
+  }
   const int ept = (E + 1023) / 1024;
   const bool small = E <= 1024;
   const int G = counts_in || !small ? 1 : max(1, min(16, 1024 / E));
@@ -117,7 +130,7 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(
       if (counts_in) {
         count[c] = counts_in[e];
         if (count[c] < 0 || count[c] > n_rows) {
-          atomicAdd(err_counter, 1);
+          atomicAdd(&n_err, 1);
           count[c] = count[c] < 0 ? 0 : n_rows;
         }
       } else if (G > 1) {
@@ -137,7 +150,7 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(
       if (seg_hi[c] > n_rows) seg_hi[c] = n_rows;
     }
   }
-  if (counts_in && t == 0 && carry != n_rows) atomicAdd(err_counter, 1);
+  if (counts_in && t == 0 && carry != n_rows) atomicAdd(&n_err, 1);
   if (small && t < E) start_s[t] = start[0];
   __syncthreads();
   if (gact) {
@@ -202,6 +215,8 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(
       *num = static_cast<int32_t>(tcarry);
     }
   }
+  __syncthreads();
+  if (t == 0) *err_counter = n_err;
 }
 
 template <int SCORE_DTYPE>
@@ -265,11 +280,6 @@ __global__ __launch_bounds__(256) void plan_scatter_kernel(
 
 constexpr int kPlanMaxEpt = kPlanMaxExperts / 1024;
 
-__global__ void zero_i32_kernel(int32_t *p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
-}
-
 }  // namespace
 
 int slots_per_plan_block(int num_experts, int64_t rows) {
@@ -312,6 +322,8 @@ PlanLayout plan_layout(int64_t num_rows, int num_experts) {
   off = align_up(off + sizeof(int32_t) * num_rows, 256);
   L.off_row_slot = off;
   off = align_up(off + sizeof(int32_t) * num_rows, 256);
+  L.off_block_err = off;
+  off = align_up(off + sizeof(int32_t) * L.blocks, 256);
   L.bytes = off;
   return L;
 }
@@ -333,6 +345,7 @@ PlanView plan_view(void *ws, const PlanLayout &L) {
   v.tilesr = reinterpret_cast<int2 *>(b + L.off_tilesr);
   v.row_token = reinterpret_cast<int32_t *>(b + L.off_row_token);
   v.row_slot = reinterpret_cast<int32_t *>(b + L.off_row_slot);
+  v.block_err = reinterpret_cast<int32_t *>(b + L.off_block_err);
   return v;
 }
 
@@ -343,14 +356,15 @@ int build_plan(const int64_t *top_idx, const void *top_scores, int score_dtype,
   const int64_t R = num_tokens * top_k;
   const PlanLayout L = plan_layout(R, num_experts);
   const PlanView v = plan_view(workspace, L);
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, v.err, 5);
   if (L.blocks > 0) {
     const size_t lds = sizeof(uint32_t) * num_experts * (L.slots_per_block / 32);
     hipLaunchKernelGGL(plan_count_kernel, dim3(L.blocks), dim3(256), lds, s, top_idx, R,
-                       num_experts, L.slots_per_block, v.block_counts, v.err);
+                       num_experts, L.slots_per_block, v.block_counts, v.block_err);
   }
   hipLaunchKernelGGL(num_experts <= 1024 ? plan_scan_kernel<1> : plan_scan_kernel<kPlanMaxEpt>,
-                     dim3(1), dim3(1024), 0, s, v.block_counts, L.blocks, num_experts, R,
+                     dim3(1), dim3(1024), 0, s, v.block_counts,
+                     L.blocks > 0 ? v.block_err : static_cast<int32_t *>(nullptr), L.blocks,
+                     num_experts, R,
                      kPlanTileM, static_cast<const int64_t *>(nullptr), v.block_base, v.seg,
                      v.tiles, v.num_tiles, v.tiles2, v.num_tiles2, v.tiles2m, v.num_tiles2m,
                      v.tilesr, v.num_tilesr, v.err, counts, starts, offsets);
@@ -377,10 +391,10 @@ int plan_from_counts(const int64_t *counts, int64_t num_rows, int num_experts, v
                      hipStream_t s) {
   const PlanLayout L = plan_layout(num_rows, num_experts);
   const PlanView v = plan_view(workspace, L);
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, v.err, 5);
   hipLaunchKernelGGL(num_experts <= 1024 ? plan_scan_kernel<1> : plan_scan_kernel<kPlanMaxEpt>,
                      dim3(1), dim3(1024), 0, s,
-                     static_cast<const int32_t *>(nullptr), 0, num_experts, num_rows,
+                     static_cast<const int32_t *>(nullptr), static_cast<const int32_t *>(nullptr),
+                     0, num_experts, num_rows,
                      kPlanTileM, counts, static_cast<int32_t *>(nullptr), v.seg, v.tiles,
                      v.num_tiles, v.tiles2, v.num_tiles2, v.tiles2m, v.num_tiles2m, v.tilesr,
                      v.num_tilesr, v.err, static_cast<int64_t *>(nullptr),
