@@ -775,7 +775,7 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
       const int r = wid * RPW + it * 4 + (lane >> 4);
       const u32x4 v = *reinterpret_cast<const u32x4 *>(h_stage(r) + ((c ^ (r & 15)) << 4));
       if (row0 + r < row_end && col < p.N)
-        *reinterpret_cast<u32x4 *>(p.out + (row0 + r) * p.ldo + col) = v;
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(p.out + (row0 + r) * p.ldo + col));
     }
   } else if (EPI == EPI_SWIGLU) {
     const uint32_t ld2 = static_cast<uint32_t>(p.ldo) * 2u, n2 = static_cast<uint32_t>(p.N) * 2u;
@@ -849,6 +849,21 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
     uint8_t *stg = (wid < 4 ? sB0 : sB1) + (wid & 3) * WSB;
     const int c = lane % CH;
     const int64_t col = static_cast<int64_t>(nt) * T::BN + wn * T::WN + c * 8;
+    // Output row of each of the lane's stores (-1: past the segment end),
+    // read through the row map before any store: as far as the compiler
+    // knows a store may alias the map, so a map load between stores would
+    // wait for every store before it to complete.
+    constexpr int NIT = 32 / RPI;
+    int32_t orow[T::MB][NIT];
+#pragma unroll
+    for (int mb = 0; mb < T::MB; ++mb)
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int64_t rr = row0 + wm * T::WM + mb * 32 + it * RPI + lane / CH;
+        const int64_t rc = min(rr, row_end - 1);
+        const int32_t o = p.out_row ? p.out_row[rc] : static_cast<int32_t>(rc);
+        orow[mb][it] = rr < row_end ? o : -1;
+      }
 #pragma unroll
     for (int mb = 0; mb < T::MB; ++mb) {
 #pragma unroll
@@ -873,14 +888,11 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-      for (int it = 0; it < 32 / RPI; ++it) {
+      for (int it = 0; it < NIT; ++it) {
         const int r = it * RPI + lane / CH;
         const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + r * (T::WN * 2) + ((c ^ (r & (CH - 1))) << 4));
-        const int64_t rr = row0 + wm * T::WM + mb * 32 + r;
-        if (rr < row_end && col < p.N) {
-          const int64_t o = p.out_row ? static_cast<int64_t>(p.out_row[rr]) : rr;
-          *reinterpret_cast<u32x4 *>(p.out + o * p.ldo + col) = v;
-        }
+        if (orow[mb][it] >= 0 && col < p.N)
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(p.out + static_cast<int64_t>(orow[mb][it]) * p.ldo + col));
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
