@@ -562,6 +562,17 @@ int mx_moe_for_loop(const void *tokens_sorted, const int64_t *counts, int64_t nu
                     void *stream);
 
 /*
+ * mx_moe_for_loop with the expert activation `act` (MX_ACT_SILU or
+ * MX_ACT_SWIGLU7, the MAGI-2 swiglu7 of grouped_moe.py:287-306): run_for_loop
+ * of a module whose spec names either activation (experts.py:1656-1747).
+ */
+int mx_moe_for_loop_act(const void *tokens_sorted, const int64_t *counts, int64_t num_rows,
+                        int num_experts, int64_t hidden, int64_t ffn, int act,
+                        const mx_weight *w1, const mx_weight *w3, const mx_weight *w2,
+                        const mx_lora *l1, const mx_lora *l3, const mx_lora *l2, void *out,
+                        void *workspace, void *stream);
+
+/*
  * One grouped projection over expert-sorted rows: out[i] = x[i] W_e^T (+LoRA)
  * for the expert e owning row i (segments from `counts`). Replaces
  * CompressedGroupedExperts.grouped_linear (experts.py:803-827) and the

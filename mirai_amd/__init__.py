@@ -16,7 +16,15 @@ from ._native import RouteIndexError, check_route_errors, set_route_check
 from .chunking import MoETokenChunkPolicy, fused_chunk_runner
 from .experts import CompressedGroupedExperts
 from .lora import ActiveExpertLoRA, lora_scale
-from .magi2 import Magi2FusedMoEBackend, Magi2GroupedExperts, route_topk_heads
+from .magi2 import (
+    Magi2FusedMoEBackend,
+    Magi2GroupedExperts,
+    Magi2PackedExpertStateError,
+    Magi2QuantizedExpertError,
+    load_magi2_packed_state,
+    route_topk_heads,
+    save_magi2_packed_state,
+)
 from .router import FusedRouter, fused_router_forward, router_weight_planes
 from .routing import route_topk
 from .specs import (
@@ -37,6 +45,8 @@ __all__ = [
     "ExpertProjectionRole",
     "Magi2FusedMoEBackend",
     "Magi2GroupedExperts",
+    "Magi2PackedExpertStateError",
+    "Magi2QuantizedExpertError",
     "MoETokenChunkPolicy",
     "as_execution_spec",
     "build_dispatch_plan",
@@ -45,10 +55,12 @@ __all__ = [
     "combine_routed_tokens",
     "fused_chunk_runner",
     "fused_router_forward",
+    "load_magi2_packed_state",
     "lora_scale",
     "permute_routed_tokens",
     "route_topk",
     "route_topk_heads",
     "router_weight_planes",
+    "save_magi2_packed_state",
     "set_route_check",
 ]

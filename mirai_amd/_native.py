@@ -150,6 +150,9 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
          _L, _P, c_int, _P]),
     "mx_moe_for_loop": (
         c_int, [_P, _P, c_int64, c_int, c_int64, c_int64, _W, _W, _W, _L, _L, _L, _P, _P, _P]),
+    "mx_moe_for_loop_act": (
+        c_int, [_P, _P, c_int64, c_int, c_int64, c_int64, c_int, _W, _W, _W, _L, _L, _L, _P, _P,
+                _P]),
     "mx_grouped_linear": (c_int, [_P, _P, c_int64, c_int, _W, _L, _P, _P, _P]),
     "mx_moe_backward_workspace_size": (c_size_t,
                                        [c_int64, c_int, c_int, c_int64, c_int64, c_int]),

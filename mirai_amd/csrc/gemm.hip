@@ -2014,15 +2014,19 @@ extern "C" int mx_set_stage_events(void **events, int count) {
   return MX_OK;
 }
 
-extern "C" int mx_moe_for_loop(const void *tokens_sorted, const int64_t *counts, int64_t num_rows,
-                               int num_experts, int64_t hidden, int64_t ffn, const mx_weight *w1,
-                               const mx_weight *w3, const mx_weight *w2, const mx_lora *l1,
-                               const mx_lora *l3, const mx_lora *l2, void *out, void *workspace,
-                               void *stream) {
+extern "C" int mx_moe_for_loop_act(const void *tokens_sorted, const int64_t *counts,
+                                   int64_t num_rows, int num_experts, int64_t hidden, int64_t ffn,
+                                   int act, const mx_weight *w1, const mx_weight *w3,
+                                   const mx_weight *w2, const mx_lora *l1, const mx_lora *l3,
+                                   const mx_lora *l2, void *out, void *workspace, void *stream) {
   clear_error();
   const char *name = "mx_moe_for_loop";
   int rc = validate_plan_args(name, num_rows, 1, num_experts);
   if (rc) return rc;
+  if (act != MX_ACT_SILU && act != MX_ACT_SWIGLU7) {
+    set_error("%s: unknown activation %d", name, act);
+    return MX_ERR_INVALID;
+  }
   if ((rc = check_layer(name, hidden, ffn, w1, w3, w2, l1, l3, l2))) return rc;
   if (w1->format == MX_FMT_F32X3) {
     set_error("%s: MX_FMT_F32X3 (fp32) weights are supported by mx_moe_forward only", name);
@@ -2040,10 +2044,19 @@ extern "C" int mx_moe_for_loop(const void *tokens_sorted, const int64_t *counts,
   const PlanView v = plan_view(ws, L.plan);
   if ((rc = plan_from_counts(counts, num_rows, num_experts, ws, s))) return rc;
   return expert_mlp(L.plan, v, num_experts, static_cast<const uint16_t *>(tokens_sorted), hidden,
-                    nullptr, hidden, ffn, MX_ACT_SILU, w1, w3, w2, l1, l3, l2,
+                    nullptr, hidden, ffn, act, w1, w3, w2, l1, l3, l2,
                     reinterpret_cast<uint16_t *>(ws + L.off_lora), lrc,
                     reinterpret_cast<uint16_t *>(ws + L.off_h), nullptr, nullptr,
                     static_cast<uint16_t *>(out), hidden, nullptr, s);
+}
+
+extern "C" int mx_moe_for_loop(const void *tokens_sorted, const int64_t *counts, int64_t num_rows,
+                               int num_experts, int64_t hidden, int64_t ffn, const mx_weight *w1,
+                               const mx_weight *w3, const mx_weight *w2, const mx_lora *l1,
+                               const mx_lora *l3, const mx_lora *l2, void *out, void *workspace,
+                               void *stream) {
+  return mx_moe_for_loop_act(tokens_sorted, counts, num_rows, num_experts, hidden, ffn,
+                             MX_ACT_SILU, w1, w3, w2, l1, l3, l2, out, workspace, stream);
 }
 
 extern "C" int mx_grouped_linear(const void *x, const int64_t *counts, int64_t num_rows,

@@ -222,6 +222,36 @@ class CompressedGroupedExperts(nn.Module):
                                  offset=state[base + "_offset"], code=state[base + "_code"],
                                  nested_code=state[base + "_ncode"], shape=shape)
 
+    def packed_buffer_names(self, key: str) -> tuple[str, ...]:
+        """Names of the buffers that hold expert tensor ``key`` in this format."""
+        data_suffix, scale_suffix = _BUFFER_SUFFIXES[self._quant_format]
+        return (f"{key}{data_suffix}",) + ((f"{key}{scale_suffix}",) if scale_suffix else ())
+
+    def adopt_packed(self, key: str, buffers: dict, shape: tuple[int, int, int]) -> None:
+        """Install an already packed [E, out, in] projection (the buffers named by
+        ``packed_buffer_names``), checking each tensor against the layout this
+        format's quantiser produces; nothing is re-quantised."""
+        if key not in self._spec.tensor_names:
+            raise ValueError(f"Unknown compressed_weights grouped expert tensor '{key}'.")
+        shape = tuple(int(v) for v in shape)
+        if len(shape) != 3 or shape[0] != self.num_experts:
+            raise ValueError(f"packed expert tensor {key} must be [{self.num_experts}, out, in], "
+                             f"got {shape}.")
+        names = self.packed_buffer_names(key)
+        layouts = quant.packed_layout(self._quant_format, shape)
+        for name, layout in zip(names, layouts):
+            value = buffers.get(name)
+            if not isinstance(value, torch.Tensor):
+                raise ValueError(f"packed expert tensor {key} lacks buffer '{name}'.")
+            dtypes, want = layout
+            if value.dtype not in dtypes or tuple(value.shape) != want:
+                raise ValueError(f"buffer '{name}' is {value.dtype} {tuple(value.shape)}, "
+                                 f"expected one of {dtypes} {want}.")
+        for name in names:
+            self._set_buffer(name, buffers[name].contiguous())
+        self._shapes[key] = shape
+        self._loaded_dense_keys.add(key)
+
     def packed_weight(self, key: str) -> quant.PackedWeight:
         if key not in self._loaded_dense_keys:
             raise RuntimeError(f"compressed_weights grouped experts are missing weight '{key}'.")

@@ -403,8 +403,6 @@ def sorted_experts(module, tokens, counts):
     c = counts.detach().to(device=device, dtype=torch.int64).contiguous()
     if int(c.numel()) != module.num_experts:
         raise ValueError("counts must hold one entry per expert.")
-    if kernel_activation(module) != nat.ACT_SILU:
-        raise NotImplementedError("run_for_loop implements the SwiGLU expert MLP only.")
     S, d = (int(v) for v in x.shape)
     (w1, w3, w2), packed = _weight_descriptors(module, device)
     f = int(packed[0].shape[1])
@@ -413,8 +411,9 @@ def sorted_experts(module, tokens, counts):
     lib = nat.load_library()
     ws = nat.workspace(lib.mx_moe_workspace_size(S, 1, module.num_experts, d, f,
                                                  lora_rank(module)), device)
-    nat.call("mx_moe_for_loop", x.data_ptr(), c.data_ptr(), S, module.num_experts, d, f, w1, w3,
-             w2, lora[0], lora[1], lora[2], out.data_ptr(), ws.data_ptr(), nat.stream(device))
+    nat.call("mx_moe_for_loop_act", x.data_ptr(), c.data_ptr(), S, module.num_experts, d, f,
+             kernel_activation(module), w1, w3, w2, lora[0], lora[1], lora[2], out.data_ptr(),
+             ws.data_ptr(), nat.stream(device))
     del keep
     nat.watch_plan_errors(ws, device, "a run_for_loop call")
     return out.to(tokens.dtype)

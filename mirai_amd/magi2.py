@@ -24,11 +24,28 @@ import torch.nn as nn
 
 from . import _native as nat
 from .experts import CompressedGroupedExperts
+from .quant import NF4_BLOCKSIZE
 from .specs import MAGI2_EXPERT_MLP_SPEC
 
 MAGI2_ROUTED_EXPERT_TENSOR_NAMES = ("W_gate", "W_up", "W_down")
 SCORE_FUNCS = {"softmax": nat.SCORE_SOFTMAX, "sigmoid": nat.SCORE_SIGMOID}
 _LAYOUTS = {"heads": nat.ROUTE_LAYOUT_HEADS, "rows": nat.ROUTE_LAYOUT_ROWS}
+
+
+class Magi2QuantizedExpertError(ValueError):
+    """Raised when quantized MAGI-2 expert storage cannot be built, persisted or
+    restored (quantized_experts.py:63-64)."""
+
+
+def _dtype_name(dtype: torch.dtype) -> str:
+    return str(dtype).removeprefix("torch.")
+
+
+def _parse_dtype(value: object) -> torch.dtype:
+    dtype = getattr(torch, str(value), None)
+    if not isinstance(dtype, torch.dtype):
+        raise Magi2QuantizedExpertError(f"Packed MAGI-2 store declares unknown dtype '{value}'.")
+    return dtype
 
 
 def route_topk_heads(router_logits: torch.Tensor, top_k: int, *, score_func: str = "sigmoid",
@@ -108,9 +125,109 @@ class Magi2GroupedExperts(nn.Module):
             expert_dequant_chunk_size=expert_dequant_chunk_size,
             execution_spec=MAGI2_EXPERT_MLP_SPEC)
 
+        # The reference layer's [G, in, out] shape and dtype of every loaded tensor.
+        self._source_shapes: dict[str, tuple[int, int, int]] = {}
+        self._source_dtypes: dict[str, torch.dtype] = {}
+
     @property
     def num_groups(self) -> int:
         return self.num_heads * self.num_experts
+
+    @property
+    def blocksize(self) -> int:
+        """NF4 block size of the stored codes (one absmax per 64 inputs)."""
+        return NF4_BLOCKSIZE
+
+    def expert_weight_shape(self, key: str) -> tuple[int, int, int]:
+        """The reference layer's shape of ``key`` ([G, in, out])."""
+        if key not in self._source_shapes:
+            raise Magi2QuantizedExpertError(f"MAGI-2 NF4 expert tensor '{key}' has not been quantized.")
+        return self._source_shapes[key]
+
+    def expert_weight_dtype(self, key: str) -> torch.dtype:
+        if key not in self._source_dtypes:
+            raise Magi2QuantizedExpertError(f"MAGI-2 NF4 expert tensor '{key}' has not been quantized.")
+        return self._source_dtypes[key]
+
+    def packed_buffers(self) -> dict[str, torch.Tensor]:
+        """The packed payload of the loaded tensors, by buffer name."""
+        out = {}
+        for key in MAGI2_ROUTED_EXPERT_TENSOR_NAMES:
+            if key in self._source_shapes:
+                for name in self.experts.packed_buffer_names(key):
+                    out[name] = getattr(self.experts, name)
+        return out
+
+    def payload_bytes(self) -> int:
+        return int(sum(t.numel() * t.element_size() for t in self.packed_buffers().values()))
+
+    def quantized_numel(self) -> int:
+        return int(sum(g * a * b for g, a, b in self._source_shapes.values()))
+
+    def packed_state_descriptor(self) -> dict[str, object]:
+        """Metadata that restores this exact payload (quantized_experts.py:140-163):
+        group count, block size, the reference shapes and dtypes of the three
+        tensors, the storage format and the buffer inventory. The payload is this
+        build's packed layout ([G, out, in] codes or int8 values and their scales),
+        restored as stored, never through dense weights."""
+        if not self.is_fully_loaded():
+            raise Magi2QuantizedExpertError(
+                "MAGI-2 NF4 store must be complete before it can be persisted.")
+        fmt = self.experts.quant_format
+        meta: dict[str, object] = {"format": fmt, "blocksize": NF4_BLOCKSIZE}
+        if fmt == "nf4":
+            scale = getattr(self.experts, self.experts.packed_buffer_names("W_gate")[1])
+            meta["absmax_dtype"] = _dtype_name(scale.dtype)
+        return {
+            "num_groups": self.num_groups,
+            "blocksize": NF4_BLOCKSIZE,
+            "expert_shapes": {k: list(self._source_shapes[k]) for k in MAGI2_ROUTED_EXPERT_TENSOR_NAMES},
+            "expert_dtypes": {k: _dtype_name(self._source_dtypes[k])
+                              for k in MAGI2_ROUTED_EXPERT_TENSOR_NAMES},
+            "packed_meta": meta,
+            "buffers": sorted(self.packed_buffers()),
+        }
+
+    def restore_packed_state(self, *, descriptor: dict[str, object],
+                             buffers: dict[str, torch.Tensor]) -> None:
+        """Restore a validated persisted payload without dense reconstruction
+        (quantized_experts.py:165-219)."""
+        if int(descriptor.get("num_groups", -1)) != self.num_groups:
+            raise Magi2QuantizedExpertError("Packed MAGI-2 store has incompatible groups.")
+        if int(descriptor.get("blocksize", -1)) != NF4_BLOCKSIZE:
+            raise Magi2QuantizedExpertError("Packed MAGI-2 store has incompatible NF4 blocksize.")
+        shapes, dtypes = descriptor.get("expert_shapes"), descriptor.get("expert_dtypes")
+        if not isinstance(shapes, dict) or not isinstance(dtypes, dict):
+            raise Magi2QuantizedExpertError("Packed MAGI-2 store has incomplete tensor metadata.")
+        names = set(MAGI2_ROUTED_EXPERT_TENSOR_NAMES)
+        if set(shapes) != names or set(dtypes) != names:
+            raise Magi2QuantizedExpertError("Packed MAGI-2 store has incomplete expert metadata.")
+        meta = descriptor.get("packed_meta")
+        if not isinstance(meta, dict):
+            raise Magi2QuantizedExpertError("Packed MAGI-2 store has no NF4 metadata.")
+        if str(meta.get("format")) != self.experts.quant_format:
+            raise Magi2QuantizedExpertError(
+                f"Packed MAGI-2 store holds '{meta.get('format')}' weights, this module "
+                f"stores '{self.experts.quant_format}'.")
+        parsed_dtypes = {k: _parse_dtype(dtypes[k]) for k in names}
+        parsed_shapes = {}
+        for k in names:
+            shape = tuple(int(v) for v in shapes[k])
+            if len(shape) != 3 or shape[0] != self.num_groups:
+                raise Magi2QuantizedExpertError(
+                    f"Packed MAGI-2 store gives {k} the shape {shape}.")
+            parsed_shapes[k] = shape
+        if set(descriptor.get("buffers", [])) != set(buffers):
+            raise Magi2QuantizedExpertError(
+                "Packed MAGI-2 store buffer inventory does not match its descriptor.")
+        for key in MAGI2_ROUTED_EXPERT_TENSOR_NAMES:
+            g, rows, cols = parsed_shapes[key]
+            try:
+                self.experts.adopt_packed(key, buffers, (g, cols, rows))
+            except ValueError as err:
+                raise Magi2QuantizedExpertError(f"Packed MAGI-2 store: {err}") from err
+            self._source_shapes[key] = parsed_shapes[key]
+            self._source_dtypes[key] = parsed_dtypes[key]
 
     @classmethod
     def from_dense(cls, W_gate: torch.Tensor, W_up: torch.Tensor, W_down: torch.Tensor, *,
@@ -132,6 +249,8 @@ class Magi2GroupedExperts(nn.Module):
                 f"MAGI-2 tensor {key} must be [{self.num_groups}, in, out], got "
                 f"{tuple(source.shape)}.")
         self.experts.load_dense_weight(key, source.detach().transpose(1, 2).contiguous())
+        self._source_shapes[key] = tuple(int(v) for v in source.shape)
+        self._source_dtypes[key] = source.dtype
 
     def attach_expert_lora(self, *, tensor_name: str, adapter_name: str, rank: int,
                            alpha: float, init: str = "kaiming", use_rslora: bool = False):
@@ -174,6 +293,108 @@ class Magi2GroupedExperts(nn.Module):
                                              expert_bias=expert_bias, route_norm=route_norm,
                                              route_scale=route_scale, layout="rows")
         return self.run_rows(x_heads.reshape(S * H, d), probs, groups).view(S, H, d)
+
+
+MAGI2_PACKED_SCHEMA = "mirai_amd.magi2.packed_experts"
+MAGI2_PACKED_SCHEMA_VERSION = 1
+_MANIFEST = "manifest.json"
+
+
+class Magi2PackedExpertStateError(ValueError):
+    """Raised when a packed MAGI-2 expert artifact is incompatible
+    (packed_experts.py:24-25)."""
+
+
+def _magi2_layers(model) -> dict[str, Magi2GroupedExperts]:
+    if isinstance(model, dict):
+        return dict(model)
+    if isinstance(model, Magi2GroupedExperts):
+        return {"": model}
+    return {name: m for name, m in model.named_modules() if isinstance(m, Magi2GroupedExperts)}
+
+
+def save_magi2_packed_state(path, model, *, metadata: dict | None = None):
+    """Write every layer's packed payload (one safetensors shard per layer) and a
+    versioned manifest holding each layer's descriptor, with no dense
+    reconstruction (save_magi2_nf4_packed_state, packed_experts.py:28-78).
+    ``model``: a module holding Magi2GroupedExperts layers, one such layer, or a
+    {name: layer} mapping."""
+    import json
+    from pathlib import Path
+
+    from safetensors.torch import save_file
+
+    target = Path(path).expanduser()
+    if target.exists() and any(target.iterdir()):
+        raise FileExistsError(f"Packed MAGI-2 export directory must be empty: {target}")
+    target.mkdir(parents=True, exist_ok=True)
+    layers = {}
+    for index, (name, layer) in enumerate(_magi2_layers(model).items()):
+        if not layer.is_fully_loaded():
+            raise Magi2PackedExpertStateError(
+                f"MAGI-2 layer '{name}' has no complete packed expert store.")
+        descriptor = layer.packed_state_descriptor()
+        shard = f"layer_{index:03d}.safetensors"
+        save_file({k: v.detach().cpu().contiguous() for k, v in layer.packed_buffers().items()},
+                  str(target / shard))
+        layers[name] = {"shard": shard, **descriptor}
+    if not layers:
+        raise Magi2PackedExpertStateError("MAGI-2 packed expert export matched no routed-expert layers.")
+    manifest = {"schema": MAGI2_PACKED_SCHEMA, "schema_version": MAGI2_PACKED_SCHEMA_VERSION,
+                "layers": layers, "metadata": dict(metadata or {})}
+    (target / _MANIFEST).write_text(json.dumps(manifest, indent=2, sort_keys=True), encoding="utf-8")
+    return target
+
+
+def load_magi2_packed_state(path, model, *, expected_metadata: dict | None = None,
+                            device=None) -> dict[str, Magi2GroupedExperts]:
+    """Restore every layer's payload from ``save_magi2_packed_state`` output,
+    rejecting schema, lineage, layer-inventory and buffer mismatches
+    (load_magi2_nf4_packed_state, packed_experts.py:81-183). Tensors land on
+    ``device`` (default: the current GPU)."""
+    import json
+    from pathlib import Path
+
+    from safetensors import safe_open
+
+    source = Path(path).expanduser()
+    if not source.is_dir():
+        raise FileNotFoundError(f"Packed MAGI-2 expert state not found: {source}")
+    layers = _magi2_layers(model)
+    manifest_path = source / _MANIFEST
+    if not manifest_path.is_file():
+        raise Magi2PackedExpertStateError("Packed MAGI-2 expert state has no versioned manifest.")
+    manifest = json.loads(manifest_path.read_text(encoding="utf-8"))
+    if manifest.get("schema") != MAGI2_PACKED_SCHEMA or int(
+            manifest.get("schema_version", -1)) != MAGI2_PACKED_SCHEMA_VERSION:
+        raise Magi2PackedExpertStateError(
+            "Packed MAGI-2 expert state has an unsupported schema or version.")
+    lineage = manifest.get("metadata")
+    if not isinstance(lineage, dict):
+        raise Magi2PackedExpertStateError("Packed MAGI-2 expert state has invalid lineage metadata.")
+    for key, value in (expected_metadata or {}).items():
+        if str(lineage.get(key, "")) != str(value):
+            raise Magi2PackedExpertStateError(f"Packed MAGI-2 expert state has incompatible {key}.")
+    specs = manifest.get("layers")
+    if not isinstance(specs, dict) or set(specs) != set(layers):
+        raise Magi2PackedExpertStateError(
+            "Packed MAGI-2 expert layer inventory does not match the model.")
+    target = torch.device(device) if device is not None else torch.device("cuda")
+    for name, layer in layers.items():
+        spec = specs[name]
+        shard = str(spec.get("shard", ""))
+        if not shard or Path(shard).name != shard:
+            raise Magi2PackedExpertStateError(f"Packed MAGI-2 layer '{name}' has an invalid shard path.")
+        shard_path = source / shard
+        if not shard_path.is_file():
+            raise Magi2PackedExpertStateError(f"Packed MAGI-2 layer '{name}' is missing shard '{shard}'.")
+        with safe_open(str(shard_path), framework="pt", device="cpu") as handle:
+            if set(handle.keys()) != set(spec.get("buffers", [])):
+                raise Magi2PackedExpertStateError(
+                    f"Packed MAGI-2 layer '{name}' shard inventory is invalid.")
+            buffers = {k: handle.get_tensor(k).to(target).contiguous() for k in handle.keys()}
+        layer.restore_packed_state(descriptor=spec, buffers=buffers)
+    return layers
 
 
 class Magi2FusedMoEBackend:

@@ -109,6 +109,22 @@ def quantize(source: torch.Tensor, fmt: str) -> PackedWeight:
     return PackedWeight("int8", q, scale, (E, out_f, in_f))
 
 
+def packed_layout(fmt: str, shape: tuple[int, int, int]) -> tuple[tuple, tuple | None]:
+    """(dtypes, shape) of the data and scale tensors ``quantize`` produces for an
+    [E, out, in] projection in ``fmt`` (NF4 absmax: bf16, or fp32 for ingested
+    bitsandbytes payloads)."""
+    E, out_f, in_f = (int(v) for v in shape)
+    fmt = normalize_quant_format(fmt)
+    if fmt == "nf4":
+        return (((torch.uint8,), (E, out_f, in_f // 2)),
+                ((torch.bfloat16, torch.float32), (E, out_f, in_f // NF4_BLOCKSIZE)))
+    if fmt == "int8":
+        return ((torch.int8,), (E, out_f, in_f)), ((torch.bfloat16,), (E, out_f))
+    if fmt == "fp32":
+        return ((torch.bfloat16,), (E, out_f, 3 * in_f)), None
+    return ((torch.bfloat16,), (E, out_f, in_f)), None
+
+
 def dequantize(packed: PackedWeight, *, dtype: torch.dtype = torch.bfloat16,
                experts: slice | None = None) -> torch.Tensor:
     """Dense weights (bit-exact codec output) of all or a slice of experts."""

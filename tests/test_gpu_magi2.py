@@ -109,6 +109,49 @@ def test_reduced_magi2_layer_matches_oracle(fmt):
     assert torch.equal(out2, out)
 
 
+def test_run_for_loop_with_swiglu7_matches_oracle():
+    # run_for_loop over rows already grouped by (head, expert) with the MAGI-2
+    # swiglu7 activation (experts.py:1656-1747): the routed layer with one
+    # unit-score route per row.
+    H, E = 2, 4
+    dense, x, _, _, _, _ = _magi2_case(H=H, E=E, seed=5)
+    S, d = int(x.shape[0]), int(x.shape[2])
+    g = torch.Generator().manual_seed(6)
+    idx = torch.randint(0, E, (H, S, 1), generator=g)
+    probs = torch.ones(H, S, 1)
+    m = Magi2GroupedExperts.from_dense(*(dense[k].cuda() for k in ("W_gate", "W_up", "W_down")),
+                                       num_heads=H, quant_format="nf4")
+    groups = (idx[:, :, 0] + torch.arange(H).view(H, 1) * E).t().reshape(-1)  # row s*H+h
+    order = torch.argsort(groups, stable=True)
+    counts = torch.bincount(groups, minlength=H * E)
+    rows = x.reshape(S * H, d)[order]
+    with torch.no_grad():
+        out = m.experts.run_for_loop(rows.cuda(), counts.cuda())
+    ref = om.layer_forward(x, probs, idx, _oracle_weights("nf4", dense), E).reshape(S * H, d)
+    print(f"magi2 for-loop: {assert_layer_close(out.cpu(), ref[order])}")
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "int8"])
+def test_packed_state_restores_the_exact_layer(fmt, tmp_path):
+    # Persist the quantised payload (descriptor + safetensors shard), restore it
+    # into a fresh module with no dense weights, and run both: the restored layer
+    # computes bit-identical outputs (quantized_experts.py:140-219,
+    # packed_experts.py:28-183).
+    from mirai_amd import load_magi2_packed_state, save_magi2_packed_state
+
+    dense, x, _, _, probs, idx = _magi2_case(seed=11)
+    m = Magi2GroupedExperts.from_dense(*(dense[k].cuda() for k in ("W_gate", "W_up", "W_down")),
+                                       num_heads=2, quant_format=fmt)
+    path = save_magi2_packed_state(tmp_path / "packed", {"layer": m}, metadata={"seed": "11"})
+    fresh = Magi2GroupedExperts(num_heads=2, num_experts=4, quant_format=fmt)
+    load_magi2_packed_state(path, {"layer": fresh}, expected_metadata={"seed": "11"})
+    assert fresh.packed_state_descriptor() == m.packed_state_descriptor()
+    with torch.no_grad():
+        out = m.execute(x.cuda(), probs.cuda(), idx.cuda())
+        out2 = fresh.execute(x.cuda(), probs.cuda(), idx.cuda())
+    assert torch.equal(out2, out)
+
+
 def test_magi2_layer_at_production_group_count():
     # 12 heads x 256 experts = 3072 groups in one pass (no segmenting).
     dense, x, _, _, probs, idx = _magi2_case(H=12, E=256, d=64, f=64, S=96, k=2, seed=3)
