@@ -395,6 +395,19 @@ def expert_choice_experts(module, tokens, expert_token_scores, expert_token_indi
 def sorted_experts(module, tokens, counts):
     """Expert MLP over expert-grouped rows (forward kernels; run_for_loop)."""
     device = nat.require_gpu(tokens)
+    if module.quant_format == "fp32":
+        # The fp32 layer is the split-precision routed layer: a pre-grouped row
+        # is a route of k = 1 to its own expert with a unit score, whose fp32
+        # combine returns the expert output unchanged.
+        c = counts.detach().to(device=device, dtype=torch.int64)
+        if int(c.numel()) != module.num_experts:
+            raise ValueError("counts must hold one entry per expert.")
+        S = int(tokens.shape[0])
+        idx = torch.repeat_interleave(torch.arange(module.num_experts, device=device), c)
+        if int(idx.numel()) != S:
+            raise ValueError(f"counts sum to {int(idx.numel())}, but {S} rows were given.")
+        ones = torch.ones((S, 1), dtype=torch.float32, device=device)
+        return routed_experts(module, tokens, ones, idx.view(S, 1))
     if torch.is_grad_enabled() and (tokens.requires_grad or any(
             p is not None and p.requires_grad for p in _lora_params(module))):
         from .backward import sorted_experts_autograd

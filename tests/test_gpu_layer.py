@@ -95,10 +95,23 @@ def test_fp32_layer_is_inference_only():
     idx, scores = oroute.route_topk(wl.router_logits(w).numpy(), w.top_k)
     with pytest.raises(NotImplementedError, match="inference-only"):
         m.run_direct_routed(x, torch.from_numpy(scores).cuda(), torch.from_numpy(idx).cuda())
-    counts = torch.bincount(torch.from_numpy(idx).reshape(-1), minlength=w.experts)
-    rows = torch.randn(int(counts.sum()), w.hidden).cuda()
-    with pytest.raises(ValueError, match="mx_moe_forward only"), torch.no_grad():
-        m.run_for_loop(rows, counts.cuda())
+
+
+def test_fp32_run_for_loop_matches_oracle():
+    # run_for_loop of the fp32 layer (experts.py:1656-1747 is dtype-agnostic):
+    # rows grouped by expert, fp32 in and out, against the oracle's fp32 loop.
+    w = small("fp32", dtype=torch.float32, r=8, alpha=16.0, T=300, E=6, k=1, d=192, f=320)
+    dense, lora = wl.dense_weights(w), wl.lora_factors(w)
+    m = build_module(w, dense, lora)
+    counts = torch.tensor([60, 0, 90, 1, 149, 0])
+    x = wl.tokens(w)
+    with torch.no_grad():
+        out = m.run_for_loop(x.cuda(), counts.cuda())
+    assert out.dtype == torch.float32
+    ref = olayer.for_loop_forward(x, counts, oracle_weights(w, dense, dtype=w.dtype),
+                                  oracle_loras(w, lora))
+    stats = assert_layer_close(out.cpu(), ref)
+    assert stats["mean_rel"] < 1e-4, stats
 
 
 def test_c2_full_size_on_token_subset():
