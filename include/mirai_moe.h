@@ -587,7 +587,8 @@ int mx_grouped_linear(const void *x, const int64_t *counts, int64_t num_rows, in
  * Backward of mx_moe_forward (adapter training, frozen base): given
  * grad_out [T, hidden] and the activations saved by the forward, produces
  * grad_tokens [T, hidden] (fp32 accumulation, out_dtype), grad_scores [T, k]
- * fp32, and fp32 LoRA gradients dA/dB for each adapter (NULL if absent).
+ * fp32, and fp32 LoRA gradients dA/dB for each adapter (NULL if absent; all
+ * zero when num_tokens is 0, the gradient of an empty sum).
  * Base weights are re-decoded in-kernel, never materialised. Replaces the
  * autograd of _FrozenDequantBatchedLinear(Pair).backward (linear.py:117-125,
  * 192-203), the LoRA bmm chain (active_expert_lora.py:434-477) and

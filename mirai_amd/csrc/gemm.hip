@@ -1212,6 +1212,34 @@ LayerLayout layer_layout(int64_t rows, int num_experts, int64_t hidden, int64_t 
 
 bool has_lora(const mx_lora *l) { return l && l->rank > 0; }
 
+__global__ __launch_bounds__(256) void zero_f32_kernel(float *p, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
+    p[i] = 0.0f;
+}
+
+// The LoRA gradients of a backward that sees no routed rows: the gradient of
+// an empty sum, zero in every present buffer (dA [E, r, in], dB [E, out, r]),
+// written here since the weight-gradient kernels never run.
+int zero_lora_grads(const char *name, int64_t experts, int64_t hidden, int64_t ffn,
+                    const mx_lora *l1, const mx_lora *l3, const mx_lora *l2, float *ga1,
+                    float *gb1, float *ga3, float *gb3, float *ga2, float *gb2, hipStream_t s) {
+  auto rank = [](const mx_lora *l) { return has_lora(l) ? static_cast<int64_t>(l->rank) : 0; };
+  const struct {
+    float *p;
+    int64_t n;
+  } bufs[6] = {{ga1, experts * rank(l1) * hidden}, {gb1, experts * ffn * rank(l1)},
+               {ga3, experts * rank(l3) * hidden}, {gb3, experts * ffn * rank(l3)},
+               {ga2, experts * rank(l2) * ffn},    {gb2, experts * hidden * rank(l2)}};
+  for (const auto &b : bufs) {
+    if (!b.p || b.n <= 0) continue;
+    const int64_t blocks = std::min<int64_t>(ceil_div(b.n, 256), 4096);
+    hipLaunchKernelGGL(zero_f32_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, b.p,
+                       b.n);
+  }
+  return check_launch(name);
+}
+
 int lora_width(const mx_lora *a, const mx_lora *b, const mx_lora *c) {
   int r = 0;
   for (const mx_lora *l : {a, b, c})
@@ -1716,7 +1744,9 @@ extern "C" int mx_moe_backward_act(const void *grad_out, int grad_dtype, const v
     set_error("%s: the fp32 (MX_FMT_F32X3) layer is inference-only", name);
     return MX_ERR_INVALID;
   }
-  if (num_tokens == 0) return MX_OK;
+  if (num_tokens == 0)
+    return zero_lora_grads(name, num_experts, hidden, ffn, l1, l3, l2, grad_a1, grad_b1, grad_a3,
+                           grad_b3, grad_a2, grad_b2, as_stream(stream));
   const bool lora1 = has_lora(l1), lora3 = has_lora(l3), lora2 = has_lora(l2);
   if (!grad_out || !tokens || !top_idx || !top_scores || !save_gate || !save_up || !save_h ||
       !save_y || !grad_tokens || !grad_scores || !workspace ||
@@ -2524,7 +2554,9 @@ extern "C" int mx_moe_backward_expert_choice(
   }
   const int64_t T = static_cast<int64_t>(batch) * tokens_per_sample;
   const int64_t slots = static_cast<int64_t>(batch) * logical_experts * capacity;
-  if (T == 0) return MX_OK;
+  if (T == 0)
+    return zero_lora_grads(name, num_experts, hidden, ffn, l1, l3, l2, grad_a1, grad_b1, grad_a3,
+                           grad_b3, grad_a2, grad_b2, as_stream(stream));
   const bool lora = has_lora(l1) || has_lora(l3) || has_lora(l2);
   if (!grad_out || !tokens || !grad_tokens || !workspace ||
       (slots > 0 && (!expert_token_indices || !expert_token_scores || !grad_scores ||
@@ -2579,6 +2611,9 @@ extern "C" int mx_moe_backward_expert_choice(
                        reinterpret_cast<uint16_t *>(ws + L.back.off_dz), fact, grad_a1, grad_b1,
                        grad_a3, grad_b3, grad_a2, grad_b2, s);
     if (rc) return rc;
+  } else if ((rc = zero_lora_grads(name, num_experts, hidden, ffn, l1, l3, l2, grad_a1, grad_b1,
+                                   grad_a3, grad_b3, grad_a2, grad_b2, s))) {
+    return rc;
   }
   // grad_tokens[t] = sum of its slots' dx rows (fp32, ascending (physical,
   // logical) order; zero for tokens no expert picked).

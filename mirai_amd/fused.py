@@ -122,7 +122,8 @@ def _forward(module, tokens, top_scores, top_indices, need_grad, addend=None, ad
              nat.ptr(addend), addend_ready.cuda_event if addend_ready is not None else None,
              *[nat.ptr(t) for t in saves], ws.data_ptr(), nat.stream(device))
     del keep
-    nat.watch_plan_errors(ws, device, "a routed expert layer call")
+    if T > 0:  # a call with no tokens builds no plan (and writes no error count)
+        nat.watch_plan_errors(ws, device, "a routed expert layer call")
     return out.to(tokens.dtype), ((x, scores, idx, *saves) if need_grad else None)
 
 
@@ -428,7 +429,8 @@ def sorted_experts(module, tokens, counts):
              kernel_activation(module), w1, w3, w2, lora[0], lora[1], lora[2], out.data_ptr(),
              ws.data_ptr(), nat.stream(device))
     del keep
-    nat.watch_plan_errors(ws, device, "a run_for_loop call")
+    if S > 0:
+        nat.watch_plan_errors(ws, device, "a run_for_loop call")
     return out.to(tokens.dtype)
 
 
@@ -461,5 +463,6 @@ def grouped_projection(module, key, x, offsets):
     nat.call("mx_grouped_linear", xb.data_ptr(), counts.data_ptr(), S, module.num_experts,
              packed.descriptor(), lora, out.data_ptr(), ws.data_ptr(), nat.stream(device))
     del keep
-    nat.watch_plan_errors(ws, device, "a grouped_linear call")
+    if S > 0:
+        nat.watch_plan_errors(ws, device, "a grouped_linear call")
     return out.to(x.dtype)

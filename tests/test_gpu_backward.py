@@ -232,3 +232,26 @@ def test_c5_full_size_linearity_and_determinism():
         assert torch.equal(g1[name], g1b[name]), f"{name} is not deterministic"
         assert torch.equal(g2[name], 2 * g1[name]), f"{name} is not linear in dY"
         assert torch.isfinite(g1[name]).all(), name
+
+
+def test_empty_batch_forward_and_backward():
+    """Zero tokens (the reference's grouped matmuls over empty tensors): an empty
+    output, empty token / score gradients and all-zero LoRA factor gradients."""
+    w = small("nf4")
+    dense = wl.dense_weights(w)
+    m = build_module(w, dense, wl.lora_factors(w))
+    x = torch.empty(0, w.hidden, dtype=torch.bfloat16)
+    scores = torch.empty(0, w.top_k, dtype=torch.float32)
+    idx = torch.empty(0, w.top_k, dtype=torch.int64)
+    dy = torch.empty(0, w.hidden, dtype=torch.bfloat16)
+    out, grads = _gpu_grads(m, x, scores, idx, dy)
+    assert tuple(out.shape) == (0, w.hidden)
+    assert tuple(grads["tokens"].shape) == (0, w.hidden)
+    assert tuple(grads["scores"].shape) == (0, w.top_k)
+    for key, ad in m.expert_lora.items():
+        for name in ("a", "b"):
+            g = grads[f"{key}.{name}"]
+            if g is not None:
+                assert not bool(g.abs().gt(0).any()), key + "." + name
+    with torch.no_grad():
+        assert tuple(m.run_direct_routed(x.cuda(), scores.cuda(), idx.cuda()).shape) == (0, w.hidden)
