@@ -297,3 +297,30 @@ def test_out_of_range_route_ids_are_reported():
             m.run_direct_routed(x.cuda(), scores.cuda(), bad.cuda())
     finally:
         mirai_amd.set_route_check(previous)
+
+
+def test_empty_inputs_through_every_inference_entry_point():
+    """No rows: each call returns an empty result and leaves no deferred route
+    error behind (the next call with rows checks the plan it builds)."""
+    w = small("nf4", T=64, E=4, k=2, d=128, f=128)
+    dense = wl.dense_weights(w)
+    lora = wl.lora_factors(w)
+    m = build_module(w, dense, lora)
+    d = w.hidden
+    empty = torch.empty(0, d, dtype=torch.bfloat16, device="cuda")
+    with torch.no_grad():
+        assert tuple(m.run_direct_routed(empty, torch.empty(0, 2, device="cuda"),
+                                         torch.empty(0, 2, dtype=torch.int64, device="cuda")).shape) == (0, d)
+        assert tuple(m.run_for_loop(empty, torch.zeros(w.experts, dtype=torch.int64,
+                                                        device="cuda")).shape) == (0, d)
+        ec = m.run_expert_choice_routed(empty, torch.empty(0, w.experts, 4, device="cuda"),
+                                        torch.empty(0, w.experts, 4, dtype=torch.int64,
+                                                    device="cuda"), tokens_per_sample=16)
+        assert tuple(ec.shape) == (0, d)
+    fl = build_module(w, dense, lora, access="full_dequant")
+    with torch.no_grad():
+        out = fl.grouped_linear("w1", empty, offsets=torch.zeros(w.experts, dtype=torch.int32,
+                                                                 device="cuda"))
+    assert tuple(out.shape) == (0, w.ffn)
+    # A call with rows afterwards still matches the oracle (and raises nothing).
+    _run_case(w)
