@@ -460,8 +460,8 @@ using namespace mx;
 
 static int validate_route(const char *name, const void *logits, int64_t num_tokens,
                           int num_experts, int top_k, int renorm) {
-  if (!logits || num_tokens < 0) {
-    set_error("%s: logits must be non-null and num_tokens >= 0", name);
+  if (num_tokens < 0 || (!logits && num_tokens > 0)) {
+    set_error("%s: need num_tokens >= 0 and non-null logits when it is positive", name);
     return MX_ERR_INVALID;
   }
   if (num_experts <= 0 || num_experts > 1024) {
@@ -485,7 +485,7 @@ extern "C" int mx_route_topk(const float *logits, int64_t num_tokens, int num_ex
   clear_error();
   int rc = validate_route("mx_route_topk", logits, num_tokens, num_experts, top_k, renorm);
   if (rc) return rc;
-  if (!top_idx || !top_scores) {
+  if (num_tokens > 0 && (!top_idx || !top_scores)) {
     set_error("mx_route_topk: outputs must be non-null");
     return MX_ERR_INVALID;
   }
@@ -532,7 +532,7 @@ extern "C" int mx_route_topk_backward(const float *logits, int64_t num_tokens, i
   int rc = validate_route("mx_route_topk_backward", logits, num_tokens, num_experts, top_k,
                           renorm);
   if (rc) return rc;
-  if (!top_idx || !grad_scores || !grad_logits) {
+  if (num_tokens > 0 && (!top_idx || !grad_scores || !grad_logits)) {
     set_error("mx_route_topk_backward: buffers must be non-null");
     return MX_ERR_INVALID;
   }
@@ -550,7 +550,7 @@ extern "C" int mx_route_topk_heads(const float *logits, int num_heads, int64_t n
   clear_error();
   int rc = validate_route("mx_route_topk_heads", logits, num_tokens, num_experts, top_k, renorm);
   if (rc) return rc;
-  if (num_heads <= 0 || !top_idx || !top_scores) {
+  if (num_heads <= 0 || (num_tokens > 0 && (!top_idx || !top_scores))) {
     set_error("mx_route_topk_heads: need num_heads > 0 and non-null outputs");
     return MX_ERR_INVALID;
   }

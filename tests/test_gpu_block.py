@@ -152,3 +152,20 @@ def test_token_chunked_training_matches_unchunked():
     for k in g0:
         rel = float((g1[k] - g0[k]).abs().sum() / g0[k].abs().sum().clamp_min(1e-30))
         assert rel < 1e-5, (k, rel)
+
+
+def test_empty_batch_through_the_block():
+    """A batch with no tokens: router, routed experts and shared expert return
+    an empty output, and a training step's backward leaves zero LoRA grads."""
+    w = _workload(64)
+    blk, _ = _block(w)
+    x = torch.empty(2, 0, H, dtype=torch.bfloat16, device="cuda")
+    with torch.no_grad():
+        assert tuple(blk(x).shape) == (2, 0, H)
+    xg = x.clone().requires_grad_(True)
+    out = blk(xg)
+    out.float().sum().backward()
+    assert tuple(xg.grad.shape) == (2, 0, H)
+    for ad in blk.experts.expert_lora.values():
+        for p in (ad.lora_a, ad.lora_b):
+            assert p.grad is None or not bool(p.grad.abs().gt(0).any())

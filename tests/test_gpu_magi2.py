@@ -212,3 +212,15 @@ def test_backend_seam_executes_attached_experts():
     assert torch.equal(a, b)
     with pytest.raises(RuntimeError, match="attached"):
         backend.execute(torch.nn.Module(), x.cuda(), probs.cuda(), idx.cuda())
+
+
+def test_empty_sequence_through_the_magi2_layer():
+    dense, _, _, bias, _, _ = _magi2_case()
+    m = Magi2GroupedExperts.from_dense(*(dense[k].cuda() for k in ("W_gate", "W_up", "W_down")),
+                                       num_heads=2, quant_format="nf4")
+    x = torch.empty(0, 2, 128, dtype=torch.bfloat16, device="cuda")
+    logits = torch.empty(2, 0, 4, device="cuda")
+    with torch.no_grad():
+        out = m(x, logits, top_k=2, score_func="sigmoid", expert_bias=bias.cuda(),
+                route_norm=True, route_scale=4.9)
+    assert out.shape[0] == 0 and out.shape[-1] == 128

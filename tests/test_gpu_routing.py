@@ -68,3 +68,11 @@ def test_route_misaligned_logits_view(experts, k):
     ref_idx, ref_scores = oroute.route_topk(logits.numpy(), k)
     np.testing.assert_array_equal(idx.cpu().numpy(), ref_idx)
     np.testing.assert_allclose(scores.cpu().numpy(), ref_scores, rtol=3e-6, atol=1e-7)
+
+
+def test_route_no_tokens_forward_and_backward():
+    lg = torch.empty(0, 64, device="cuda").requires_grad_(True)
+    idx, s = route_topk(lg, 4, renorm="clamp")
+    assert tuple(idx.shape) == (0, 4) and tuple(s.shape) == (0, 4)
+    s.sum().backward()
+    assert tuple(lg.grad.shape) == (0, 64)
