@@ -405,7 +405,8 @@ extern "C" int mx_gather_rows(const void *tokens, int64_t src_rows, const int64_
                               int64_t rows, int64_t cols, int dtype, void *out, void *stream) {
   clear_error();
   const int64_t esize = dtype == MX_DTYPE_BF16 ? 2 : 4;
-  if (!tokens || !index || !out || rows < 0 || cols <= 0 || (cols * esize) % 16 != 0) {
+  if (rows < 0 || cols <= 0 || (cols * esize) % 16 != 0 ||
+      (rows > 0 && (!tokens || !index || !out))) {
     set_error("mx_gather_rows: need non-null buffers and rows of a multiple of 16 bytes");
     return MX_ERR_INVALID;
   }
@@ -423,7 +424,8 @@ extern "C" int mx_scatter_add_rows(const void *rows_in, const float *row_scale,
   clear_error();
   float *grad_tokens = out;
   const void *grad = rows_in;
-  if (!grad_tokens || out_rows < 0 || rows < 0 || cols <= 0 || (rows > 0 && (!grad || !index))) {
+  if ((!grad_tokens && out_rows > 0) || out_rows < 0 || rows < 0 || cols <= 0 ||
+      (rows > 0 && (!grad || !index))) {
     set_error("mx_scatter_add_rows: invalid arguments");
     return MX_ERR_INVALID;
   }

@@ -50,6 +50,17 @@ def build_dispatch_plan(top_indices: torch.Tensor, top_scores: torch.Tensor, num
     scores = top_scores.contiguous()
     if scores.dtype not in (torch.float32, torch.bfloat16):
         scores = scores.float()
+    if S == 0:
+        # No routes: every expert's segment is empty and there is nothing to sort.
+        def none(dtype):
+            return torch.empty(0, dtype=dtype, device=device)
+        return DispatchPlan(counts=torch.zeros(E, dtype=torch.int64, device=device),
+                            starts=torch.zeros(E, dtype=torch.int64, device=device),
+                            offsets=torch.zeros(E, dtype=torch.int32, device=device),
+                            sort_positions=none(torch.int64),
+                            sorted_token_indices=none(torch.int64),
+                            sorted_scores=none(scores.dtype), inverse_order=none(torch.int64),
+                            total_slots=0, top_k=k, max_count_bound=T)
     counts = torch.empty(E, dtype=torch.int64, device=device)
     starts = torch.empty(E, dtype=torch.int64, device=device)
     offsets = torch.empty(E, dtype=torch.int32, device=device)

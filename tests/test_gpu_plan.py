@@ -92,3 +92,24 @@ def test_permute_and_combine_match_index_add_with_duplicates():
     reference.backward(grad)
     torch.testing.assert_close(tg.grad.cpu(), tokens.grad)
     torch.testing.assert_close(sg.grad.cpu(), scores.grad)
+
+
+def test_empty_routes_plan_permute_and_combine():
+    """No routed slots: an all-zero plan, empty permutation arrays, and
+    permute / combine (forward and backward) over empty rows."""
+    idx = torch.empty(0, 2, dtype=torch.int64, device="cuda")
+    scores = torch.empty(0, 2, device="cuda")
+    plan = build_dispatch_plan(idx, scores, 5)
+    assert plan.counts.tolist() == [0] * 5 and plan.starts.tolist() == [0] * 5
+    assert plan.offsets.tolist() == [0] * 5 and plan.total_slots == 0
+    assert plan.sort_positions.numel() == 0 and plan.inverse_order.numel() == 0
+    tokens = torch.randn(3, 8, device="cuda").requires_grad_(True)
+    none = torch.empty(0, dtype=torch.int64, device="cuda")
+    rows = permute_routed_tokens(tokens, none)
+    assert tuple(rows.shape) == (0, 8)
+    sc = torch.empty(0, device="cuda").requires_grad_(True)
+    out = combine_routed_tokens(rows, sc, none, output_rows=3, output_dtype=torch.float32)
+    assert torch.equal(out, torch.zeros(3, 8, device="cuda"))
+    out.sum().backward()
+    assert torch.equal(tokens.grad, torch.zeros_like(tokens))
+    assert tuple(sc.grad.shape) == (0,)
