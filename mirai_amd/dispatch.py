@@ -29,6 +29,19 @@ class DispatchPlan:
     max_count_bound: int
 
 
+def _empty_plan(E: int, score_dtype, device, *, k: int, bound: int) -> DispatchPlan:
+    """The plan of no routed slots: every expert's segment is empty and there
+    is nothing to sort (no kernel runs)."""
+    def none(dtype):
+        return torch.empty(0, dtype=dtype, device=device)
+    return DispatchPlan(counts=torch.zeros(E, dtype=torch.int64, device=device),
+                        starts=torch.zeros(E, dtype=torch.int64, device=device),
+                        offsets=torch.zeros(E, dtype=torch.int32, device=device),
+                        sort_positions=none(torch.int64), sorted_token_indices=none(torch.int64),
+                        sorted_scores=none(score_dtype), inverse_order=none(torch.int64),
+                        total_slots=0, top_k=k, max_count_bound=bound)
+
+
 def build_dispatch_plan(top_indices: torch.Tensor, top_scores: torch.Tensor, num_experts: int,
                         *, backend: str = "device") -> DispatchPlan:
     """Device-resident plan (no host sync): a stable counting sort by expert.
@@ -51,16 +64,7 @@ def build_dispatch_plan(top_indices: torch.Tensor, top_scores: torch.Tensor, num
     if scores.dtype not in (torch.float32, torch.bfloat16):
         scores = scores.float()
     if S == 0:
-        # No routes: every expert's segment is empty and there is nothing to sort.
-        def none(dtype):
-            return torch.empty(0, dtype=dtype, device=device)
-        return DispatchPlan(counts=torch.zeros(E, dtype=torch.int64, device=device),
-                            starts=torch.zeros(E, dtype=torch.int64, device=device),
-                            offsets=torch.zeros(E, dtype=torch.int32, device=device),
-                            sort_positions=none(torch.int64),
-                            sorted_token_indices=none(torch.int64),
-                            sorted_scores=none(scores.dtype), inverse_order=none(torch.int64),
-                            total_slots=0, top_k=k, max_count_bound=T)
+        return _empty_plan(E, scores.dtype, device, k=k, bound=T)
     counts = torch.empty(E, dtype=torch.int64, device=device)
     starts = torch.empty(E, dtype=torch.int64, device=device)
     offsets = torch.empty(E, dtype=torch.int32, device=device)
@@ -117,6 +121,8 @@ def build_expert_choice_dispatch_plan(expert_token_indices: torch.Tensor,
     scores = expert_token_scores.contiguous()
     if scores.dtype not in (torch.float32, torch.bfloat16):
         scores = scores.float()
+    if S == 0:
+        return _empty_plan(E, scores.dtype, device, k=0, bound=0)
     l2p = torch.tensor(aliases, dtype=torch.int32, device=device) if aliases else None
     counts = torch.empty(E, dtype=torch.int64, device=device)
     starts = torch.empty(E, dtype=torch.int64, device=device)

@@ -113,3 +113,13 @@ def test_empty_routes_plan_permute_and_combine():
     out.sum().backward()
     assert torch.equal(tokens.grad, torch.zeros_like(tokens))
     assert tuple(sc.grad.shape) == (0,)
+
+
+def test_empty_expert_choice_plan():
+    from mirai_amd import build_expert_choice_dispatch_plan
+
+    idx = torch.empty(0, 4, 3, dtype=torch.int64, device="cuda")
+    plan = build_expert_choice_dispatch_plan(idx, torch.empty(0, 4, 3, device="cuda"),
+                                             tokens_per_sample=8, num_physical_experts=4)
+    assert plan.counts.tolist() == [0] * 4 and plan.total_slots == 0
+    assert plan.sorted_token_indices.numel() == 0
