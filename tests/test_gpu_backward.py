@@ -255,3 +255,13 @@ def test_empty_batch_forward_and_backward():
                 assert not bool(g.abs().gt(0).any()), key + "." + name
     with torch.no_grad():
         assert tuple(m.run_direct_routed(x.cuda(), scores.cuda(), idx.cuda()).shape) == (0, w.hidden)
+
+
+@pytest.mark.parametrize("keys", [("w2",), ("w1",), ("w1", "w3"), ("w3", "w2")])
+def test_backward_with_a_subset_of_adapters(keys):
+    """LoRA on some projections only (the others frozen without an adapter): the
+    absent adapters' columns are skipped in every epilogue and their gradients
+    are not produced; tall and remainder tiles both run (R >= 256 E)."""
+    w = small("nf4", T=1100, E=4, k=2, d=192, f=256)
+    lora = {k: v for k, v in wl.lora_factors(w).items() if k in keys}
+    _case(w, lora=lora)
