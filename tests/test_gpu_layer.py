@@ -324,3 +324,10 @@ def test_empty_inputs_through_every_inference_entry_point():
     assert tuple(out.shape) == (0, w.ffn)
     # A call with rows afterwards still matches the oracle (and raises nothing).
     _run_case(w)
+
+
+@pytest.mark.parametrize("keys", [("w2",), ("w1",), ("w3", "w2")])
+def test_inference_with_a_subset_of_adapters(keys):
+    w = small("nf4", T=1100, E=4, k=2, d=192, f=256)
+    lora = {k: v for k, v in wl.lora_factors(w).items() if k in keys}
+    _run_case(w, lora=lora)
