@@ -331,3 +331,9 @@ def test_inference_with_a_subset_of_adapters(keys):
     w = small("nf4", T=1100, E=4, k=2, d=192, f=256)
     lora = {k: v for k, v in wl.lora_factors(w).items() if k in keys}
     _run_case(w, lora=lora)
+
+
+@pytest.mark.parametrize("k", [1, 3, 5, 7])
+def test_routed_layer_top_k(k):
+    """top-1 and the odd top-k values (the combine's unrolled and generic paths)."""
+    _run_case(small("nf4", T=300, E=8, k=k, d=128, f=192))
