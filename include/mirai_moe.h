@@ -406,6 +406,8 @@ int mx_split_f32(const float *x, int64_t rows, int64_t cols, int pattern, void *
  * with the canonical gated SwiGLU spec (mirai/core/moe/runtime/specs.py:222-231):
  * gate = w1, up = w3, down = w2, h = silu(x w1^T + dA1) * (x w3^T + dA3),
  * y = h w2^T + dA2, out[t] = sum_j score[t,j] * y[t,j] (fp32) -> out_dtype.
+ * hidden and ffn must be multiples of 64 (one NF4 block per K step of the
+ * GEMMs); other sizes return MX_ERR_INVALID.
  * Optional saved activations for backward (any may be NULL):
  *   save_gate/save_up [R, ffn] bf16 pre-activation projections (sorted order),
  *   save_h [R, ffn] bf16, save_y [R, hidden] bf16 (flat slot order t*k+j),
