@@ -265,3 +265,10 @@ def test_backward_with_a_subset_of_adapters(keys):
     w = small("nf4", T=1100, E=4, k=2, d=192, f=256)
     lora = {k: v for k, v in wl.lora_factors(w).items() if k in keys}
     _case(w, lora=lora)
+
+
+@pytest.mark.parametrize("r", [4, 12, 36])
+def test_backward_ranks_off_the_multiple_of_eight(r):
+    """Ranks the kernels pad with zero rank rows (to a multiple of 8): the
+    padded factors' gradients are cut back to the adapter's own rank."""
+    _case(small("nf4", r=r, alpha=2.0 * r, E=5, k=3, T=300, f=320, d=192))

@@ -337,3 +337,8 @@ def test_inference_with_a_subset_of_adapters(keys):
 def test_routed_layer_top_k(k):
     """top-1 and the odd top-k values (the combine's unrolled and generic paths)."""
     _run_case(small("nf4", T=300, E=8, k=k, d=128, f=192))
+
+
+@pytest.mark.parametrize("r", [4, 12, 36])
+def test_lora_ranks_off_the_multiple_of_eight(r):
+    _run_case(small("nf4", r=r, alpha=2.0 * r, E=5, k=3, T=300, f=320, d=192))
