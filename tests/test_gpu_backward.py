@@ -272,3 +272,25 @@ def test_backward_ranks_off_the_multiple_of_eight(r):
     """Ranks the kernels pad with zero rank rows (to a multiple of 8): the
     padded factors' gradients are cut back to the adapter's own rank."""
     _case(small("nf4", r=r, alpha=2.0 * r, E=5, k=3, T=300, f=320, d=192))
+
+
+def test_lora_only_backward_when_inputs_need_no_grad():
+    """Tokens and scores that do not require gradients (the adapters alone
+    train): the LoRA gradients equal those of the full backward."""
+    w = small("nf4", T=400, E=6, k=2)
+    dense, lora = wl.dense_weights(w), wl.lora_factors(w)
+    x = wl.tokens(w)
+    idx_np, scores_np = oroute.route_topk(wl.router_logits(w).numpy(), w.top_k)
+    idx, scores = torch.from_numpy(idx_np), torch.from_numpy(scores_np)
+    dy = wl.upstream_grad(w)
+    m = build_module(w, dense, lora)
+    _, full = _gpu_grads(m, x, scores, idx, dy)
+    for ad in m.expert_lora.values():
+        ad.lora_a.grad = None
+        ad.lora_b.grad = None
+    out = m.run_direct_routed(x.cuda(), scores.cuda(), idx.cuda())
+    assert out.requires_grad
+    out.backward(dy.cuda())
+    for key, ad in m.expert_lora.items():
+        assert torch.equal(ad.lora_a.grad, full[f"{key}.a"]), key
+        assert torch.equal(ad.lora_b.grad, full[f"{key}.b"]), key
