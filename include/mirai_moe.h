@@ -57,6 +57,14 @@ extern "C" {
 #define MX_FMT_F32X3 3
 #define MX_FMT_NF4_F32 4  /* NF4 codes with an fp32 absmax per block (ingested bitsandbytes) */
 
+/* Expert id of a route slot that is left out of the layer on purpose: the
+ * plan skips it without counting it as an invalid route (any other id outside
+ * [0, E) is counted, see mx_plan_error_counter), and the combine skips it like
+ * any id outside [0, E). Used for the zero-score slots of coalesced logical
+ * expert aliases, which the reference leaves out of the dispatch
+ * (experts.py:2361-2367). */
+#define MX_ROUTE_DROPPED (-9223372036854775807LL - 1)
+
 /* Plane orders of mx_split_f32. */
 #define MX_SPLIT_ACT 0     /* [hi | hi | lo]: activations */
 #define MX_SPLIT_WEIGHT 1  /* [hi | lo | hi]: weights and LoRA factors */
@@ -115,15 +123,43 @@ int mx_route_topk_backward(const float *logits, int64_t num_tokens, int num_expe
                            float *grad_logits, void *stream);
 
 /*
+ * Router-gate gradient of any of the routers above: d(logits) [rows, E] fp32
+ * from d(top_scores) [rows, k] fp32 for the picks top_idx [rows, k], where the
+ * scores were softmax or sigmoid (score_func) of the fp32 logits, the picks'
+ * scores were renormalised by `renorm` with the floor `renorm_floor`
+ * (MX_RENORM_CLAMP: p / max(sum p, floor); MX_RENORM_EPS: p / (sum p + floor))
+ * and multiplied by route_scale. The bias that steered the selection carries
+ * no gradient. This is the autograd of the score path of
+ * LingBotVideoRouter.forward (transformer_lingbot_video.py:1002-1033: softmax /
+ * sigmoid, gather, / (sum + 1e-20), * route_scale) and of CoreMultiHeadMoE._route
+ * (mirai/vendors/magi2_preview/model/magi2_preview.py:2727-2743 with
+ * flash_mh_moe/route.py:28-148: F.normalize(p=1, eps) is MX_RENORM_CLAMP) with
+ * one logits row per (head, token). Slots whose expert id lies outside [0, E)
+ * get no gradient. The gradient of the router GEMM itself (d tokens =
+ * d logits . W, d W = d logits^T . tokens) is a plain fp32 GEMM left to the
+ * caller. E <= 1024, 1 <= k <= 16.
+ */
+int mx_route_scores_backward(const float *logits, int64_t num_rows, int num_experts, int top_k,
+                             int score_func, int renorm, float renorm_floor, float route_scale,
+                             const int64_t *top_idx, const float *grad_scores,
+                             float *grad_logits, void *stream);
+
+/*
  * Multi-head top-k routing (MAGI-2). Replaces compute_topk_probs_and_indices
- * (mirai/vendors/magi2_preview/flash_mh_moe/route.py:28-148,157-196, with
- * num_virtual_group = 1) followed by `* route_scale` in CoreMultiHeadMoE._route
+ * (mirai/vendors/magi2_preview/flash_mh_moe/route.py:28-148,157-196) followed
+ * by `* route_scale` in CoreMultiHeadMoE._route
  * (mirai/vendors/magi2_preview/model/magi2_preview.py:2727-2743) and the
  * head-flattening of Magi2GroupedMoEBackend._execute_routed_chunk
  * (mirai/core/models/magi2_preview/grouped_moe.py:658-663).
  * logits [H, S, E] fp32; scores = softmax or sigmoid (score_func); experts are
  * picked by score + expert_bias[h, e] (expert_bias [H, E] fp32, may be NULL;
- * it steers selection only); ties go to the lower expert id. Probabilities are
+ * it steers selection only); ties go to the lower expert id. With
+ * num_virtual_group > 1 (dividing E, at most 64) the experts form that many
+ * groups of consecutive ids, each scored by the sum of its two largest biased
+ * scores; only the topk_virtual_group best groups (ties to the lower group id)
+ * keep their experts' keys, every other key is set to 0.0 before the expert
+ * selection (route.py:62-105); num_virtual_group = 1 disables it and ignores
+ * topk_virtual_group. Probabilities are
  * the picks' unbiased scores, renormalised by renorm (MX_RENORM_CLAMP:
  * p / max(sum p, renorm_floor), the L1 F.normalize with eps = renorm_floor;
  * MX_RENORM_EPS: p / (sum p + renorm_floor)), times route_scale.
@@ -134,8 +170,9 @@ int mx_route_topk_backward(const float *logits, int64_t num_tokens, int num_expe
  */
 int mx_route_topk_heads(const float *logits, int num_heads, int64_t num_tokens, int num_experts,
                         int top_k, int score_func, const float *expert_bias, int renorm,
-                        float renorm_floor, float route_scale, int layout, int64_t *top_idx,
-                        void *top_scores, int score_dtype, void *stream);
+                        float renorm_floor, float route_scale, int num_virtual_group,
+                        int topk_virtual_group, int layout, int64_t *top_idx, void *top_scores,
+                        int score_dtype, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* Fused router front end (router GEMM + scores + selection)                 */
@@ -376,7 +413,10 @@ size_t mx_moe_f32x3_workspace_size(int64_t num_tokens, int top_k, int num_expert
  * mx_moe_workspace_size (mx_moe_f32x3_workspace_size for MX_FMT_F32X3
  * weights) exceeds MX_STATIC_SCRATCH_BYTES fail with MX_ERR_INVALID. Every
  * call on one GPU shares that GPU's array: calls that overlap on one GPU (on
- * different streams or threads) race.
+ * different streams or threads) race. The first call on a device resolves
+ * that device's array address (hipGetSymbolAddress); make it once outside
+ * any stream capture (a warm-up call), after which the call can be captured
+ * into a HIP graph and replayed.
  */
 int mx_moe_forward_static(const void *tokens, const int64_t *top_idx, const void *top_scores,
                           int score_dtype, int64_t num_tokens, int top_k, int num_experts,
@@ -584,6 +624,31 @@ int mx_moe_for_loop_act(const void *tokens_sorted, const int64_t *counts, int64_
 int mx_grouped_linear(const void *x, const int64_t *counts, int64_t num_rows, int num_experts,
                       const mx_weight *w, const mx_lora *lora, void *out, void *workspace,
                       void *stream);
+
+/* Bytes of scratch for mx_grouped_linear_backward. */
+size_t mx_grouped_linear_backward_workspace_size(int64_t num_rows, int num_experts,
+                                                 int64_t in_features, int64_t out_features,
+                                                 int lora_rank);
+
+/*
+ * Backward of mx_grouped_linear over the same rows (x [S, in] bf16, the
+ * forward's input) and grad_out [S, out] bf16: grad_x [S, in] bf16 (may be
+ * NULL) = grad_out W_e + dz A_e with the frozen W_e re-decoded in-kernel and
+ * dz = bf16(s bf16(grad_out B_e)); with LoRA also the fp32 factor gradients
+ * grad_a [E, r, in] = sum dz^T x and grad_b [E, out, r] = sum grad_out^T p
+ * per expert, p = bf16(s bf16(x A_e^T)) recomputed as the forward formed it
+ * (zero when num_rows is 0). Replaces _FrozenGroupedMMLinear.backward
+ * (mirai/core/models/compressed_weights/execution/torch_grouped.py:71-91:
+ * dX = grouped_mm(dY, W) over the re-dequantised weight) plus the autograd of
+ * ActiveExpertLoRA.grouped_forward (active_expert_lora.py:348-399), the
+ * backward of CompressedGroupedExperts.grouped_linear (experts.py:803-827).
+ * in_features and out_features are multiples of 64; BF16, NF4, NF4_F32 and
+ * INT8 weights.
+ */
+int mx_grouped_linear_backward(const void *grad_out, const void *x, const int64_t *counts,
+                               int64_t num_rows, int num_experts, const mx_weight *w,
+                               const mx_lora *lora, void *grad_x, float *grad_a, float *grad_b,
+                               void *workspace, void *stream);
 
 /*
  * Backward of mx_moe_forward (adapter training, frozen base): given

@@ -19,11 +19,9 @@ from .lora import ActiveExpertLoRA, lora_scale
 from .magi2 import (
     Magi2FusedMoEBackend,
     Magi2GroupedExperts,
-    Magi2PackedExpertStateError,
     Magi2QuantizedExpertError,
-    load_magi2_packed_state,
+    compute_topk_probs_and_indices,
     route_topk_heads,
-    save_magi2_packed_state,
 )
 from .router import FusedRouter, fused_router_forward, router_weight_planes
 from .routing import route_topk
@@ -45,22 +43,20 @@ __all__ = [
     "ExpertProjectionRole",
     "Magi2FusedMoEBackend",
     "Magi2GroupedExperts",
-    "Magi2PackedExpertStateError",
     "Magi2QuantizedExpertError",
     "MoETokenChunkPolicy",
     "as_execution_spec",
     "build_dispatch_plan",
     "build_expert_choice_dispatch_plan",
     "check_route_errors",
+    "compute_topk_probs_and_indices",
     "combine_routed_tokens",
     "fused_chunk_runner",
     "fused_router_forward",
-    "load_magi2_packed_state",
     "lora_scale",
     "permute_routed_tokens",
     "route_topk",
     "route_topk_heads",
     "router_weight_planes",
-    "save_magi2_packed_state",
     "set_route_check",
 ]

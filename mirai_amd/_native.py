@@ -45,6 +45,13 @@ SCORE_SIGMOID = 1
 ROUTE_LAYOUT_HEADS = 0
 ROUTE_LAYOUT_ROWS = 1
 
+# A route slot whose expert id is ROUTE_DROPPED is left out of the layer
+# without counting as an invalid route (zero-score slots of coalesced aliases).
+ROUTE_DROPPED = -(1 << 63)
+
+# mx_abi_version() of the library these bindings describe.
+ABI_VERSION = 8
+
 PLAN_MAX_EXPERTS = 8192
 STATIC_SCRATCH_BYTES = 64 << 20  # MX_STATIC_SCRATCH_BYTES
 ROUTER_MAX_EXPERTS = 256  # mx_router_forward
@@ -79,10 +86,12 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "mx_route_topk": (c_int, [_P, c_int64, c_int, c_int, c_int, c_float, _P, _P, c_int, _P]),
     "mx_route_topk_backward": (
         c_int, [_P, c_int64, c_int, c_int, c_int, c_float, _P, _P, _P, _P]),
+    "mx_route_scores_backward": (
+        c_int, [_P, c_int64, c_int, c_int, c_int, c_int, c_float, c_float, _P, _P, _P, _P]),
     "mx_route_topk_heads": (
         c_int,
-        [_P, c_int, c_int64, c_int, c_int, c_int, _P, c_int, c_float, c_float, c_int, _P, _P,
-         c_int, _P]),
+        [_P, c_int, c_int64, c_int, c_int, c_int, _P, c_int, c_float, c_float, c_int, c_int,
+         c_int, _P, _P, c_int, _P]),
     "mx_router_padded_experts": (c_int, [c_int]),
     "mx_router_planes_size": (c_size_t, [c_int, c_int64]),
     "mx_router_weight_planes": (c_int, [_P, c_int, c_int64, _P, _P]),
@@ -154,6 +163,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         c_int, [_P, _P, c_int64, c_int, c_int64, c_int64, c_int, _W, _W, _W, _L, _L, _L, _P, _P,
                 _P]),
     "mx_grouped_linear": (c_int, [_P, _P, c_int64, c_int, _W, _L, _P, _P, _P]),
+    "mx_grouped_linear_backward_workspace_size": (
+        c_size_t, [c_int64, c_int, c_int64, c_int64, c_int]),
+    "mx_grouped_linear_backward": (
+        c_int, [_P, _P, _P, c_int64, c_int, _W, _L, _P, _P, _P, _P, _P]),
     "mx_moe_backward_workspace_size": (c_size_t,
                                        [c_int64, c_int, c_int, c_int64, c_int64, c_int]),
     "mx_moe_backward": (
@@ -183,10 +196,19 @@ def load_library() -> ctypes.CDLL:
         lib = ctypes.CDLL(str(LIB_PATH))
     except OSError as exc:  # pragma: no cover - depends on the ROCm install
         raise NativeLibraryError(f"cannot load {LIB_PATH}: {exc}") from exc
+    version = getattr(lib, "mx_abi_version", None)
+    found = int(version()) if version is not None else -1
+    if found != ABI_VERSION:
+        raise NativeLibraryError(
+            f"{LIB_PATH} has ABI version {found}, these bindings need {ABI_VERSION}; rebuild "
+            "with `python -m mirai_amd.csrc.build`.")
+    missing = [name for name in SIGNATURES if getattr(lib, name, None) is None]
+    if missing:
+        raise NativeLibraryError(
+            f"{LIB_PATH} lacks {', '.join(missing[:4])}; rebuild with "
+            "`python -m mirai_amd.csrc.build`.")
     for name, (restype, argtypes) in SIGNATURES.items():
-        fn = getattr(lib, name, None)
-        if fn is None:
-            continue
+        fn = getattr(lib, name)
         fn.restype = restype
         fn.argtypes = argtypes
     _lib = lib

@@ -100,9 +100,10 @@ class FusedSparseMoeBlock(nn.Module):
         return self._side_streams[device]
 
     def _routes(self, tokens, padding_mask, router_logit_delta):
-        with torch.no_grad():
-            top_indices, top_scores, _, _, _ = self.router(tokens.detach(),
-                                                           logit_delta=router_logit_delta)
+        # Live tokens, as the reference routes them (:2259-2264): in training
+        # the gating scores carry the router's gradient to the tokens and the
+        # router weight.
+        top_indices, top_scores, _, _, _ = self.router(tokens, logit_delta=router_logit_delta)
         if padding_mask is not None:  # :2282-2287
             pm = padding_mask.reshape(-1, 1).to(top_scores.dtype)
             top_scores = top_scores * pm
@@ -116,7 +117,8 @@ class FusedSparseMoeBlock(nn.Module):
         tokens = hidden_states.reshape(-1, self.hidden_size)
         device = nat.require_gpu(tokens)
         grad = torch.is_grad_enabled() and (
-            tokens.requires_grad or any(p.requires_grad for p in self.experts.parameters()))
+            tokens.requires_grad or any(p.requires_grad for p in self.experts.parameters())
+            or self.router.weight.requires_grad)
 
         shared, ready = None, None
         if self.shared_experts is not None:

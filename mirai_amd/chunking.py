@@ -36,9 +36,8 @@ class FusedChunkRunner:
         self.experts = experts
 
     def __call__(self, tokens, top_scores, top_indices, token_offset: int = 0):
-        from .fused import routed_experts
-
-        return routed_experts(self.experts, tokens, top_scores, top_indices)
+        # run_direct_routed: its checks, alias coalescing, then the fused layer.
+        return self.experts.run_direct_routed(tokens, top_scores, top_indices)
 
 
 def fused_chunk_runner(experts) -> FusedChunkRunner:
@@ -94,8 +93,11 @@ class MoETokenChunkPolicy:
         if isinstance(runner, FusedChunkRunner):
             from .fused import routed_experts_chunked
 
-            return routed_experts_chunked(runner.experts, tokens, top_scores, top_indices,
-                                          bounds)
+            # Checks and alias coalescing once over all tokens: coalescing
+            # merges slots within a token, so every chunk then runs exactly
+            # the physical routes of the unchunked layer.
+            scores, indices = runner.experts.direct_routes(tokens, top_scores, top_indices)
+            return routed_experts_chunked(runner.experts, tokens, scores, indices, bounds)
         if not torch.is_grad_enabled():
             return torch.cat([runner(tokens[a:b], top_scores[a:b], top_indices[a:b], a)
                               for a, b in bounds], dim=0)

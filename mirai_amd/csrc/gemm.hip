@@ -2149,6 +2149,142 @@ extern "C" int mx_grouped_linear(const void *x, const int64_t *counts, int64_t n
   return launch_any<EPI_STORE>(w->format, lr, p, L.plan, v, s);
 }
 
+namespace mx {
+namespace gemm {
+
+// Scratch of the grouped-linear backward: plan | p [S, rc] (the forward's
+// low-rank rows, recomputed) | dz [S, rc] | B^T [E, rc, out] | A^T [E, in, rc].
+struct LinearBackLayout {
+  PlanLayout plan;
+  size_t off_p = 0, off_dz = 0, off_bt = 0, off_at = 0, bytes = 0;
+};
+
+LinearBackLayout linear_back_layout(int64_t rows, int num_experts, int64_t in_f, int64_t out_f,
+                                    int rc) {
+  LinearBackLayout L;
+  L.plan = plan_layout(rows, num_experts);
+  size_t off = align_up(L.plan.bytes, 256);
+  L.off_p = off;
+  off = align_up(off + sizeof(uint16_t) * rows * rc, 256);
+  L.off_dz = off;
+  off = align_up(off + sizeof(uint16_t) * rows * rc, 256);
+  L.off_bt = off;
+  off = align_up(off + sizeof(uint16_t) * num_experts * rc * out_f, 256);
+  L.off_at = off;
+  off = align_up(off + sizeof(uint16_t) * num_experts * rc * in_f, 256);
+  L.bytes = off;
+  return L;
+}
+
+}  // namespace gemm
+}  // namespace mx
+
+extern "C" size_t mx_grouped_linear_backward_workspace_size(int64_t num_rows, int num_experts,
+                                                           int64_t in_features,
+                                                           int64_t out_features, int lora_rank) {
+  if (num_rows < 0 || num_experts <= 0 || in_features <= 0 || out_features <= 0 ||
+      lora_rank < 0 || lora_rank > kLoraMaxRank)
+    return 0;
+  return linear_back_layout(num_rows, num_experts, in_features, out_features,
+                            lora_width(lora_rank)).bytes;
+}
+
+extern "C" int mx_grouped_linear_backward(const void *grad_out, const void *x,
+                                          const int64_t *counts, int64_t num_rows,
+                                          int num_experts, const mx_weight *w,
+                                          const mx_lora *lora, void *grad_x, float *grad_a,
+                                          float *grad_b, void *workspace, void *stream) {
+  clear_error();
+  const char *name = "mx_grouped_linear_backward";
+  int rc = validate_plan_args(name, num_rows, 1, num_experts);
+  if (rc) return rc;
+  if (!w) {
+    set_error("%s: weight is missing", name);
+    return MX_ERR_INVALID;
+  }
+  const int64_t in_f = w->in_features, out_f = w->out_features;
+  if (in_f <= 0 || in_f % 64 != 0 || out_f <= 0 || out_f % 64 != 0) {
+    set_error("%s: in_features and out_features must be multiples of 64 (got %lld, %lld)", name,
+              static_cast<long long>(in_f), static_cast<long long>(out_f));
+    return MX_ERR_INVALID;
+  }
+  if ((rc = check_weight(name, "w", w, out_f, in_f))) return rc;
+  if ((rc = check_lora(name, "w", lora))) return rc;
+  if (w->format == MX_FMT_F32X3) {
+    set_error("%s: MX_FMT_F32X3 (fp32) weights are inference-only", name);
+    return MX_ERR_INVALID;
+  }
+  hipStream_t s = as_stream(stream);
+  const bool lr = has_lora(lora);
+  if (num_rows == 0) {
+    // The gradient of an empty sum: zero LoRA gradients, nothing else to write.
+    if (!lr) return MX_OK;
+    return zero_lora_grads(name, num_experts, in_f, out_f, lora, nullptr, nullptr, grad_a,
+                           grad_b, nullptr, nullptr, nullptr, nullptr, s);
+  }
+  if (!grad_out || !x || !counts || !workspace || (!grad_x && !lr)) {
+    set_error("%s: gradient, x, counts and workspace must be non-null", name);
+    return MX_ERR_INVALID;
+  }
+  const int lrc = lora_width(lora, nullptr, nullptr);
+  const LinearBackLayout L = linear_back_layout(num_rows, num_experts, in_f, out_f, lrc);
+  char *ws = static_cast<char *>(workspace);
+  const PlanView v = plan_view(ws, L.plan);
+  if ((rc = plan_from_counts(counts, num_rows, num_experts, ws, s))) return rc;
+  const uint16_t *dy = static_cast<const uint16_t *>(grad_out);
+  const uint16_t *xr = static_cast<const uint16_t *>(x);
+  uint16_t *prow = reinterpret_cast<uint16_t *>(ws + L.off_p);
+  uint16_t *dz = reinterpret_cast<uint16_t *>(ws + L.off_dz);
+  uint16_t *bt = reinterpret_cast<uint16_t *>(ws + L.off_bt);
+  uint16_t *at = reinterpret_cast<uint16_t *>(ws + L.off_at);
+  if (lr) {
+    const int r = lora->rank;
+    FactorTransposes jobs = {};
+    jobs.job[jobs.n++] = {static_cast<const uint16_t *>(lora->b), bt, out_f, r,
+                          static_cast<int64_t>(num_experts) * out_f * r};
+    jobs.job[jobs.n++] = {static_cast<const uint16_t *>(lora->a), at, r, in_f,
+                          static_cast<int64_t>(num_experts) * r * in_f};
+    if ((rc = transpose_factors_multi(jobs, s))) return rc;
+    // p = bf16(s bf16(x A^T)) as the forward formed it, and dz = bf16(s bf16(dy B)).
+    const mx_lora *fwd[1] = {lora};
+    if ((rc = lora_down(v, num_experts, L.plan.max_tiles, xr, in_f, nullptr, in_f, fwd, 1, lrc,
+                        prow, lrc, s)))
+      return rc;
+    const mx_lora t = {bt, nullptr, r, lora->scale};
+    const mx_lora *bwd[1] = {&t};
+    if ((rc = lora_down(v, num_experts, L.plan.max_tiles, dy, out_f, nullptr, out_f, bwd, 1, lrc,
+                        dz, lrc, s)))
+      return rc;
+  }
+  if (grad_x) {
+    // dx = dy W + dz A, W re-decoded (B = W, K along the weight's out rows).
+    Params p = base_params(v);
+    p.x = dy;
+    p.ldx = out_f;
+    p.K = out_f;
+    p.w[0] = w->data;
+    p.wscale[0] = w->scale;
+    p.wn[0] = out_f;
+    p.k_split = out_f;
+    p.N = in_f;
+    p.lora_p = dz;
+    p.ldp = lrc;
+    p.lora_rc = lrc;
+    p.lora_b[0] = lr ? at : nullptr;
+    p.lora_r[0] = lr ? lora->rank : 0;
+    p.seg_end = v.seg + num_experts;
+    p.out = static_cast<uint16_t *>(grad_x);
+    p.ldo = in_f;
+    if ((rc = launch_any<EPI_STORE2>(w->format, lr, p, L.plan, v, s))) return rc;
+  }
+  if (!lr) return MX_OK;
+  // dB = sum dy^T p and dA = sum dz^T x per expert, one launch.
+  GradPhase ph;
+  ph.add({dy, out_f, nullptr, out_f}, prow, lrc, lora->rank, grad_b, false);
+  ph.add({xr, in_f, nullptr, in_f}, dz, lrc, lora->rank, grad_a, true);
+  return ph.run(v, num_experts, s);
+}
+
 // ------------------------------------------------------------ expert choice
 // Expert-choice routes [B, L, C] (each of L logical experts picks C tokens of
 // each sample) through the same plan and grouped GEMMs: the flat slots

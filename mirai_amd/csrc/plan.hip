@@ -25,7 +25,7 @@ __device__ __forceinline__ void build_masks(const int64_t *top_idx, int64_t slot
     const int64_t e = top_idx[slot0 + p];
     if (e >= 0 && e < E) {
       atomicOr(&mask[e * words + (p >> 5)], 1u << (p & 31));
-    } else if (lds_err) {
+    } else if (lds_err && e != MX_ROUTE_DROPPED) {
       atomicAdd(lds_err, 1);
     }
   }

@@ -253,46 +253,59 @@ __global__ __launch_bounds__(64) void route_topk_lane_kernel(const float *logits
   }
 }
 
-// d(logits) for the selected experts of each token; one wavefront per token.
+// d(logits) for the selected experts of each row; one wavefront per row of
+// fp32 logits [rows, E]. The scores p are softmax or sigmoid of the logits
+// (recomputed here); the picks' scores were renormalised by `renorm` with the
+// floor `floor` (MX_RENORM_CLAMP: p / max(sum, floor); MX_RENORM_EPS:
+// p / (sum + floor)) and multiplied by route_scale. The chain: dL/dp of the
+// picks through the renormalisation, then the softmax Jacobian
+// (dl_e = p_e (dp_e - sum_m p_m dp_m)) or the sigmoid's (dl_e = dp_e p_e (1 - p_e)).
 template <int PER_LANE>
 __global__ __launch_bounds__(256) void route_topk_backward_kernel(
-    const float *logits, int64_t T, int E, int k, int renorm, float route_scale,
-    const int64_t *top_idx, const float *grad_scores, float *grad_logits) {
+    const float *logits, int64_t T, int E, int k, int score_func, int renorm, float floor,
+    float route_scale, const int64_t *top_idx, const float *grad_scores, float *grad_logits) {
   const int lane = threadIdx.x & 63;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const float *row = logits + t * E;
-  float v[PER_LANE];
-  float m = -INFINITY;
+  const bool softmax = score_func == MX_SCORE_SOFTMAX;
+  float pr[PER_LANE];
+  float m = -INFINITY, z = 1.0f;
 #pragma unroll
   for (int j = 0; j < PER_LANE; ++j) {
     const int e = lane + 64 * j;
-    v[j] = e < E ? row[e] : -INFINITY;
-    m = fmaxf(m, v[j]);
+    pr[j] = e < E ? row[e] : -INFINITY;
+    m = fmaxf(m, pr[j]);
   }
+  if (softmax) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-  float z = 0.0f;
-  float pr[PER_LANE];
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    z = 0.0f;
 #pragma unroll
-  for (int j = 0; j < PER_LANE; ++j) {
-    pr[j] = lane + 64 * j < E ? __expf(v[j] - m) : 0.0f;
-    z += pr[j];
+    for (int j = 0; j < PER_LANE; ++j) {
+      pr[j] = lane + 64 * j < E ? expf(pr[j] - m) : 0.0f;
+      z += pr[j];
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) z += __shfl_xor(z, off, 64);
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j) pr[j] /= z;
+  } else {
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j)
+      pr[j] = lane + 64 * j < E ? 1.0f / (1.0f + expf(-pr[j])) : 0.0f;
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) z += __shfl_xor(z, off, 64);
-#pragma unroll
-  for (int j = 0; j < PER_LANE; ++j) pr[j] /= z;
 
-  // Selected slot of this lane (lane < k): its expert, probability and grad.
+  // Selected slot of this lane (lane < k): its expert, score and grad.
   int se = -1;
   float sg = 0.0f;
   if (lane < k) {
     se = static_cast<int>(top_idx[t * k + lane]);
     sg = grad_scores[t * k + lane];
   }
+  const bool sel_ok = se >= 0 && se < E;
   float sp = 0.0f;
-  if (se >= 0 && se < E) sp = __expf(row[se] - m) / z;
+  if (sel_ok) sp = softmax ? expf(row[se] - m) / z : 1.0f / (1.0f + expf(-row[se]));
   float ssum = sp;
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) ssum += __shfl_xor(ssum, off, 64);
@@ -301,15 +314,15 @@ __global__ __launch_bounds__(256) void route_topk_backward_kernel(
   if (renorm == MX_RENORM_NONE) {
     dp = route_scale * sg;
   } else {
-    float denom = renorm == MX_RENORM_CLAMP ? fmaxf(ssum, 1e-20f) : ssum + 1e-20f;
-    const bool denom_active = renorm == MX_RENORM_EPS || ssum >= 1e-20f;
+    const float denom = renorm == MX_RENORM_CLAMP ? fmaxf(ssum, floor) : ssum + floor;
+    const bool denom_active = renorm == MX_RENORM_EPS || ssum >= floor;
     float gp = sg * sp;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) gp += __shfl_xor(gp, off, 64);
     dp = route_scale * (sg / denom - (denom_active ? gp / (denom * denom) : 0.0f));
   }
-  // Softmax backward: dl_n = p_n * (dp_n - sum_m p_m dp_m).
-  float pdp = se >= 0 && se < E ? sp * dp : 0.0f;
+  if (!sel_ok) dp = 0.0f;
+  float pdp = sp * dp;
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) pdp += __shfl_xor(pdp, off, 64);
   // Broadcast the k selections to every lane before any lane diverges.
@@ -327,7 +340,8 @@ __global__ __launch_bounds__(256) void route_topk_backward_kernel(
 #pragma unroll
     for (int s = 0; s < kMaxTopK; ++s)
       if (s < k && sel_e[s] == e) dpe += sel_dp[s];
-    if (e < E) grad_logits[t * E + e] = pr[j] * (dpe - pdp);
+    if (e < E)
+      grad_logits[t * E + e] = softmax ? pr[j] * (dpe - pdp) : dpe * pr[j] * (1.0f - pr[j]);
   }
 }
 
@@ -342,8 +356,8 @@ __global__ __launch_bounds__(256) void route_topk_backward_kernel(
 template <int PER_LANE>
 __global__ __launch_bounds__(256) void route_heads_kernel(
     const float *logits, int64_t S, int H, int E, int k, int score_func, const float *bias,
-    int renorm, float renorm_floor, float route_scale, int layout, int64_t *top_idx,
-    void *top_scores, int score_dtype) {
+    int renorm, float renorm_floor, float route_scale, int n_vg, int topk_vg, int layout,
+    int64_t *top_idx, void *top_scores, int score_dtype) {
   const int lane = threadIdx.x & 63;
   const int64_t q = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // h * S + s
   if (q >= static_cast<int64_t>(H) * S) return;
@@ -379,6 +393,61 @@ __global__ __launch_bounds__(256) void route_heads_kernel(
   for (int j = 0; j < PER_LANE; ++j) {
     const int e = lane + 64 * j;
     key[j] = e < E ? sc[j] + (bias ? bias[static_cast<int64_t>(h) * E + e] : 0.0f) : -INFINITY;
+  }
+  if (n_vg > 1) {
+    // Virtual groups (route.py:62-105): the E experts form n_vg groups of
+    // epg consecutive ids; a group scores the sum of its two largest keys
+    // (its largest when it holds one expert), the topk_vg best groups are
+    // kept (ties to the lower group id), and every other expert's key becomes
+    // 0.0 (masked_fill(~mask, 0.0), not -inf) before the expert selection.
+    const int epg = E / n_vg;
+    float gscore = -INFINITY;  // lane g < n_vg: the score of group g
+    for (int g = 0; g < n_vg; ++g) {
+      float m1 = -INFINITY, m2 = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < PER_LANE; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E && e / epg == g) {
+          const float v = key[j];
+          if (v > m1) {
+            m2 = m1;
+            m1 = v;
+          } else if (v > m2) {
+            m2 = v;
+          }
+        }
+      }
+      // Top two of the union of two (largest, second) pairs.
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float o1 = __shfl_xor(m1, off, 64), o2 = __shfl_xor(m2, off, 64);
+        const float second = fmaxf(fminf(m1, o1), fmaxf(m2, o2));
+        m1 = fmaxf(m1, o1);
+        m2 = second;
+      }
+      if (lane == g) gscore = epg >= 2 ? m1 + m2 : m1;
+    }
+    uint64_t keep = 0;
+    for (int r = 0; r < topk_vg; ++r) {
+      const bool cand = lane < n_vg && !((keep >> lane) & 1ull);
+      float bv = cand ? gscore : -INFINITY;
+      int bg = cand ? lane : 0x7fffffff;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int og = __shfl_xor(bg, off, 64);
+        if (better(ov, og, bv, bg)) {
+          bv = ov;
+          bg = og;
+        }
+      }
+      keep |= 1ull << (bg & 63);
+    }
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E && !((keep >> (e / epg)) & 1ull)) key[j] = 0.0f;
+    }
   }
   uint32_t taken = 0;
   int my_e = 0;
@@ -524,28 +593,48 @@ extern "C" int mx_route_topk(const float *logits, int64_t num_tokens, int num_ex
   return check_launch("mx_route_topk");
 }
 
+extern "C" int mx_route_scores_backward(const float *logits, int64_t num_rows, int num_experts,
+                                        int top_k, int score_func, int renorm, float renorm_floor,
+                                        float route_scale, const int64_t *top_idx,
+                                        const float *grad_scores, float *grad_logits,
+                                        void *stream) {
+  clear_error();
+  const char *name = "mx_route_scores_backward";
+  const int64_t num_tokens = num_rows;
+  int rc = validate_route(name, logits, num_tokens, num_experts, top_k, renorm);
+  if (rc) return rc;
+  if (score_func != MX_SCORE_SOFTMAX && score_func != MX_SCORE_SIGMOID) {
+    set_error("%s: unknown score function %d", name, score_func);
+    return MX_ERR_INVALID;
+  }
+  if (!(renorm_floor >= 0.0f)) {
+    set_error("%s: renorm_floor must be >= 0", name);
+    return MX_ERR_INVALID;
+  }
+  if (num_tokens > 0 && (!top_idx || !grad_scores || !grad_logits)) {
+    set_error("%s: buffers must be non-null", name);
+    return MX_ERR_INVALID;
+  }
+  if (num_tokens == 0) return MX_OK;
+  MX_ROUTE_DISPATCH(route_topk_backward_kernel, logits, num_tokens, num_experts, top_k,
+                    score_func, renorm, renorm_floor, route_scale, top_idx, grad_scores,
+                    grad_logits);
+  return check_launch(name);
+}
+
 extern "C" int mx_route_topk_backward(const float *logits, int64_t num_tokens, int num_experts,
                                       int top_k, int renorm, float route_scale,
                                       const int64_t *top_idx, const float *grad_scores,
                                       float *grad_logits, void *stream) {
-  clear_error();
-  int rc = validate_route("mx_route_topk_backward", logits, num_tokens, num_experts, top_k,
-                          renorm);
-  if (rc) return rc;
-  if (num_tokens > 0 && (!top_idx || !grad_scores || !grad_logits)) {
-    set_error("mx_route_topk_backward: buffers must be non-null");
-    return MX_ERR_INVALID;
-  }
-  if (num_tokens == 0) return MX_OK;
-  MX_ROUTE_DISPATCH(route_topk_backward_kernel, logits, num_tokens, num_experts, top_k, renorm,
-                    route_scale, top_idx, grad_scores, grad_logits);
-  return check_launch("mx_route_topk_backward");
+  return mx_route_scores_backward(logits, num_tokens, num_experts, top_k, MX_SCORE_SOFTMAX, renorm,
+                                  1e-20f, route_scale, top_idx, grad_scores, grad_logits, stream);
 }
 
 extern "C" int mx_route_topk_heads(const float *logits, int num_heads, int64_t num_tokens,
                                    int num_experts, int top_k, int score_func,
                                    const float *expert_bias, int renorm, float renorm_floor,
-                                   float route_scale, int layout, int64_t *top_idx,
+                                   float route_scale, int num_virtual_group,
+                                   int topk_virtual_group, int layout, int64_t *top_idx,
                                    void *top_scores, int score_dtype, void *stream) {
   clear_error();
   int rc = validate_route("mx_route_topk_heads", logits, num_tokens, num_experts, top_k, renorm);
@@ -566,13 +655,23 @@ extern "C" int mx_route_topk_heads(const float *logits, int num_heads, int64_t n
     set_error("mx_route_topk_heads: renorm_floor must be >= 0");
     return MX_ERR_INVALID;
   }
+  if (num_virtual_group < 1 || num_virtual_group > 64 ||
+      num_experts % num_virtual_group != 0 ||
+      (num_virtual_group > 1 &&
+       (topk_virtual_group < 1 || topk_virtual_group > num_virtual_group))) {
+    set_error("mx_route_topk_heads: num_virtual_group must divide num_experts and lie in "
+              "[1, 64], topk_virtual_group in [1, num_virtual_group] (got %d, %d)",
+              num_virtual_group, topk_virtual_group);
+    return MX_ERR_INVALID;
+  }
   const int64_t rows = num_tokens * num_heads;
   if (rows == 0) return MX_OK;
   const int per_lane = (num_experts + 63) / 64;
   const dim3 grid(static_cast<unsigned>(ceil_div(rows, 4))), block(256);
   hipStream_t s = as_stream(stream);
 #define MX_HEADS_ARGS logits, num_tokens, num_heads, num_experts, top_k, score_func, expert_bias, \
-    renorm, renorm_floor, route_scale, layout, top_idx, top_scores, score_dtype
+    renorm, renorm_floor, route_scale, num_virtual_group, topk_virtual_group, layout, top_idx, \
+    top_scores, score_dtype
   switch (per_lane) {
     case 1: hipLaunchKernelGGL(route_heads_kernel<1>, grid, block, 0, s, MX_HEADS_ARGS); break;
     case 2: hipLaunchKernelGGL(route_heads_kernel<2>, grid, block, 0, s, MX_HEADS_ARGS); break;

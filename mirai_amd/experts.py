@@ -325,6 +325,16 @@ class CompressedGroupedExperts(nn.Module):
                           top_indices: torch.Tensor) -> torch.Tensor:
         """Gate-weighted routed layer output [T, d] in ``tokens.dtype``
         (experts.py:1749-1912); fp32 accumulation of the k expert outputs."""
+        top_scores, top_indices = self.direct_routes(tokens, top_scores, top_indices)
+        from .fused import routed_experts
+        return routed_experts(self, tokens, top_scores, top_indices)
+
+    def direct_routes(self, tokens: torch.Tensor, top_scores: torch.Tensor,
+                      top_indices: torch.Tensor):
+        """The checks of run_direct_routed (experts.py:1755-1769) and the physical
+        routes it executes: logical aliases coalesced (experts.py:339,
+        2361-2367). Token chunking applies this once over all tokens, so each
+        chunk runs exactly the routes the unchunked layer would."""
         if not self.prefers_for_loop():
             raise RuntimeError(
                 "Direct routed compressed_weights execution requires active_dequant, "
@@ -336,9 +346,7 @@ class CompressedGroupedExperts(nn.Module):
         if int(top_indices.shape[0]) != int(tokens.shape[0]):
             raise ValueError("Direct routed expert indices do not match token count.")
         self._require_loaded()
-        top_scores, top_indices = self._coalesce_logical_routes(top_scores, top_indices)
-        from .fused import routed_experts
-        return routed_experts(self, tokens, top_scores, top_indices)
+        return self._coalesce_logical_routes(top_scores, top_indices)
 
     def logical_to_physical_map(self) -> tuple[int, ...]:
         """Logical -> physical expert aliases (empty: identity)."""
@@ -390,7 +398,11 @@ class CompressedGroupedExperts(nn.Module):
         (experts.py:529-542 with coalesce_alias_routes, storage/aliases.py:156-199):
         each slot takes its logical expert's physical id, and the scores of a
         token's slots that land on one physical expert are summed into the
-        first such slot (the others keep the id with score 0). A logical id
+        first such slot. Every slot whose coalesced score is zero (the later
+        duplicates, and routes the router scored zero) is then left out of the
+        layer, as the reference's dispatch keeps only nonzero scores when
+        aliases are active (experts.py:2361-2367): its id becomes
+        ROUTE_DROPPED, which the plan and the combine skip. A logical id
         outside the map becomes an invalid physical id, which the dispatch plan
         reports (mirai_amd.check_route_errors) instead of a host sync here."""
         aliases = self.logical_to_physical_map()
@@ -414,6 +426,8 @@ class CompressedGroupedExperts(nn.Module):
         first = torch.where(eligible, candidate.expand_as(eligible),
                             torch.full_like(eligible, k, dtype=torch.long)).amin(dim=2)
         coalesced = torch.zeros_like(top_scores).scatter_add(1, first, top_scores)
+        dropped = valid & (coalesced.detach() == 0)
+        physical = torch.where(dropped, torch.full_like(physical, nat.ROUTE_DROPPED), physical)
         return coalesced, physical
 
     def run_expert_choice_routed(self, tokens: torch.Tensor, expert_token_scores: torch.Tensor,

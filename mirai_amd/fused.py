@@ -216,6 +216,10 @@ def routed_experts_chunked(module, tokens, top_scores, top_indices, bounds):
     params = _lora_params(module)
     if torch.is_grad_enabled() and any(
             t is not None and t.requires_grad for t in (tokens, top_scores, *params)):
+        if module.quant_format == "fp32":
+            raise NotImplementedError(
+                "the fp32 (quant_format='fp32') expert layer is inference-only; train adapters "
+                "over bf16, nf4 or int8 weights")
         return _ChunkedRoutedExperts.apply(module, tuple(bounds), tokens, top_scores, top_indices,
                                            *params)
     with torch.no_grad():
@@ -434,35 +438,105 @@ def sorted_experts(module, tokens, counts):
     return out.to(tokens.dtype)
 
 
-def grouped_projection(module, key, x, offsets):
-    """x [S, in] rows grouped by expert with inclusive int32 offsets -> [S, out]."""
+def _grouped_inputs(module, key, x, offsets):
+    """(device, counts [E] int64, bf16 rows, packed weight, adapter or None)."""
     device = nat.require_gpu(x)
     offs = offsets.detach().to(device=device, dtype=torch.int64)
     if int(offs.numel()) != module.num_experts:
         raise ValueError("offsets must hold one inclusive row end per expert.")
     counts = torch.diff(offs, prepend=offs.new_zeros(1)).contiguous()
-    xb = x.detach().to(torch.bfloat16).contiguous()
     packed = module.packed_weight(key)
-    _, out_f, in_f = packed.shape
-    if int(xb.shape[-1]) != in_f:
-        raise ValueError(f"x has {int(xb.shape[-1])} features, weight '{key}' expects {in_f}.")
-    S = int(xb.shape[0])
+    in_f = int(packed.shape[2])
+    if int(x.shape[-1]) != in_f:
+        raise ValueError(f"x has {int(x.shape[-1])} features, weight '{key}' expects {in_f}.")
+    xb = x.detach().to(torch.bfloat16).contiguous()
     adapter = module.expert_lora[key] if key in module.expert_lora else None
-    keep = []
+    return device, counts, xb, packed, adapter
+
+
+def _single_lora(adapter, device):
     if adapter is None:
-        lora = nat.MxLora(None, None, 0, 0.0)
-    else:
-        a, b = adapter.kernel_factors(device)
-        keep = [a, b]
-        lora = nat.MxLora(a.data_ptr(), b.data_ptr(), adapter.padded_rank(), float(adapter.scale()))
+        return nat.MxLora(None, None, 0, 0.0), [], 0
+    a, b = adapter.kernel_factors(device)
+    return (nat.MxLora(a.data_ptr(), b.data_ptr(), adapter.padded_rank(), float(adapter.scale())),
+            [a, b], adapter.padded_rank())
+
+
+def _grouped_linear_forward(module, key, device, counts, xb, packed, adapter):
+    S = int(xb.shape[0])
+    out_f = int(packed.shape[1])
+    lora, keep, rank = _single_lora(adapter, device)
     out = torch.empty((S, out_f), dtype=torch.bfloat16, device=device)
     lib = nat.load_library()
-    rank = adapter.padded_rank() if adapter is not None else 0
-    ws = nat.workspace(lib.mx_moe_workspace_size(S, 1, module.num_experts, in_f, out_f, rank),
-                       device)
+    ws = nat.workspace(lib.mx_moe_workspace_size(S, 1, module.num_experts, int(packed.shape[2]),
+                                                 out_f, rank), device)
     nat.call("mx_grouped_linear", xb.data_ptr(), counts.data_ptr(), S, module.num_experts,
              packed.descriptor(), lora, out.data_ptr(), ws.data_ptr(), nat.stream(device))
     del keep
     if S > 0:
         nat.watch_plan_errors(ws, device, "a grouped_linear call")
-    return out.to(x.dtype)
+    return out
+
+
+class _GroupedLinear(torch.autograd.Function):
+    """grouped_linear with gradients to x and to the projection's LoRA factors:
+    the autograd of _FrozenGroupedMMLinear (torch_grouped.py:53-91, dX through
+    the re-decoded frozen weight) plus ActiveExpertLoRA.grouped_forward
+    (active_expert_lora.py:348-399), one mx_grouped_linear_backward call."""
+
+    @staticmethod
+    def forward(ctx, module, key, x, offsets, *lora_params):
+        device, counts, xb, packed, adapter = _grouped_inputs(module, key, x, offsets)
+        out = _grouped_linear_forward(module, key, device, counts, xb, packed, adapter)
+        ctx.module, ctx.key, ctx.x_dtype = module, key, x.dtype
+        ctx.save_for_backward(xb, counts)
+        return out.to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        xb, counts = ctx.saved_tensors
+        module, key = ctx.module, ctx.key
+        device = xb.device
+        packed = module.packed_weight(key)
+        adapter = module.expert_lora[key] if key in module.expert_lora else None
+        S, in_f = (int(v) for v in xb.shape)
+        out_f = int(packed.shape[1])
+        E = module.num_experts
+        lora, keep, rank = _single_lora(adapter, device)
+        need_x = ctx.needs_input_grad[2]
+        need_a = adapter is not None and ctx.needs_input_grad[4]
+        need_b = adapter is not None and ctx.needs_input_grad[5]
+        if not (need_x or need_a or need_b):
+            return (None,) * (4 + len(ctx.needs_input_grad[4:]))
+        g = grad_out.detach().to(torch.bfloat16).contiguous()
+        grad_x = torch.empty((S, in_f), dtype=torch.bfloat16, device=device) if need_x else None
+        ga = gb = None
+        if adapter is not None:
+            # The kernel writes both factor gradients together.
+            ga = torch.empty((E, rank, in_f), dtype=torch.float32, device=device)
+            gb = torch.empty((E, out_f, rank), dtype=torch.float32, device=device)
+        lib = nat.load_library()
+        ws = nat.workspace(lib.mx_grouped_linear_backward_workspace_size(S, E, in_f, out_f, rank),
+                           device)
+        nat.call("mx_grouped_linear_backward", g.data_ptr(), xb.data_ptr(), counts.data_ptr(), S,
+                 E, packed.descriptor(), lora, nat.ptr(grad_x), nat.ptr(ga), nat.ptr(gb),
+                 ws.data_ptr(), nat.stream(device))
+        del keep
+        grads = [grad_x.to(ctx.x_dtype) if need_x else None, None]
+        if adapter is None:
+            return (None, None, *grads)
+        r = adapter.rank
+        grads.append(ga[:, :r, :].to(adapter.lora_a.dtype) if need_a else None)
+        grads.append(gb[:, :, :r].contiguous().to(adapter.lora_b.dtype) if need_b else None)
+        return (None, None, *grads)
+
+
+def grouped_projection(module, key, x, offsets):
+    """x [S, in] rows grouped by expert with inclusive int32 offsets -> [S, out],
+    with autograd to x and the LoRA factors when either requires a gradient."""
+    adapter = module.expert_lora[key] if key in module.expert_lora else None
+    params = [] if adapter is None else [adapter.lora_a, adapter.lora_b]
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (x, *params)):
+        return _GroupedLinear.apply(module, key, x, offsets, *params)
+    device, counts, xb, packed, adapter = _grouped_inputs(module, key, x, offsets)
+    return _grouped_linear_forward(module, key, device, counts, xb, packed, adapter).to(x.dtype)

@@ -37,21 +37,64 @@ class Magi2QuantizedExpertError(ValueError):
     restored (quantized_experts.py:63-64)."""
 
 
-def _dtype_name(dtype: torch.dtype) -> str:
-    return str(dtype).removeprefix("torch.")
+def _route_heads_native(logits, top_k, score_func, bias, route_norm, norm_eps, route_scale,
+                        num_virtual_group, topk_virtual_group, layout, score_dtype):
+    H, S, E = (int(v) for v in logits.shape)
+    device = logits.device
+    shape = (H, S, int(top_k)) if layout == "heads" else (S * H, int(top_k))
+    idx = torch.empty(shape, dtype=torch.int64, device=device)
+    probs = torch.empty(shape, dtype=score_dtype, device=device)
+    nat.call("mx_route_topk_heads", logits.data_ptr(), H, S, E, int(top_k),
+             SCORE_FUNCS[score_func], nat.ptr(bias),
+             nat.RENORM_CLAMP if route_norm else nat.RENORM_NONE, float(norm_eps),
+             float(route_scale), int(num_virtual_group), int(topk_virtual_group),
+             _LAYOUTS[layout], idx.data_ptr(), probs.data_ptr(), nat.dtype_code(score_dtype),
+             nat.stream(device))
+    return probs, idx
 
 
-def _parse_dtype(value: object) -> torch.dtype:
-    dtype = getattr(torch, str(value), None)
-    if not isinstance(dtype, torch.dtype):
-        raise Magi2QuantizedExpertError(f"Packed MAGI-2 store declares unknown dtype '{value}'.")
-    return dtype
+class _HeadRoutes(torch.autograd.Function):
+    """Per-head routing with the gradient of the probabilities back to the
+    logits: the autograd of _compute_topk_probs_and_indices_torch_impl
+    (route.py:28-148; softmax / sigmoid, gather, F.normalize(p=1, eps)) and
+    CoreMultiHeadMoE._route's `* route_scale` (magi2_preview.py:2741), one
+    mx_route_scores_backward call over the H * S logits rows."""
+
+    @staticmethod
+    def forward(ctx, logits_in, args):
+        logits = logits_in.detach().float().contiguous()
+        probs, idx = _route_heads_native(logits, *args)
+        ctx.mark_non_differentiable(idx)
+        ctx.args = args
+        ctx.logits_dtype = logits_in.dtype
+        ctx.save_for_backward(logits, idx)
+        return probs, idx
+
+    @staticmethod
+    def backward(ctx, g_probs, _g_idx):
+        logits, idx = ctx.saved_tensors
+        top_k, score_func, _bias, route_norm, norm_eps, route_scale, _, _, layout, _ = ctx.args
+        H, S, E = (int(v) for v in logits.shape)
+        g = g_probs.float()
+        if layout == "rows":
+            # rows s*H+h with group ids h*E+e -> [H, S, k] per-head expert ids
+            heads = torch.arange(H, device=idx.device).view(1, H, 1) * E
+            idx = (idx.view(S, H, top_k) - heads).permute(1, 0, 2)
+            g = g.view(S, H, top_k).permute(1, 0, 2)
+        from .router import router_scores_backward
+
+        dl = router_scores_backward(logits.view(H * S, E), idx.reshape(H * S, top_k),
+                                    g.reshape(H * S, top_k), score_func=score_func,
+                                    renorm=nat.RENORM_CLAMP if route_norm else nat.RENORM_NONE,
+                                    renorm_floor=norm_eps, route_scale=route_scale)
+        return dl.view(H, S, E).to(ctx.logits_dtype), None
 
 
 def route_topk_heads(router_logits: torch.Tensor, top_k: int, *, score_func: str = "sigmoid",
                      expert_bias: torch.Tensor | None = None, route_norm: bool = True,
-                     norm_eps: float = 1e-12, route_scale: float = 1.0, layout: str = "heads",
-                     score_dtype: torch.dtype = torch.float32):
+                     norm_eps: float = 1e-12, route_scale: float = 1.0,
+                     num_virtual_group: int = 1, topk_virtual_group: int = 0,
+                     layout: str = "heads", score_dtype: torch.dtype = torch.float32):
     """Multi-head top-k routing of fp32 logits [H, S, E] on the GPU.
 
     Returns ``(probs, indices)``: with layout "heads" both are [H, S, k] and the
@@ -60,7 +103,10 @@ def route_topk_heads(router_logits: torch.Tensor, top_k: int, *, score_func: str
     does, magi2_preview.py:2735-2742); with layout "rows" both are [S*H, k], row
     s*H+h, and the indices are flattened group ids h*E+e, ready for
     Magi2GroupedExperts.run_rows. Selection is by score + expert_bias (ties to
-    the lower expert id); the probabilities carry no gradient here.
+    the lower expert id), within the topk_virtual_group best of
+    num_virtual_group expert groups when num_virtual_group > 1
+    (route.py:62-105). When the logits require a gradient, the probabilities
+    carry one back to them.
     """
     if router_logits.ndim != 3:
         raise ValueError("router logits must be [heads, tokens, experts].")
@@ -68,27 +114,25 @@ def route_topk_heads(router_logits: torch.Tensor, top_k: int, *, score_func: str
         raise ValueError(f"Unknown score_func: {score_func}")
     if layout not in _LAYOUTS:
         raise ValueError(f"layout must be one of {sorted(_LAYOUTS)}.")
-    if torch.is_grad_enabled() and router_logits.requires_grad:
-        raise NotImplementedError(
-            "route_topk_heads computes routes without a router gradient; call it under "
-            "torch.no_grad() or on detached logits")
     H, S, E = (int(v) for v in router_logits.shape)
     if int(top_k) <= 0 or int(top_k) > min(E, 16):
         raise ValueError("top_k must be in [1, min(num_experts, 16)].")
+    nvg, tvg = int(num_virtual_group), int(topk_virtual_group)
+    if nvg > 1 and not (0 < tvg <= nvg):
+        raise ValueError(
+            f"topk_virtual_group ({tvg}) must be in (0, num_virtual_group ({nvg})]")
+    if nvg > 1 and E % nvg:
+        raise ValueError(f"num_experts ({E}) must be divisible by num_virtual_group ({nvg})")
     device = nat.require_gpu(router_logits)
-    logits = router_logits.detach().float().contiguous()
     bias = None
     if expert_bias is not None:
         bias = expert_bias.detach().to(device=device, dtype=torch.float32).reshape(H, E)
         bias = bias.contiguous()
-    shape = (H, S, int(top_k)) if layout == "heads" else (S * H, int(top_k))
-    idx = torch.empty(shape, dtype=torch.int64, device=device)
-    probs = torch.empty(shape, dtype=score_dtype, device=device)
-    nat.call("mx_route_topk_heads", logits.data_ptr(), H, S, E, int(top_k), SCORE_FUNCS[score_func],
-             nat.ptr(bias), nat.RENORM_CLAMP if route_norm else nat.RENORM_NONE, float(norm_eps),
-             float(route_scale), _LAYOUTS[layout], idx.data_ptr(), probs.data_ptr(),
-             nat.dtype_code(score_dtype), nat.stream(device))
-    return probs, idx
+    args = (int(top_k), score_func, bias, bool(route_norm), float(norm_eps), float(route_scale),
+            nvg, tvg, layout, score_dtype)
+    if torch.is_grad_enabled() and router_logits.requires_grad:
+        return _HeadRoutes.apply(router_logits, args)
+    return _route_heads_native(router_logits.detach().float().contiguous(), *args)
 
 
 def compute_topk_probs_and_indices(router_logits: torch.Tensor, top_k: int,
@@ -97,11 +141,11 @@ def compute_topk_probs_and_indices(router_logits: torch.Tensor, top_k: int,
                                    num_virtual_group: int = 1, topk_virtual_group: int = 0,
                                    route_norm: bool = True, norm_eps: float = 1e-12):
     """Drop-in for flash_mh_moe.route.compute_topk_probs_and_indices
-    (flash_mh_moe/route.py:157-196) without virtual groups."""
-    if int(num_virtual_group) != 1:
-        raise NotImplementedError("virtual-group routing (num_virtual_group > 1) is not built")
+    (flash_mh_moe/route.py:157-196)."""
     return route_topk_heads(router_logits, top_k, score_func=score_func, expert_bias=expert_bias,
-                            route_norm=route_norm, norm_eps=norm_eps)
+                            route_norm=route_norm, norm_eps=norm_eps,
+                            num_virtual_group=num_virtual_group,
+                            topk_virtual_group=topk_virtual_group)
 
 
 class Magi2GroupedExperts(nn.Module):
@@ -164,71 +208,6 @@ class Magi2GroupedExperts(nn.Module):
     def quantized_numel(self) -> int:
         return int(sum(g * a * b for g, a, b in self._source_shapes.values()))
 
-    def packed_state_descriptor(self) -> dict[str, object]:
-        """Metadata that restores this exact payload (quantized_experts.py:140-163):
-        group count, block size, the reference shapes and dtypes of the three
-        tensors, the storage format and the buffer inventory. The payload is this
-        build's packed layout ([G, out, in] codes or int8 values and their scales),
-        restored as stored, never through dense weights."""
-        if not self.is_fully_loaded():
-            raise Magi2QuantizedExpertError(
-                "MAGI-2 NF4 store must be complete before it can be persisted.")
-        fmt = self.experts.quant_format
-        meta: dict[str, object] = {"format": fmt, "blocksize": NF4_BLOCKSIZE}
-        if fmt == "nf4":
-            scale = getattr(self.experts, self.experts.packed_buffer_names("W_gate")[1])
-            meta["absmax_dtype"] = _dtype_name(scale.dtype)
-        return {
-            "num_groups": self.num_groups,
-            "blocksize": NF4_BLOCKSIZE,
-            "expert_shapes": {k: list(self._source_shapes[k]) for k in MAGI2_ROUTED_EXPERT_TENSOR_NAMES},
-            "expert_dtypes": {k: _dtype_name(self._source_dtypes[k])
-                              for k in MAGI2_ROUTED_EXPERT_TENSOR_NAMES},
-            "packed_meta": meta,
-            "buffers": sorted(self.packed_buffers()),
-        }
-
-    def restore_packed_state(self, *, descriptor: dict[str, object],
-                             buffers: dict[str, torch.Tensor]) -> None:
-        """Restore a validated persisted payload without dense reconstruction
-        (quantized_experts.py:165-219)."""
-        if int(descriptor.get("num_groups", -1)) != self.num_groups:
-            raise Magi2QuantizedExpertError("Packed MAGI-2 store has incompatible groups.")
-        if int(descriptor.get("blocksize", -1)) != NF4_BLOCKSIZE:
-            raise Magi2QuantizedExpertError("Packed MAGI-2 store has incompatible NF4 blocksize.")
-        shapes, dtypes = descriptor.get("expert_shapes"), descriptor.get("expert_dtypes")
-        if not isinstance(shapes, dict) or not isinstance(dtypes, dict):
-            raise Magi2QuantizedExpertError("Packed MAGI-2 store has incomplete tensor metadata.")
-        names = set(MAGI2_ROUTED_EXPERT_TENSOR_NAMES)
-        if set(shapes) != names or set(dtypes) != names:
-            raise Magi2QuantizedExpertError("Packed MAGI-2 store has incomplete expert metadata.")
-        meta = descriptor.get("packed_meta")
-        if not isinstance(meta, dict):
-            raise Magi2QuantizedExpertError("Packed MAGI-2 store has no NF4 metadata.")
-        if str(meta.get("format")) != self.experts.quant_format:
-            raise Magi2QuantizedExpertError(
-                f"Packed MAGI-2 store holds '{meta.get('format')}' weights, this module "
-                f"stores '{self.experts.quant_format}'.")
-        parsed_dtypes = {k: _parse_dtype(dtypes[k]) for k in names}
-        parsed_shapes = {}
-        for k in names:
-            shape = tuple(int(v) for v in shapes[k])
-            if len(shape) != 3 or shape[0] != self.num_groups:
-                raise Magi2QuantizedExpertError(
-                    f"Packed MAGI-2 store gives {k} the shape {shape}.")
-            parsed_shapes[k] = shape
-        if set(descriptor.get("buffers", [])) != set(buffers):
-            raise Magi2QuantizedExpertError(
-                "Packed MAGI-2 store buffer inventory does not match its descriptor.")
-        for key in MAGI2_ROUTED_EXPERT_TENSOR_NAMES:
-            g, rows, cols = parsed_shapes[key]
-            try:
-                self.experts.adopt_packed(key, buffers, (g, cols, rows))
-            except ValueError as err:
-                raise Magi2QuantizedExpertError(f"Packed MAGI-2 store: {err}") from err
-            self._source_shapes[key] = parsed_shapes[key]
-            self._source_dtypes[key] = parsed_dtypes[key]
-
     @classmethod
     def from_dense(cls, W_gate: torch.Tensor, W_up: torch.Tensor, W_down: torch.Tensor, *,
                    num_heads: int, quant_format: str = "nf4", **kwargs) -> "Magi2GroupedExperts":
@@ -288,113 +267,10 @@ class Magi2GroupedExperts(nn.Module):
                 route_norm: bool = True, route_scale: float = 1.0) -> torch.Tensor:
         """Route [H, S, E] logits and run the experts: [S, H, d_head] out."""
         S, H, d = (int(v) for v in x_heads.shape)
-        with torch.no_grad():
-            probs, groups = route_topk_heads(router_logits, top_k, score_func=score_func,
-                                             expert_bias=expert_bias, route_norm=route_norm,
-                                             route_scale=route_scale, layout="rows")
+        probs, groups = route_topk_heads(router_logits, top_k, score_func=score_func,
+                                         expert_bias=expert_bias, route_norm=route_norm,
+                                         route_scale=route_scale, layout="rows")
         return self.run_rows(x_heads.reshape(S * H, d), probs, groups).view(S, H, d)
-
-
-MAGI2_PACKED_SCHEMA = "mirai_amd.magi2.packed_experts"
-MAGI2_PACKED_SCHEMA_VERSION = 1
-_MANIFEST = "manifest.json"
-
-
-class Magi2PackedExpertStateError(ValueError):
-    """Raised when a packed MAGI-2 expert artifact is incompatible
-    (packed_experts.py:24-25)."""
-
-
-def _magi2_layers(model) -> dict[str, Magi2GroupedExperts]:
-    if isinstance(model, dict):
-        return dict(model)
-    if isinstance(model, Magi2GroupedExperts):
-        return {"": model}
-    return {name: m for name, m in model.named_modules() if isinstance(m, Magi2GroupedExperts)}
-
-
-def save_magi2_packed_state(path, model, *, metadata: dict | None = None):
-    """Write every layer's packed payload (one safetensors shard per layer) and a
-    versioned manifest holding each layer's descriptor, with no dense
-    reconstruction (save_magi2_nf4_packed_state, packed_experts.py:28-78).
-    ``model``: a module holding Magi2GroupedExperts layers, one such layer, or a
-    {name: layer} mapping."""
-    import json
-    from pathlib import Path
-
-    from safetensors.torch import save_file
-
-    target = Path(path).expanduser()
-    if target.exists() and any(target.iterdir()):
-        raise FileExistsError(f"Packed MAGI-2 export directory must be empty: {target}")
-    target.mkdir(parents=True, exist_ok=True)
-    layers = {}
-    for index, (name, layer) in enumerate(_magi2_layers(model).items()):
-        if not layer.is_fully_loaded():
-            raise Magi2PackedExpertStateError(
-                f"MAGI-2 layer '{name}' has no complete packed expert store.")
-        descriptor = layer.packed_state_descriptor()
-        shard = f"layer_{index:03d}.safetensors"
-        save_file({k: v.detach().cpu().contiguous() for k, v in layer.packed_buffers().items()},
-                  str(target / shard))
-        layers[name] = {"shard": shard, **descriptor}
-    if not layers:
-        raise Magi2PackedExpertStateError("MAGI-2 packed expert export matched no routed-expert layers.")
-    manifest = {"schema": MAGI2_PACKED_SCHEMA, "schema_version": MAGI2_PACKED_SCHEMA_VERSION,
-                "layers": layers, "metadata": dict(metadata or {})}
-    (target / _MANIFEST).write_text(json.dumps(manifest, indent=2, sort_keys=True), encoding="utf-8")
-    return target
-
-
-def load_magi2_packed_state(path, model, *, expected_metadata: dict | None = None,
-                            device=None) -> dict[str, Magi2GroupedExperts]:
-    """Restore every layer's payload from ``save_magi2_packed_state`` output,
-    rejecting schema, lineage, layer-inventory and buffer mismatches
-    (load_magi2_nf4_packed_state, packed_experts.py:81-183). Tensors land on
-    ``device`` (default: the current GPU)."""
-    import json
-    from pathlib import Path
-
-    from safetensors import safe_open
-
-    source = Path(path).expanduser()
-    if not source.is_dir():
-        raise FileNotFoundError(f"Packed MAGI-2 expert state not found: {source}")
-    layers = _magi2_layers(model)
-    manifest_path = source / _MANIFEST
-    if not manifest_path.is_file():
-        raise Magi2PackedExpertStateError("Packed MAGI-2 expert state has no versioned manifest.")
-    manifest = json.loads(manifest_path.read_text(encoding="utf-8"))
-    if manifest.get("schema") != MAGI2_PACKED_SCHEMA or int(
-            manifest.get("schema_version", -1)) != MAGI2_PACKED_SCHEMA_VERSION:
-        raise Magi2PackedExpertStateError(
-            "Packed MAGI-2 expert state has an unsupported schema or version.")
-    lineage = manifest.get("metadata")
-    if not isinstance(lineage, dict):
-        raise Magi2PackedExpertStateError("Packed MAGI-2 expert state has invalid lineage metadata.")
-    for key, value in (expected_metadata or {}).items():
-        if str(lineage.get(key, "")) != str(value):
-            raise Magi2PackedExpertStateError(f"Packed MAGI-2 expert state has incompatible {key}.")
-    specs = manifest.get("layers")
-    if not isinstance(specs, dict) or set(specs) != set(layers):
-        raise Magi2PackedExpertStateError(
-            "Packed MAGI-2 expert layer inventory does not match the model.")
-    target = torch.device(device) if device is not None else torch.device("cuda")
-    for name, layer in layers.items():
-        spec = specs[name]
-        shard = str(spec.get("shard", ""))
-        if not shard or Path(shard).name != shard:
-            raise Magi2PackedExpertStateError(f"Packed MAGI-2 layer '{name}' has an invalid shard path.")
-        shard_path = source / shard
-        if not shard_path.is_file():
-            raise Magi2PackedExpertStateError(f"Packed MAGI-2 layer '{name}' is missing shard '{shard}'.")
-        with safe_open(str(shard_path), framework="pt", device="cpu") as handle:
-            if set(handle.keys()) != set(spec.get("buffers", [])):
-                raise Magi2PackedExpertStateError(
-                    f"Packed MAGI-2 layer '{name}' shard inventory is invalid.")
-            buffers = {k: handle.get_tensor(k).to(target).contiguous() for k in handle.keys()}
-        layer.restore_packed_state(descriptor=spec, buffers=buffers)
-    return layers
 
 
 class Magi2FusedMoEBackend:

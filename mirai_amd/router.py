@@ -1,13 +1,14 @@
 """Fused router front end on the MI355X kernels.
 
-``FusedRouter`` is a drop-in for the inference path of LingBotVideoRouter
+``FusedRouter`` is a drop-in for LingBotVideoRouter's standard path
 (mirai/vendors/lingbot_video/transformer_lingbot_video.py:502-560, 962-1033):
 same constructor arguments, parameter and buffer names (``weight`` [E, d]
 fp32, ``e_score_correction_bias`` [E]), same forward signature and return
 tuple. One HIP kernel (mx_router_forward) computes the fp32 router GEMM, the
 softmax / sigmoid scores, the bias-steered (optionally group-limited) top-k
 selection, the renormalisation and route_scale; the logits and scores come
-out of the same pass.
+out of the same pass. In training the gating scores carry gradients back to
+the tokens, the router weight and the logit delta (``_FusedRouterFn``).
 """
 
 from __future__ import annotations
@@ -76,8 +77,66 @@ def fused_router_forward(tokens: torch.Tensor, planes: torch.Tensor, num_experts
     return idx, top, logits, scores
 
 
+def router_scores_backward(logits: torch.Tensor, top_idx: torch.Tensor, grad_top: torch.Tensor,
+                           *, score_func: str, renorm: int, renorm_floor: float,
+                           route_scale: float) -> torch.Tensor:
+    """d(logits) [rows, E] fp32 from d(top_scores) [rows, k] (mx_route_scores_backward)."""
+    device = nat.require_gpu(logits, top_idx, grad_top)
+    rows, E = (int(v) for v in logits.shape)
+    k = int(top_idx.shape[-1])
+    lg = logits.detach().float().contiguous()
+    idx = top_idx.detach().to(torch.int64).reshape(rows, k).contiguous()
+    g = grad_top.detach().float().reshape(rows, k).contiguous()
+    out = torch.empty((rows, E), dtype=torch.float32, device=device)
+    nat.call("mx_route_scores_backward", lg.data_ptr(), rows, E, k, SCORE_FUNCS[score_func],
+             int(renorm), float(renorm_floor), float(route_scale), idx.data_ptr(), g.data_ptr(),
+             out.data_ptr(), nat.stream(device))
+    return out
+
+
+class _FusedRouterFn(torch.autograd.Function):
+    """The fused router with gradients through the gating scores: d top_scores
+    -> d logits (softmax / sigmoid Jacobian through the `/ (sum + 1e-20)`
+    renormalisation and route_scale, mx_route_scores_backward), then the fp32
+    router GEMM's d tokens = d logits . W, d W = d logits^T . tokens.float()
+    and d logit_delta = d logits: the autograd of LingBotVideoRouter.forward
+    (transformer_lingbot_video.py:975-1033). Indices, logits and scores are
+    returned without gradients."""
+
+    @staticmethod
+    def forward(ctx, router, tokens, weight, logit_delta):
+        idx, top, logits, scores = fused_router_forward(
+            tokens, router.weight_planes(), router.num_experts, router.top_k,
+            score_func=router.score_func, expert_bias=router.e_score_correction_bias,
+            logit_delta=logit_delta, norm_topk_prob=router.norm_topk_prob, n_group=router.n_group,
+            topk_group=router.topk_group, route_scale=router.route_scale)
+        ctx.mark_non_differentiable(idx, logits, scores)
+        ctx.cfg = (router.score_func, router.top_k > 1 and router.norm_topk_prob,
+                   float(router.route_scale), tokens.dtype)
+        ctx.save_for_backward(tokens, weight, logits, idx)
+        return idx, top, logits, scores
+
+    @staticmethod
+    def backward(ctx, _g_idx, g_top, _g_logits, _g_scores):
+        tokens, weight, logits, idx = ctx.saved_tensors
+        score_func, renorm, route_scale, token_dtype = ctx.cfg
+        if g_top is None:
+            return None, None, None, None
+        dl = router_scores_backward(logits, idx, g_top, score_func=score_func,
+                                    renorm=nat.RENORM_EPS if renorm else nat.RENORM_NONE,
+                                    renorm_floor=1e-20, route_scale=route_scale)
+        g_tokens = g_weight = g_delta = None
+        if ctx.needs_input_grad[1]:
+            g_tokens = (dl @ weight.detach().float()).to(token_dtype)
+        if ctx.needs_input_grad[2]:
+            g_weight = (dl.t() @ tokens.detach().float()).to(weight.dtype)
+        if ctx.needs_input_grad[3]:
+            g_delta = dl
+        return None, g_tokens, g_weight, g_delta
+
+
 class FusedRouter(nn.Module):
-    """LingBotVideoRouter's inference path as one kernel.
+    """LingBotVideoRouter's standard path as one kernel, with its backward.
 
     The asymmetry of the reference is kept: selection uses the bias-added
     score, the gating weights gather the bias-free score.
@@ -130,12 +189,19 @@ class FusedRouter(nn.Module):
                 valid_token_mask: torch.Tensor | None = None,
                 route_scope_mask: torch.Tensor | None = None):
         """Returns (top_indices, top_scores in tokens' dtype, logits, scores,
-        scores_for_choice), as the reference does (:1132)."""
+        scores_for_choice), as the reference does (:1132). When tokens, the
+        router weight or logit_delta require a gradient, top_scores carries
+        one back to them (the other outputs are returned without gradients)."""
         del valid_token_mask, route_scope_mask  # consumed by extensions only
-        if torch.is_grad_enabled() and (tokens.requires_grad or self.weight.requires_grad):
-            raise NotImplementedError(
-                "FusedRouter is the inference front end: call it under torch.no_grad() (or "
-                "freeze the router weight and detach the tokens) for routing without gradients")
+        if torch.is_grad_enabled() and any(
+                t is not None and t.requires_grad for t in (tokens, self.weight, logit_delta)):
+            idx, top, logits, scores = _FusedRouterFn.apply(self, tokens, self.weight,
+                                                             logit_delta)
+            choice = scores + self.e_score_correction_bias.float().unsqueeze(0)
+            self.last_top_indices = idx
+            self.last_top_scores = top.detach()
+            self.last_scores = scores
+            return idx, top, logits, scores, choice
         idx, top, logits, scores = fused_router_forward(
             tokens, self.weight_planes(), self.num_experts, self.top_k,
             score_func=self.score_func, expert_bias=self.e_score_correction_bias,

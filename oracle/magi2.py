@@ -3,9 +3,10 @@ on the CPU -- TEST INFRASTRUCTURE ONLY (the checker for the HIP path; the
 product package never imports it).
 
 * Routing follows _compute_topk_probs_and_indices_torch_impl
-  (mirai/vendors/magi2_preview/flash_mh_moe/route.py:28-148) with
-  num_virtual_group = 1: scores = softmax or sigmoid of the [H, S, E] logits,
-  experts picked by score + expert_bias[h] (selection only), probabilities
+  (mirai/vendors/magi2_preview/flash_mh_moe/route.py:28-148): scores =
+  softmax or sigmoid of the [H, S, E] logits, experts picked by score +
+  expert_bias[h] (selection only), within the best virtual groups when
+  num_virtual_group > 1 (route.py:62-105), probabilities
   gathered from the unbiased scores and L1-normalised with eps when
   route_norm; CoreMultiHeadMoE._route then multiplies by route_scale
   (mirai/vendors/magi2_preview/model/magi2_preview.py:2727-2743). Selection
@@ -31,19 +32,42 @@ import torch.nn.functional as F
 SCORE_SOFTMAX, SCORE_SIGMOID = "softmax", "sigmoid"
 
 
+def _scores(logits: torch.Tensor, score_func: str) -> torch.Tensor:
+    if score_func == SCORE_SOFTMAX:
+        return F.softmax(logits, dim=-1)
+    if score_func == SCORE_SIGMOID:
+        return torch.sigmoid(logits)
+    raise ValueError(score_func)
+
+
+def virtual_group_keys(keys: torch.Tensor, num_virtual_group: int,
+                       topk_virtual_group: int) -> torch.Tensor:
+    """route.py:62-105: each of the num_virtual_group groups of consecutive
+    experts scores the sum of its two largest keys (its largest when it holds
+    one expert); the topk_virtual_group best groups keep their keys (ties to
+    the lower group id), all other keys become 0.0."""
+    H, S, E = keys.shape
+    G = int(num_virtual_group)
+    epg = E // G
+    gs = keys.reshape(H, S, G, epg).topk(min(2, epg), dim=-1)[0].sum(dim=-1)
+    keep = np.argsort(-gs.numpy(), axis=-1, kind="stable")[..., :topk_virtual_group]
+    gmask = np.zeros((H, S, G), dtype=bool)
+    np.put_along_axis(gmask, keep, True, axis=-1)
+    emask = torch.from_numpy(np.repeat(gmask, epg, axis=-1))
+    return keys.masked_fill(~emask, 0.0)
+
+
 def route_topk_heads(router_logits: torch.Tensor, top_k: int, *, score_func: str = "sigmoid",
                      expert_bias: torch.Tensor | None = None, route_norm: bool = True,
-                     norm_eps: float = 1e-12, route_scale: float = 1.0):
+                     norm_eps: float = 1e-12, route_scale: float = 1.0,
+                     num_virtual_group: int = 1, topk_virtual_group: int = 0):
     """Return (probs [H,S,k] fp32, indices [H,S,k] int64), slots in selection order."""
     logits = router_logits.detach().float()
-    if score_func == SCORE_SOFTMAX:
-        scores = F.softmax(logits, dim=-1)
-    elif score_func == SCORE_SIGMOID:
-        scores = torch.sigmoid(logits)
-    else:
-        raise ValueError(score_func)
+    scores = _scores(logits, score_func)
     keys = scores if expert_bias is None else scores + expert_bias.float().view(
         logits.shape[0], 1, logits.shape[2])
+    if num_virtual_group > 1:
+        keys = virtual_group_keys(keys, num_virtual_group, topk_virtual_group)
     H, S, E = keys.shape
     kn = keys.numpy().reshape(H * S, E)
     # Canonical order: descending key, ties to the lower expert id (stable).
@@ -53,6 +77,19 @@ def route_topk_heads(router_logits: torch.Tensor, top_k: int, *, score_func: str
     if route_norm:
         probs = F.normalize(probs, p=1, dim=-1, eps=norm_eps)
     return probs * route_scale, idx
+
+
+def route_probs_for_picks(router_logits: torch.Tensor, idx: torch.Tensor, *,
+                          score_func: str = "sigmoid", route_norm: bool = True,
+                          norm_eps: float = 1e-12, route_scale: float = 1.0) -> torch.Tensor:
+    """The probabilities of given picks idx [H,S,k] as torch ops on the logits
+    (autograd-capable; route.py:115-147 and the `* route_scale` of
+    magi2_preview.py:2741): the backward oracle of the routing."""
+    z = router_logits.to(torch.promote_types(router_logits.dtype, torch.float32))
+    probs = _scores(z, score_func).gather(-1, idx)
+    if route_norm:
+        probs = F.normalize(probs, p=1, dim=-1, eps=norm_eps)
+    return probs * route_scale
 
 
 def heads_to_rows(probs: torch.Tensor, idx: torch.Tensor, num_experts: int):

@@ -55,7 +55,8 @@ def group_mask(keys: torch.Tensor, n_group: int, topk_group: int) -> torch.Tenso
 def route_from_logits(logits: torch.Tensor, top_k: int, *, score_func: str = "sigmoid",
                       expert_bias: torch.Tensor | None = None, norm_topk_prob: bool = True,
                       n_group: int | None = None, topk_group: int | None = None,
-                      route_scale: float = 1.0, out_dtype: torch.dtype = torch.float32):
+                      route_scale: float = 1.0, out_dtype: torch.dtype = torch.float32,
+                      picks: torch.Tensor | None = None):
     """Selection and scores from fp32 logits: (top_idx int64 [T,k], top_scores [T,k],
     scores [T,E] fp32, scores_for_choice [T,E] fp32)."""
     logits = logits.float()
@@ -67,22 +68,29 @@ def route_from_logits(logits: torch.Tensor, top_k: int, *, score_func: str = "si
         raise ValueError(score_func)
     return route_from_scores(scores, top_k, expert_bias=expert_bias,
                              norm_topk_prob=norm_topk_prob, n_group=n_group,
-                             topk_group=topk_group, route_scale=route_scale, out_dtype=out_dtype)
+                             topk_group=topk_group, route_scale=route_scale, out_dtype=out_dtype,
+                             picks=picks)
 
 
 def route_from_scores(scores: torch.Tensor, top_k: int, *,
                       expert_bias: torch.Tensor | None = None, norm_topk_prob: bool = True,
                       n_group: int | None = None, topk_group: int | None = None,
-                      route_scale: float = 1.0, out_dtype: torch.dtype = torch.float32):
-    """The selection and gating of :1006-1033 from fp32 scores [T, E]."""
+                      route_scale: float = 1.0, out_dtype: torch.dtype = torch.float32,
+                      picks: torch.Tensor | None = None):
+    """The selection and gating of :1006-1033 from fp32 scores [T, E]. With
+    ``picks`` [T, k] the selection is taken as given (only the gating is
+    computed): the autograd-capable path of the backward checks."""
     scores = scores.float()
     bias = torch.zeros(scores.shape[1]) if expert_bias is None else expert_bias.float()
     choice = scores + bias.unsqueeze(0)
-    keys = choice
+    keys = choice.detach()
     if n_group is not None and n_group > 1:
-        keep = group_mask(choice, n_group, topk_group)
-        keys = choice.masked_fill(~keep, float("-inf"))
-    idx = torch.from_numpy(_topk_desc(keys.numpy(), top_k).astype(np.int64))
+        keep = group_mask(keys, n_group, topk_group)
+        keys = keys.masked_fill(~keep, float("-inf"))
+    if picks is not None:
+        idx = picks.to(torch.int64)
+    else:
+        idx = torch.from_numpy(_topk_desc(keys.numpy(), top_k).astype(np.int64))
     top = scores.gather(1, idx)
     if top_k > 1 and norm_topk_prob:
         top = top / (top.sum(dim=-1, keepdim=True) + 1e-20)

@@ -7,7 +7,7 @@ reduction in fp32 and rounds intermediates (dy, dh, dG, dU, dz) to bf16 where
 the bf16 reference composition does, but the reference's autograd also sums
 the k routes of a token and the base/LoRA parts of each gradient in bf16, in
 an order torch does not fix. Bounds (stated per gradient, relative to the
-oracle): mean-relative error <= 1e-2 and max-abs error <= 3e-2 * max|oracle|.
+oracle): mean-relative error <= 5e-3 and max-abs error <= 3e-2 * max|oracle|.
 Production tile shapes: experts averaging >= 256 rows run 256-row tiles plus
 one 128-row remainder tile per expert whose last rows number 1..128 (an
 expert whose last rows number 129..255 gets a partial 256-row tile). The
@@ -31,7 +31,7 @@ from helpers import build_module, mixed_rank_factors, oracle_weights
 
 pytestmark = pytest.mark.gpu
 
-MEAN_REL = 1e-2
+MEAN_REL = 5e-3
 MAX_REL = 3e-2
 
 

@@ -7,7 +7,7 @@ chunk, so the chunked forward output and token / score gradients are the
 unchunked layer's bit for bit; the LoRA factor gradients are fp32 sums over
 chunks (order of the sum differs: relative 1e-5). Against the oracle the
 layer tolerance holds (max-abs 2e-2 / mean-rel 5e-3) and the gradients meet
-the backward bound (mean-rel <= 1e-2, max <= 3e-2 of the oracle's max).
+the backward bound (mean-rel <= 5e-3, max <= 3e-2 of the oracle's max).
 """
 
 import pytest
@@ -22,7 +22,7 @@ from helpers import assert_layer_close, build_module, oracle_weights
 
 pytestmark = pytest.mark.gpu
 
-MEAN_REL = 1e-2
+MEAN_REL = 5e-3
 MAX_REL = 3e-2
 
 

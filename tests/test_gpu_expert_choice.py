@@ -102,7 +102,7 @@ def test_reference_contract_routes():
         m.run_expert_choice_routed(x.cuda(), scores.cuda(), idx.cuda(), tokens_per_sample=2)
 
 
-def _close_grad(name, actual, expected, mean_rel=1e-2, max_rel=3e-2):
+def _close_grad(name, actual, expected, mean_rel=5e-3, max_rel=3e-2):
     a, e = actual.detach().float().cpu(), expected.detach().float().cpu()
     diff = (a - e).abs()
     stats = {"mean_rel": float(diff.sum() / e.abs().sum().clamp_min(1e-30)),
@@ -117,7 +117,7 @@ def _close_grad(name, actual, expected, mean_rel=1e-2, max_rel=3e-2):
 def test_backward_matches_oracle_autograd(fmt, alias, rank):
     # Gradients to tokens, [B, L, C] scores and every LoRA factor against torch
     # autograd through the oracle's gather / per-expert MLP / index_add
-    # composition (bounds as the token-choice backward: mean-rel 1e-2, max
+    # composition (bounds as the token-choice backward: mean-rel 5e-3, max
     # 3e-2 of the oracle's max). Tokens picked by several experts sum their
     # slots' dx rows; tokens no expert picked get zero.
     B, L, C, tps = 2, 8, 24, 96

@@ -131,27 +131,6 @@ def test_run_for_loop_with_swiglu7_matches_oracle():
     print(f"magi2 for-loop: {assert_layer_close(out.cpu(), ref[order])}")
 
 
-@pytest.mark.parametrize("fmt", ["nf4", "int8"])
-def test_packed_state_restores_the_exact_layer(fmt, tmp_path):
-    # Persist the quantised payload (descriptor + safetensors shard), restore it
-    # into a fresh module with no dense weights, and run both: the restored layer
-    # computes bit-identical outputs (quantized_experts.py:140-219,
-    # packed_experts.py:28-183).
-    from mirai_amd import load_magi2_packed_state, save_magi2_packed_state
-
-    dense, x, _, _, probs, idx = _magi2_case(seed=11)
-    m = Magi2GroupedExperts.from_dense(*(dense[k].cuda() for k in ("W_gate", "W_up", "W_down")),
-                                       num_heads=2, quant_format=fmt)
-    path = save_magi2_packed_state(tmp_path / "packed", {"layer": m}, metadata={"seed": "11"})
-    fresh = Magi2GroupedExperts(num_heads=2, num_experts=4, quant_format=fmt)
-    load_magi2_packed_state(path, {"layer": fresh}, expected_metadata={"seed": "11"})
-    assert fresh.packed_state_descriptor() == m.packed_state_descriptor()
-    with torch.no_grad():
-        out = m.execute(x.cuda(), probs.cuda(), idx.cuda())
-        out2 = fresh.execute(x.cuda(), probs.cuda(), idx.cuda())
-    assert torch.equal(out2, out)
-
-
 def test_magi2_layer_at_production_group_count():
     # 12 heads x 256 experts = 3072 groups in one pass (no segmenting).
     dense, x, _, _, probs, idx = _magi2_case(H=12, E=256, d=64, f=64, S=96, k=2, seed=3)

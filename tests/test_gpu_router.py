@@ -146,8 +146,9 @@ def test_module_matches_the_reference_router_surface():
         r.weight.mul_(-1.0)
         idx2, _, logits2, _, _ = r(x.cuda())
     torch.testing.assert_close(logits2, -logits)
-    with pytest.raises(NotImplementedError):
-        r(x.cuda().requires_grad_(True))
+    # With a gradient the scores carry one; the picks are unchanged.
+    idx3, top3, _, _, _ = r(x.cuda().requires_grad_(True))
+    assert top3.requires_grad and torch.equal(idx3, idx2)
 
 
 def test_empty_and_invalid_inputs():

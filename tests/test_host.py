@@ -11,6 +11,8 @@ mirai/core/models/compressed_weights/execution/experts.py:189-196, 544-558,
 import pytest
 import torch
 
+from mirai_amd._native import ROUTE_DROPPED
+
 from mirai_amd import CompressedGroupedExperts, route_topk
 from mirai_amd import _native as nat
 from mirai_amd import quant
@@ -252,7 +254,9 @@ def test_lora_scale_follows_alpha_buffer_updates():
 
 
 def _coalesce_brute(scores, idx, aliases):
-    """coalesce_alias_routes (storage/aliases.py:156-199) one slot at a time."""
+    """coalesce_alias_routes (storage/aliases.py:156-199) one slot at a time,
+    then every slot whose coalesced score is zero left out of the dispatch
+    (experts.py:2361-2367: only nonzero scores are routed with aliases)."""
     T, k = idx.shape
     phys = torch.tensor([[aliases[int(idx[t, j])] for j in range(k)] for t in range(T)])
     out = torch.zeros_like(scores)
@@ -260,6 +264,10 @@ def _coalesce_brute(scores, idx, aliases):
         for j in range(k):
             first = min(i for i in range(k) if phys[t, i] == phys[t, j])
             out[t, first] += scores[t, j]
+    for t in range(T):
+        for j in range(k):
+            if float(out[t, j]) == 0.0:
+                phys[t, j] = ROUTE_DROPPED
     return out, phys
 
 
@@ -276,8 +284,15 @@ def test_logical_alias_coalescing_matches_slot_by_slot_rule():
     want_s, want_p = _coalesce_brute(scores, idx, aliases)
     assert torch.equal(got_p, want_p)
     torch.testing.assert_close(got_s, want_s, rtol=0, atol=1e-7)
-    # At least one token must have had two slots on one physical expert.
+    # At least one token must have had two slots on one physical expert; the
+    # later slots are dropped, not routed with score 0.
     assert bool((got_s == 0).any())
+    assert bool((got_p[got_s == 0] == ROUTE_DROPPED).all())
+    # A route the router itself scored zero is dropped too.
+    zs = scores.clone()
+    zs[3, :] = 0.0
+    _, zp = m._coalesce_logical_routes(zs, idx)
+    assert bool((zp[3] == ROUTE_DROPPED).all())
     # Out-of-range logical ids become invalid physical ids (reported by the plan).
     bad = idx.clone()
     bad[5, 1] = 9

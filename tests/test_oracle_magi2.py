@@ -40,6 +40,68 @@ def test_route_with_bias_matches_brute_force():
         np.testing.assert_allclose(probs[h, s].numpy(), 2.5 * sel / sel.sum(), rtol=1e-6)
 
 
+@pytest.mark.parametrize("E,nvg,tvg,k", [(12, 4, 2, 3), (8, 8, 3, 2), (9, 3, 1, 3)])
+def test_virtual_group_route_matches_brute_force(E, nvg, tvg, k):
+    # route.py:62-105 restated one token at a time: group score = sum of the
+    # two largest biased scores of the group (the largest for a one-expert
+    # group), keep the tvg best groups (ties to the lower id), keys of the
+    # other experts become 0.0, then the k largest keys (ties to the lower id).
+    g = torch.Generator().manual_seed(E * 7 + nvg)
+    H, S = 2, 25
+    logits = torch.randn(H, S, E, generator=g) * 2
+    bias = torch.randn(H, E, generator=g) * 0.2  # negative keys occur: 0.0 can win
+    probs, idx = om.route_topk_heads(logits, k, score_func="sigmoid", expert_bias=bias,
+                                     route_norm=False, num_virtual_group=nvg,
+                                     topk_virtual_group=tvg)
+    scores = torch.sigmoid(logits)
+    keys = (scores + bias.view(H, 1, E)).tolist()
+    epg = E // nvg
+    saw_zero_pick = False
+    for h, s in itertools.product(range(H), range(S)):
+        kv = keys[h][s]
+        gs = []
+        for grp in range(nvg):
+            vals = sorted(kv[grp * epg:(grp + 1) * epg], reverse=True)
+            gs.append(np.float32(vals[0]) + (np.float32(vals[1]) if epg >= 2 else np.float32(0)))
+        kept = [grp for _, grp in sorted((-float(v), grp) for grp, v in enumerate(gs))[:tvg]]
+        masked = [kv[e] if e // epg in kept else 0.0 for e in range(E)]
+        pick = [e for _, e in sorted((-masked[e], e) for e in range(E))[:k]]
+        assert idx[h, s].tolist() == pick, (h, s)
+        saw_zero_pick |= any(e // epg not in kept for e in pick)
+        torch.testing.assert_close(probs[h, s], scores[h, s, pick])
+    if nvg == 3:
+        assert saw_zero_pick  # a masked expert outranked negative kept keys somewhere
+
+
+def test_virtual_groups_reduce_to_plain_selection():
+    # Every group kept: the plain selection. One expert per group and
+    # topk_virtual_group = k with positive keys: the plain top-k as well.
+    g = torch.Generator().manual_seed(2)
+    logits = torch.randn(2, 30, 16, generator=g)
+    plain = om.route_topk_heads(logits, 4, score_func="softmax")
+    allg = om.route_topk_heads(logits, 4, score_func="softmax", num_virtual_group=4,
+                               topk_virtual_group=4)
+    single = om.route_topk_heads(logits, 4, score_func="softmax", num_virtual_group=16,
+                                 topk_virtual_group=4)
+    for got in (allg, single):
+        assert torch.equal(got[1], plain[1])
+        torch.testing.assert_close(got[0], plain[0])
+
+
+def test_route_probs_for_picks_is_the_forward_and_its_gradient():
+    g = torch.Generator().manual_seed(6)
+    logits = torch.randn(2, 10, 8, generator=g, dtype=torch.float64)
+    probs, idx = om.route_topk_heads(logits.float(), 3, score_func="softmax", route_scale=1.5)
+    again = om.route_probs_for_picks(logits.float(), idx, score_func="softmax", route_scale=1.5)
+    torch.testing.assert_close(again, probs)
+    # Its autograd against central differences of the same function in fp64.
+    lg = logits.clone().requires_grad_(True)
+    w = torch.randn(2, 10, 3, generator=g, dtype=torch.float64)
+    f = lambda z: (om.route_probs_for_picks(z, idx, score_func="softmax", route_scale=1.5)
+                   .double() * w).sum()
+    assert torch.autograd.gradcheck(f, (lg,), eps=1e-6, atol=1e-7)
+
+
 def test_route_norm_floor_known_answer():
     # Sigmoid scores of -110 are ~1.7e-48 (zero in fp32): the sum stays below
     # the 1e-12 floor, so F.normalize divides by the floor, not by the sum.

@@ -68,3 +68,40 @@ def test_static_scratch_forward_matches_the_workspace_forward():
     with pytest.raises(ValueError, match="static"):
         nat.call("mx_moe_forward_static", *common, nat.stream(xb.device))
     del keep
+
+
+def test_static_forward_allocates_nothing_and_replays_in_a_graph():
+    """After one warm-up call (which resolves the device's scratch address),
+    the static forward allocates no device memory and can be captured into a
+    HIP graph; every replay, with eager work and synchronisation between the
+    replays, reproduces the workspace forward bit for bit."""
+    w = wl.Workload("noalloc_graph", 13, 300, 256, 192, 8, 4, 16, 16.0, "nf4", torch.bfloat16)
+    m = build_module(w, wl.dense_weights(w), wl.lora_factors(w))
+    x = wl.tokens(w).cuda()
+    idx_np, scores_np = oroute.route_topk(wl.router_logits(w).numpy(), w.top_k)
+    idx = torch.from_numpy(idx_np).cuda()
+    scores = torch.from_numpy(scores_np).cuda()
+    _, want = _both(m, x, idx, scores)  # also the warm-up of the static entry point
+    out = torch.empty_like(want)
+    common, keep, _ = _args(m, x, idx, scores, out)
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    nat.call("mx_moe_forward_static", *common, nat.stream(x.device))
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated() == before
+    assert torch.equal(out, want)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        out.zero_()
+        with torch.cuda.graph(graph, stream=side):
+            nat.call("mx_moe_forward_static", *common, nat.stream(x.device))
+    torch.cuda.current_stream().wait_stream(side)
+    for i in range(3):
+        out.fill_(float(i + 1))  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), i
+    del graph, keep
