@@ -19,6 +19,11 @@
  *                   i+4 in the high nibble), absmax [E, out, in/64] bf16
  *   NF4_F32 weight  codes as NF4, absmax [E, out, in/64] fp32 (the double-quant
  *                   absmax of a bitsandbytes payload, decoded by mx_nf4_from_bnb)
+ *   NF4_F32_KN      the same codes and fp32 absmax for a weight stored
+ *                   [E, in, out] (y = x @ W[e], the MAGI-2 group layout of
+ *                   magi2_preview.py:2680-2704): codes [E, in, out/2] packed
+ *                   along out, absmax [E, in, out/64]. out_features /
+ *                   in_features keep their meaning (N and K of the forward)
  *   INT8 weight     q [E, out, in] int8, scale [E, out] bf16
  *   BF16 weight     w [E, out, in] bf16
  *   F32X3 weight    w [E, out, 3*in] bf16: an fp32 weight split into bf16
@@ -56,6 +61,7 @@ extern "C" {
 #define MX_FMT_INT8 2
 #define MX_FMT_F32X3 3
 #define MX_FMT_NF4_F32 4  /* NF4 codes with an fp32 absmax per block (ingested bitsandbytes) */
+#define MX_FMT_NF4_F32_KN 5  /* NF4_F32 stored [E, in, out], blocks along out (MAGI-2 groups) */
 
 /* Expert id of a route slot that is left out of the layer on purpose: the
  * plan skips it without counting it as an invalid route (any other id outside
@@ -78,6 +84,12 @@ extern "C" {
 #define MX_ACT_SILU 0     /* h = bf16(silu(g)) * u  (SwiGLU, experts.py:289-317) */
 #define MX_ACT_SWIGLU7 1  /* h = min(g,7) * sigmoid(1.702 min(g,7)) * (clamp(u,-7,7) + 1)
                              in fp32 (MAGI-2, grouped_moe.py:287-306) */
+/* Flag or-ed into `act` of the token-choice layer forward: the combine forms
+ * each term bf16(y * bf16(score)) and rounds the running sum to bf16 after
+ * every add, in ascending expert order -- the bf16 index_add of the
+ * reference's MAGI-2 backend (grouped_moe.py:750-754) -- instead of the fp32
+ * sum of run_direct_routed. Entry points that do not combine ignore it. */
+#define MX_ACT_FLAG_BF16_COMBINE 0x100
 
 /* Router score functions and output layouts of mx_route_topk_heads. */
 #define MX_SCORE_SOFTMAX 0

@@ -21,6 +21,8 @@ from .magi2 import (
     Magi2GroupedExperts,
     Magi2QuantizedExpertError,
     compute_topk_probs_and_indices,
+    load_reference_magi2_artifact,
+    read_reference_magi2_artifact,
     route_topk_heads,
 )
 from .router import FusedRouter, fused_router_forward, router_weight_planes
@@ -53,8 +55,10 @@ __all__ = [
     "combine_routed_tokens",
     "fused_chunk_runner",
     "fused_router_forward",
+    "load_reference_magi2_artifact",
     "lora_scale",
     "permute_routed_tokens",
+    "read_reference_magi2_artifact",
     "route_topk",
     "route_topk_heads",
     "router_weight_planes",

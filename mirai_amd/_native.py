@@ -29,6 +29,7 @@ FMT_NF4 = 1
 FMT_INT8 = 2
 FMT_F32X3 = 3      # fp32 weights as bf16 planes [hi | lo | hi] along in_features
 FMT_NF4_F32 = 4    # NF4 codes with an fp32 block absmax (ingested bitsandbytes payloads)
+FMT_NF4_F32_KN = 5  # the same, stored [E, in, out] with the blocks along out (MAGI-2 groups)
 
 SPLIT_ACT = 0      # mx_split_f32 plane orders
 SPLIT_WEIGHT = 1
@@ -39,6 +40,7 @@ RENORM_EPS = 2
 
 ACT_SILU = 0       # expert activations
 ACT_SWIGLU7 = 1
+ACT_FLAG_BF16_COMBINE = 0x100  # or-ed into act: bf16 terms and sums in the combine (MAGI-2)
 
 SCORE_SOFTMAX = 0  # mx_route_topk_heads score functions and output layouts
 SCORE_SIGMOID = 1

@@ -40,21 +40,29 @@ enum { EPI_SWIGLU = 0, EPI_STORE = 1, EPI_LORA_A = 2, EPI_STORE2 = 4 };
 
 // NF4 codes with a bf16 absmax (the build's own quantiser) or an fp32 absmax
 // (bitsandbytes payloads, whose double-quantised absmax decodes to fp32).
-constexpr bool is_nf4(int fmt) { return fmt == MX_FMT_NF4 || fmt == MX_FMT_NF4_F32; }
+constexpr bool is_nf4(int fmt) {
+  return fmt == MX_FMT_NF4 || fmt == MX_FMT_NF4_F32 || fmt == MX_FMT_NF4_F32_KN;
+}
+constexpr bool f32_absmax(int fmt) { return fmt == MX_FMT_NF4_F32 || fmt == MX_FMT_NF4_F32_KN; }
+// Weights stored [E, in, out] with the NF4 blocks along out (a MAGI-2 packed
+// group, x @ W[g]): the forward reads them as the backward reads [E, out, in]
+// weights (B = W, transposed decode) and the backward as the forward does.
+constexpr bool is_kn(int fmt) { return fmt == MX_FMT_NF4_F32_KN; }
 
 // Block absmax i of a row as raw bits (a bf16 in the low half, or fp32 bits).
 template <int FMT>
 __device__ __forceinline__ uint32_t load_absmax(const void *row, int64_t i) {
-  if (FMT == MX_FMT_NF4_F32) return static_cast<const uint32_t *>(row)[i];
+  if (f32_absmax(FMT)) return static_cast<const uint32_t *>(row)[i];
   return static_cast<const uint16_t *>(row)[i];
 }
 template <int FMT>
 __device__ __forceinline__ float absmax_value(uint32_t raw) {
-  return FMT == MX_FMT_NF4_F32 ? __uint_as_float(raw) : bf16_bits_to_f32(raw);
+  return f32_absmax(FMT) ? __uint_as_float(raw) : bf16_bits_to_f32(raw);
 }
 
-// Backward epilogues multiply by W itself rather than W^T.
-constexpr bool trans_b(int epi) { return epi == EPI_STORE2; }
+// Backward epilogues multiply by W itself rather than W^T; with weights stored
+// [E, in, out] the forward does.
+constexpr bool trans_b(int epi, int fmt) { return (epi == EPI_STORE2) != is_kn(fmt); }
 
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 
@@ -135,7 +143,7 @@ __device__ __forceinline__ void b_row(int j, int nt, int &which, int64_t &n) {
     constexpr int H = T::WN / 2;
     which = (j / H) & 1;
     n = static_cast<int64_t>(nt) * (T::BN / 2) + (j / T::WN) * H + (j % H);
-  } else if (EPI == EPI_STORE) {
+  } else if (EPI == EPI_STORE || EPI == EPI_STORE2) {
     which = 0;
     n = static_cast<int64_t>(nt) * T::BN + j;
   } else {
@@ -250,6 +258,67 @@ constexpr int lora_tile_bytes() {
   return LORA ? (EPI == EPI_STORE2 ? 2 : 1) * T::BN * 64 : 16;
 }
 
+// Gate / up run of 4 columns -> the packed bf16 h run. gv / uv (the fp32
+// projections) end rounded as the reference's bf16 gate / up with the bf16
+// LoRA deltas a / b added (experts.py:3370-3374), then the gated activation:
+// silu(g) rounded to bf16 times u (experts.py:289-317), or swiglu7 in fp32
+// rounded once (grouped_moe.py:287-306).
+template <bool LORA>
+__device__ __forceinline__ void gated_run(float (&gv)[4], float (&uv)[4], float (&a)[4],
+                                          float (&b)[4], int act, uint32_t &h0, uint32_t &h1) {
+  round2(gv[0], gv[1]);
+  round2(gv[2], gv[3]);
+  round2(uv[0], uv[1]);
+  round2(uv[2], uv[3]);
+  if (LORA) {
+    round2(a[0], a[1]);
+    round2(a[2], a[3]);
+    round2(b[0], b[1]);
+    round2(b[2], b[3]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      gv[q] += a[q];
+      uv[q] += b[q];
+    }
+    round2(gv[0], gv[1]);
+    round2(gv[2], gv[3]);
+    round2(uv[0], uv[1]);
+    round2(uv[2], uv[3]);
+  }
+  if (act == MX_ACT_SWIGLU7) {
+    float hq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) hq[q] = swiglu7(gv[q], uv[q]);
+    h0 = pack_bf16x2(hq[0], hq[1]);
+    h1 = pack_bf16x2(hq[2], hq[3]);
+  } else {
+    float sv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sv[q] = gv[q] * __builtin_amdgcn_rcpf(1.0f + __expf(-gv[q]));
+    round2(sv[0], sv[1]);
+    round2(sv[2], sv[3]);
+    h0 = pack_bf16x2(sv[0] * uv[0], sv[1] * uv[1]);
+    h1 = pack_bf16x2(sv[2] * uv[2], sv[3] * uv[3]);
+  }
+}
+
+// Down / backward run of 4 columns: the bf16 projection plus the bf16 LoRA
+// delta a, rounded again (experts.py:3370-3374).
+template <bool LORA>
+__device__ __forceinline__ void projection_run(float (&v)[4], float (&a)[4], uint32_t &w0,
+                                               uint32_t &w1) {
+  round2(v[0], v[1]);
+  round2(v[2], v[3]);
+  if (LORA) {
+    round2(a[0], a[1]);
+    round2(a[2], a[3]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] += a[q];
+  }
+  w0 = pack_bf16x2(v[0], v[1]);
+  w1 = pack_bf16x2(v[2], v[3]);
+}
+
 // One (row tile, column tile) of the grouped GEMM: `tile` = (expert, first
 // sorted row), `nt` the column tile. The LDS stages are the caller's four
 // distinct __shared__ arrays (two stages of A and of B): once this is
@@ -304,7 +373,7 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   for (int i = 0; i < T::A_CHUNKS; ++i) a_ptr[i] = p.x + a_src[i] * p.ldx + a_col[i];
 
   // ------------------------------------------------------- B (weights)
-  constexpr bool TRANS = trans_b(EPI);
+  constexpr bool TRANS = trans_b(EPI, FMT);
   static_assert(!TRANS || (T::NT == 512 && T::BK == 64 && T::BN == 256),
                 "transposed B assumes 8 waves, BK 64 and BN 256");
   const int bj = tid / T::B_TPR, bh = tid % T::B_TPR;
@@ -313,8 +382,15 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   if (!TRANS) b_row<EPI, T>(bj, nt, which, bn);
   // Transposed B: lane = k row of the stage, wave = 32-column slice. Columns
   // past N re-read the last full 32-column slice (discarded by the epilogue).
+  // SwiGLU with transposed B (weights [E, in, out]): slice tc holds 32 gate
+  // columns (tc even) or the 32 up columns of the same ffn columns (tc odd),
+  // the order b_row gives the B rows of the other layout.
   const int tk = tid & 63, tc = wave;
-  const int64_t t_col0 = TRANS ? min(static_cast<int64_t>(nt) * T::BN + 32 * tc, p.N - 32) : 0;
+  const int t_which = (TRANS && EPI == EPI_SWIGLU) ? (tc & 1) : 0;
+  const int64_t t_col_raw = (TRANS && EPI == EPI_SWIGLU)
+                                ? static_cast<int64_t>(nt) * (T::BN / 2) + 32 * (tc >> 1)
+                                : static_cast<int64_t>(nt) * T::BN + 32 * tc;
+  const int64_t t_col0 = TRANS ? min(t_col_raw, p.N - 32) : 0;
   // Weight rows past N (a partial column tile) re-read row N-1: they only
   // feed output columns the epilogue discards. The LoRA down-projection
   // keeps explicit zeros, as its absent adapters have no rows at all.
@@ -325,13 +401,25 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
       static_cast<int64_t>(e) * (EPI == EPI_LORA_A ? pick(p.lora_stride, which) : wn_rows) + bn;
   const uint8_t *b_base = nullptr;
   const void *b_absmax = nullptr;  // the row's absmax entries
+  // The backward over [E, in, out] weights reads its K rows from w[0] up to
+  // k_split and from w[1] after it (dx = [dG | dU] [W1; W3]): two row bases.
+  constexpr bool kSplitK = EPI == EPI_STORE2 && !TRANS;
+  const int64_t row_k = kSplitK ? p.k_split : p.K;  // K extent of one weight row
+  const uint8_t *b_base1 = nullptr;
+  const void *b_absmax1 = nullptr;
   float b_scale = 0.0f;
   if (b_valid) {
     const uint8_t *w = static_cast<const uint8_t *>(pick(p.w, which));
     if (is_nf4(FMT)) {
-      b_base = w + wrow * (p.K / 2) + bh * (T::B_ELEMS / 2);
+      b_base = w + wrow * (row_k / 2) + bh * (T::B_ELEMS / 2);
       b_absmax = static_cast<const uint8_t *>(pick(p.wscale, which)) +
-                 wrow * (p.K / kNf4Block) * (FMT == MX_FMT_NF4_F32 ? 4 : 2);
+                 wrow * (row_k / kNf4Block) * (f32_absmax(FMT) ? 4 : 2);
+      if (kSplitK && p.k_split < p.K) {
+        const int64_t wrow1 = static_cast<int64_t>(e) * p.wn[1] + bn;
+        b_base1 = static_cast<const uint8_t *>(p.w[1]) + wrow1 * (row_k / 2) + bh * (T::B_ELEMS / 2);
+        b_absmax1 = static_cast<const uint8_t *>(p.wscale[1]) +
+                    wrow1 * (row_k / kNf4Block) * (f32_absmax(FMT) ? 4 : 2);
+      }
     } else if (FMT == MX_FMT_INT8) {
       b_base = w + wrow * p.K + bh * T::B_ELEMS;
       b_scale = bf16_bits_to_f32(static_cast<const uint16_t *>(pick(p.wscale, which))[wrow]);
@@ -366,8 +454,9 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   auto load_b = [&](int kt, BRegs &rb) __attribute__((always_inline)) {
     if (TRANS) {
       const int64_t kb = static_cast<int64_t>(kt) * BK;
-      const bool second = kb >= p.k_split;
-      const int64_t krow = kb - (second ? p.k_split : 0) + tk;
+      // K split (backward dx) or, for the SwiGLU pair, the slice's weight.
+      const bool second = EPI == EPI_SWIGLU ? t_which != 0 : (EPI == EPI_STORE2 && kb >= p.k_split);
+      const int64_t krow = kb - ((EPI == EPI_STORE2 && second) ? p.k_split : 0) + tk;
       const uint8_t *w = static_cast<const uint8_t *>(second ? p.w[1] : p.w[0]);
       const void *ws = second ? p.wscale[1] : p.wscale[0];
       const int64_t wrow = static_cast<int64_t>(e) * (second ? p.wn[1] : p.wn[0]) + krow;
@@ -386,10 +475,18 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
         rb.abs = 0;
       }
     } else if (b_valid) {
+      const uint8_t *bb = b_base;
+      const void *ba = b_absmax;
+      int ks = kt;
+      if (kSplitK && static_cast<int64_t>(kt) * BK >= p.k_split) {
+        bb = b_base1;
+        ba = b_absmax1;
+        ks = kt - static_cast<int>(p.k_split / BK);
+      }
 #pragma unroll
       for (int q = 0; q < kBRegs; ++q)
-        rb.q[q] = *reinterpret_cast<const u32x4 *>(b_base + static_cast<int64_t>(kt) * kBStageBytes + 16 * q);
-      rb.abs = is_nf4(FMT) ? load_absmax<FMT>(b_absmax, kt * BK / kNf4Block) : 0u;
+        rb.q[q] = *reinterpret_cast<const u32x4 *>(bb + static_cast<int64_t>(ks) * kBStageBytes + 16 * q);
+      rb.abs = is_nf4(FMT) ? load_absmax<FMT>(ba, ks * BK / kNf4Block) : 0u;
     } else {
 #pragma unroll
       for (int q = 0; q < kBRegs; ++q) rb.q[q] = u32x4{0u, 0u, 0u, 0u};
@@ -659,66 +756,22 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   // reference's bf16 gate / up (with the bf16 LoRA deltas added).
   auto swiglu_run = [&](float (&gv)[4], float (&uv)[4], const f32x16 &lg, const f32x16 &lu, int g,
                         uint32_t &h0, uint32_t &h1) __attribute__((always_inline)) {
-    round2(gv[0], gv[1]);
-    round2(gv[2], gv[3]);
-    round2(uv[0], uv[1]);
-    round2(uv[2], uv[3]);
-    if (LORA) {
-      float a[4], b[4];
+    float a[4], b[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        a[q] = lg[4 * g + q];
-        b[q] = lu[4 * g + q];
-      }
-      round2(a[0], a[1]);
-      round2(a[2], a[3]);
-      round2(b[0], b[1]);
-      round2(b[2], b[3]);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        gv[q] += a[q];
-        uv[q] += b[q];
-      }
-      round2(gv[0], gv[1]);
-      round2(gv[2], gv[3]);
-      round2(uv[0], uv[1]);
-      round2(uv[2], uv[3]);
+    for (int q = 0; q < 4; ++q) {
+      a[q] = LORA ? lg[4 * g + q] : 0.0f;
+      b[q] = LORA ? lu[4 * g + q] : 0.0f;
     }
-    if (p.act == MX_ACT_SWIGLU7) {
-      // bf16 gate / up in, fp32 swiglu7, one rounding (grouped_moe.py:287-306).
-      float hq[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) hq[q] = swiglu7(gv[q], uv[q]);
-      h0 = pack_bf16x2(hq[0], hq[1]);
-      h1 = pack_bf16x2(hq[2], hq[3]);
-    } else {
-      // silu(g) rounded to bf16, then the bf16 product (experts.py:289-317).
-      float sv[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) sv[q] = gv[q] * __builtin_amdgcn_rcpf(1.0f + __expf(-gv[q]));
-      round2(sv[0], sv[1]);
-      round2(sv[2], sv[3]);
-      h0 = pack_bf16x2(sv[0] * uv[0], sv[1] * uv[1]);
-      h1 = pack_bf16x2(sv[2] * uv[2], sv[3] * uv[3]);
-    }
+    gated_run<LORA>(gv, uv, a, b, p.act, h0, h1);
   };
   // Down / backward run of 4 columns of block (mb, nb): the bf16 projection
   // plus the bf16 LoRA delta, rounded again (experts.py:3370-3374).
   auto store_run = [&](float (&v)[4], const f32x16 &l2, int g, uint32_t &w0, uint32_t &w1)
       __attribute__((always_inline)) {
-    round2(v[0], v[1]);
-    round2(v[2], v[3]);
-    if (LORA) {
-      float a[4];
+    float a[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) a[q] = l2[4 * g + q];
-      round2(a[0], a[1]);
-      round2(a[2], a[3]);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[q] += a[q];
-    }
-    w0 = pack_bf16x2(v[0], v[1]);
-    w1 = pack_bf16x2(v[2], v[3]);
+    for (int q = 0; q < 4; ++q) a[q] = LORA ? l2[4 * g + q] : 0.0f;
+    projection_run<LORA>(v, a, w0, w1);
   };
   // Staged stores: a lane's runs are 8 bytes of one row, 32 rows per store
   // instruction, which the memory system takes as partial-line writes. The
@@ -1097,6 +1150,8 @@ int launch_tile(int fmt, const Params &p, int64_t max_tiles, hipStream_t s) {
       return launch<MX_FMT_NF4, EPI, LORA, Short>(p, max_tiles, s);
     case MX_FMT_NF4_F32:
       return launch<MX_FMT_NF4_F32, EPI, LORA, Short>(p, max_tiles, s);
+    case MX_FMT_NF4_F32_KN:
+      return launch<MX_FMT_NF4_F32_KN, EPI, LORA, Short>(p, max_tiles, s);
     case MX_FMT_INT8:
       return launch<MX_FMT_INT8, EPI, LORA, Short>(p, max_tiles, s);
     case MX_FMT_F32X3:
@@ -1118,6 +1173,8 @@ int launch_tile_dual(int fmt, const Params &p, int64_t max_tall, int64_t max_sho
       return launch_dual<MX_FMT_NF4, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
     case MX_FMT_NF4_F32:
       return launch_dual<MX_FMT_NF4_F32, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
+    case MX_FMT_NF4_F32_KN:
+      return launch_dual<MX_FMT_NF4_F32_KN, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
     case MX_FMT_INT8:
       return launch_dual<MX_FMT_INT8, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
     case MX_FMT_F32X3:
@@ -1212,6 +1269,12 @@ LayerLayout layer_layout(int64_t rows, int num_experts, int64_t hidden, int64_t 
 
 bool has_lora(const mx_lora *l) { return l && l->rank > 0; }
 
+// Rows per expert of a stored weight: its out rows, or its in rows when it is
+// stored [E, in, out] (MX_FMT_NF4_F32_KN).
+int64_t wn_of(const mx_weight *w) {
+  return w->format == MX_FMT_NF4_F32_KN ? w->in_features : w->out_features;
+}
+
 __global__ __launch_bounds__(256) void zero_f32_kernel(float *p, int64_t n) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
@@ -1260,11 +1323,13 @@ int check_weight(const char *name, const char *key, const mx_weight *w, int64_t 
     return MX_ERR_INVALID;
   }
   if (w->format != MX_FMT_BF16 && w->format != MX_FMT_NF4 && w->format != MX_FMT_INT8 &&
-      w->format != MX_FMT_F32X3 && w->format != MX_FMT_NF4_F32) {
+      w->format != MX_FMT_F32X3 && w->format != MX_FMT_NF4_F32 &&
+      w->format != MX_FMT_NF4_F32_KN) {
     set_error("%s: weight %s has unknown format %d", name, key, w->format);
     return MX_ERR_INVALID;
   }
-  if ((w->format == MX_FMT_NF4 || w->format == MX_FMT_NF4_F32 || w->format == MX_FMT_INT8) &&
+  if ((w->format == MX_FMT_NF4 || w->format == MX_FMT_NF4_F32 ||
+       w->format == MX_FMT_NF4_F32_KN || w->format == MX_FMT_INT8) &&
       !w->scale) {
     set_error("%s: weight %s needs its scale / absmax buffer", name, key);
     return MX_ERR_INVALID;
@@ -1390,7 +1455,8 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
     p.w[1] = w3->data;
     p.wscale[0] = w1->scale;
     p.wscale[1] = w3->scale;
-    p.wn[0] = p.wn[1] = ffn;
+    p.wn[0] = wn_of(w1);
+    p.wn[1] = wn_of(w3);
     p.N = ffn;
     p.lora_p = lora_buf;
     p.ldp = 3 * lrc;
@@ -1423,7 +1489,7 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
   p.K = kx * ffn;
   p.w[0] = w2->data;
   p.wscale[0] = w2->scale;
-  p.wn[0] = hidden;
+  p.wn[0] = wn_of(w2);
   p.N = hidden;
   p.lora_p = lora_buf + 2 * lrc;
   p.ldp = 3 * lrc;
@@ -1628,7 +1694,7 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
     p.K = hidden;
     p.w[0] = w2->data;
     p.wscale[0] = w2->scale;
-    p.wn[0] = hidden;
+    p.wn[0] = wn_of(w2);
     p.k_split = hidden;
     p.N = ffn;
     p.lora_p = dz + 2 * lrc;
@@ -1676,7 +1742,8 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
     p.w[1] = w3->data;
     p.wscale[0] = w1->scale;
     p.wscale[1] = w3->scale;
-    p.wn[0] = p.wn[1] = ffn;
+    p.wn[0] = wn_of(w1);
+    p.wn[1] = wn_of(w3);
     p.k_split = ffn;
     p.N = hidden;
     p.lora_p = dz;
@@ -1735,6 +1802,8 @@ extern "C" int mx_moe_backward_act(const void *grad_out, int grad_dtype, const v
   const char *name = "mx_moe_backward";
   int rc = validate_plan_args(name, num_tokens, top_k, num_experts);
   if (rc) return rc;
+  const bool bf16_combine = (act & MX_ACT_FLAG_BF16_COMBINE) != 0;
+  act &= ~MX_ACT_FLAG_BF16_COMBINE;
   if (act != MX_ACT_SILU && act != MX_ACT_SWIGLU7) {
     set_error("%s: unknown activation %d", name, act);
     return MX_ERR_INVALID;
@@ -1842,6 +1911,8 @@ extern "C" int mx_moe_forward_ex(const void *tokens, const int64_t *top_idx,
   const char *name = "mx_moe_forward";
   int rc = validate_plan_args(name, num_tokens, top_k, num_experts);
   if (rc) return rc;
+  const bool bf16_combine = (act & MX_ACT_FLAG_BF16_COMBINE) != 0;
+  act &= ~MX_ACT_FLAG_BF16_COMBINE;
   if (act != MX_ACT_SILU && act != MX_ACT_SWIGLU7) {
     set_error("%s: unknown activation %d", name, act);
     return MX_ERR_INVALID;
@@ -1913,7 +1984,7 @@ extern "C" int mx_moe_forward_ex(const void *tokens, const int64_t *top_idx,
       }
     }
     rc = combine_ex(y, top_idx, top_scores, score_dtype, num_tokens, top_k, num_experts, hidden,
-                    out, out_dtype, addend, stream);
+                    out, out_dtype, addend, stream, bf16_combine);
   }
   mark_stage(6, s);
   return rc;
@@ -2053,6 +2124,8 @@ extern "C" int mx_moe_for_loop_act(const void *tokens_sorted, const int64_t *cou
   const char *name = "mx_moe_for_loop";
   int rc = validate_plan_args(name, num_rows, 1, num_experts);
   if (rc) return rc;
+  const bool bf16_combine = (act & MX_ACT_FLAG_BF16_COMBINE) != 0;
+  act &= ~MX_ACT_FLAG_BF16_COMBINE;
   if (act != MX_ACT_SILU && act != MX_ACT_SWIGLU7) {
     set_error("%s: unknown activation %d", name, act);
     return MX_ERR_INVALID;
@@ -2136,7 +2209,7 @@ extern "C" int mx_grouped_linear(const void *x, const int64_t *counts, int64_t n
   p.K = in_f;
   p.w[0] = w->data;
   p.wscale[0] = w->scale;
-  p.wn[0] = out_f;
+  p.wn[0] = wn_of(w);
   p.N = out_f;
   p.lora_p = lora_buf;
   p.ldp = 3 * lrc;
@@ -2264,7 +2337,7 @@ extern "C" int mx_grouped_linear_backward(const void *grad_out, const void *x,
     p.K = out_f;
     p.w[0] = w->data;
     p.wscale[0] = w->scale;
-    p.wn[0] = out_f;
+    p.wn[0] = wn_of(w);
     p.k_split = out_f;
     p.N = in_f;
     p.lora_p = dz;
@@ -2575,6 +2648,8 @@ extern "C" int mx_moe_forward_expert_choice_ex(
   int rc = validate_ec(name, batch, logical_experts, capacity, tokens_per_sample, num_experts,
                        logical_to_physical);
   if (rc) return rc;
+  const bool bf16_combine = (act & MX_ACT_FLAG_BF16_COMBINE) != 0;
+  act &= ~MX_ACT_FLAG_BF16_COMBINE;
   if (act != MX_ACT_SILU && act != MX_ACT_SWIGLU7) {
     set_error("%s: unknown activation %d", name, act);
     return MX_ERR_INVALID;
@@ -2679,6 +2754,8 @@ extern "C" int mx_moe_backward_expert_choice(
   int rc = validate_ec(name, batch, logical_experts, capacity, tokens_per_sample, num_experts,
                        logical_to_physical);
   if (rc) return rc;
+  const bool bf16_combine = (act & MX_ACT_FLAG_BF16_COMBINE) != 0;
+  act &= ~MX_ACT_FLAG_BF16_COMBINE;
   if (act != MX_ACT_SILU && act != MX_ACT_SWIGLU7) {
     set_error("%s: unknown activation %d", name, act);
     return MX_ERR_INVALID;

@@ -15,9 +15,11 @@ int sum_halves(const float *in, int64_t rows, int64_t cols, void *out, int out_d
                hipStream_t s);
 
 // mx_combine with an optional addend [T, cols] of out's dtype:
-// out = out_dtype(out_dtype(sum) + addend).
+// out = out_dtype(out_dtype(sum) + addend). With bf16_terms each term is
+// bf16(y * bf16(score)) and the running sum is rounded to bf16 after every
+// add (expert order), the bf16 index_add of the reference's MAGI-2 backend.
 int combine_ex(const void *y, const int64_t *top_idx, const void *top_scores, int score_dtype,
                int64_t num_tokens, int top_k, int num_experts, int64_t cols, void *out,
-               int out_dtype, const void *addend, void *stream);
+               int out_dtype, const void *addend, void *stream, bool bf16_terms = false);
 
 }  // namespace mx

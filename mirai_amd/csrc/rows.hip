@@ -109,7 +109,14 @@ __device__ __forceinline__ void store_combined(void *out, int out_dtype, const v
 // the slot order (ascending expert id, slot order for ties, invalid ids last)
 // is formed with static indices, and the KC slot rows of each 512-column span
 // are all loaded before the fp32 accumulation, which runs in that order.
-template <int KC>
+// BF16T: each term is formed and added in bf16 -- acc = bf16(acc +
+// bf16(y * bf16(score))) in the same order -- the bf16 index_add of the
+// reference's MAGI-2 backend (grouped_moe.py:750-754) run in expert order.
+__device__ __forceinline__ float bf16_term_add(float acc, float y, float s_bf16) {
+  return round_bf16(acc + round_bf16(y * s_bf16));
+}
+
+template <int KC, bool BF16T>
 __global__ __launch_bounds__(256) void combine_wave_kernel(const uint16_t *y, const int64_t *top_idx,
                                                           const void *top_scores, int score_dtype,
                                                           int E, int64_t cols, int64_t num_tokens,
@@ -139,7 +146,8 @@ __global__ __launch_bounds__(256) void combine_wave_kernel(const uint16_t *y, co
 #pragma unroll
     for (int i = 0; i < KC; ++i) rank += (key[i] < key[j] || (key[i] == key[j] && i < j)) ? 1 : 0;
     const bool valid = key[j] != 0x7fffffff;
-    const float s = valid ? (top_scores ? load_score(top_scores, t * KC + j, score_dtype) : 1.0f) : 0.0f;
+    float s = valid ? (top_scores ? load_score(top_scores, t * KC + j, score_dtype) : 1.0f) : 0.0f;
+    if (BF16T) s = round_bf16(s);
 #pragma unroll
     for (int q = 0; q < KC; ++q) {
       if (rank == q) {
@@ -159,6 +167,11 @@ __global__ __launch_bounds__(256) void combine_wave_kernel(const uint16_t *y, co
       const uint32_t w[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
+        if (BF16T) {
+          acc[2 * i] = bf16_term_add(acc[2 * i], bf16_bits_to_f32(w[i] & 0xffffu), sc[q]);
+          acc[2 * i + 1] = bf16_term_add(acc[2 * i + 1], bf16_bits_to_f32(w[i] >> 16), sc[q]);
+          continue;
+        }
         // Product then sum, each rounded once, as in index_add_(y.float() * score).
         acc[2 * i] = __fadd_rn(acc[2 * i], __fmul_rn(bf16_bits_to_f32(w[i] & 0xffffu), sc[q]));
         acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __fmul_rn(bf16_bits_to_f32(w[i] >> 16), sc[q]));
@@ -194,6 +207,7 @@ __global__ __launch_bounds__(256) void combine_wave_kernel(const uint16_t *y, co
 }
 
 // One workgroup per token; each thread owns 8 consecutive columns per step.
+template <bool BF16T>
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *y, const int64_t *top_idx,
                                                       const void *top_scores, int score_dtype,
                                                       int k, int E, int64_t cols, void *out,
@@ -202,8 +216,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *y, const i
   int slot[kMaxK];
   const int n = sorted_slots(top_idx + t * k, k, E, slot);
   float sc[kMaxK];
-  for (int j = 0; j < n; ++j)
+  for (int j = 0; j < n; ++j) {
     sc[j] = top_scores ? load_score(top_scores, t * k + slot[j], score_dtype) : 1.0f;
+    if (BF16T) sc[j] = round_bf16(sc[j]);
+  }
   for (int64_t c0 = static_cast<int64_t>(threadIdx.x) * 8; c0 < cols; c0 += 256 * 8) {
     float acc[8];
 #pragma unroll
@@ -213,6 +229,11 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *y, const i
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
+        if (BF16T) {
+          acc[2 * q] = bf16_term_add(acc[2 * q], bf16_bits_to_f32(w[q] & 0xffffu), sc[j]);
+          acc[2 * q + 1] = bf16_term_add(acc[2 * q + 1], bf16_bits_to_f32(w[q] >> 16), sc[j]);
+          continue;
+        }
         // Product then sum, each rounded once, as in index_add_(y.float() * score).
         acc[2 * q] = __fadd_rn(acc[2 * q], __fmul_rn(bf16_bits_to_f32(w[q] & 0xffffu), sc[j]));
         acc[2 * q + 1] = __fadd_rn(acc[2 * q + 1], __fmul_rn(bf16_bits_to_f32(w[q] >> 16), sc[j]));
@@ -443,7 +464,7 @@ namespace mx {
 
 int combine_ex(const void *y, const int64_t *top_idx, const void *top_scores, int score_dtype,
                int64_t num_tokens, int top_k, int num_experts, int64_t cols, void *out,
-               int out_dtype, const void *addend, void *stream) {
+               int out_dtype, const void *addend, void *stream, bool bf16_terms) {
   if (num_tokens < 0 || top_k <= 0 || top_k > kMaxK || cols <= 0 || cols % 8 != 0 ||
       num_experts <= 0) {
     set_error("mx_combine: need top_k in [1,16], cols a positive multiple of 8");
@@ -458,9 +479,14 @@ int combine_ex(const void *y, const int64_t *top_idx, const void *top_scores, in
   const uint16_t *yb = static_cast<const uint16_t *>(y);
 #define MX_COMBINE_K(KC)                                                                     \
   case KC:                                                                                   \
-    hipLaunchKernelGGL(combine_wave_kernel<KC>, wave_grid, dim3(256), 0, as_stream(stream), yb, \
-                       top_idx, top_scores, score_dtype, num_experts, cols, num_tokens, out,   \
-                       out_dtype, addend);                                                   \
+    if (bf16_terms)                                                                          \
+      hipLaunchKernelGGL((combine_wave_kernel<KC, true>), wave_grid, dim3(256), 0,             \
+                         as_stream(stream), yb, top_idx, top_scores, score_dtype, num_experts,  \
+                         cols, num_tokens, out, out_dtype, addend);                            \
+    else                                                                                     \
+      hipLaunchKernelGGL((combine_wave_kernel<KC, false>), wave_grid, dim3(256), 0,            \
+                         as_stream(stream), yb, top_idx, top_scores, score_dtype, num_experts,  \
+                         cols, num_tokens, out, out_dtype, addend);                            \
     break;
   switch (top_k) {
     MX_COMBINE_K(1)
@@ -470,9 +496,14 @@ int combine_ex(const void *y, const int64_t *top_idx, const void *top_scores, in
     MX_COMBINE_K(6)
     MX_COMBINE_K(8)
     default:
-      hipLaunchKernelGGL(combine_kernel, dim3(num_tokens), dim3(256), 0, as_stream(stream), yb,
-                         top_idx, top_scores, score_dtype, top_k, num_experts, cols, out, out_dtype,
-                         addend);
+      if (bf16_terms)
+        hipLaunchKernelGGL(combine_kernel<true>, dim3(num_tokens), dim3(256), 0,
+                           as_stream(stream), yb, top_idx, top_scores, score_dtype, top_k,
+                           num_experts, cols, out, out_dtype, addend);
+      else
+        hipLaunchKernelGGL(combine_kernel<false>, dim3(num_tokens), dim3(256), 0,
+                           as_stream(stream), yb, top_idx, top_scores, score_dtype, top_k,
+                           num_experts, cols, out, out_dtype, addend);
   }
 #undef MX_COMBINE_K
   return check_launch("mx_combine");

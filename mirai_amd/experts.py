@@ -104,6 +104,7 @@ class CompressedGroupedExperts(nn.Module):
         self._quant_format = quant.normalize_quant_format(quant_format)
         self._nf4_blocksize = int(nf4_blocksize)
         self._shapes: dict[str, tuple[int, int, int]] = {}
+        self._layouts: dict[str, str] = {}  # key -> "out_in" or "in_out" (PackedWeight.layout)
         self._loaded_dense_keys: set[str] = set()
         self.expert_lora = nn.ModuleDict()
         self.logical_num_experts = int(num_experts)
@@ -181,14 +182,18 @@ class CompressedGroupedExperts(nn.Module):
         if scale_suffix is not None:
             self._set_buffer(f"{key}{scale_suffix}", packed.scale)
         self._shapes[key] = packed.shape
+        self._layouts[key] = packed.layout
         self._loaded_dense_keys.add(key)
 
     def load_packed_nf4(self, key: str, *, packed: torch.Tensor, absmax: torch.Tensor,
                         nested_absmax: torch.Tensor, offset: torch.Tensor, code: torch.Tensor,
-                        nested_code: torch.Tensor, shape: tuple[int, int, int]) -> None:
+                        nested_code: torch.Tensor, shape: tuple[int, int, int],
+                        layout: str = "out_in") -> None:
         """Adopt a bitsandbytes double-quantised NF4 stack as the reference stores it
         (the {key}_nf4* buffers of _store_nf4_grouped, experts.py:998-1031) without
-        re-quantising: the GEMMs decode the payload's weights (fp32 absmax)."""
+        re-quantising: the GEMMs decode the payload's weights (fp32 absmax).
+        ``shape`` is the logical [E, out, in]; ``layout="in_out"`` takes payloads
+        that quantise each expert's [in, out] matrix (MAGI-2 groups)."""
         if self._quant_format != "nf4":
             raise ValueError("packed NF4 payloads load into a module with quant_format='nf4'.")
         if key not in self._spec.tensor_names:
@@ -199,11 +204,12 @@ class CompressedGroupedExperts(nn.Module):
                 f"expected {self.num_experts}.")
         packed_w = quant.from_bnb_nf4(packed=packed, absmax=absmax, nested_absmax=nested_absmax,
                                       offset=offset, code=code, nested_code=nested_code,
-                                      shape=tuple(int(v) for v in shape))
+                                      shape=tuple(int(v) for v in shape), layout=layout)
         data_suffix, scale_suffix = _BUFFER_SUFFIXES["nf4"]
         self._set_buffer(f"{key}{data_suffix}", packed_w.data)
         self._set_buffer(f"{key}{scale_suffix}", packed_w.scale)
         self._shapes[key] = packed_w.shape
+        self._layouts[key] = packed_w.layout
         self._loaded_dense_keys.add(key)
 
     def load_bnb_state_dict(self, state: dict, shapes: dict, *, prefix: str = "") -> None:
@@ -227,38 +233,14 @@ class CompressedGroupedExperts(nn.Module):
         data_suffix, scale_suffix = _BUFFER_SUFFIXES[self._quant_format]
         return (f"{key}{data_suffix}",) + ((f"{key}{scale_suffix}",) if scale_suffix else ())
 
-    def adopt_packed(self, key: str, buffers: dict, shape: tuple[int, int, int]) -> None:
-        """Install an already packed [E, out, in] projection (the buffers named by
-        ``packed_buffer_names``), checking each tensor against the layout this
-        format's quantiser produces; nothing is re-quantised."""
-        if key not in self._spec.tensor_names:
-            raise ValueError(f"Unknown compressed_weights grouped expert tensor '{key}'.")
-        shape = tuple(int(v) for v in shape)
-        if len(shape) != 3 or shape[0] != self.num_experts:
-            raise ValueError(f"packed expert tensor {key} must be [{self.num_experts}, out, in], "
-                             f"got {shape}.")
-        names = self.packed_buffer_names(key)
-        layouts = quant.packed_layout(self._quant_format, shape)
-        for name, layout in zip(names, layouts):
-            value = buffers.get(name)
-            if not isinstance(value, torch.Tensor):
-                raise ValueError(f"packed expert tensor {key} lacks buffer '{name}'.")
-            dtypes, want = layout
-            if value.dtype not in dtypes or tuple(value.shape) != want:
-                raise ValueError(f"buffer '{name}' is {value.dtype} {tuple(value.shape)}, "
-                                 f"expected one of {dtypes} {want}.")
-        for name in names:
-            self._set_buffer(name, buffers[name].contiguous())
-        self._shapes[key] = shape
-        self._loaded_dense_keys.add(key)
-
     def packed_weight(self, key: str) -> quant.PackedWeight:
         if key not in self._loaded_dense_keys:
             raise RuntimeError(f"compressed_weights grouped experts are missing weight '{key}'.")
         data_suffix, scale_suffix = _BUFFER_SUFFIXES[self._quant_format]
         data = getattr(self, f"{key}{data_suffix}")
         scale = getattr(self, f"{key}{scale_suffix}") if scale_suffix else None
-        return quant.PackedWeight(self._quant_format, data, scale, self._shapes[key])
+        return quant.PackedWeight(self._quant_format, data, scale, self._shapes[key],
+                                  self._layouts.get(key, "out_in"))
 
     def packed_nbytes(self) -> int:
         return sum(self.packed_weight(k).nbytes() for k in self._loaded_dense_keys)

@@ -30,8 +30,13 @@ def lora_row(module) -> int:
 
 def kernel_activation(module) -> int:
     """Expert activation of the fused kernels: SwiGLU (the canonical packed
-    expert MLP) unless a wrapper such as the MAGI-2 experts selects swiglu7."""
-    return int(getattr(module, "_kernel_activation", nat.ACT_SILU))
+    expert MLP) unless a wrapper such as the MAGI-2 experts selects swiglu7;
+    with ACT_FLAG_BF16_COMBINE when the module combines in bf16 like the
+    reference's MAGI-2 backend (``_combine_bf16_terms``)."""
+    act = int(getattr(module, "_kernel_activation", nat.ACT_SILU))
+    if getattr(module, "_combine_bf16_terms", False):
+        act |= nat.ACT_FLAG_BF16_COMBINE
+    return act
 
 
 def _lora_descriptors(module, device, split=False):

@@ -168,6 +168,10 @@ class Magi2GroupedExperts(nn.Module):
             expert_weight_access=expert_weight_access,
             expert_dequant_chunk_size=expert_dequant_chunk_size,
             execution_spec=MAGI2_EXPERT_MLP_SPEC)
+        # The reference's MAGI-2 backend sums the weighted expert outputs with
+        # a bf16 index_add (grouped_moe.py:750-754): each term bf16(y *
+        # bf16(prob)), the running sum rounded to bf16 (expert order here).
+        self.experts._combine_bf16_terms = True
 
         # The reference layer's [G, in, out] shape and dtype of every loaded tensor.
         self._source_shapes: dict[str, tuple[int, int, int]] = {}
@@ -207,6 +211,52 @@ class Magi2GroupedExperts(nn.Module):
 
     def quantized_numel(self) -> int:
         return int(sum(g * a * b for g, a, b in self._source_shapes.values()))
+
+    def load_reference_nf4_store(self, buffers: dict, expert_shapes: dict,
+                                 expert_dtypes: dict | None = None) -> None:
+        """Adopt the payload of the reference's Magi2Nf4ExpertStore for this layer
+        without re-quantising (quantized_experts.py:275-347): per key the
+        double-quantised NF4 buffers ``{key}_nf4`` (codes of each group's
+        [in, out] matrix, element 2j in the high nibble of byte j),
+        ``_nf4_absmax`` (uint8 codes), ``_nf4_nabsmax``, ``_nf4_offset``,
+        ``_nf4_code`` (the NF4 levels) and ``_nf4_ncode`` (256 fp32), with
+        ``expert_shapes[key] = (G, in, out)``. The group payloads keep their
+        [in, out] orientation (64-blocks along out): the kernels read them as
+        stored (MX_FMT_NF4_F32_KN), the absmax decoded once to fp32."""
+        if self.experts.quant_format != "nf4":
+            raise Magi2QuantizedExpertError(
+                "a reference NF4 store loads into a module with quant_format='nf4'.")
+        for key in MAGI2_ROUTED_EXPERT_TENSOR_NAMES:
+            shape = tuple(int(v) for v in expert_shapes[key])
+            if len(shape) != 3 or shape[0] != self.num_groups:
+                raise Magi2QuantizedExpertError(
+                    f"{key} has the shape {shape}; this layer holds {self.num_groups} groups.")
+            g, rows, cols = shape
+            fields = {}
+            for field in _NF4_FIELDS:
+                name = f"{key}_{field}"
+                if name not in buffers:
+                    raise Magi2QuantizedExpertError(f"the NF4 store lacks '{name}'.")
+                fields[field] = buffers[name]
+            device = self.experts_device()
+            t = {f: v.to(device) for f, v in fields.items()}
+            try:
+                self.experts.load_packed_nf4(
+                    key, packed=t["nf4"], absmax=t["nf4_absmax"], nested_absmax=t["nf4_nabsmax"],
+                    offset=t["nf4_offset"], code=t["nf4_code"], nested_code=t["nf4_ncode"],
+                    shape=(g, cols, rows), layout="in_out")
+            except ValueError as err:
+                raise Magi2QuantizedExpertError(f"{key}: {err}") from err
+            self._source_shapes[key] = shape
+            dtype = (expert_dtypes or {}).get(key, torch.bfloat16)
+            self._source_dtypes[key] = dtype if isinstance(dtype, torch.dtype) else getattr(
+                torch, str(dtype), torch.bfloat16)
+
+    def experts_device(self) -> torch.device:
+        """The device the packed weights live on (the current GPU before any is loaded)."""
+        for t in self.experts.buffers():
+            return t.device
+        return torch.device("cuda", torch.cuda.current_device())
 
     @classmethod
     def from_dense(cls, W_gate: torch.Tensor, W_up: torch.Tensor, W_down: torch.Tensor, *,
@@ -271,6 +321,87 @@ class Magi2GroupedExperts(nn.Module):
                                          expert_bias=expert_bias, route_norm=route_norm,
                                          route_scale=route_scale, layout="rows")
         return self.run_rows(x_heads.reshape(S * H, d), probs, groups).view(S, H, d)
+
+
+# Field suffixes of one weight's double-quantised NF4 payload in the
+# reference's store (quantized_experts.py:325-346).
+_NF4_FIELDS = ("nf4", "nf4_absmax", "nf4_nabsmax", "nf4_offset", "nf4_code", "nf4_ncode")
+# The artifact format the reference writes (packed_experts.py:19-20): its
+# schema name and version, and the file naming its shards.
+REFERENCE_MAGI2_ARTIFACT = ("mirai.magi2_preview.nf4_experts", 2)
+_ARTIFACT_MANIFEST = "manifest.json"
+
+
+def read_reference_magi2_artifact(path) -> dict[str, dict]:
+    """Read a MAGI-2 NF4 expert artifact as the reference writes it
+    (save_magi2_nf4_packed_state, packed_experts.py:28-78): a manifest naming
+    one safetensors shard per MoE layer, each shard holding the six NF4
+    buffers of W_gate, W_up and W_down. Returns {layer name: {"shapes":
+    {key: (G, in, out)}, "dtypes": {key: dtype}, "buffers": {name: CPU
+    tensor}}}. Only the safetensors loader touches the shards (no pickle).
+    Anything this build cannot ingest raises Magi2QuantizedExpertError."""
+    import json
+    from pathlib import Path
+
+    from safetensors import safe_open
+
+    root = Path(path).expanduser()
+    try:
+        manifest = json.loads((root / _ARTIFACT_MANIFEST).read_text(encoding="utf-8"))
+    except (OSError, ValueError) as err:
+        raise Magi2QuantizedExpertError(f"no readable MAGI-2 artifact manifest in {root}") from err
+    found = (manifest.get("schema"), manifest.get("schema_version"))
+    if found != REFERENCE_MAGI2_ARTIFACT or manifest.get("quant_format") != "nf4":
+        raise Magi2QuantizedExpertError(
+            f"{root} holds artifact {found} ({manifest.get('quant_format')}); this reader takes "
+            f"{REFERENCE_MAGI2_ARTIFACT} NF4 experts.")
+    layers = manifest.get("layers")
+    if not isinstance(layers, dict) or not layers:
+        raise Magi2QuantizedExpertError(f"the artifact in {root} lists no layers.")
+    wanted = sorted(f"{k}_{f}" for k in MAGI2_ROUTED_EXPERT_TENSOR_NAMES for f in _NF4_FIELDS)
+    out = {}
+    for name, spec in layers.items():
+        meta = spec.get("nf4_meta") or {}
+        if int(meta.get("blocksize", -1)) != NF4_BLOCKSIZE or int(
+                meta.get("nested_blocksize", -1)) != 256:
+            raise Magi2QuantizedExpertError(
+                f"layer '{name}': NF4 blocks {meta.get('blocksize')} / nested "
+                f"{meta.get('nested_blocksize')}; the kernels take 64 / 256.")
+        shard = root / str(spec.get("shard", ""))
+        if shard.parent != root or not shard.is_file():
+            raise Magi2QuantizedExpertError(f"layer '{name}': shard {spec.get('shard')!r} "
+                                            f"is not a file of {root}.")
+        with safe_open(str(shard), framework="pt", device="cpu") as handle:
+            absent = sorted(set(wanted) - set(handle.keys()))
+            if absent:
+                raise Magi2QuantizedExpertError(f"layer '{name}': shard lacks {absent}.")
+            buffers = {n: handle.get_tensor(n) for n in wanted}
+        shapes = spec.get("expert_shapes") or {}
+        dtypes = spec.get("expert_dtypes") or {}
+        try:
+            out[name] = {
+                "shapes": {k: tuple(int(v) for v in shapes[k])
+                           for k in MAGI2_ROUTED_EXPERT_TENSOR_NAMES},
+                "dtypes": {k: getattr(torch, str(dtypes.get(k, "bfloat16")), torch.bfloat16)
+                           for k in MAGI2_ROUTED_EXPERT_TENSOR_NAMES},
+                "buffers": buffers,
+            }
+        except (KeyError, TypeError, ValueError) as err:
+            raise Magi2QuantizedExpertError(f"layer '{name}': bad expert shapes {shapes}") from err
+    return out
+
+
+def load_reference_magi2_artifact(path, layers: dict) -> dict:
+    """Ingest a reference MAGI-2 NF4 artifact into ``layers`` ({layer name:
+    Magi2GroupedExperts with quant_format "nf4"}, names as in the manifest)
+    without re-quantising; returns ``layers``."""
+    entries = read_reference_magi2_artifact(path)
+    if set(entries) != set(layers):
+        raise Magi2QuantizedExpertError(
+            f"artifact layers {sorted(entries)} do not match the model's {sorted(layers)}.")
+    for name, entry in entries.items():
+        layers[name].load_reference_nf4_store(entry["buffers"], entry["shapes"], entry["dtypes"])
+    return layers
 
 
 class Magi2FusedMoEBackend:

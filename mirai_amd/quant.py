@@ -51,10 +51,16 @@ class PackedWeight:
     data: torch.Tensor
     scale: torch.Tensor | None
     shape: tuple[int, int, int]
+    # "out_in": data [E, out, ...] (the quantiser's layout); "in_out": data
+    # [E, in, ...] with the NF4 blocks along out (an ingested MAGI-2 group
+    # payload, x @ W[g]).
+    layout: str = "out_in"
 
     def format_code(self) -> int:
         if self.fmt == "nf4" and self.scale is not None and self.scale.dtype == torch.float32:
-            return nat.FMT_NF4_F32
+            return nat.FMT_NF4_F32_KN if self.layout == "in_out" else nat.FMT_NF4_F32
+        if self.layout != "out_in":
+            raise ValueError(f"the {self.fmt} format has no [E, in, out] kernel layout")
         return _FORMAT_CODES[self.fmt]
 
     def descriptor(self) -> nat.MxWeight:
@@ -109,22 +115,6 @@ def quantize(source: torch.Tensor, fmt: str) -> PackedWeight:
     return PackedWeight("int8", q, scale, (E, out_f, in_f))
 
 
-def packed_layout(fmt: str, shape: tuple[int, int, int]) -> tuple[tuple, tuple | None]:
-    """(dtypes, shape) of the data and scale tensors ``quantize`` produces for an
-    [E, out, in] projection in ``fmt`` (NF4 absmax: bf16, or fp32 for ingested
-    bitsandbytes payloads)."""
-    E, out_f, in_f = (int(v) for v in shape)
-    fmt = normalize_quant_format(fmt)
-    if fmt == "nf4":
-        return (((torch.uint8,), (E, out_f, in_f // 2)),
-                ((torch.bfloat16, torch.float32), (E, out_f, in_f // NF4_BLOCKSIZE)))
-    if fmt == "int8":
-        return ((torch.int8,), (E, out_f, in_f)), ((torch.bfloat16,), (E, out_f))
-    if fmt == "fp32":
-        return ((torch.bfloat16,), (E, out_f, 3 * in_f)), None
-    return ((torch.bfloat16,), (E, out_f, in_f)), None
-
-
 def dequantize(packed: PackedWeight, *, dtype: torch.dtype = torch.bfloat16,
                experts: slice | None = None) -> torch.Tensor:
     """Dense weights (bit-exact codec output) of all or a slice of experts."""
@@ -138,6 +128,14 @@ def dequantize(packed: PackedWeight, *, dtype: torch.dtype = torch.bfloat16,
     if packed.fmt == "fp32":  # hi + lo planes
         return (data[..., :in_f].float() + data[..., in_f:2 * in_f].float()).to(dtype)
     nat.require_gpu(data)
+    if packed.layout == "in_out":
+        # Rows of the stored [E, in, out] payload, then the [E, out, in] view.
+        flat = torch.empty((E, in_f, out_f), dtype=dtype, device=device)
+        nat.call("mx_nf4_dequantize_ex", data.contiguous().data_ptr(),
+                 packed.scale[sel].contiguous().data_ptr(),
+                 nat.dtype_code(packed.scale.dtype), E * in_f, out_f, flat.data_ptr(),
+                 nat.dtype_code(dtype), nat.stream(device))
+        return flat.transpose(1, 2).contiguous()
     out = torch.empty((E, out_f, in_f), dtype=dtype, device=device)
     rows = E * out_f
     s = nat.stream(device)
@@ -155,7 +153,7 @@ def dequantize(packed: PackedWeight, *, dtype: torch.dtype = torch.bfloat16,
 def from_bnb_nf4(*, packed: torch.Tensor, absmax: torch.Tensor, nested_absmax: torch.Tensor,
                  offset: torch.Tensor, code: torch.Tensor, nested_code: torch.Tensor,
                  shape: tuple[int, int, int], blocksize: int = NF4_BLOCKSIZE,
-                 nested_blocksize: int = 256) -> PackedWeight:
+                 nested_blocksize: int = 256, layout: str = "out_in") -> PackedWeight:
     """Ingest a bitsandbytes double-quantised NF4 expert stack without
     re-quantising (mx_nf4_from_bnb).
 
@@ -165,14 +163,20 @@ def from_bnb_nf4(*, packed: torch.Tensor, absmax: torch.Tensor, nested_absmax: t
     quantised absmax [E, out*in/64] uint8, ``{key}_nf4_nabsmax`` [E, n2] fp32,
     ``{key}_nf4_offset`` [E] fp32, ``{key}_nf4_code`` (the 16 NF4 levels) and
     ``{key}_nf4_ncode`` (256 fp32). Returns the codes in this library's layout
-    with the decoded fp32 absmax.
+    with the decoded fp32 absmax. ``shape`` is the logical [E, out, in]; with
+    ``layout="in_out"`` each expert's payload quantises the [in, out] matrix
+    (the MAGI-2 store's [G, in, out] groups, quantized_experts.py:275-347, whose
+    64-blocks run along out) and is kept in that orientation.
     """
     E, out_f, in_f = (int(v) for v in shape)
+    if layout not in ("out_in", "in_out"):
+        raise ValueError(f"unknown layout {layout!r}")
+    rows_f, cols_f = (out_f, in_f) if layout == "out_in" else (in_f, out_f)
     if int(blocksize) != NF4_BLOCKSIZE or int(nested_blocksize) != 256:
         raise ValueError("bitsandbytes NF4 payloads are ingested with blocksize 64 and "
                          "nested blocksize 256.")
-    if in_f % NF4_BLOCKSIZE:
-        raise ValueError(f"in_features must be a multiple of 64, got {in_f}.")
+    if cols_f % NF4_BLOCKSIZE:
+        raise ValueError(f"the payload's row length must be a multiple of 64, got {cols_f}.")
     device = packed.device
     nat.require_gpu(packed)
     levels = code.detach().to(device="cpu", dtype=torch.float32).reshape(-1)
@@ -189,13 +193,13 @@ def from_bnb_nf4(*, packed: torch.Tensor, absmax: torch.Tensor, nested_absmax: t
             raise ValueError(f"bitsandbytes field {name} must hold {numel} {dtype} values, got "
                              f"{int(t.numel())} {t.dtype}.")
         flat[name] = t.detach().to(device).reshape(-1).contiguous()
-    codes = torch.empty((E, out_f, in_f // 2), dtype=torch.uint8, device=device)
-    amax = torch.empty((E, out_f, in_f // NF4_BLOCKSIZE), dtype=torch.float32, device=device)
+    codes = torch.empty((E, rows_f, cols_f // 2), dtype=torch.uint8, device=device)
+    amax = torch.empty((E, rows_f, cols_f // NF4_BLOCKSIZE), dtype=torch.float32, device=device)
     nat.call("mx_nf4_from_bnb", flat["packed"].data_ptr(), flat["absmax"].data_ptr(),
              flat["nested_absmax"].data_ptr(), flat["offset"].data_ptr(),
-             flat["nested_code"].data_ptr(), E, out_f, in_f, codes.data_ptr(), amax.data_ptr(),
-             nat.stream(device))
-    return PackedWeight("nf4", codes, amax, (E, out_f, in_f))
+             flat["nested_code"].data_ptr(), E, rows_f, cols_f, codes.data_ptr(),
+             amax.data_ptr(), nat.stream(device))
+    return PackedWeight("nf4", codes, amax, (E, out_f, in_f), layout)
 
 
 def nf4_levels() -> torch.Tensor:

@@ -88,3 +88,59 @@ def mixed_rank_factors(w: wl.Workload, ranks: dict, seed: int = 0) -> dict:
         r = int(ranks[key])
         out[key] = (torch.randn(E, r, i, generator=g) * 0.02, torch.randn(E, o, r, generator=g) * 0.02)
     return out
+
+
+# ---------------------------------------------------------------- MAGI-2 artifacts
+MAGI2_KEYS = ("W_gate", "W_up", "W_down")
+
+
+def bnb_group_payload(w_groups: np.ndarray, nested_code: np.ndarray) -> dict:
+    """Double-quantised NF4 buffers of one weight [G, in, out] as the reference's
+    Magi2Nf4ExpertStore stacks them (quantized_experts.py:296-346): one
+    bitsandbytes payload per group over the flattened [in, out] matrix
+    (restated by oracle.codec.bnb_nf4_quantize), codes [G, in*out/2, 1]."""
+    from oracle import codec
+
+    parts = [codec.bnb_nf4_quantize(w, nested_code) for w in w_groups]
+    return {
+        "nf4": np.stack([p["packed"].reshape(-1, 1) for p in parts]),
+        "nf4_absmax": np.stack([p["absmax"] for p in parts]),
+        "nf4_nabsmax": np.stack([p["nested_absmax"] for p in parts]),
+        "nf4_offset": np.array([p["offset"] for p in parts], dtype=np.float32),
+        "nf4_code": parts[0]["code"].astype(np.float32),
+        "nf4_ncode": np.asarray(nested_code, dtype=np.float32),
+    }, parts
+
+
+def write_reference_magi2_artifact(root, layers: dict, *, schema=("mirai.magi2_preview.nf4_experts", 2),
+                                   blocksize=64) -> None:
+    """Fixture writer: the directory layout the reference's
+    save_magi2_nf4_packed_state produces (packed_experts.py:28-78) -- a
+    manifest.json and one safetensors shard per layer -- for payloads
+    {layer: {key: (buffers dict, (G, in, out))}}."""
+    import json
+    from pathlib import Path
+
+    from safetensors.torch import save_file
+
+    root = Path(root)
+    root.mkdir(parents=True, exist_ok=True)
+    specs = {}
+    for i, (name, weights) in enumerate(layers.items()):
+        tensors, shapes = {}, {}
+        for key, (bufs, shape) in weights.items():
+            for field, value in bufs.items():
+                tensors[f"{key}_{field}"] = torch.from_numpy(np.array(value, copy=True))
+            shapes[key] = list(shape)
+        shard = f"layer_{i:03d}.safetensors"
+        save_file(tensors, str(root / shard))
+        groups = next(iter(shapes.values()))[0]
+        specs[name] = {"shard": shard, "num_groups": groups, "blocksize": blocksize,
+                       "expert_shapes": shapes,
+                       "expert_dtypes": {k: "bfloat16" for k in shapes},
+                       "nf4_meta": {"blocksize": blocksize, "nested_blocksize": 256,
+                                    "nested_dtype": "float32", "weight_dtype": "bfloat16"},
+                       "buffers": sorted(tensors)}
+    manifest = {"schema": schema[0], "schema_version": schema[1], "quant_format": "nf4",
+                "layers": specs, "metadata": {}}
+    (root / "manifest.json").write_text(json.dumps(manifest, indent=2), encoding="utf-8")

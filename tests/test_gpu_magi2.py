@@ -203,3 +203,86 @@ def test_empty_sequence_through_the_magi2_layer():
         out = m(x, logits, top_k=2, score_func="sigmoid", expert_bias=bias.cuda(),
                 route_norm=True, route_scale=4.9)
     assert out.shape[0] == 0 and out.shape[-1] == 128
+
+
+def _reference_artifact(tmp_path, *, H=2, E=4, d=128, f=192, seed=12):
+    """A MAGI-2 artifact as the reference writes it (bitsandbytes double-quant
+    per group over [in, out], quantized_experts.py:275-347, packed_experts.py:
+    28-78) and the dense bf16 weights [G, in, out] it decodes to (the
+    oracle's restatement of bitsandbytes' dequantisation)."""
+    from oracle import codec
+
+    from helpers import bnb_group_payload, write_reference_magi2_artifact
+
+    rng = np.random.default_rng(seed)
+    table = np.sort(np.concatenate([np.linspace(-1, 1, 255), [0.0]])).astype(np.float32)
+    G = H * E
+    weights, dense = {}, {}
+    for key, (i_f, o_f) in {"W_gate": (d, f), "W_up": (d, f), "W_down": (f, d)}.items():
+        w = (rng.standard_normal((G, i_f, o_f)) * 0.05).astype(np.float32)
+        bufs, parts = bnb_group_payload(w, table)
+        weights[key] = (bufs, (G, i_f, o_f))
+        bits = np.stack([codec.bnb_nf4_dequantize(p["packed"], p["absmax"], p["nested_absmax"],
+                                                  p["offset"], table, i_f, o_f) for p in parts])
+        dense[key] = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+    write_reference_magi2_artifact(tmp_path / "artifact", {"blocks.3.moe": weights})
+    return tmp_path / "artifact", dense
+
+
+@pytest.mark.parametrize("S", [80, 1200])  # 128-row tiles; 256-row + remainder tiles
+def test_reference_artifact_ingests_without_requantisation(tmp_path, S):
+    """The reference's NF4 store loads as stored: the [G, in, out] group payloads
+    keep their orientation (blocks along out) and the kernels decode them in
+    place (MX_FMT_NF4_F32_KN); the decoded weights equal bitsandbytes'
+    dequantisation of the payload (oracle restatement) bit for bit, and the
+    layer matches the MAGI-2 oracle on those weights, forward and backward."""
+    from mirai_amd import load_reference_magi2_artifact
+    from mirai_amd import _native as nat
+    from mirai_amd import quant
+
+    H, E, d, f = 2, 4, 128, 192
+    path, dense = _reference_artifact(tmp_path, H=H, E=E, d=d, f=f)
+    layer = Magi2GroupedExperts(num_heads=H, num_experts=E, quant_format="nf4")
+    load_reference_magi2_artifact(path, {"blocks.3.moe": layer})
+    assert layer.is_fully_loaded()
+    assert layer.expert_weight_shape("W_down") == (H * E, f, d)
+    for key in ("W_gate", "W_up", "W_down"):
+        pw = layer.experts.packed_weight(key)
+        assert pw.layout == "in_out" and pw.format_code() == nat.FMT_NF4_F32_KN
+        deq = quant.dequantize(pw)  # [G, out, in]
+        assert torch.equal(deq.transpose(1, 2).cpu(), dense[key])
+
+    _, x, _, _, probs, idx = _magi2_case(H=H, E=E, d=d, f=f, S=S, k=2, seed=13)
+    with torch.no_grad():
+        out = layer.execute(x.cuda(), probs.cuda(), idx.cuda())
+    ref = om.layer_forward(x, probs, idx, dense, E)
+    print(f"magi2 reference artifact forward: {assert_layer_close(out.cpu(), ref)}")
+
+    # Backward with expert LoRA on every weight (the ingested weights stay frozen).
+    g = torch.Generator().manual_seed(21)
+    r = 16
+    leaves = {}
+    for key, (i_f, o_f) in {"W_gate": (d, f), "W_up": (d, f), "W_down": (f, d)}.items():
+        a = (torch.randn(H * E, r, i_f, generator=g) * 0.05).to(torch.bfloat16)
+        b = (torch.randn(H * E, o_f, r, generator=g) * 0.05).to(torch.bfloat16)
+        ad = layer.attach_expert_lora(tensor_name=key, adapter_name="t", rank=r, alpha=32.0)
+        with torch.no_grad():
+            ad.lora_a.copy_(a.cuda())
+            ad.lora_b.copy_(b.cuda())
+        leaves[key] = (a.float().requires_grad_(True), b.float().requires_grad_(True))
+    dy = torch.randn(x.shape, generator=g).to(torch.bfloat16)
+    xg = x.cuda().requires_grad_(True)
+    pg = probs.cuda().requires_grad_(True)
+    layer.execute(xg, pg, idx.cuda()).backward(dy.cuda())
+    xo = x.clone().requires_grad_(True)
+    po = probs.clone().requires_grad_(True)
+    ol = {k: (a, b, 2.0) for k, (a, b) in leaves.items()}  # alpha 32 / rank 16
+    om.layer_forward(xo, po, idx, dense, E, loras=ol).backward(dy)
+    pairs = [("tokens", xg.grad, xo.grad), ("probs", pg.grad, po.grad)]
+    for k, (a, b) in leaves.items():
+        pairs += [(f"{k}.a", layer.experts.expert_lora[k].lora_a.grad, a.grad),
+                  (f"{k}.b", layer.experts.expert_lora[k].lora_b.grad, b.grad)]
+    for name, got, want in pairs:
+        rel = float((got.float().cpu() - want.float()).abs().sum() / want.float().abs().sum())
+        print(f"magi2 reference artifact backward {name}: mean_rel={rel:.3e}")
+        assert rel <= 1e-2, (name, rel)
