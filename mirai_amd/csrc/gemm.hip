@@ -782,7 +782,7 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   const bool saves = EPI == EPI_SWIGLU && p.save_gate != nullptr;
   if (EPI == EPI_SWIGLU && !kSplit && !saves) {
     // Inference h: the whole [BM][BN/2] tile is staged (BM/2 rows per B
-    // stage), then every wave stores BM/8 rows, 16 lanes per 256-byte row.
+    // stage), then every wave stores BM/waves rows, 16 lanes per 256-byte row.
     constexpr int HC = T::BN / 2;
     constexpr int RSB = HC * 2;
     constexpr int CPRH = RSB / 16;
@@ -820,7 +820,7 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
       }
     }
     __syncthreads();
-    constexpr int RPW = T::BM / 8;  // rows stored per wave
+    constexpr int RPW = T::BM / kWaves;  // rows stored per wave
     const int c = lane & 15;
     const int64_t col = static_cast<int64_t>(nt) * HC + c * 8;
 #pragma unroll
