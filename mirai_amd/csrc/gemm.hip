@@ -1040,6 +1040,236 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   }
 }
 
+// ------------------------------------------------------------ light tiles
+// An expert with at most kLightRows rows in a launch (skewed routing leaves
+// many such) would pay a whole 128-row tile: the decode of its 256 x K weight
+// tile into LDS plus 128-row MFMA work, for a few rows. Its light tile keeps
+// the work per weight at one decode: all of the expert's token rows are staged
+// in LDS once (the four stage buffers, one barrier), and each wave decodes its
+// 32 weight rows straight into MFMA operands, each lane one whole 64-element
+// NF4 block per 128-wide K step, with no B stage and no per-step barrier.
+//
+// K permutation: in K step b a lane of half h (lane / 32) supplies, for MFMA
+// sub-step s, the 8 elements 128 b + 64 h + 8 s .. + 7 of its row, for the
+// weight operand and the token operand alike; the sum over K is the same sum.
+constexpr int kLightRows = 32;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <int FMT, int EPI>
+constexpr bool light_capable() {
+  return (FMT == MX_FMT_NF4 || FMT == MX_FMT_NF4_F32) && (EPI == EPI_SWIGLU || EPI == EPI_STORE);
+}
+
+// Columns of K the four stage buffers hold for 32 rows (two of SA bytes, two of SB).
+template <int SA, int SB>
+constexpr int light_max_k() {
+  return (2 * SA + 2 * SB) / (32 * 2);
+}
+
+// K in whole 128-wide steps (a lane takes one 64-block per step) that the
+// stage buffers hold.
+template <int SA, int SB>
+__device__ __forceinline__ bool light_tile_fits(const Params &p, int2 tile) {
+  return p.seg_end[tile.x] - tile.y <= kLightRows && p.K % 128 == 0 &&
+         p.K <= light_max_k<SA, SB>();
+}
+
+template <int FMT, int EPI, bool LORA, int SA, int SB>
+__device__ __forceinline__ void light_tile(const Params &p, int2 tile, int nt, uint8_t *sA0,
+                                           uint8_t *sA1, uint8_t *sB0, uint8_t *sB1) {
+  static_assert(SA % 8192 == 0 && SB % 8192 == 0, "stage rows must be whole 256-byte groups");
+  const int e = tile.x;
+  const int64_t row0 = tile.y;
+  const int64_t row_end = p.seg_end[e];
+  const int m = static_cast<int>(row_end - row0);  // 1 .. kLightRows
+  const int wave = uniform_wave_index(), lane = threadIdx.x & 63;
+  const int K = static_cast<int>(p.K);
+  // Stage region q holds K columns [kq0, kq0 + kq) of the 32 rows, row stride
+  // 2 kq bytes, 16-byte chunks XOR-swizzled by (row & 15) inside each 256-byte
+  // group so the 32 rows a fragment read touches spread over the banks.
+  constexpr int kA = SA / 64, kB = SB / 64;  // K columns per region
+  auto region = [&](int q) __attribute__((always_inline)) -> uint8_t * {
+    return q == 0 ? sA0 : q == 1 ? sA1 : q == 2 ? sB0 : sB1;
+  };
+  auto region_k0 = [](int q) { return q < 2 ? q * kA : 2 * kA + (q - 2) * kB; };
+  auto region_k = [](int q) { return q < 2 ? kA : kB; };
+
+  // ------------------------------------------- token rows -> LDS (by DMA)
+  // One DMA instruction fills 1 KB of a region (lane l at byte 16 l): rows of
+  // that region whose K range starts inside the layer's K. Rows past the
+  // segment are not loaded: they only feed output rows that are dropped.
+  {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int kq = region_k(q), kq0 = region_k0(q);
+      if (kq0 >= K) break;
+      const int rows_per_dma = 1024 / (2 * kq);  // 1 (kq = 512) or 2 (kq = 256)
+      const int n_dma = 32 / rows_per_dma;
+      for (int d = wave; d < n_dma; d += 8) {
+        if (d * rows_per_dma >= m) break;  // wave-uniform: the DMA's rows are past the segment
+        const int row = d * rows_per_dma + (lane * 16) / (2 * kq);
+        const int phys = ((lane * 16) % (2 * kq)) >> 4;
+        const int chunk = phys ^ (row & 15);
+        const int k = kq0 + 8 * chunk;
+        if (row < m && k < K) {
+          const int64_t sr = row0 + row;
+          const int64_t src = p.row_token ? static_cast<int64_t>(p.row_token[sr]) : sr;
+          __builtin_amdgcn_global_load_lds(
+              reinterpret_cast<const void *>(p.x + src * p.ldx + k),
+              reinterpret_cast<__attribute__((address_space(3))) void *>(
+                  reinterpret_cast<uintptr_t>(region(q) + d * 1024)),
+              16, 0, 0);
+        }
+      }
+    }
+  }
+
+  // ----------------------------------------------------- the wave's weights
+  const int li = lane & 31, h = lane >> 5;
+  int which = 0;
+  int64_t n;
+  if (EPI == EPI_SWIGLU) {
+    // Rows 0..15 of the wave's block: gate rows of ffn columns f0 .. f0 + 15;
+    // rows 16..31: the up rows of the same columns, so value v and v + 8 of a
+    // lane's accumulator are one (gate, up) pair.
+    which = li >> 4;
+    n = static_cast<int64_t>(nt) * 128 + 16 * wave + (li & 15);
+  } else {
+    n = static_cast<int64_t>(nt) * 256 + 32 * wave + li;
+  }
+  const int64_t n_row = min(n, p.N - 1);  // rows past N feed dropped columns
+  const int64_t wrow = static_cast<int64_t>(e) * pick(p.wn, which) + n_row;
+  const uint8_t *codes = static_cast<const uint8_t *>(pick(p.w, which)) + wrow * (p.K / 2);
+  const uint8_t *absrow = static_cast<const uint8_t *>(pick(p.wscale, which)) +
+                          wrow * (p.K / kNf4Block) * (f32_absmax(FMT) ? 4 : 2);
+  const int KS = K / 128;  // K steps
+  struct Codes {
+    u32x4 q[2];
+    uint32_t abs;
+  };
+  auto load_codes = [&](int b, Codes &c) __attribute__((always_inline)) {
+    const int blk = 2 * b + h;
+    c.q[0] = *reinterpret_cast<const u32x4 *>(codes + blk * 32);
+    c.q[1] = *reinterpret_cast<const u32x4 *>(codes + blk * 32 + 16);
+    c.abs = load_absmax<FMT>(absrow, blk);
+  };
+
+  f32x16 acc;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+  Codes c0, c1;
+  load_codes(0, c0);
+  __syncthreads();  // the staged token rows of every wave
+
+  auto kstep = [&](int b, const Codes &c) __attribute__((always_inline)) {
+    const int k = 128 * b + 64 * h;
+    int q = 0;
+#pragma unroll
+    for (int r = 1; r < 4; ++r) q += k >= region_k0(r) ? 1 : 0;
+    const int kq = region_k(q);
+    const uint8_t *arow = region(q) + li * (2 * kq);
+    const int c0k = (k - region_k0(q)) >> 3;  // first 16-byte chunk of the lane's 64 elements
+    const Nf4Table t = nf4_table(absmax_value<FMT>(c.abs));
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int chunk = c0k + s;
+      const int phys = (chunk & ~15) | ((chunk & 15) ^ (li & 15));
+      const bf16x8 a = *reinterpret_cast<const bf16x8 *>(arow + phys * 16);
+      uint32_t d[4];
+      const u32x4 v = c.q[s >> 2];
+      const uint32_t word = (s & 3) == 0 ? v[0] : (s & 3) == 1 ? v[1] : (s & 3) == 2 ? v[2] : v[3];
+      nf4_decode8(t, word, d);
+      const bf16x8 w = __builtin_bit_cast(bf16x8, u32x4{d[0], d[1], d[2], d[3]});
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w, a, acc, 0, 0, 0);
+    }
+  };
+  int b = 0;
+  for (; b + 1 < KS; b += 2) {
+    load_codes(b + 1, c1);
+    kstep(b, c0);
+    load_codes(min(b + 2, KS - 1), c0);
+    kstep(b + 1, c1);
+  }
+  if (b < KS) kstep(b, c0);
+
+  // --------------------------------------------------- LoRA up-projection
+  // The low-rank row holds [gate rc | up rc] (SwiGLU) or the down adapter's
+  // rc columns; one MFMA chain over them with each lane's factor row zero
+  // outside its own adapter gives the gate and up deltas of the block apart.
+  const int lrow = li;
+  const int64_t prow_i = min(row0 + lrow, row_end - 1);
+  f32x16 lacc;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) lacc[j] = 0.0f;
+  if (LORA) {
+    constexpr int n_ad = EPI == EPI_SWIGLU ? 2 : 1;
+#pragma unroll
+    for (int ad = 0; ad < n_ad; ++ad) {
+      const int r = pick2(p.lora_r, ad);
+      if (r == 0) continue;
+      const bool own = EPI == EPI_SWIGLU ? (which == ad) : true;
+      const uint16_t *frow = pick2(p.lora_b, ad) + (static_cast<int64_t>(e) * p.N + n_row) * r;
+      const uint16_t *arow = p.lora_p + prow_i * p.ldp + ad * p.lora_rc;
+      for (int c = 0; c < r; c += 16) {
+        const int col = c + 8 * h;
+        // Columns past the rank hold zero activations; their factor read
+        // stays inside the row.
+        const bf16x8 a = *reinterpret_cast<const bf16x8 *>(arow + col);
+        bf16x8 f = *reinterpret_cast<const bf16x8 *>(frow + (col < r ? col : 0));
+        if (!own) f = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+        lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f, a, lacc, 0, 0, 0);
+      }
+    }
+  }
+
+  // ------------------------------------------------------------ epilogue
+  // Value v of a lane is output row lane % 32 of the block and block row
+  // 8 (v / 4) + 4 h + v % 4: runs of 4 consecutive columns.
+  if (lrow >= m) return;
+  if (EPI == EPI_SWIGLU) {
+    const int64_t r = row0 + lrow;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int64_t f0 = static_cast<int64_t>(nt) * 128 + 16 * wave + 8 * g + 4 * h;
+      float gv[4], uv[4], a[4], bb[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        gv[q] = acc[4 * g + q];
+        uv[q] = acc[8 + 4 * g + q];
+        a[q] = LORA ? lacc[4 * g + q] : 0.0f;
+        bb[q] = LORA ? lacc[8 + 4 * g + q] : 0.0f;
+      }
+      uint32_t h0, h1;
+      gated_run<LORA>(gv, uv, a, bb, p.act, h0, h1);
+      if (f0 < p.N) {
+        *reinterpret_cast<u32x2 *>(p.out + r * p.ldo + f0) = u32x2{h0, h1};
+        if (p.save_gate != nullptr) {
+          *reinterpret_cast<u32x2 *>(p.save_gate + r * p.N + f0) =
+              u32x2{pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3])};
+          *reinterpret_cast<u32x2 *>(p.save_up + r * p.N + f0) =
+              u32x2{pack_bf16x2(uv[0], uv[1]), pack_bf16x2(uv[2], uv[3])};
+        }
+      }
+    }
+  } else {
+    const int64_t sr = row0 + lrow;
+    const int64_t o = p.out_row ? static_cast<int64_t>(p.out_row[sr]) : sr;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int64_t n0 = static_cast<int64_t>(nt) * 256 + 32 * wave + 8 * g + 4 * h;
+      float v[4], a[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v[q] = acc[4 * g + q];
+        a[q] = LORA ? lacc[4 * g + q] : 0.0f;
+      }
+      uint32_t w0, w1;
+      projection_run<LORA>(v, a, w0, w1);
+      if (n0 < p.N) *reinterpret_cast<u32x2 *>(p.out + o * p.ldo + n0) = u32x2{w0, w1};
+    }
+  }
+}
+
 // One launch over one tile list (p.tiles, *p.num_tiles row tiles). The
 // blockIdx -> tile map gives each of the 8 XCDs (workgroups go to XCDs
 // round-robin) a contiguous run of tiles, row-tile major, so the column tiles
@@ -1060,8 +1290,15 @@ void grouped_gemm_kernel(Params p) {
   const int logical = (blockIdx.x & 7) * per_xcd + slot;
   if (logical >= total) return;
   const int mt = logical / p.n_tiles_n;
-  gemm_tile<FMT, EPI, LORA, T>(p, p.tiles[mt], logical - mt * p.n_tiles_n, sA0, sA1, sB0, sB1,
-                               sLt);
+  const int2 tile = p.tiles[mt];
+  if constexpr (light_capable<FMT, EPI>() && T::BM == 128) {
+    if (light_tile_fits<T::STAGE_A, T::STAGE_B>(p, tile)) {
+      light_tile<FMT, EPI, LORA, T::STAGE_A, T::STAGE_B>(p, tile, logical - mt * p.n_tiles_n, sA0,
+                                                         sA1, sB0, sB1);
+      return;
+    }
+  }
+  gemm_tile<FMT, EPI, LORA, T>(p, tile, logical - mt * p.n_tiles_n, sA0, sA1, sB0, sB1, sLt);
 }
 
 // 256-row tiles (p.tiles) and the 128-row remainder tiles (p.tiles_r) in one
@@ -1098,8 +1335,16 @@ void grouped_gemm_dual_kernel(Params p) {
     const int logical = xcd * per_xcd + s2;
     if (logical >= total) return;
     const int mt = logical / p.n_tiles_n;
-    gemm_tile<FMT, EPI, LORA, Short>(p, p.tiles_r[mt], logical - mt * p.n_tiles_n, sA0, sA1, sB0,
-                                     sB1, sLt);
+    const int2 tile = p.tiles_r[mt];
+    // An expert's only tile, when it has at most kLightRows rows.
+    if constexpr (light_capable<FMT, EPI>()) {
+      if (light_tile_fits<Tall::STAGE_A, Tall::STAGE_B>(p, tile)) {
+        light_tile<FMT, EPI, LORA, Tall::STAGE_A, Tall::STAGE_B>(p, tile, logical - mt * p.n_tiles_n,
+                                                               sA0, sA1, sB0, sB1);
+        return;
+      }
+    }
+    gemm_tile<FMT, EPI, LORA, Short>(p, tile, logical - mt * p.n_tiles_n, sA0, sA1, sB0, sB1, sLt);
   }
 }
 
