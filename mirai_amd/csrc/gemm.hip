@@ -111,6 +111,7 @@ struct Params {
   const int2 *tiles_r;       // dual launch: the 128-row remainder tiles
   const int32_t *num_tiles_r;
   int slots_tall;            // dual launch: per-XCD slots of the 256-row tiles
+  int stagger;               // dual launch: leading per-XCD slots given to remainder tiles
   const int64_t *seg_end;
   uint16_t *out;
   int64_t ldo;
@@ -1183,6 +1184,7 @@ __device__ __forceinline__ void light_tile(const Params &p, int2 tile, int nt, u
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w, a, acc, 0, 0, 0);
     }
   };
+  // The codes of step b + 1 load while step b decodes.
   int b = 0;
   for (; b + 1 < KS; b += 2) {
     load_codes(b + 1, c1);
@@ -1278,8 +1280,13 @@ __device__ __forceinline__ void light_tile(const Params &p, int2 tile, int nt, u
 template <int FMT, int EPI, bool LORA, class T>
 __global__ __launch_bounds__(T::NT) __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_SIMD)))
 void grouped_gemm_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) uint8_t sA0[T::STAGE_A];
-  __shared__ __attribute__((aligned(16))) uint8_t sA1[T::STAGE_A];
+  // 128-row tiles of the layer GEMMs: A stages of 32 KB, so that the light
+  // tile stages up to 2048 K columns (the kernel runs one workgroup per CU
+  // by its registers, so the LDS costs no occupancy).
+  constexpr bool kLight = light_capable<FMT, EPI>() && T::BM == 128;
+  constexpr int kStageA = kLight && T::STAGE_A < 32768 ? 32768 : T::STAGE_A;
+  __shared__ __attribute__((aligned(16))) uint8_t sA0[kStageA];
+  __shared__ __attribute__((aligned(16))) uint8_t sA1[kStageA];
   __shared__ __attribute__((aligned(16))) uint8_t sB0[T::STAGE_B];
   __shared__ __attribute__((aligned(16))) uint8_t sB1[T::STAGE_B];
   __shared__ __attribute__((aligned(16))) uint8_t sLt[lora_tile_bytes<EPI, LORA, T>()];
@@ -1291,10 +1298,10 @@ void grouped_gemm_kernel(Params p) {
   if (logical >= total) return;
   const int mt = logical / p.n_tiles_n;
   const int2 tile = p.tiles[mt];
-  if constexpr (light_capable<FMT, EPI>() && T::BM == 128) {
-    if (light_tile_fits<T::STAGE_A, T::STAGE_B>(p, tile)) {
-      light_tile<FMT, EPI, LORA, T::STAGE_A, T::STAGE_B>(p, tile, logical - mt * p.n_tiles_n, sA0,
-                                                         sA1, sB0, sB1);
+  if constexpr (kLight) {
+    if (light_tile_fits<kStageA, T::STAGE_B>(p, tile)) {
+      light_tile<FMT, EPI, LORA, kStageA, T::STAGE_B>(p, tile, logical - mt * p.n_tiles_n, sA0,
+                                                      sA1, sB0, sB1);
       return;
     }
   }
@@ -1302,10 +1309,12 @@ void grouped_gemm_kernel(Params p) {
 }
 
 // 256-row tiles (p.tiles) and the 128-row remainder tiles (p.tiles_r) in one
-// launch. Each XCD runs its share of the tall tiles first (slots below
-// p.slots_tall, in the map above) and then its share of the remainder tiles,
-// which so fill the tail of the tall ones instead of running as a launch of
-// their own after it.
+// launch. Each XCD runs its share of the tall tiles (slots p.stagger ..
+// p.stagger + p.slots_tall - 1, in the map above) and then the rest of its
+// share of the remainder tiles, which so fill the tail of the tall ones
+// instead of running as a launch of their own after it. The first p.stagger
+// slots of an XCD take remainder tiles: those CUs start their tall tiles half
+// a tile later, so the CUs' epilogues (the output stores) stop coinciding.
 template <int FMT, int EPI, bool LORA, class Tall, class Short>
 __global__ __launch_bounds__(Tall::NT) __attribute__((amdgpu_waves_per_eu(Tall::WAVES_PER_SIMD)))
 void grouped_gemm_dual_kernel(Params p) {
@@ -1318,11 +1327,13 @@ void grouped_gemm_dual_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t sB1[Tall::STAGE_B];
   __shared__ __attribute__((aligned(16))) uint8_t sLt[lora_tile_bytes<EPI, LORA, Tall>()];
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  if (slot < p.slots_tall) {
+  const bool tall = slot >= p.stagger && slot < p.stagger + p.slots_tall;
+  if (tall) {
     const int total = *p.num_tiles * p.n_tiles_n;
     const int per_xcd = (total + 7) >> 3;
-    if (slot >= per_xcd) return;
-    const int logical = xcd * per_xcd + slot;
+    const int st = slot - p.stagger;
+    if (st >= per_xcd) return;
+    const int logical = xcd * per_xcd + st;
     if (logical >= total) return;
     const int mt = logical / p.n_tiles_n;
     gemm_tile<FMT, EPI, LORA, Tall>(p, p.tiles[mt], logical - mt * p.n_tiles_n, sA0, sA1, sB0,
@@ -1330,7 +1341,7 @@ void grouped_gemm_dual_kernel(Params p) {
   } else {
     const int total = *p.num_tiles_r * p.n_tiles_n;
     const int per_xcd = (total + 7) >> 3;
-    const int s2 = slot - p.slots_tall;
+    const int s2 = slot < p.stagger ? slot : slot - p.slots_tall;
     if (s2 >= per_xcd) return;
     const int logical = xcd * per_xcd + s2;
     if (logical >= total) return;
@@ -1375,6 +1386,9 @@ int launch_dual(Params p, int64_t max_tall, int64_t max_short, hipStream_t s) {
     return MX_ERR_INVALID;
   }
   p.slots_tall = static_cast<int>(slots_tall);
+  // Half of the 32 CUs of an XCD (gfx950: 256 CUs in 8 XCDs) start on a
+  // remainder tile, when there are that many.
+  p.stagger = static_cast<int>(std::min<int64_t>(16, slots_short));
   hipLaunchKernelGGL((grouped_gemm_dual_kernel<FMT, EPI, LORA, Tall, Short>),
                      dim3(static_cast<unsigned>(grid)), dim3(Tall::NT), 0, s, p);
   return check_launch("grouped GEMM launch");
