@@ -342,3 +342,30 @@ def test_routed_layer_top_k(k):
 @pytest.mark.parametrize("r", [4, 12, 36])
 def test_lora_ranks_off_the_multiple_of_eight(r):
     _run_case(small("nf4", r=r, alpha=2.0 * r, E=5, k=3, T=300, f=320, d=192))
+
+
+@pytest.mark.parametrize("fmt,r,T,E,k", [("nf4", 16, 1400, 9, 2), ("int8", 32, 600, 8, 2),
+                                         ("bf16", 8, 300, 16, 2), ("nf4", 64, 700, 6, 2),
+                                         ("nf4", 24, 500, 12, 4)])
+def test_inference_forward_equals_training_forward(fmt, r, T, E, k):
+    # The training forward (saved activations, LoRA rows kept) and the
+    # inference forward run the same kernels on the same rows: the outputs
+    # agree bit for bit. Skewed routes put light experts (at most 32 rows)
+    # next to tall tiles.
+    from test_gpu_light_tiles import LIGHT_COUNTS, skewed_routes
+
+    w = wl.Workload(f"inf_train_{fmt}", 12, T, 256, 384, E, k, r, 16.0, fmt, torch.bfloat16)
+    dense = wl.dense_weights(w)
+    lora = wl.lora_factors(w)
+    m = build_module(w, dense, lora)
+    counts = LIGHT_COUNTS[: E - k]
+    idx, scores = skewed_routes(T, E, k, counts, seed=9)
+    x = wl.tokens(w).cuda()
+    with torch.no_grad():
+        out_inf = m.run_direct_routed(x, scores.cuda(), idx.cuda())
+    xg = x.clone().requires_grad_(True)
+    out_train = m.run_direct_routed(xg, scores.cuda(), idx.cuda())
+    assert torch.equal(out_inf, out_train.detach())
+    ref = olayer.layer_forward(x.cpu(), scores, idx, oracle_weights(w, dense, dtype=w.dtype),
+                               oracle_loras(w, lora), w.experts)
+    assert_layer_close(out_inf.cpu(), ref)
