@@ -19,6 +19,11 @@
  *                   i+4 in the high nibble), absmax [E, out, in/64] bf16
  *   NF4_F32 weight  codes as NF4, absmax [E, out, in/64] fp32 (the double-quant
  *                   absmax of a bitsandbytes payload, decoded by mx_nf4_from_bnb)
+ *   NF4_DQ weight   codes as NF4; `scale` points to a host-side mx_nf4_dq
+ *                   holding the bitsandbytes two-level absmax as stored
+ *                   (uint8 codes, fp32 nested scales, fp32 offsets, 256-entry
+ *                   code table), decoded inside the GEMMs
+ *   NF4_DQ_KN       NF4_DQ for a weight stored [E, in, out] (as NF4_F32_KN)
  *   NF4_F32_KN      the same codes and fp32 absmax for a weight stored
  *                   [E, in, out] (y = x @ W[e], the MAGI-2 group layout of
  *                   magi2_preview.py:2680-2704): codes [E, in, out/2] packed
@@ -62,6 +67,26 @@ extern "C" {
 #define MX_FMT_F32X3 3
 #define MX_FMT_NF4_F32 4  /* NF4 codes with an fp32 absmax per block (ingested bitsandbytes) */
 #define MX_FMT_NF4_F32_KN 5  /* NF4_F32 stored [E, in, out], blocks along out (MAGI-2 groups) */
+#define MX_FMT_NF4_DQ 6      /* NF4 codes with the two-level absmax of a bitsandbytes payload */
+#define MX_FMT_NF4_DQ_KN 7   /* NF4_DQ stored [E, in, out], blocks along out */
+
+/*
+ * Two-level (double-quantised) absmax of an MX_FMT_NF4_DQ / _DQ_KN weight, as a
+ * bitsandbytes payload stores it (quantize_4bit with compress_statistics=True,
+ * blocksize 64, nested blocksize 256; quant.py:294-302, 407-431 and
+ * quantized_experts.py:325-346 of the reference): block b of expert e, the
+ * blocks numbered along the stored rows in order, has the absmax
+ * fp32(fp32(code[absmax_q[e][b]] * nested_absmax[e][b / 256]) + offsets[e]),
+ * two roundings, as mx_nf4_from_bnb decodes it. The pointers are device
+ * pointers; the struct itself is read on the host during the call.
+ */
+typedef struct mx_nf4_dq {
+  const uint8_t *absmax_q;     /* [E, blocks per expert] */
+  const float *nested_absmax;  /* [E, nested_per_expert] */
+  const float *offsets;        /* [E] */
+  const float *code;           /* [256] */
+  int64_t nested_per_expert;   /* ceil(blocks per expert / 256) */
+} mx_nf4_dq;
 
 /* Expert id of a route slot that is left out of the layer on purpose: the
  * plan skips it without counting it as an invalid route (any other id outside
@@ -353,11 +378,22 @@ int mx_nf4_dequantize_ex(const uint8_t *codes, const void *absmax, int absmax_dt
  * absmax bitsandbytes dequantises with (quant.py:413-431), so the GEMMs decode
  * the payload's weights without re-quantisation. The 16-entry NF4 code table
  * of the payload ({key}_nf4_code) must equal the NF4 levels (checked by the
- * caller). cols a multiple of 64.
+ * caller). cols a multiple of 64. With absmax NULL only the codes are written
+ * (MX_FMT_NF4_DQ keeps the payload's two-level absmax as it is).
  */
 int mx_nf4_from_bnb(const uint8_t *packed, const uint8_t *absmax_q, const float *nested_absmax,
                     const float *offsets, const float *nested_code, int64_t experts, int64_t rows,
                     int64_t cols, uint8_t *codes, float *absmax, void *stream);
+
+/*
+ * The fp32 block absmax of a two-level (MX_FMT_NF4_DQ) payload, as the GEMMs
+ * decode it per K step: absmax[e][b] = fp32(fp32(code[absmax_q[e][b]] *
+ * nested_absmax[e][b / 256]) + offsets[e]) for b < blocks_per_expert (the
+ * dequantize_blockwise + offset step of quant.py:413-424). With it,
+ * mx_nf4_dequantize_ex dequantises NF4_DQ weights.
+ */
+int mx_nf4_dq_absmax(const mx_nf4_dq *dq, int64_t experts, int64_t blocks_per_expert,
+                     float *absmax, void *stream);
 
 /*
  * Symmetric per-output-row INT8: scale = bf16(max(absmax_row/127, 1e-30)),
@@ -377,10 +413,12 @@ int mx_int8_dequantize(const int8_t *q, const void *scale, int64_t rows, int64_t
 /* ------------------------------------------------------------------------ */
 
 /* Frozen projection weight in one of the MX_FMT_* formats, [E, out, in]. */
+
 typedef struct mx_weight {
   int format;           /* MX_FMT_* */
   const void *data;     /* bf16 w | uint8 codes | int8 q */
-  const void *scale;    /* NULL | bf16 absmax [E,out,in/64] | bf16 scale [E,out] */
+  const void *scale;    /* NULL | absmax [E,out,in/64] (bf16, fp32) | bf16 scale [E,out]
+                           | const mx_nf4_dq * (NF4_DQ formats, host memory) */
   int64_t out_features;
   int64_t in_features;
 } mx_weight;

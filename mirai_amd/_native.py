@@ -30,6 +30,8 @@ FMT_INT8 = 2
 FMT_F32X3 = 3      # fp32 weights as bf16 planes [hi | lo | hi] along in_features
 FMT_NF4_F32 = 4    # NF4 codes with an fp32 block absmax (ingested bitsandbytes payloads)
 FMT_NF4_F32_KN = 5  # the same, stored [E, in, out] with the blocks along out (MAGI-2 groups)
+FMT_NF4_DQ = 6     # NF4 codes with a bitsandbytes two-level absmax decoded in the GEMMs
+FMT_NF4_DQ_KN = 7  # the same, stored [E, in, out]
 
 SPLIT_ACT = 0      # mx_split_f32 plane orders
 SPLIT_WEIGHT = 1
@@ -52,7 +54,7 @@ ROUTE_LAYOUT_ROWS = 1
 ROUTE_DROPPED = -(1 << 63)
 
 # mx_abi_version() of the library these bindings describe.
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 PLAN_MAX_EXPERTS = 8192
 STATIC_SCRATCH_BYTES = 64 << 20  # MX_STATIC_SCRATCH_BYTES
@@ -70,6 +72,17 @@ class MxWeight(ctypes.Structure):
         ("scale", c_void_p),
         ("out_features", c_int64),
         ("in_features", c_int64),
+    ]
+
+
+class MxNf4Dq(ctypes.Structure):
+    """mx_nf4_dq: the two-level absmax of an NF4_DQ weight (device pointers)."""
+    _fields_ = [
+        ("absmax_q", c_void_p),
+        ("nested_absmax", c_void_p),
+        ("offsets", c_void_p),
+        ("code", c_void_p),
+        ("nested_per_expert", c_int64),
     ]
 
 
@@ -137,6 +150,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "mx_nf4_dequantize_ex": (c_int, [_P, _P, c_int, c_int64, c_int64, _P, c_int, _P]),
     "mx_nf4_from_bnb": (
         c_int, [_P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P]),
+    "mx_nf4_dq_absmax": (c_int, [POINTER(MxNf4Dq), c_int64, c_int64, _P, _P]),
     "mx_int8_quantize": (c_int, [_P, c_int, c_int64, c_int64, _P, _P, _P]),
     "mx_int8_dequantize": (c_int, [_P, _P, c_int64, c_int64, _P, c_int, _P]),
     "mx_set_stage_events": (c_int, [POINTER(c_void_p), c_int]),

@@ -30,4 +30,4 @@ int check_launch(const char *what) {
 
 extern "C" const char *mx_last_error(void) { return mx::g_error; }
 
-extern "C" int mx_abi_version(void) { return 8; }
+extern "C" int mx_abi_version(void) { return 9; }

@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void nf4_from_bnb_kernel(
     out |= e_odd << (8 * (k1 & 3) + 4 * (k1 >> 2));
   }
   codes[g] = out;
-  if ((g & 7) == 0) {  // first group of a 64-element block
+  if (absmax != nullptr && (g & 7) == 0) {  // first group of a 64-element block
 #pragma clang fp contract(off)
     const int64_t e = g / groups_per_expert;
     const int64_t b = (g - e * groups_per_expert) >> 3;  // block within the expert
@@ -160,6 +160,21 @@ __global__ __launch_bounds__(256) void int8_dequantize_kernel(const int8_t *q,
   const float s = bf16_bits_to_f32(scale[i / cols]);
   const float v = static_cast<float>(q[i]) * s;  // exact: 7-bit integer times 8-bit mantissa
   store_value(out, i, bf16_bits_to_f32(f32_to_bf16_bits(v)), out_dtype);
+}
+
+// absmax[e][b] = fp32(fp32(code[q[e][b]] * nested[e][b / 256]) + offsets[e]).
+__global__ __launch_bounds__(256) void nf4_dq_absmax_kernel(const uint8_t *q, const float *nested,
+                                                            const float *offsets, const float *code,
+                                                            int64_t blocks_per_expert,
+                                                            int64_t nested_per_expert, int64_t total,
+                                                            float *absmax) {
+#pragma clang fp contract(off)
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int64_t e = i / blocks_per_expert, b = i - e * blocks_per_expert;
+  // Two roundings (product, then sum), never one fused multiply-add.
+  const float scaled = code[q[i]] * nested[e * nested_per_expert + (b >> 8)];
+  absmax[i] = scaled + offsets[e];
 }
 
 }  // namespace
@@ -227,8 +242,8 @@ extern "C" int mx_nf4_from_bnb(const uint8_t *packed, const uint8_t *absmax_q,
                                const float *nested_code, int64_t experts, int64_t rows,
                                int64_t cols, uint8_t *codes, float *absmax, void *stream) {
   clear_error();
-  if (!packed || !absmax_q || !nested_absmax || !offsets || !nested_code || !codes || !absmax) {
-    set_error("mx_nf4_from_bnb: buffers must be non-null");
+  if (!packed || !codes || (absmax && (!absmax_q || !nested_absmax || !offsets || !nested_code))) {
+    set_error("mx_nf4_from_bnb: buffers must be non-null (absmax may be null: codes only)");
     return MX_ERR_INVALID;
   }
   if (experts < 0 || rows < 0 || cols <= 0 || cols % 64 != 0) {
@@ -248,6 +263,27 @@ extern "C" int mx_nf4_from_bnb(const uint8_t *packed, const uint8_t *absmax_q,
                      absmax_q, nested_absmax, offsets, nested_code, groups_per_expert,
                      nested_per_expert, total, reinterpret_cast<uint32_t *>(codes), absmax);
   return check_launch("mx_nf4_from_bnb");
+}
+
+extern "C" int mx_nf4_dq_absmax(const mx_nf4_dq *dq, int64_t experts, int64_t blocks_per_expert,
+                                float *absmax, void *stream) {
+  clear_error();
+  if (!dq || !absmax || !dq->absmax_q || !dq->nested_absmax || !dq->offsets || !dq->code) {
+    set_error("mx_nf4_dq_absmax: buffers must be non-null");
+    return MX_ERR_INVALID;
+  }
+  if (experts < 0 || blocks_per_expert < 0 ||
+      dq->nested_per_expert < ceil_div(blocks_per_expert, 256)) {
+    set_error("mx_nf4_dq_absmax: need experts, blocks >= 0 and ceil(blocks / 256) nested scales "
+              "per expert");
+    return MX_ERR_INVALID;
+  }
+  const int64_t total = experts * blocks_per_expert;
+  if (total == 0) return MX_OK;
+  hipLaunchKernelGGL(nf4_dq_absmax_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))),
+                     dim3(256), 0, as_stream(stream), dq->absmax_q, dq->nested_absmax, dq->offsets,
+                     dq->code, blocks_per_expert, dq->nested_per_expert, total, absmax);
+  return check_launch("mx_nf4_dq_absmax");
 }
 
 extern "C" int mx_int8_quantize(const void *w, int w_dtype, int64_t rows, int64_t cols,

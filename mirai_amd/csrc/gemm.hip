@@ -38,22 +38,37 @@ constexpr int kLoraMaxRank = 256; // largest LoRA rank the layer takes
 
 enum { EPI_SWIGLU = 0, EPI_STORE = 1, EPI_LORA_A = 2, EPI_STORE2 = 4 };
 
-// NF4 codes with a bf16 absmax (the build's own quantiser) or an fp32 absmax
-// (bitsandbytes payloads, whose double-quantised absmax decodes to fp32).
+// NF4 codes with a bf16 absmax (the build's own quantiser), an fp32 absmax
+// (bitsandbytes payloads, the double-quantised absmax decoded at load) or the
+// payload's two-level absmax decoded per K step (NF4_DQ: a uint8 code into a
+// 256-entry table, a nested fp32 scale per 256 blocks, an fp32 offset per
+// expert).
+constexpr bool is_dq(int fmt) { return fmt == MX_FMT_NF4_DQ || fmt == MX_FMT_NF4_DQ_KN; }
 constexpr bool is_nf4(int fmt) {
-  return fmt == MX_FMT_NF4 || fmt == MX_FMT_NF4_F32 || fmt == MX_FMT_NF4_F32_KN;
+  return fmt == MX_FMT_NF4 || fmt == MX_FMT_NF4_F32 || fmt == MX_FMT_NF4_F32_KN || is_dq(fmt);
 }
 constexpr bool f32_absmax(int fmt) { return fmt == MX_FMT_NF4_F32 || fmt == MX_FMT_NF4_F32_KN; }
+// Bytes of one block's absmax entry (DQ: the uint8 code).
+constexpr int absmax_bytes(int fmt) { return f32_absmax(fmt) ? 4 : is_dq(fmt) ? 1 : 2; }
 // Weights stored [E, in, out] with the NF4 blocks along out (a MAGI-2 packed
 // group, x @ W[g]): the forward reads them as the backward reads [E, out, in]
 // weights (B = W, transposed decode) and the backward as the forward does.
-constexpr bool is_kn(int fmt) { return fmt == MX_FMT_NF4_F32_KN; }
+constexpr bool is_kn(int fmt) { return fmt == MX_FMT_NF4_F32_KN || fmt == MX_FMT_NF4_DQ_KN; }
 
-// Block absmax i of a row as raw bits (a bf16 in the low half, or fp32 bits).
+// Block absmax i of a row as raw bits (a bf16 in the low half, fp32 bits, or
+// the DQ absmax code).
 template <int FMT>
 __device__ __forceinline__ uint32_t load_absmax(const void *row, int64_t i) {
   if (f32_absmax(FMT)) return static_cast<const uint32_t *>(row)[i];
+  if (is_dq(FMT)) return static_cast<const uint8_t *>(row)[i];
   return static_cast<const uint16_t *>(row)[i];
+}
+// The two-level absmax of a DQ block: fp32(fp32(code * nested) + offset), two
+// roundings as in the payload's dequantisation (no fused multiply-add).
+__device__ __forceinline__ float dq_absmax(float code, float nested, float offset) {
+#pragma clang fp contract(off)
+  const float scaled = code * nested;
+  return scaled + offset;
 }
 template <int FMT>
 __device__ __forceinline__ float absmax_value(uint32_t raw) {
@@ -121,6 +136,13 @@ struct Params {
   float scale[4];
   int split_r[4];            // MX_FMT_F32X3 LoRA down-projection: rank of each adapter
   int act;                   // EPI_SWIGLU: MX_ACT_SILU or MX_ACT_SWIGLU7
+  // MX_FMT_NF4_DQ*: per weight group (as w[0], w[1]) the nested scales [E,
+  // dq_npe], the offsets [E] and the 256-entry code table; wscale holds the
+  // uint8 absmax codes.
+  const float *dq_nested[2];
+  const float *dq_offset[2];
+  const float *dq_code[2];
+  int64_t dq_npe[2];
 };
 
 // Per-thread choice among the small kernel-argument arrays by explicit
@@ -329,7 +351,7 @@ __device__ __forceinline__ void projection_run(float (&v)[4], float (&a)[4], uin
 template <int FMT, int EPI, bool LORA, class T>
 __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *sA0,
                                           uint8_t *sA1, uint8_t *sB0, uint8_t *sB1,
-                                          uint8_t *sLt) {
+                                          uint8_t *sLt, const float *sCode) {
   constexpr int kLTile = lora_tile_bytes<EPI, LORA, T>();
   const int tid = threadIdx.x;
   // MX_FMT_F32X3: bf16 planes with K = 3 * in (loaded as bf16); the
@@ -414,12 +436,12 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
     if (is_nf4(FMT)) {
       b_base = w + wrow * (row_k / 2) + bh * (T::B_ELEMS / 2);
       b_absmax = static_cast<const uint8_t *>(pick(p.wscale, which)) +
-                 wrow * (row_k / kNf4Block) * (f32_absmax(FMT) ? 4 : 2);
+                 wrow * (row_k / kNf4Block) * absmax_bytes(FMT);
       if (kSplitK && p.k_split < p.K) {
         const int64_t wrow1 = static_cast<int64_t>(e) * p.wn[1] + bn;
         b_base1 = static_cast<const uint8_t *>(p.w[1]) + wrow1 * (row_k / 2) + bh * (T::B_ELEMS / 2);
         b_absmax1 = static_cast<const uint8_t *>(p.wscale[1]) +
-                    wrow1 * (row_k / kNf4Block) * (f32_absmax(FMT) ? 4 : 2);
+                    wrow1 * (row_k / kNf4Block) * absmax_bytes(FMT);
       }
     } else if (FMT == MX_FMT_INT8) {
       b_base = w + wrow * p.K + bh * T::B_ELEMS;
@@ -427,6 +449,28 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
     } else {
       b_base = w + wrow * p.K * 2 + bh * T::B_ELEMS * 2;
     }
+  }
+  // NF4_DQ, row decode: the nested scales of this thread's row. With K <= 16384
+  // a row's blocks span at most two 256-block groups: `lo` up to block `sw` of
+  // the row, `hi` after it (the same value when the row stays in one group).
+  struct DqRow {
+    float lo = 0.0f, hi = 0.0f, off = 0.0f;
+    int sw = 0;
+  };
+  auto dq_row = [&](int wsel, int64_t row_in_expert, int64_t kblocks) -> DqRow {
+    DqRow r;
+    const float *nest = pick2(p.dq_nested, wsel) + static_cast<int64_t>(e) * pick2(p.dq_npe, wsel);
+    const int64_t b0 = row_in_expert * kblocks;
+    r.lo = nest[b0 >> 8];
+    r.hi = nest[(b0 + kblocks - 1) >> 8];
+    r.sw = static_cast<int>((((b0 >> 8) + 1) << 8) - b0);
+    r.off = pick2(p.dq_offset, wsel)[e];
+    return r;
+  };
+  DqRow dq0, dq1;
+  if (is_dq(FMT) && !TRANS && b_valid) {
+    dq0 = dq_row(which, bn, row_k / kNf4Block);
+    if (kSplitK && p.k_split < p.K) dq1 = dq_row(1, bn, row_k / kNf4Block);
   }
 
   // Bytes of B per thread per stage, in 16-byte registers.
@@ -438,6 +482,7 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   struct BRegs {
     u32x4 q[kBRegs];
     uint32_t abs;
+    uint32_t nest;  // NF4_DQ, transposed decode: the block's nested scale (fp32 bits)
   };
   BRegs rb0, rb1;
 
@@ -464,6 +509,12 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
       if (is_nf4(FMT)) {
         rb.q[0] = *reinterpret_cast<const u32x4 *>(w + wrow * (p.N / 2) + t_col0 / 2);
         rb.abs = load_absmax<FMT>(ws, wrow * (p.N / kNf4Block) + t_col0 / kNf4Block);
+        if (is_dq(FMT)) {
+          const int wsel = second ? 1 : 0;
+          const int64_t blk = krow * (p.N / kNf4Block) + t_col0 / kNf4Block;  // within the expert
+          rb.nest = __float_as_uint(
+              pick2(p.dq_nested, wsel)[static_cast<int64_t>(e) * pick2(p.dq_npe, wsel) + (blk >> 8)]);
+        }
       } else if (FMT == MX_FMT_INT8) {
 #pragma unroll
         for (int q = 0; q < kBRegs; ++q)
@@ -492,6 +543,36 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
 #pragma unroll
       for (int q = 0; q < kBRegs; ++q) rb.q[q] = u32x4{0u, 0u, 0u, 0u};
       rb.abs = 0;
+    }
+  };
+  // The decode table of K stage `stage`'s block: level x absmax, the absmax
+  // from the loaded bits (DQ: the code through its weight's table in LDS, times
+  // the block's nested scale, plus the expert's offset).
+  auto block_table = [&](const BRegs &rb, int stage) __attribute__((always_inline)) -> Nf4Table {
+    if constexpr (is_dq(FMT)) {
+      int wsel;
+      float nested, off;
+      if (TRANS) {
+        const int64_t kb = static_cast<int64_t>(stage) * BK;
+        const bool second = EPI == EPI_SWIGLU ? t_which != 0 : (EPI == EPI_STORE2 && kb >= p.k_split);
+        wsel = second ? 1 : 0;
+        nested = __uint_as_float(rb.nest);
+        off = pick2(p.dq_offset, wsel)[e];
+      } else {
+        int ks = stage;
+        DqRow d = dq0;
+        wsel = which;
+        if (kSplitK && static_cast<int64_t>(stage) * BK >= p.k_split) {
+          ks = stage - static_cast<int>(p.k_split / BK);
+          d = dq1;
+          wsel = 1;
+        }
+        nested = ks < d.sw ? d.lo : d.hi;
+        off = d.off;
+      }
+      return nf4_table(dq_absmax(sCode[wsel * 256 + rb.abs], nested, off));
+    } else {
+      return is_nf4(FMT) ? nf4_table(absmax_value<FMT>(rb.abs)) : Nf4Table{};
     }
   };
   // Decode part `part` (of KSUB) of this thread's B elements into LDS stage st.
@@ -647,7 +728,7 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
     else
       load_a(min(kt + 1, KT - 1), nA);
     load_b(min(kt + 2, KT - 1), b_after);
-    const Nf4Table t = is_nf4(FMT) ? nf4_table(absmax_value<FMT>(b_next.abs)) : Nf4Table{};
+    const Nf4Table t = block_table(b_next, min(kt + 1, KT - 1));
 #pragma unroll
     for (int kk = 0; kk < T::KSUB; ++kk) {
       Frags &cur = (kk & 1) ? f1 : f0;
@@ -664,7 +745,7 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   load_b(0, rb0);
   load_b(min(1, KT - 1), rb1);
   {
-    const Nf4Table t = is_nf4(FMT) ? nf4_table(absmax_value<FMT>(rb0.abs)) : Nf4Table{};
+    const Nf4Table t = block_table(rb0, 0);
 #pragma unroll
     for (int part = 0; part < T::KSUB; ++part) decode_b(rb0, t, sB0, part);
   }
@@ -1058,7 +1139,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 template <int FMT, int EPI>
 constexpr bool light_capable() {
-  return (FMT == MX_FMT_NF4 || FMT == MX_FMT_NF4_F32) && (EPI == EPI_SWIGLU || EPI == EPI_STORE);
+  return (FMT == MX_FMT_NF4 || FMT == MX_FMT_NF4_F32 || FMT == MX_FMT_NF4_DQ) &&
+         (EPI == EPI_SWIGLU || EPI == EPI_STORE);
 }
 
 // Columns of K the four stage buffers hold for 32 rows (two of SA bytes, two of SB).
@@ -1077,7 +1159,8 @@ __device__ __forceinline__ bool light_tile_fits(const Params &p, int2 tile) {
 
 template <int FMT, int EPI, bool LORA, int SA, int SB>
 __device__ __forceinline__ void light_tile(const Params &p, int2 tile, int nt, uint8_t *sA0,
-                                           uint8_t *sA1, uint8_t *sB0, uint8_t *sB1) {
+                                           uint8_t *sA1, uint8_t *sB0, uint8_t *sB1,
+                                           const float *sCode) {
   static_assert(SA % 8192 == 0 && SB % 8192 == 0, "stage rows must be whole 256-byte groups");
   const int e = tile.x;
   const int64_t row0 = tile.y;
@@ -1142,7 +1225,18 @@ __device__ __forceinline__ void light_tile(const Params &p, int2 tile, int nt, u
   const int64_t wrow = static_cast<int64_t>(e) * pick(p.wn, which) + n_row;
   const uint8_t *codes = static_cast<const uint8_t *>(pick(p.w, which)) + wrow * (p.K / 2);
   const uint8_t *absrow = static_cast<const uint8_t *>(pick(p.wscale, which)) +
-                          wrow * (p.K / kNf4Block) * (f32_absmax(FMT) ? 4 : 2);
+                          wrow * (p.K / kNf4Block) * absmax_bytes(FMT);
+  // NF4_DQ: the row's nested scales (K <= 2048 here: at most two groups).
+  float dq_lo = 0.0f, dq_hi = 0.0f, dq_off = 0.0f;
+  int dq_sw = 0;
+  if constexpr (is_dq(FMT)) {
+    const int64_t kblocks = p.K / kNf4Block, b0 = n_row * kblocks;
+    const float *nest = pick2(p.dq_nested, which) + static_cast<int64_t>(e) * pick2(p.dq_npe, which);
+    dq_lo = nest[b0 >> 8];
+    dq_hi = nest[(b0 + kblocks - 1) >> 8];
+    dq_sw = static_cast<int>((((b0 >> 8) + 1) << 8) - b0);
+    dq_off = pick2(p.dq_offset, which)[e];
+  }
   const int KS = K / 128;  // K steps
   struct Codes {
     u32x4 q[2];
@@ -1170,7 +1264,13 @@ __device__ __forceinline__ void light_tile(const Params &p, int2 tile, int nt, u
     const int kq = region_k(q);
     const uint8_t *arow = region(q) + li * (2 * kq);
     const int c0k = (k - region_k0(q)) >> 3;  // first 16-byte chunk of the lane's 64 elements
-    const Nf4Table t = nf4_table(absmax_value<FMT>(c.abs));
+    Nf4Table t;
+    if constexpr (is_dq(FMT)) {
+      const int blk = 2 * b + h;
+      t = nf4_table(dq_absmax(sCode[which * 256 + c.abs], blk < dq_sw ? dq_lo : dq_hi, dq_off));
+    } else {
+      t = nf4_table(absmax_value<FMT>(c.abs));
+    }
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const int chunk = c0k + s;
@@ -1272,6 +1372,19 @@ __device__ __forceinline__ void light_tile(const Params &p, int2 tile, int nt, u
   }
 }
 
+// NF4_DQ: the code tables of the launch's weights (w[0], w[1]) into LDS,
+// published by a barrier before any tile builds a decode table from them.
+template <int FMT>
+__device__ __forceinline__ void load_code_tables(const Params &p, float *sCode) {
+  if constexpr (is_dq(FMT)) {
+    for (int t = threadIdx.x; t < 512; t += blockDim.x) {
+      const float *code = t < 256 ? p.dq_code[0] : p.dq_code[1];
+      sCode[t] = code ? code[t & 255] : 0.0f;
+    }
+    __syncthreads();
+  }
+}
+
 // One launch over one tile list (p.tiles, *p.num_tiles row tiles). The
 // blockIdx -> tile map gives each of the 8 XCDs (workgroups go to XCDs
 // round-robin) a contiguous run of tiles, row-tile major, so the column tiles
@@ -1290,6 +1403,7 @@ void grouped_gemm_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t sB0[T::STAGE_B];
   __shared__ __attribute__((aligned(16))) uint8_t sB1[T::STAGE_B];
   __shared__ __attribute__((aligned(16))) uint8_t sLt[lora_tile_bytes<EPI, LORA, T>()];
+  __shared__ float sCode[is_dq(FMT) ? 512 : 1];
   const int total = *p.num_tiles * p.n_tiles_n;
   const int per_xcd = (total + 7) >> 3;
   const int slot = blockIdx.x >> 3;
@@ -1298,14 +1412,15 @@ void grouped_gemm_kernel(Params p) {
   if (logical >= total) return;
   const int mt = logical / p.n_tiles_n;
   const int2 tile = p.tiles[mt];
+  load_code_tables<FMT>(p, sCode);
   if constexpr (kLight) {
     if (light_tile_fits<kStageA, T::STAGE_B>(p, tile)) {
       light_tile<FMT, EPI, LORA, kStageA, T::STAGE_B>(p, tile, logical - mt * p.n_tiles_n, sA0,
-                                                      sA1, sB0, sB1);
+                                                      sA1, sB0, sB1, sCode);
       return;
     }
   }
-  gemm_tile<FMT, EPI, LORA, T>(p, tile, logical - mt * p.n_tiles_n, sA0, sA1, sB0, sB1, sLt);
+  gemm_tile<FMT, EPI, LORA, T>(p, tile, logical - mt * p.n_tiles_n, sA0, sA1, sB0, sB1, sLt, sCode);
 }
 
 // 256-row tiles (p.tiles) and the 128-row remainder tiles (p.tiles_r) in one
@@ -1326,6 +1441,7 @@ void grouped_gemm_dual_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t sB0[Tall::STAGE_B];
   __shared__ __attribute__((aligned(16))) uint8_t sB1[Tall::STAGE_B];
   __shared__ __attribute__((aligned(16))) uint8_t sLt[lora_tile_bytes<EPI, LORA, Tall>()];
+  __shared__ float sCode[is_dq(FMT) ? 512 : 1];
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const bool tall = slot >= p.stagger && slot < p.stagger + p.slots_tall;
   if (tall) {
@@ -1336,8 +1452,9 @@ void grouped_gemm_dual_kernel(Params p) {
     const int logical = xcd * per_xcd + st;
     if (logical >= total) return;
     const int mt = logical / p.n_tiles_n;
+    load_code_tables<FMT>(p, sCode);
     gemm_tile<FMT, EPI, LORA, Tall>(p, p.tiles[mt], logical - mt * p.n_tiles_n, sA0, sA1, sB0,
-                                    sB1, sLt);
+                                    sB1, sLt, sCode);
   } else {
     const int total = *p.num_tiles_r * p.n_tiles_n;
     const int per_xcd = (total + 7) >> 3;
@@ -1347,15 +1464,17 @@ void grouped_gemm_dual_kernel(Params p) {
     if (logical >= total) return;
     const int mt = logical / p.n_tiles_n;
     const int2 tile = p.tiles_r[mt];
+    load_code_tables<FMT>(p, sCode);
     // An expert's only tile, when it has at most kLightRows rows.
     if constexpr (light_capable<FMT, EPI>()) {
       if (light_tile_fits<Tall::STAGE_A, Tall::STAGE_B>(p, tile)) {
         light_tile<FMT, EPI, LORA, Tall::STAGE_A, Tall::STAGE_B>(p, tile, logical - mt * p.n_tiles_n,
-                                                               sA0, sA1, sB0, sB1);
+                                                               sA0, sA1, sB0, sB1, sCode);
         return;
       }
     }
-    gemm_tile<FMT, EPI, LORA, Short>(p, tile, logical - mt * p.n_tiles_n, sA0, sA1, sB0, sB1, sLt);
+    gemm_tile<FMT, EPI, LORA, Short>(p, tile, logical - mt * p.n_tiles_n, sA0, sA1, sB0, sB1, sLt,
+                                     sCode);
   }
 }
 
@@ -1411,6 +1530,10 @@ int launch_tile(int fmt, const Params &p, int64_t max_tiles, hipStream_t s) {
       return launch<MX_FMT_NF4_F32, EPI, LORA, Short>(p, max_tiles, s);
     case MX_FMT_NF4_F32_KN:
       return launch<MX_FMT_NF4_F32_KN, EPI, LORA, Short>(p, max_tiles, s);
+    case MX_FMT_NF4_DQ:
+      return launch<MX_FMT_NF4_DQ, EPI, LORA, Short>(p, max_tiles, s);
+    case MX_FMT_NF4_DQ_KN:
+      return launch<MX_FMT_NF4_DQ_KN, EPI, LORA, Short>(p, max_tiles, s);
     case MX_FMT_INT8:
       return launch<MX_FMT_INT8, EPI, LORA, Short>(p, max_tiles, s);
     case MX_FMT_F32X3:
@@ -1434,6 +1557,16 @@ int launch_tile_dual(int fmt, const Params &p, int64_t max_tall, int64_t max_sho
       return launch_dual<MX_FMT_NF4_F32, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
     case MX_FMT_NF4_F32_KN:
       return launch_dual<MX_FMT_NF4_F32_KN, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
+    // The backward's dual launch with LoRA fills the 160 KB of LDS without the
+    // DQ code tables: DQ backward GEMMs take the 128-row launch (launch_fmt).
+    case MX_FMT_NF4_DQ:
+      if constexpr (EPI != EPI_STORE2)
+        return launch_dual<MX_FMT_NF4_DQ, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
+      break;
+    case MX_FMT_NF4_DQ_KN:
+      if constexpr (EPI != EPI_STORE2)
+        return launch_dual<MX_FMT_NF4_DQ_KN, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
+      break;
     case MX_FMT_INT8:
       return launch_dual<MX_FMT_INT8, EPI, LORA, Tall, Short>(p, max_tall, max_short, s);
     case MX_FMT_F32X3:
@@ -1454,6 +1587,7 @@ int launch_fmt(int fmt, Params p, const PlanLayout &PL, const PlanView &v, bool 
                                          Tile<256, 256, 2, 4, 64>>::type;
   using Short = Tile<128, 256, 2, 4, 64>;
   p.n_tiles_n = static_cast<int>(EPI == EPI_SWIGLU ? ceil_div(p.N, 128) : ceil_div(p.N, 256));
+  if (EPI == EPI_STORE2 && (fmt == MX_FMT_NF4_DQ || fmt == MX_FMT_NF4_DQ_KN)) tall = false;
   if (!tall) {
     p.tiles = v.tiles;
     p.num_tiles = v.num_tiles;
@@ -1531,7 +1665,25 @@ bool has_lora(const mx_lora *l) { return l && l->rank > 0; }
 // Rows per expert of a stored weight: its out rows, or its in rows when it is
 // stored [E, in, out] (MX_FMT_NF4_F32_KN).
 int64_t wn_of(const mx_weight *w) {
-  return w->format == MX_FMT_NF4_F32_KN ? w->in_features : w->out_features;
+  return w->format == MX_FMT_NF4_F32_KN || w->format == MX_FMT_NF4_DQ_KN ? w->in_features
+                                                                           : w->out_features;
+}
+
+// Weight group i (0 or 1) of a launch: its data, rows per expert and absmax
+// (NF4_DQ: the uint8 codes, with the nested scales, offsets and code table).
+void set_weight(Params &p, int i, const mx_weight *w) {
+  p.w[i] = w->data;
+  p.wn[i] = wn_of(w);
+  if (w->format == MX_FMT_NF4_DQ || w->format == MX_FMT_NF4_DQ_KN) {
+    const mx_nf4_dq *dq = static_cast<const mx_nf4_dq *>(w->scale);
+    p.wscale[i] = dq->absmax_q;
+    p.dq_nested[i] = dq->nested_absmax;
+    p.dq_offset[i] = dq->offsets;
+    p.dq_code[i] = dq->code;
+    p.dq_npe[i] = dq->nested_per_expert;
+  } else {
+    p.wscale[i] = w->scale;
+  }
 }
 
 __global__ __launch_bounds__(256) void zero_f32_kernel(float *p, int64_t n) {
@@ -1581,17 +1733,31 @@ int check_weight(const char *name, const char *key, const mx_weight *w, int64_t 
               static_cast<long long>(out_f), static_cast<long long>(in_f));
     return MX_ERR_INVALID;
   }
-  if (w->format != MX_FMT_BF16 && w->format != MX_FMT_NF4 && w->format != MX_FMT_INT8 &&
-      w->format != MX_FMT_F32X3 && w->format != MX_FMT_NF4_F32 &&
-      w->format != MX_FMT_NF4_F32_KN) {
+  if (w->format < MX_FMT_BF16 || w->format > MX_FMT_NF4_DQ_KN) {
     set_error("%s: weight %s has unknown format %d", name, key, w->format);
     return MX_ERR_INVALID;
   }
-  if ((w->format == MX_FMT_NF4 || w->format == MX_FMT_NF4_F32 ||
-       w->format == MX_FMT_NF4_F32_KN || w->format == MX_FMT_INT8) &&
-      !w->scale) {
+  if (w->format != MX_FMT_BF16 && w->format != MX_FMT_F32X3 && !w->scale) {
     set_error("%s: weight %s needs its scale / absmax buffer", name, key);
     return MX_ERR_INVALID;
+  }
+  if (w->format == MX_FMT_NF4_DQ || w->format == MX_FMT_NF4_DQ_KN) {
+    const mx_nf4_dq *dq = static_cast<const mx_nf4_dq *>(w->scale);
+    // The stored rows: [out, in] or, for _KN, [in, out]; blocks of 64 along them.
+    const int64_t row_len = w->format == MX_FMT_NF4_DQ ? in_f : out_f;
+    const int64_t blocks = out_f * in_f / kNf4Block;
+    if (!dq->absmax_q || !dq->nested_absmax || !dq->offsets || !dq->code ||
+        dq->nested_per_expert < ceil_div(blocks, 256)) {
+      set_error("%s: weight %s: the two-level absmax needs its codes, nested scales (%lld per "
+                "expert), offsets and code table", name, key,
+                static_cast<long long>(ceil_div(blocks, 256)));
+      return MX_ERR_INVALID;
+    }
+    if (row_len % kNf4Block != 0 || row_len > 16384) {
+      set_error("%s: weight %s: two-level absmax rows hold a multiple of 64 and at most 16384 "
+                "elements, got %lld", name, key, static_cast<long long>(row_len));
+      return MX_ERR_INVALID;
+    }
   }
   return MX_OK;
 }
@@ -1710,12 +1876,8 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
     p.ldx = ldx;
     p.row_token = row_token;
     p.K = kx * hidden;
-    p.w[0] = w1->data;
-    p.w[1] = w3->data;
-    p.wscale[0] = w1->scale;
-    p.wscale[1] = w3->scale;
-    p.wn[0] = wn_of(w1);
-    p.wn[1] = wn_of(w3);
+    set_weight(p, 0, w1);
+    set_weight(p, 1, w3);
     p.N = ffn;
     p.lora_p = lora_buf;
     p.ldp = 3 * lrc;
@@ -1746,9 +1908,7 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
   p.ldx = kx * ffn;
   p.row_token = nullptr;
   p.K = kx * ffn;
-  p.w[0] = w2->data;
-  p.wscale[0] = w2->scale;
-  p.wn[0] = wn_of(w2);
+  set_weight(p, 0, w2);
   p.N = hidden;
   p.lora_p = lora_buf + 2 * lrc;
   p.ldp = 3 * lrc;
@@ -1951,9 +2111,7 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
     p.ldx = hidden;
     p.row_token = v.row_slot;
     p.K = hidden;
-    p.w[0] = w2->data;
-    p.wscale[0] = w2->scale;
-    p.wn[0] = wn_of(w2);
+    set_weight(p, 0, w2);
     p.k_split = hidden;
     p.N = ffn;
     p.lora_p = dz + 2 * lrc;
@@ -1997,12 +2155,8 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
     p.ldx = 2 * ffn;
     p.row_token = nullptr;
     p.K = 2 * ffn;
-    p.w[0] = w1->data;
-    p.w[1] = w3->data;
-    p.wscale[0] = w1->scale;
-    p.wscale[1] = w3->scale;
-    p.wn[0] = wn_of(w1);
-    p.wn[1] = wn_of(w3);
+    set_weight(p, 0, w1);
+    set_weight(p, 1, w3);
     p.k_split = ffn;
     p.N = hidden;
     p.lora_p = dz;
@@ -2466,9 +2620,7 @@ extern "C" int mx_grouped_linear(const void *x, const int64_t *counts, int64_t n
   p.x = static_cast<const uint16_t *>(x);
   p.ldx = in_f;
   p.K = in_f;
-  p.w[0] = w->data;
-  p.wscale[0] = w->scale;
-  p.wn[0] = wn_of(w);
+  set_weight(p, 0, w);
   p.N = out_f;
   p.lora_p = lora_buf;
   p.ldp = 3 * lrc;
@@ -2594,9 +2746,7 @@ extern "C" int mx_grouped_linear_backward(const void *grad_out, const void *x,
     p.x = dy;
     p.ldx = out_f;
     p.K = out_f;
-    p.w[0] = w->data;
-    p.wscale[0] = w->scale;
-    p.wn[0] = wn_of(w);
+    set_weight(p, 0, w);
     p.k_split = out_f;
     p.N = in_f;
     p.lora_p = dz;

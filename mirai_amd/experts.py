@@ -37,6 +37,11 @@ NF4_BLOCKSIZE = quant.NF4_BLOCKSIZE
 # which a 288 GB MI355X falls into.
 DEFAULT_DEQUANT_CHUNK = 16
 
+# A two-level (bitsandbytes double-quant) absmax kept as stored: buffer suffix
+# -> PackedWeight.dq field (the uint8 codes are the _nf4_absmax buffer).
+_TWO_LEVEL_BUFFERS = (("_nf4_nabsmax", "nested_absmax"), ("_nf4_offset", "offsets"),
+                      ("_nf4_ncode", "code"))
+
 _BUFFER_SUFFIXES = {
     "nf4": ("_nf4", "_nf4_absmax"),
     "int8": ("_int8", "_scale"),
@@ -105,6 +110,8 @@ class CompressedGroupedExperts(nn.Module):
         self._nf4_blocksize = int(nf4_blocksize)
         self._shapes: dict[str, tuple[int, int, int]] = {}
         self._layouts: dict[str, str] = {}  # key -> "out_in" or "in_out" (PackedWeight.layout)
+        # Keys whose NF4 absmax is a bitsandbytes two-level absmax kept as stored.
+        self._two_level: set[str] = set()
         self._loaded_dense_keys: set[str] = set()
         self.expert_lora = nn.ModuleDict()
         self.logical_num_experts = int(num_experts)
@@ -188,12 +195,15 @@ class CompressedGroupedExperts(nn.Module):
     def load_packed_nf4(self, key: str, *, packed: torch.Tensor, absmax: torch.Tensor,
                         nested_absmax: torch.Tensor, offset: torch.Tensor, code: torch.Tensor,
                         nested_code: torch.Tensor, shape: tuple[int, int, int],
-                        layout: str = "out_in") -> None:
+                        layout: str = "out_in", two_level: bool = False) -> None:
         """Adopt a bitsandbytes double-quantised NF4 stack as the reference stores it
         (the {key}_nf4* buffers of _store_nf4_grouped, experts.py:998-1031) without
-        re-quantising: the GEMMs decode the payload's weights (fp32 absmax).
-        ``shape`` is the logical [E, out, in]; ``layout="in_out"`` takes payloads
-        that quantise each expert's [in, out] matrix (MAGI-2 groups)."""
+        re-quantising: the GEMMs decode the payload's weights. ``shape`` is the
+        logical [E, out, in]; ``layout="in_out"`` takes payloads that quantise
+        each expert's [in, out] matrix (MAGI-2 groups). The absmax is decoded to
+        fp32 once, or with ``two_level=True`` kept as the payload stores it
+        ({key}_nf4_absmax uint8, _nf4_nabsmax, _nf4_offset, _nf4_ncode) and
+        decoded by the GEMMs per K step."""
         if self._quant_format != "nf4":
             raise ValueError("packed NF4 payloads load into a module with quant_format='nf4'.")
         if key not in self._spec.tensor_names:
@@ -204,18 +214,31 @@ class CompressedGroupedExperts(nn.Module):
                 f"expected {self.num_experts}.")
         packed_w = quant.from_bnb_nf4(packed=packed, absmax=absmax, nested_absmax=nested_absmax,
                                       offset=offset, code=code, nested_code=nested_code,
-                                      shape=tuple(int(v) for v in shape), layout=layout)
+                                      shape=tuple(int(v) for v in shape), layout=layout,
+                                      two_level=two_level)
         data_suffix, scale_suffix = _BUFFER_SUFFIXES["nf4"]
         self._set_buffer(f"{key}{data_suffix}", packed_w.data)
         self._set_buffer(f"{key}{scale_suffix}", packed_w.scale)
+        for suffix, field in _TWO_LEVEL_BUFFERS:
+            name = f"{key}{suffix}"
+            if packed_w.dq is not None:
+                self._set_buffer(name, packed_w.dq[field])
+            elif name in self._buffers:
+                del self._buffers[name]
+        if packed_w.dq is not None:
+            self._two_level.add(key)
+        else:
+            self._two_level.discard(key)
         self._shapes[key] = packed_w.shape
         self._layouts[key] = packed_w.layout
         self._loaded_dense_keys.add(key)
 
-    def load_bnb_state_dict(self, state: dict, shapes: dict, *, prefix: str = "") -> None:
+    def load_bnb_state_dict(self, state: dict, shapes: dict, *, prefix: str = "",
+                            two_level: bool = False) -> None:
         """Load every expert tensor of ``shapes`` ({key: (E, out, in)}) from a
         reference state dict holding its {key}_nf4, _nf4_absmax, _nf4_nabsmax,
-        _nf4_offset, _nf4_code and _nf4_ncode buffers."""
+        _nf4_offset, _nf4_code and _nf4_ncode buffers (``two_level``: see
+        load_packed_nf4)."""
         for key, shape in shapes.items():
             base = f"{prefix}{key}_nf4"
             missing = [n for n in ("", "_absmax", "_nabsmax", "_offset", "_code", "_ncode")
@@ -226,12 +249,16 @@ class CompressedGroupedExperts(nn.Module):
             self.load_packed_nf4(key, packed=state[base], absmax=state[base + "_absmax"],
                                  nested_absmax=state[base + "_nabsmax"],
                                  offset=state[base + "_offset"], code=state[base + "_code"],
-                                 nested_code=state[base + "_ncode"], shape=shape)
+                                 nested_code=state[base + "_ncode"], shape=shape,
+                                 two_level=two_level)
 
     def packed_buffer_names(self, key: str) -> tuple[str, ...]:
         """Names of the buffers that hold expert tensor ``key`` in this format."""
         data_suffix, scale_suffix = _BUFFER_SUFFIXES[self._quant_format]
-        return (f"{key}{data_suffix}",) + ((f"{key}{scale_suffix}",) if scale_suffix else ())
+        names = (f"{key}{data_suffix}",) + ((f"{key}{scale_suffix}",) if scale_suffix else ())
+        if key in self._two_level:
+            names += tuple(f"{key}{suffix}" for suffix, _ in _TWO_LEVEL_BUFFERS)
+        return names
 
     def packed_weight(self, key: str) -> quant.PackedWeight:
         if key not in self._loaded_dense_keys:
@@ -239,8 +266,11 @@ class CompressedGroupedExperts(nn.Module):
         data_suffix, scale_suffix = _BUFFER_SUFFIXES[self._quant_format]
         data = getattr(self, f"{key}{data_suffix}")
         scale = getattr(self, f"{key}{scale_suffix}") if scale_suffix else None
+        dq = None
+        if key in self._two_level:
+            dq = {field: getattr(self, f"{key}{suffix}") for suffix, field in _TWO_LEVEL_BUFFERS}
         return quant.PackedWeight(self._quant_format, data, scale, self._shapes[key],
-                                  self._layouts.get(key, "out_in"))
+                                  self._layouts.get(key, "out_in"), dq)
 
     def packed_nbytes(self) -> int:
         return sum(self.packed_weight(k).nbytes() for k in self._loaded_dense_keys)

@@ -213,7 +213,8 @@ class Magi2GroupedExperts(nn.Module):
         return int(sum(g * a * b for g, a, b in self._source_shapes.values()))
 
     def load_reference_nf4_store(self, buffers: dict, expert_shapes: dict,
-                                 expert_dtypes: dict | None = None) -> None:
+                                 expert_dtypes: dict | None = None, *,
+                                 two_level: bool = False) -> None:
         """Adopt the payload of the reference's Magi2Nf4ExpertStore for this layer
         without re-quantising (quantized_experts.py:275-347): per key the
         double-quantised NF4 buffers ``{key}_nf4`` (codes of each group's
@@ -222,7 +223,9 @@ class Magi2GroupedExperts(nn.Module):
         ``_nf4_code`` (the NF4 levels) and ``_nf4_ncode`` (256 fp32), with
         ``expert_shapes[key] = (G, in, out)``. The group payloads keep their
         [in, out] orientation (64-blocks along out): the kernels read them as
-        stored (MX_FMT_NF4_F32_KN), the absmax decoded once to fp32."""
+        stored (MX_FMT_NF4_F32_KN), the absmax decoded once to fp32, or with
+        ``two_level=True`` kept as stored and decoded by the GEMMs
+        (MX_FMT_NF4_DQ_KN)."""
         if self.experts.quant_format != "nf4":
             raise Magi2QuantizedExpertError(
                 "a reference NF4 store loads into a module with quant_format='nf4'.")
@@ -244,7 +247,7 @@ class Magi2GroupedExperts(nn.Module):
                 self.experts.load_packed_nf4(
                     key, packed=t["nf4"], absmax=t["nf4_absmax"], nested_absmax=t["nf4_nabsmax"],
                     offset=t["nf4_offset"], code=t["nf4_code"], nested_code=t["nf4_ncode"],
-                    shape=(g, cols, rows), layout="in_out")
+                    shape=(g, cols, rows), layout="in_out", two_level=two_level)
             except ValueError as err:
                 raise Magi2QuantizedExpertError(f"{key}: {err}") from err
             self._source_shapes[key] = shape
@@ -391,7 +394,7 @@ def read_reference_magi2_artifact(path) -> dict[str, dict]:
     return out
 
 
-def load_reference_magi2_artifact(path, layers: dict) -> dict:
+def load_reference_magi2_artifact(path, layers: dict, *, two_level: bool = False) -> dict:
     """Ingest a reference MAGI-2 NF4 artifact into ``layers`` ({layer name:
     Magi2GroupedExperts with quant_format "nf4"}, names as in the manifest)
     without re-quantising; returns ``layers``."""
@@ -400,7 +403,8 @@ def load_reference_magi2_artifact(path, layers: dict) -> dict:
         raise Magi2QuantizedExpertError(
             f"artifact layers {sorted(entries)} do not match the model's {sorted(layers)}.")
     for name, entry in entries.items():
-        layers[name].load_reference_nf4_store(entry["buffers"], entry["shapes"], entry["dtypes"])
+        layers[name].load_reference_nf4_store(entry["buffers"], entry["shapes"], entry["dtypes"],
+                                              two_level=two_level)
     return layers
 
 

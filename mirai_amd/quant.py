@@ -20,7 +20,8 @@ formats; the per-element rules are documented in include/mirai_moe.h.
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+import ctypes
+from dataclasses import dataclass, field
 
 import torch
 
@@ -55,26 +56,49 @@ class PackedWeight:
     # [E, in, ...] with the NF4 blocks along out (an ingested MAGI-2 group
     # payload, x @ W[g]).
     layout: str = "out_in"
+    # A bitsandbytes two-level absmax kept as stored (MX_FMT_NF4_DQ): ``scale``
+    # holds the uint8 absmax codes [E, rows, cols / 64], this dict the nested
+    # scales ``nested_absmax`` [E, n] fp32, the ``offsets`` [E] fp32 and the
+    # 256-entry ``code`` table (fp32).
+    dq: dict | None = None
+    _dq_struct: object = field(default=None, repr=False, compare=False)
 
     def format_code(self) -> int:
+        if self.fmt == "nf4" and self.dq is not None:
+            return nat.FMT_NF4_DQ_KN if self.layout == "in_out" else nat.FMT_NF4_DQ
         if self.fmt == "nf4" and self.scale is not None and self.scale.dtype == torch.float32:
             return nat.FMT_NF4_F32_KN if self.layout == "in_out" else nat.FMT_NF4_F32
         if self.layout != "out_in":
             raise ValueError(f"the {self.fmt} format has no [E, in, out] kernel layout")
         return _FORMAT_CODES[self.fmt]
 
+    def dq_struct(self, experts: slice | None = None) -> nat.MxNf4Dq:
+        """The mx_nf4_dq of a two-level absmax (of an expert slice). The whole
+        weight's struct is kept with the weight, which must outlive the calls
+        that use its descriptor."""
+        if experts is None and self._dq_struct is not None:
+            return self._dq_struct
+        sel = experts if experts is not None else slice(None)
+        q = self.scale[sel]
+        nested = self.dq["nested_absmax"][sel]
+        offsets = self.dq["offsets"][sel]
+        st = nat.MxNf4Dq(q.data_ptr(), nested.data_ptr(), offsets.data_ptr(),
+                         self.dq["code"].data_ptr(), int(nested.shape[-1]))
+        if experts is None:
+            self._dq_struct = st
+        return st
+
     def descriptor(self) -> nat.MxWeight:
         _, out_f, in_f = self.shape
-        return nat.MxWeight(
-            self.format_code(),
-            self.data.data_ptr(),
-            self.scale.data_ptr() if self.scale is not None else None,
-            out_f,
-            in_f,
-        )
+        if self.dq is not None:
+            scale = ctypes.addressof(self.dq_struct())
+        else:
+            scale = self.scale.data_ptr() if self.scale is not None else None
+        return nat.MxWeight(self.format_code(), self.data.data_ptr(), scale, out_f, in_f)
 
     def nbytes(self) -> int:
-        return self.data.numel() * self.data.element_size() + (
+        extra = sum(t.numel() * t.element_size() for t in (self.dq or {}).values())
+        return self.data.numel() * self.data.element_size() + extra + (
             0 if self.scale is None else self.scale.numel() * self.scale.element_size()
         )
 
@@ -128,18 +152,26 @@ def dequantize(packed: PackedWeight, *, dtype: torch.dtype = torch.bfloat16,
     if packed.fmt == "fp32":  # hi + lo planes
         return (data[..., :in_f].float() + data[..., in_f:2 * in_f].float()).to(dtype)
     nat.require_gpu(data)
+    scale_all = packed.scale
+    if packed.dq is not None:
+        # The two-level absmax as the GEMMs decode it, then the fp32-absmax path.
+        scale_all = torch.empty((E, *packed.scale.shape[1:]), dtype=torch.float32, device=device)
+        st = packed.dq_struct(sel)
+        nat.call("mx_nf4_dq_absmax", ctypes.byref(st), E, int(packed.scale[0].numel()),
+                 scale_all.data_ptr(), nat.stream(device))
+        sel = slice(None)
     if packed.layout == "in_out":
         # Rows of the stored [E, in, out] payload, then the [E, out, in] view.
         flat = torch.empty((E, in_f, out_f), dtype=dtype, device=device)
         nat.call("mx_nf4_dequantize_ex", data.contiguous().data_ptr(),
-                 packed.scale[sel].contiguous().data_ptr(),
-                 nat.dtype_code(packed.scale.dtype), E * in_f, out_f, flat.data_ptr(),
+                 scale_all[sel].contiguous().data_ptr(),
+                 nat.dtype_code(scale_all.dtype), E * in_f, out_f, flat.data_ptr(),
                  nat.dtype_code(dtype), nat.stream(device))
         return flat.transpose(1, 2).contiguous()
     out = torch.empty((E, out_f, in_f), dtype=dtype, device=device)
     rows = E * out_f
     s = nat.stream(device)
-    scale = packed.scale[sel].contiguous()
+    scale = scale_all[sel].contiguous()
     data = data.contiguous()
     if packed.fmt == "nf4":
         nat.call("mx_nf4_dequantize_ex", data.data_ptr(), scale.data_ptr(),
@@ -153,7 +185,8 @@ def dequantize(packed: PackedWeight, *, dtype: torch.dtype = torch.bfloat16,
 def from_bnb_nf4(*, packed: torch.Tensor, absmax: torch.Tensor, nested_absmax: torch.Tensor,
                  offset: torch.Tensor, code: torch.Tensor, nested_code: torch.Tensor,
                  shape: tuple[int, int, int], blocksize: int = NF4_BLOCKSIZE,
-                 nested_blocksize: int = 256, layout: str = "out_in") -> PackedWeight:
+                 nested_blocksize: int = 256, layout: str = "out_in",
+                 two_level: bool = False) -> PackedWeight:
     """Ingest a bitsandbytes double-quantised NF4 expert stack without
     re-quantising (mx_nf4_from_bnb).
 
@@ -166,7 +199,10 @@ def from_bnb_nf4(*, packed: torch.Tensor, absmax: torch.Tensor, nested_absmax: t
     with the decoded fp32 absmax. ``shape`` is the logical [E, out, in]; with
     ``layout="in_out"`` each expert's payload quantises the [in, out] matrix
     (the MAGI-2 store's [G, in, out] groups, quantized_experts.py:275-347, whose
-    64-blocks run along out) and is kept in that orientation.
+    64-blocks run along out) and is kept in that orientation. With
+    ``two_level=True`` the absmax stays as the payload stores it (uint8 codes,
+    nested scales, offsets, code table) and the GEMMs decode it per K step
+    (MX_FMT_NF4_DQ); otherwise it is decoded once to fp32 here.
     """
     E, out_f, in_f = (int(v) for v in shape)
     if layout not in ("out_in", "in_out"):
@@ -194,6 +230,16 @@ def from_bnb_nf4(*, packed: torch.Tensor, absmax: torch.Tensor, nested_absmax: t
                              f"{int(t.numel())} {t.dtype}.")
         flat[name] = t.detach().to(device).reshape(-1).contiguous()
     codes = torch.empty((E, rows_f, cols_f // 2), dtype=torch.uint8, device=device)
+    if two_level:
+        if cols_f > 16384:
+            raise ValueError("two-level absmax rows hold at most 16384 elements; ingest with "
+                             "two_level=False (fp32 absmax).")
+        nat.call("mx_nf4_from_bnb", flat["packed"].data_ptr(), None, None, None, None, E, rows_f,
+                 cols_f, codes.data_ptr(), None, nat.stream(device))
+        dq = {"nested_absmax": flat["nested_absmax"].reshape(E, n2),
+              "offsets": flat["offset"], "code": flat["nested_code"]}
+        q = flat["absmax"].reshape(E, rows_f, cols_f // NF4_BLOCKSIZE)
+        return PackedWeight("nf4", codes, q, (E, out_f, in_f), layout, dq)
     amax = torch.empty((E, rows_f, cols_f // NF4_BLOCKSIZE), dtype=torch.float32, device=device)
     nat.call("mx_nf4_from_bnb", flat["packed"].data_ptr(), flat["absmax"].data_ptr(),
              flat["nested_absmax"].data_ptr(), flat["offset"].data_ptr(),

@@ -43,7 +43,7 @@ def test_binding_covers_every_declared_symbol():
 
 
 def test_abi_version_and_error_text(lib):
-    assert lib.mx_abi_version() == 8
+    assert lib.mx_abi_version() == 9
     assert isinstance(nat.last_error(), str)
 
 

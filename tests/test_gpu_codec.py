@@ -152,3 +152,100 @@ def test_layer_runs_on_ingested_bnb_nf4_weights():
         out = m.run_direct_routed(x.cuda(), scores, idx)
     ref = olayer.layer_forward(x, scores.cpu(), idx.cpu(), dense, {}, E)
     print(f"ingested bnb nf4 layer: {assert_layer_close(out.cpu(), ref)}")
+
+
+def _bnb_state(E, d, f, seed):
+    table = None
+    shapes = {"w1": (E, f, d), "w3": (E, f, d), "w2": (E, d, f)}
+    state, dense = {}, {}
+    for i, (key, (e_, o, n)) in enumerate(shapes.items()):
+        stacked, parts, table = _bnb_payload(e_, o, n, seed + i)
+        for name, suffix in (("packed", ""), ("absmax", "_absmax"), ("nested_absmax", "_nabsmax"),
+                             ("offset", "_offset"), ("code", "_code"),
+                             ("nested_code", "_ncode")):
+            state[f"{key}_nf4{suffix}"] = torch.from_numpy(np.asarray(stacked[name])).cuda()
+        bits = np.stack([codec.bnb_nf4_dequantize(p["packed"], p["absmax"], p["nested_absmax"],
+                                                  p["offset"], table, o, n) for p in parts])
+        dense[key] = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+    return state, dense, shapes
+
+
+def test_two_level_absmax_decodes_like_the_load_time_absmax():
+    # mx_nf4_dq_absmax (the GEMMs' per-step arithmetic) against mx_nf4_from_bnb's
+    # fp32 absmax, and the dequantised weights of both ingestions against the
+    # bitsandbytes restatement, bit for bit (nested blocks of 256 cross rows
+    # here: 6 blocks per row).
+    from mirai_amd import CompressedGroupedExperts, quant
+
+    E, d, f = 3, 384, 320
+    state, dense, shapes = _bnb_state(E, d, f, 70)
+    mods = {}
+    for two in (False, True):
+        m = CompressedGroupedExperts.from_empty(num_experts=E, quant_format="nf4",
+                                                expert_weight_access="fused_kernel")
+        m.load_bnb_state_dict(state, shapes, two_level=two)
+        mods[two] = m
+    for key in shapes:
+        pf, pq = mods[False].packed_weight(key), mods[True].packed_weight(key)
+        assert pf.format_code() == nat.FMT_NF4_F32 and pq.format_code() == nat.FMT_NF4_DQ
+        assert pq.nbytes() < pf.nbytes()
+        assert torch.equal(pf.data, pq.data)
+        amax = torch.empty_like(pf.scale)
+        st = pq.dq_struct()
+        import ctypes
+        nat.call("mx_nf4_dq_absmax", ctypes.byref(st), E, int(pq.scale[0].numel()),
+                 amax.data_ptr(), nat.stream(amax.device))
+        assert torch.equal(amax, pf.scale)
+        for sel in (None, slice(1, 2)):
+            a = quant.dequantize(pq, experts=sel)
+            b = quant.dequantize(pf, experts=sel)
+            assert torch.equal(a, b)
+        assert torch.equal(quant.dequantize(pq).cpu(), dense[key])
+
+
+def test_two_level_absmax_layer_equals_the_fp32_absmax_layer():
+    # The same payload ingested with its absmax decoded at load (NF4_F32) and
+    # kept two-level (NF4_DQ, decoded in the GEMMs): the same absmax arithmetic,
+    # so forward (256-row, remainder and light tiles) and backward (LoRA) agree
+    # bit for bit; and both match the oracle on the bitsandbytes weights.
+    from mirai_amd import CompressedGroupedExperts
+    from oracle import layer as olayer
+    from helpers import assert_layer_close
+    from test_gpu_light_tiles import LIGHT_COUNTS, skewed_routes
+
+    E, d, f, T, k, r = 9, 256, 384, 1400, 2, 16
+    state, dense, shapes = _bnb_state(E, d, f, 80)
+    g = torch.Generator().manual_seed(81)
+    lora = {key: (torch.randn(E, r, n, generator=g) * 0.02, torch.randn(E, o, r, generator=g) * 0.02)
+            for key, (_, o, n) in shapes.items()}
+    mods = {}
+    for two in (False, True):
+        m = CompressedGroupedExperts.from_empty(num_experts=E, quant_format="nf4",
+                                                expert_weight_access="fused_kernel")
+        m.load_bnb_state_dict(state, shapes, two_level=two)
+        for key, (a, b) in lora.items():
+            ad = m.attach_expert_lora(tensor_name=key, adapter_name="t", rank=r, alpha=16.0)
+            with torch.no_grad():
+                ad.lora_a.copy_(a.cuda())
+                ad.lora_b.copy_(b.cuda())
+        mods[two] = m
+    idx, scores = skewed_routes(T, E, k, LIGHT_COUNTS, seed=82)
+    x = torch.randn(T, d, generator=g).to(torch.bfloat16).cuda()
+    dy = torch.randn(T, d, generator=g).to(torch.bfloat16).cuda()
+    outs, grads = {}, {}
+    for two, m in mods.items():
+        with torch.no_grad():
+            outs[two] = m.run_direct_routed(x, scores.cuda(), idx.cuda())
+        xg = x.clone().requires_grad_(True)
+        sg = scores.cuda().requires_grad_(True)
+        y = m.run_direct_routed(xg, sg, idx.cuda())
+        y.backward(dy)
+        grads[two] = [xg.grad, sg.grad] + [p.grad for ad in m.expert_lora.values()
+                                           for p in (ad.lora_a, ad.lora_b)]
+        assert torch.equal(y.detach(), outs[two])
+    assert torch.equal(outs[True], outs[False])
+    for a, b in zip(grads[True], grads[False]):
+        assert torch.equal(a, b)
+    ref = olayer.layer_forward(x.cpu(), scores, idx, dense,
+                               {k_: (a, b, 16.0 / r) for k_, (a, b) in lora.items()}, E)
+    print(f"two-level absmax layer: {assert_layer_close(outs[True].cpu(), ref)}")

@@ -286,3 +286,54 @@ def test_reference_artifact_ingests_without_requantisation(tmp_path, S):
         rel = float((got.float().cpu() - want.float()).abs().sum() / want.float().abs().sum())
         print(f"magi2 reference artifact backward {name}: mean_rel={rel:.3e}")
         assert rel <= 1e-2, (name, rel)
+
+
+@pytest.mark.parametrize("S", [300])
+def test_reference_artifact_two_level_absmax_equals_the_fp32_absmax(tmp_path, S):
+    """The same reference artifact ingested with its two-level absmax kept as
+    stored (MX_FMT_NF4_DQ_KN, decoded by the GEMMs per K step) and decoded at
+    load (MX_FMT_NF4_F32_KN): the same absmax arithmetic, so the dequantised
+    weights, the forward and the backward (LoRA on every weight) agree bit for
+    bit."""
+    from mirai_amd import load_reference_magi2_artifact
+    from mirai_amd import _native as nat
+    from mirai_amd import quant
+
+    H, E, d, f = 2, 4, 128, 192
+    path, dense = _reference_artifact(tmp_path, H=H, E=E, d=d, f=f)
+    layers = {}
+    for two in (False, True):
+        layer = Magi2GroupedExperts(num_heads=H, num_experts=E, quant_format="nf4")
+        load_reference_magi2_artifact(path, {"blocks.3.moe": layer}, two_level=two)
+        layers[two] = layer
+    for key in ("W_gate", "W_up", "W_down"):
+        pq = layers[True].experts.packed_weight(key)
+        pf = layers[False].experts.packed_weight(key)
+        assert pq.format_code() == nat.FMT_NF4_DQ_KN and pf.format_code() == nat.FMT_NF4_F32_KN
+        assert torch.equal(quant.dequantize(pq), quant.dequantize(pf))
+    _, x, _, _, probs, idx = _magi2_case(H=H, E=E, d=d, f=f, S=S, k=2, seed=14)
+    g = torch.Generator().manual_seed(22)
+    r = 16
+    facs = {key: ((torch.randn(H * E, r, i_f, generator=g) * 0.05).to(torch.bfloat16),
+                  (torch.randn(H * E, o_f, r, generator=g) * 0.05).to(torch.bfloat16))
+            for key, (i_f, o_f) in {"W_gate": (d, f), "W_up": (d, f), "W_down": (f, d)}.items()}
+    dy = torch.randn(x.shape, generator=g).to(torch.bfloat16)
+    res = {}
+    for two, layer in layers.items():
+        with torch.no_grad():
+            out = layer.execute(x.cuda(), probs.cuda(), idx.cuda())
+        for key, (a, b) in facs.items():
+            ad = layer.attach_expert_lora(tensor_name=key, adapter_name="t", rank=r, alpha=32.0)
+            with torch.no_grad():
+                ad.lora_a.copy_(a.cuda())
+                ad.lora_b.copy_(b.cuda())
+        xg = x.cuda().requires_grad_(True)
+        pg = probs.cuda().requires_grad_(True)
+        layer.execute(xg, pg, idx.cuda()).backward(dy.cuda())
+        res[two] = [out, xg.grad, pg.grad] + [
+            p.grad for k in facs for p in (layer.experts.expert_lora[k].lora_a,
+                                           layer.experts.expert_lora[k].lora_b)]
+    for a, b in zip(res[True], res[False]):
+        assert torch.equal(a, b)
+    ref = om.layer_forward(x, probs, idx, dense, E)
+    print(f"magi2 two-level artifact forward: {assert_layer_close(res[True][0].cpu(), ref)}")
