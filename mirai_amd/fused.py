@@ -148,12 +148,113 @@ class _RoutedExperts(torch.autograd.Function):
         return routed_experts_backward(ctx, grad_out)
 
 
+def fp32_layer_composition(module, tokens, scores, idx, loras):
+    """The routed layer over fp32 weights as torch fp32 ops on the GPU, for
+    its backward: per expert g = x W1^T + s1 (x A1^T) B1^T, u likewise with W3,
+    h = act(g, u), y = h W2^T + s2 (h A2^T) B2^T, and out[t] the score-weighted
+    sum over the token's experts (experts.py:1749-1912 on fp32 tensors, no
+    intermediate rounding). The weights are the stored planes' hi + lo, the
+    values the split-precision kernels multiply. ``loras``: (A, B, scale) or
+    None per role (gate, up, down). Route slots outside [0, E) contribute
+    nothing."""
+    from . import quant
+
+    E = module.num_experts
+    w1, w3, w2 = (quant.dequantize(module.packed_weight(k), dtype=torch.float32)
+                  for k in module._role_keys())
+    act = int(getattr(module, "_kernel_activation", nat.ACT_SILU))
+    T, k = (int(v) for v in idx.shape)
+    flat = idx.reshape(-1)
+    token_of = torch.arange(T * k, device=idx.device) // k
+    sflat = scores.reshape(-1).float()
+    x = tokens.float()
+    out = torch.zeros((T, int(x.shape[1])), dtype=torch.float32, device=x.device)
+
+    def proj(inp, w, lora, e):
+        y = inp @ w[e].t()
+        if lora is not None:
+            a, b, sc = lora
+            y = y + sc * ((inp @ a[e].t()) @ b[e].t())
+        return y
+
+    for e in range(E):
+        sel = (flat == e).nonzero().squeeze(1)
+        if sel.numel() == 0:
+            continue
+        rows = token_of[sel]
+        xs = x[rows]
+        g = proj(xs, w1, loras[0], e)
+        u = proj(xs, w3, loras[1], e)
+        if act == nat.ACT_SWIGLU7:
+            # clamp(g, max=7) * sigmoid(1.702 clamp(g)) * (clamp(u, -7, 7) + 1)
+            gc = g.clamp(max=7.0)
+            h = gc * torch.sigmoid(1.702 * gc) * (u.clamp(-7.0, 7.0) + 1.0)
+        else:
+            h = torch.nn.functional.silu(g) * u
+        y = proj(h, w2, loras[2], e)
+        out = out.index_add(0, rows, y * sflat[sel].unsqueeze(1))
+    return out
+
+
+class _Fp32RoutedExperts(torch.autograd.Function):
+    """The layer over fp32 weights under autograd. The forward is the
+    split-precision kernel layer; the backward recomputes the layer as
+    fp32_layer_composition (torch fp32 on the GPU, the same stored weights) and
+    differentiates it: gradients to the tokens, the scores and the LoRA
+    factors, with the reference's fp32 arithmetic."""
+
+    @staticmethod
+    def forward(ctx, module, tokens, top_scores, top_indices, *lora_params):
+        out, _ = _forward(module, tokens, top_scores, top_indices, False)
+        ctx.module = module
+        ctx.save_for_backward(tokens, top_scores, top_indices)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        tokens, scores, idx = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        with torch.enable_grad():
+            t = tokens.detach().float().requires_grad_(needs[1])
+            s = scores.detach().float().requires_grad_(needs[2])
+            leaves, loras = [], []
+            for i, adapter in enumerate(ctx.module._adapters()):
+                if adapter is None:
+                    loras.append(None)
+                    leaves += [None, None]
+                    continue
+                a = adapter.lora_a.detach().float().requires_grad_(needs[4 + 2 * i])
+                b = adapter.lora_b.detach().float().requires_grad_(needs[5 + 2 * i])
+                loras.append((a, b, float(adapter.scale())))
+                leaves += [a, b]
+            out = fp32_layer_composition(ctx.module, t, s, idx, loras)
+            wrt = [v for v in (t, s, *leaves) if v is not None and v.requires_grad]
+            got = torch.autograd.grad(out, wrt, grad_out.float(), allow_unused=True) if wrt else ()
+        it = iter(got)
+
+        def take(v, like):
+            if v is None or not v.requires_grad:
+                return None
+            g = next(it)
+            if g is None:
+                g = torch.zeros_like(v)
+            return g.to(like.dtype)
+
+        grad_t = take(t, tokens)
+        grad_s = take(s, scores)
+        params = _lora_params(ctx.module)
+        grad_l = [take(v, p) if p is not None else None for v, p in zip(leaves, params)]
+        return (None, grad_t, grad_s, None, *grad_l)
+
+
 def routed_experts(module, tokens, top_scores, top_indices):
     """The routed layer; with autograd only when a gradient can flow (in
     inference nothing is saved for a backward)."""
     params = _lora_params(module)
     if torch.is_grad_enabled() and any(
             t is not None and t.requires_grad for t in (tokens, top_scores, *params)):
+        if module.quant_format == "fp32":
+            return _Fp32RoutedExperts.apply(module, tokens, top_scores, top_indices, *params)
         return _RoutedExperts.apply(module, tokens, top_scores, top_indices, *params)
     return _forward(module, tokens, top_scores, top_indices, False)[0]
 
@@ -222,9 +323,10 @@ def routed_experts_chunked(module, tokens, top_scores, top_indices, bounds):
     if torch.is_grad_enabled() and any(
             t is not None and t.requires_grad for t in (tokens, top_scores, *params)):
         if module.quant_format == "fp32":
-            raise NotImplementedError(
-                "the fp32 (quant_format='fp32') expert layer is inference-only; train adapters "
-                "over bf16, nf4 or int8 weights")
+            # Each chunk's backward recomputes only that chunk's fp32 layer.
+            return torch.cat([
+                _Fp32RoutedExperts.apply(module, tokens[a:b], top_scores[a:b], top_indices[a:b],
+                                         *params) for a, b in bounds], dim=0)
         return _ChunkedRoutedExperts.apply(module, tuple(bounds), tokens, top_scores, top_indices,
                                            *params)
     with torch.no_grad():
