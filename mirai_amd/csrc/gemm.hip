@@ -1505,9 +1505,7 @@ int launch_dual(Params p, int64_t max_tall, int64_t max_short, hipStream_t s) {
     return MX_ERR_INVALID;
   }
   p.slots_tall = static_cast<int>(slots_tall);
-  // Half of the 32 CUs of an XCD (gfx950: 256 CUs in 8 XCDs) start on a
-  // remainder tile, when there are that many.
-  p.stagger = static_cast<int>(std::min<int64_t>(16, slots_short));
+  p.stagger = static_cast<int>(std::min<int64_t>(p.stagger, slots_short));
   hipLaunchKernelGGL((grouped_gemm_dual_kernel<FMT, EPI, LORA, Tall, Short>),
                      dim3(static_cast<unsigned>(grid)), dim3(Tall::NT), 0, s, p);
   return check_launch("grouped GEMM launch");
@@ -1600,6 +1598,11 @@ int launch_fmt(int fmt, Params p, const PlanLayout &PL, const PlanView &v, bool 
   p.num_tiles = v.num_tiles2m;
   p.tiles_r = v.tilesr;
   p.num_tiles_r = v.num_tilesr;
+  // Half of the 32 CUs of an XCD (gfx950: 256 CUs in 8 XCDs) start on a
+  // remainder tile when experts average under 1024 rows, where remainder
+  // tiles are a large share of the work (A/B: C5 -2.6 %, C3 -1.3 %; at about
+  // 2048 rows per expert it gained nothing at the target and cost C4 1.2 %).
+  p.stagger = PL.rows < 1024 * static_cast<int64_t>(PL.experts) ? 16 : 0;
   return launch_tile_dual<EPI, LORA, Tall, Short>(fmt, p, PL.max_tiles2, PL.experts, s);
 }
 
