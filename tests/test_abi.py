@@ -101,3 +101,36 @@ def test_validation_errors_return_invalid_without_a_gpu():
 def test_call_maps_codes_to_python_exceptions():
     with pytest.raises(ValueError, match="mx_route_topk"):
         nat.call("mx_route_topk", None, 8, 4, 9, 1, 1.0, None, None, 0, None)
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    # The ctypes mirrors of the header's structs: sizes and field offsets as a C
+    # compiler lays them out (gcc on the header itself, no GPU involved).
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    structs = {"mx_weight": nat.MxWeight, "mx_lora": nat.MxLora, "mx_nf4_dq": nat.MxNf4Dq}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"',
+             "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in py._fields_:
+            lines.append(f'  printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    # The header declares hipStream_t-free C; it only needs stdint / stddef.
+    subprocess.run([cc, "-std=c11", "-o", str(exe), str(src)], check=True, capture_output=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    got = {}
+    for line in out.splitlines():
+        name, key, val = line.split()
+        got[(name, key)] = int(val)
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for field, _ in py._fields_:
+            assert got[(cname, field)] == getattr(py, field).offset, (cname, field)
