@@ -54,8 +54,8 @@ if str(ROOT) not in sys.path:
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 STAGES = ("plan", "lora_down_gate_up", "gate_up_gemm", "lora_down_down", "down_gemm", "combine")
-BACK_STAGES = ("plan_and_combine_bwd", "lora_dz_down", "dh_gemm", "lora_grads_down_and_dz_gate_up",
-               "dx_gemm", "lora_grads_gate_up_and_dx_sum")
+BACK_STAGES = ("plan_and_combine_bwd", "lora_dz_down", "dh_gemm",
+               "lora_grads_swiglu_bwd_and_lora_dz_gate_up", "dx_gemm", "dx_sum")
 
 
 def _parse():

@@ -2126,19 +2126,22 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
     p.out = dgu;
     p.ldo = 2 * ffn;
     if ((rc = launch_any<EPI_STORE2>(w2->format, lora2, p, L.plan, v, s))) return rc;
-    if ((rc = swiglu_backward(dgu, g_in, u_in, R, ffn, act, s))) return rc;
   }
   mark_stage(3, s);
   if (lora2) {
-    // dB2 = sum dy^T p2 and dA2 = sum dz2^T h, one launch.
+    // dB2 = sum dy^T p2 and dA2 = sum dz2^T h, one launch, right after the dh
+    // GEMM has streamed dy (much of it still in the memory-side cache) and
+    // before the SwiGLU backward leaves [dG | dU] dirty in it.
     GradPhase ph;
     ph.add({dy, hidden, v.row_slot, hidden}, lsave + 2 * lrc, ldz, l2->rank, grad_b2, false);
     ph.add({h_in, ffn, nullptr, ffn}, dz + 2 * lrc, ldz, l2->rank, grad_a2, true);
     if ((rc = ph.run(v, num_experts, s))) return rc;
   }
+  if ((rc = swiglu_backward(dgu, g_in, u_in, R, ffn, act, s))) return rc;
 
-  // Gate / up projections: dz1 = s1 * dG B1, dz3 = s3 * dU B3, then per-slot
-  // dx = dG W1 + dU W3 + dz1 A1 + dz3 A3 (written over dy, slot order).
+  // Gate / up projections: dz1 = s1 * dG B1, dz3 = s3 * dU B3, the gate / up
+  // LoRA weight gradients, then per-slot dx = dG W1 + dU W3 + dz1 A1 + dz3 A3
+  // (written over dy, slot order).
   const mx_lora *l13[2] = {l1, l3};
   for (int i = 0; i < 2; ++i) {
     const mx_lora *l = l13[i];
@@ -2150,6 +2153,22 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
     if ((rc = lora_down(v, num_experts, L.plan.max_tiles, dgu + i * ffn, 2 * ffn, nullptr, ffn, ad,
                         1, lrc, dz + lrc * i, ldz, s)))
       return rc;
+  }
+  // dB1 / dB3 = sum dG^T p1 / dU^T p3, and dA1 / dA3 = sum dz1^T x / dz3^T x
+  // from one pass over the gathered token rows, one launch, while [dG | dU]
+  // is still in the memory-side cache from the SwiGLU backward and the dz
+  // passes (nothing here reads what the dx GEMM overwrites).
+  {
+    GradPhase ph;
+    for (int i = 0; i < 2; ++i)
+      if (has_lora(l13[i]))
+        ph.add({dgu + i * ffn, 2 * ffn, nullptr, ffn}, lsave + lrc * i, ldz, l13[i]->rank,
+               i ? grad_b3 : grad_b1, false);
+    for (int i = 0; i < 2; ++i)
+      if (has_lora(l13[i]))
+        ph.add({x, hidden, v.row_token, hidden}, dz + lrc * i, ldz, l13[i]->rank,
+               i ? grad_a3 : grad_a1, true);
+    if ((rc = ph.run(v, num_experts, s))) return rc;
   }
   mark_stage(4, s);
   {
@@ -2176,18 +2195,7 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
     if ((rc = launch_any<EPI_STORE2>(w1->format, lora1 || lora3, p, L.plan, v, s))) return rc;
   }
   mark_stage(5, s);
-  // dB1 / dB3 = sum dG^T p1 / dU^T p3, and dA1 / dA3 = sum dz1^T x / dz3^T x
-  // from one pass over the gathered token rows, one launch.
-  GradPhase ph;
-  for (int i = 0; i < 2; ++i)
-    if (has_lora(l13[i]))
-      ph.add({dgu + i * ffn, 2 * ffn, nullptr, ffn}, lsave + lrc * i, ldz, l13[i]->rank,
-             i ? grad_b3 : grad_b1, false);
-  for (int i = 0; i < 2; ++i)
-    if (has_lora(l13[i]))
-      ph.add({x, hidden, v.row_token, hidden}, dz + lrc * i, ldz, l13[i]->rank,
-             i ? grad_a3 : grad_a1, true);
-  return ph.run(v, num_experts, s);
+  return MX_OK;
 }
 
 }  // namespace gemm

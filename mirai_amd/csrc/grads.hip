@@ -18,12 +18,75 @@ namespace {
 // stores are coalesced. Runs are moved as 16-byte vectors when the rank is a
 // multiple of 8 and both buffers are 16-byte aligned. Workgroups
 // [block0[j], block0[j + 1]) serve job j.
+// Jobs whose rank is a multiple of 8, whose long dimension is a multiple of 8
+// and whose buffers are 16-byte aligned go through LDS instead, a block of 32
+// ranks x 128 positions per workgroup: 16-byte loads along the source rows,
+// 16-byte stores along the destination rows (for a rank of 16 the block's
+// destination is one contiguous 4 KB run).
 struct TransposeLaunch {
   FactorTranspose job[6];
   int64_t block0[7];
   int vec[6];
+  int tiled[6];
   int n;
 };
+
+constexpr int kTileL = 128, kTileS = 32;
+
+__device__ void transpose_block(const FactorTranspose &t, bool small_rows, uint32_t S, uint32_t Lg,
+                                int64_t local, uint16_t *tile) {
+  const int64_t lblocks = (Lg + kTileL - 1) / kTileL, sblocks = (S + kTileS - 1) / kTileS;
+  const int64_t e = local / (lblocks * sblocks), rem = local - e * lblocks * sblocks;
+  const uint32_t l0 = static_cast<uint32_t>(rem / sblocks) * kTileL;
+  const uint32_t s0 = static_cast<uint32_t>(rem % sblocks) * kTileS;
+  const uint32_t nl = min(static_cast<uint32_t>(kTileL), Lg - l0);
+  const uint32_t ns = min(static_cast<uint32_t>(kTileS), S - s0);
+  const int64_t base = e * S * Lg;
+  const uint16_t *src = t.src + base;
+  uint16_t *dst = t.dst + base;
+  const int tid = threadIdx.x;
+  if (small_rows) {
+    // src [S][Lg] -> tile [s][l] -> dst [Lg][S].
+    for (int i = tid; i < kTileS * (kTileL / 8); i += 256) {
+      const uint32_t sr = i / (kTileL / 8), lp = i % (kTileL / 8);
+      if (sr < ns && lp * 8 < nl)
+        *reinterpret_cast<u32x4 *>(tile + sr * kTileL + lp * 8) =
+            *reinterpret_cast<const u32x4 *>(src + static_cast<int64_t>(s0 + sr) * Lg + l0 + lp * 8);
+    }
+    __syncthreads();
+    for (int i = tid; i < kTileL * (kTileS / 8); i += 256) {
+      const uint32_t l = i / (kTileS / 8), sp = i % (kTileS / 8);
+      if (l < nl && sp * 8 < ns) {
+        u32x4 w;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          w[q] = static_cast<uint32_t>(tile[(sp * 8 + 2 * q) * kTileL + l]) |
+                 (static_cast<uint32_t>(tile[(sp * 8 + 2 * q + 1) * kTileL + l]) << 16);
+        *reinterpret_cast<u32x4 *>(dst + static_cast<int64_t>(l0 + l) * S + s0 + sp * 8) = w;
+      }
+    }
+  } else {
+    // src [Lg][S] -> tile [l][s] -> dst [S][Lg].
+    for (int i = tid; i < kTileL * (kTileS / 8); i += 256) {
+      const uint32_t l = i / (kTileS / 8), sp = i % (kTileS / 8);
+      if (l < nl && sp * 8 < ns)
+        *reinterpret_cast<u32x4 *>(tile + l * kTileS + sp * 8) =
+            *reinterpret_cast<const u32x4 *>(src + static_cast<int64_t>(l0 + l) * S + s0 + sp * 8);
+    }
+    __syncthreads();
+    for (int i = tid; i < kTileS * (kTileL / 8); i += 256) {
+      const uint32_t sr = i / (kTileL / 8), lp = i % (kTileL / 8);
+      if (sr < ns && lp * 8 < nl) {
+        u32x4 w;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          w[q] = static_cast<uint32_t>(tile[(lp * 8 + 2 * q) * kTileS + sr]) |
+                 (static_cast<uint32_t>(tile[(lp * 8 + 2 * q + 1) * kTileS + sr]) << 16);
+        *reinterpret_cast<u32x4 *>(dst + static_cast<int64_t>(s0 + sr) * Lg + l0 + lp * 8) = w;
+      }
+    }
+  }
+}
 
 __global__ __launch_bounds__(256) void transpose_factors_multi_kernel(TransposeLaunch L) {
   int j = 0;
@@ -32,6 +95,11 @@ __global__ __launch_bounds__(256) void transpose_factors_multi_kernel(TransposeL
   const bool small_rows = t.rows <= t.cols;
   const uint32_t S = static_cast<uint32_t>(small_rows ? t.rows : t.cols);
   const uint32_t Lg = static_cast<uint32_t>(small_rows ? t.cols : t.rows);
+  if (L.tiled[j]) {
+    __shared__ __attribute__((aligned(16))) uint16_t tile[kTileS * kTileL];
+    transpose_block(t, small_rows, S, Lg, static_cast<int64_t>(blockIdx.x) - L.block0[j], tile);
+    return;
+  }
   const uint32_t idx = static_cast<uint32_t>(
       (static_cast<int64_t>(blockIdx.x) - L.block0[j]) * 256 + threadIdx.x);
   if (static_cast<int64_t>(idx) * S >= t.total) return;
@@ -149,6 +217,7 @@ __global__ __launch_bounds__(256) void lora_weight_grad_kernel(GradLaunch L) {
   const int32_t *map = J.map;
   const int64_t ldm = J.ldm, ldv = J.ldv, cols = J.cols;
   const int nv = J.nv;
+  const uint16_t *const vsrc[2] = {J.v[0], J.v[nv > 1 ? 1 : 0]};
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t start = L.seg_start[e], end = L.seg_end[e];
   f32x16 acc[2];
@@ -165,38 +234,49 @@ __global__ __launch_bounds__(256) void lora_weight_grad_kernel(GradLaunch L) {
     u32x4 vr[2];
   };
   const int vrow = tid >> 2, vch = tid & 3;
-  // M source rows of a chunk (-1 past the segment end).
+  // Every lane issues every load of a step, from an address clamped into the
+  // segment and the slice; rows past the segment end and columns past `cols`
+  // are zeroed when the chunk is staged. (With loads under a lane or
+  // workgroup condition some paths through a step issue none, and the
+  // compiler's wait counting then drains the whole queue before each use.)
+  // A chunk's source rows: the row map's entries for its rows, clamped to the
+  // segment's last row (without a map, a dummy load keeps the count even and
+  // the row index is used as it is).
+  const int32_t *const mbase = map ? map : reinterpret_cast<const int32_t *>(L.seg_start);
+  const int64_t mstep = map ? 1 : 0;
   auto rows_of = [&](int64_t r0, int32_t *src) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t grow = r0 + ((tid + 256 * i) >> 4);
-      src[i] = grow < end ? (map ? map[grow] : static_cast<int32_t>(grow)) : -1;
+      const int64_t grow = min(r0 + ((tid + 256 * i) >> 4), end - 1);
+      src[i] = mbase[grow * mstep];
     }
   };
   auto load = [&](int64_t r0, const int32_t *src, Loads &Ld) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t col = c0 + ((tid + 256 * i) & 15) * 8;
-      Ld.mr[i] = (src[i] >= 0 && col < cols)
-                     ? *reinterpret_cast<const u32x4 *>(m + static_cast<int64_t>(src[i]) * ldm + col)
-                     : u32x4{0u, 0u, 0u, 0u};
+      const int64_t grow = min(r0 + ((tid + 256 * i) >> 4), end - 1);
+      const int64_t row = map ? static_cast<int64_t>(src[i]) : grow;
+      const int64_t col = min(c0 + ((tid + 256 * i) & 15) * 8, cols - 8);
+      Ld.mr[i] = *reinterpret_cast<const u32x4 *>(m + row * ldm + col);
     }
-    const int64_t grow = r0 + vrow;
+    const int64_t grow = min(r0 + vrow, end - 1);
 #pragma unroll
     for (int vb = 0; vb < 2; ++vb)
-      Ld.vr[vb] = (vb < nv && grow < end)
-                      ? *reinterpret_cast<const u32x4 *>(J.v[vb] + grow * ldv + vch * 8)
-                      : u32x4{0u, 0u, 0u, 0u};
+      Ld.vr[vb] = *reinterpret_cast<const u32x4 *>(vsrc[vb] + grow * ldv + vch * 8);
   };
-  auto store = [&](uint8_t *sM, uint8_t *sV, const Loads &Ld) {
+  auto store = [&](int64_t r0, uint8_t *sM, uint8_t *sV, const Loads &Ld) {
+    const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int q = tid + 256 * i;
-      *reinterpret_cast<u32x4 *>(sM + swz_t128(q >> 4, q & 15)) = Ld.mr[i];
+      const bool ok = r0 + (q >> 4) < end && c0 + (q & 15) * 8 < cols;
+      *reinterpret_cast<u32x4 *>(sM + swz_t128(q >> 4, q & 15)) = ok ? Ld.mr[i] : zero;
     }
+    const bool vok = r0 + vrow < end;
 #pragma unroll
     for (int vb = 0; vb < 2; ++vb)
-      if (vb < nv) *reinterpret_cast<u32x4 *>(sV + vb * 4096 + vrow * 64 + vch * 16) = Ld.vr[vb];
+      if (vb < nv)
+        *reinterpret_cast<u32x4 *>(sV + vb * 4096 + vrow * 64 + vch * 16) = vok ? Ld.vr[vb] : zero;
   };
   auto compute = [&](const uint8_t *sM, const uint8_t *sV) {
 #pragma unroll
@@ -211,31 +291,36 @@ __global__ __launch_bounds__(256) void lora_weight_grad_kernel(GradLaunch L) {
     }
   };
   // Chunk c (rows start + 64c) is loaded in step c-2 (set c % 2), stored to
-  // stage c % 2 after the MFMAs of step c-1, and multiplied in step c.
+  // stage c % 2 after the MFMAs of step c-1, and multiplied in step c; its
+  // source rows are fetched in step c-3 into row set c % 2. Every step issues
+  // the same loads (rows past the segment end re-read its last row and stage
+  // zeros),
+  // so the waits stay counted: the chunk loaded in step c-1 stays in flight
+  // through step c's MFMAs.
   auto step = [&](int64_t r0, const uint8_t *cM, const uint8_t *cV, uint8_t *nM, uint8_t *nV,
-                  Loads &next, Loads &after, int32_t *src) {
-    if (r0 + 128 < end) load(r0 + 128, src, after);
-    if (r0 + 192 < end) rows_of(r0 + 192, src);
+                  Loads &next, Loads &after, const int32_t *src_after, int32_t *src_later) {
+    rows_of(r0 + 192, src_later);
+    load(r0 + 128, src_after, after);
     compute(cM, cV);
-    if (r0 + 64 < end) store(nM, nV, next);
+    store(r0 + 64, nM, nV, next);
     __syncthreads();
   };
   if (start < end) {
     Loads la, lb;
-    int32_t src[4];
-    rows_of(start, src);
-    load(start, src, la);
-    if (start + 64 < end) {
-      rows_of(start + 64, src);
-      load(start + 64, src, lb);
-    }
-    if (start + 128 < end) rows_of(start + 128, src);
-    store(sM0, sV0, la);
+    int32_t s0[4], s1[4];
+    rows_of(start, s0);
+    load(start, s0, la);
+    rows_of(start + 64, s1);
+    load(start + 64, s1, lb);
+    rows_of(start + 128, s0);
+    store(start, sM0, sV0, la);
     __syncthreads();
+    // Steps run in pairs, so the loop has one path: with an odd number of
+    // chunks the last step multiplies the zeros staged past the segment end,
+    // which leaves every fp32 sum as it was (a sum is never -0).
     for (int64_t r0 = start; r0 < end; r0 += 128) {
-      step(r0, sM0, sV0, sM1, sV1, lb, la, src);
-      if (r0 + 64 >= end) break;
-      step(r0 + 64, sM1, sV1, sM0, sV0, la, lb, src);
+      step(r0, sM0, sV0, sM1, sV1, lb, la, s0, s1);
+      step(r0 + 64, sM1, sV1, sM0, sV0, la, lb, s1, s0);
     }
   }
   // Accumulator value jj of a lane: column c = 8*(jj/4) + 4*(lane/32) + jj%4 of
@@ -365,7 +450,12 @@ int transpose_factors_multi(const FactorTransposes &jobs, hipStream_t s) {
     L.block0[L.n] = blocks;
     L.vec[L.n] = small % 8 == 0 && reinterpret_cast<uintptr_t>(t.src) % 16 == 0 &&
                  reinterpret_cast<uintptr_t>(t.dst) % 16 == 0;
-    blocks += t.total > 0 ? ceil_div(t.total / small, 256) : 0;
+    const int64_t lg = small == t.rows ? t.cols : t.rows;
+    L.tiled[L.n] = L.vec[L.n] && lg % 8 == 0;
+    if (t.total > 0)
+      blocks += L.tiled[L.n]
+                    ? t.total / (small * lg) * ceil_div(lg, kTileL) * ceil_div(small, kTileS)
+                    : ceil_div(t.total / small, 256);
     ++L.n;
   }
   L.block0[L.n] = blocks;
