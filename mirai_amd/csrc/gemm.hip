@@ -143,6 +143,10 @@ struct Params {
   const float *dq_offset[2];
   const float *dq_code[2];
   int64_t dq_npe[2];
+  // MX_FMT_F32X3 down projection: K parts per tile (1: none) of k_part_len
+  // columns each; part q writes its [hi | lo] planes at column 2 N q.
+  int k_parts;
+  int64_t k_part_len;
 };
 
 // Per-thread choice among the small kernel-argument arrays by explicit
@@ -351,12 +355,24 @@ __device__ __forceinline__ void projection_run(float (&v)[4], float (&a)[4], uin
 template <int FMT, int EPI, bool LORA, class T>
 __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *sA0,
                                           uint8_t *sA1, uint8_t *sB0, uint8_t *sB1,
-                                          uint8_t *sLt, const float *sCode) {
+                                          uint8_t *sLt, const float *sCode, int part = 0) {
   constexpr int kLTile = lora_tile_bytes<EPI, LORA, T>();
   const int tid = threadIdx.x;
   // MX_FMT_F32X3: bf16 planes with K = 3 * in (loaded as bf16); the
   // epilogues keep fp32 and write split outputs.
   constexpr bool kSplit = FMT == MX_FMT_F32X3;
+  // Its down projection in K parts (launches with too few tiles to fill the
+  // GPU): part q multiplies K columns [q k_part_len, (q + 1) k_part_len) and
+  // writes its own planes; the LoRA delta goes with part 0.
+  constexpr bool kKParts = kSplit && EPI == EPI_STORE;
+  int64_t k_off = 0;
+  if constexpr (kKParts) {
+    if (p.k_parts > 1) {
+      k_off = static_cast<int64_t>(part) * p.k_part_len;
+      p.out += 2 * p.N * part;
+      if (part != 0) p.lora_r[0] = p.lora_r[1] = 0;
+    }
+  }
   const int e = tile.x;
   const int64_t row0 = tile.y;
   const int64_t row_end = p.seg_end[e];
@@ -393,7 +409,7 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
     for (int i = 0; i < T::A_CHUNKS; ++i) a_src[i] = p.row_token[a_src[i]];
   }
 #pragma unroll
-  for (int i = 0; i < T::A_CHUNKS; ++i) a_ptr[i] = p.x + a_src[i] * p.ldx + a_col[i];
+  for (int i = 0; i < T::A_CHUNKS; ++i) a_ptr[i] = p.x + a_src[i] * p.ldx + a_col[i] + k_off;
 
   // ------------------------------------------------------- B (weights)
   constexpr bool TRANS = trans_b(EPI, FMT);
@@ -447,7 +463,7 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
       b_base = w + wrow * p.K + bh * T::B_ELEMS;
       b_scale = bf16_bits_to_f32(static_cast<const uint16_t *>(pick(p.wscale, which))[wrow]);
     } else {
-      b_base = w + wrow * p.K * 2 + bh * T::B_ELEMS * 2;
+      b_base = w + (wrow * p.K + k_off) * 2 + bh * T::B_ELEMS * 2;
     }
   }
   // NF4_DQ, row decode: the nested scales of this thread's row. With K <= 16384
@@ -660,7 +676,7 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   // stage's B (loaded one iteration earlier) into the other buffer; the next
   // A tile and the B tile two steps ahead are in flight meanwhile. Loads past
   // the end are clamped to the last step, so the body is branch free.
-  const int KT = static_cast<int>(p.K / BK);
+  const int KT = static_cast<int>((kKParts && p.k_parts > 1 ? p.k_part_len : p.K) / BK);
   // Stage (sA, sB) is multiplied while stage (nA, nB) is produced. f0 holds
   // the first sub-step's fragments of (sA, sB) on entry, and of (nA, nB) on
   // exit (read right after the barrier).
@@ -1404,12 +1420,15 @@ void grouped_gemm_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t sB1[T::STAGE_B];
   __shared__ __attribute__((aligned(16))) uint8_t sLt[lora_tile_bytes<EPI, LORA, T>()];
   __shared__ float sCode[is_dq(FMT) ? 512 : 1];
-  const int total = *p.num_tiles * p.n_tiles_n;
+  constexpr bool kKParts = FMT == MX_FMT_F32X3 && EPI == EPI_STORE;
+  const int parts = kKParts && p.k_parts > 1 ? p.k_parts : 1;
+  const int total = *p.num_tiles * p.n_tiles_n * parts;
   const int per_xcd = (total + 7) >> 3;
   const int slot = blockIdx.x >> 3;
   if (slot >= per_xcd) return;
-  const int logical = (blockIdx.x & 7) * per_xcd + slot;
-  if (logical >= total) return;
+  const int job = (blockIdx.x & 7) * per_xcd + slot;
+  if (job >= total) return;
+  const int logical = job / parts, part = job - logical * parts;
   const int mt = logical / p.n_tiles_n;
   const int2 tile = p.tiles[mt];
   load_code_tables<FMT>(p, sCode);
@@ -1420,7 +1439,8 @@ void grouped_gemm_kernel(Params p) {
       return;
     }
   }
-  gemm_tile<FMT, EPI, LORA, T>(p, tile, logical - mt * p.n_tiles_n, sA0, sA1, sB0, sB1, sLt, sCode);
+  gemm_tile<FMT, EPI, LORA, T>(p, tile, logical - mt * p.n_tiles_n, sA0, sA1, sB0, sB1, sLt, sCode,
+                               part);
 }
 
 // 256-row tiles (p.tiles) and the 128-row remainder tiles (p.tiles_r) in one
@@ -1480,7 +1500,9 @@ void grouped_gemm_dual_kernel(Params p) {
 
 template <int FMT, int EPI, bool LORA, class T>
 int launch(const Params &p, int64_t max_row_tiles, hipStream_t s) {
-  const int64_t total = max_row_tiles * p.n_tiles_n;
+  const int64_t total =
+      max_row_tiles * p.n_tiles_n *
+      (FMT == MX_FMT_F32X3 && EPI == EPI_STORE && p.k_parts > 1 ? p.k_parts : 1);
   if (total <= 0) return MX_OK;
   const int64_t grid = 8 * ceil_div(total, 8);
   if (grid > 0x7fffffff) {
@@ -1515,6 +1537,21 @@ int launch_dual(Params p, int64_t max_tall, int64_t max_short, hipStream_t s) {
 // taller tile's better MFMA / LDS ratio outweighs its tail waste from there
 // on, measured at C2, C3 and C5), else 128-row tiles.
 inline bool use_tall_tiles(int64_t rows, int experts) { return rows >= 256 * static_cast<int64_t>(experts); }
+
+// fp32 layer, down projection on 128-row tiles: K parts per tile, so that a
+// launch with few tiles (C1: at most 32 tiles of 48 K steps for 256 CUs)
+// still spreads over the chip. Up to 6 parts, each of at least 8 K steps,
+// while the launch stays within one workgroup per CU.
+constexpr int kChipCUs = 256;
+inline int f32x3_down_parts(int64_t rows, int experts, int64_t hidden, int64_t ffn) {
+  if (use_tall_tiles(rows, experts)) return 1;
+  const int64_t slots = (ceil_div(rows, kPlanTileM) + experts) * ceil_div(hidden, 256);
+  const int64_t steps = 3 * ffn / 64;
+  int best = 1;
+  for (int kp = 2; kp <= 6; ++kp)
+    if (steps % kp == 0 && steps / kp >= 8 && slots * kp <= kChipCUs) best = kp;
+  return best;
+}
 
 // 128-row tiles only (experts averaging under 256 rows).
 template <int EPI, bool LORA, class Short>
@@ -1640,8 +1677,8 @@ struct LayerLayout {
 // Scratch of the layer: plan | low-rank activations [R, 3 rc] (planes of rc
 // columns for gate, up and down, rc = lora_width of the largest rank) |
 // h [R, f] | y [R, d]. The fp32 (MX_FMT_F32X3) layer holds h as planes
-// [R, 3f] and y as planes [R, 2d], and adds the split tokens [T, 3d] and the
-// fp32 combine of both y planes [T, 2d].
+// [R, 3f] and y as planes [R, 2d] per K part of its down projection, and adds
+// the split tokens [T, 3d] and the fp32 combine of all y planes.
 LayerLayout layer_layout(int64_t rows, int num_experts, int64_t hidden, int64_t ffn,
                          bool split = false, int64_t tokens = 0, int rc = kLoraK) {
   LayerLayout L;
@@ -1652,12 +1689,13 @@ LayerLayout layer_layout(int64_t rows, int num_experts, int64_t hidden, int64_t 
   L.off_h = off;
   off = align_up(off + sizeof(uint16_t) * rows * ffn * (split ? 3 : 1), 256);
   L.off_y = off;
-  off = align_up(off + sizeof(uint16_t) * rows * hidden * (split ? 2 : 1), 256);
+  const int64_t y_planes = split ? 2 * f32x3_down_parts(rows, num_experts, hidden, ffn) : 1;
+  off = align_up(off + sizeof(uint16_t) * rows * hidden * y_planes, 256);
   L.off_x = off;
   if (split) {
     off = align_up(off + sizeof(uint16_t) * tokens * hidden * 3, 256);
-    L.off_sum = off;  // fp32 [T, 2d]: the combine of the two y planes
-    off = align_up(off + sizeof(float) * tokens * hidden * 2, 256);
+    L.off_sum = off;  // fp32 [T, y_planes d]: the combine of the y planes
+    off = align_up(off + sizeof(float) * tokens * hidden * y_planes, 256);
   }
   L.bytes = off;
   return L;
@@ -1922,6 +1960,10 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
   p.out = y;
   p.ldo = ldy;
   p.out_row = out_row;
+  if (split) {
+    p.k_parts = f32x3_down_parts(PL.rows, experts, hidden, ffn);
+    p.k_part_len = 3 * ffn / p.k_parts;
+  }
   return launch_any<EPI_STORE>(w2->format, lora2, p, PL, v, s);
 }
 
@@ -2385,18 +2427,19 @@ extern "C" int mx_moe_forward_ex(const void *tokens, const int64_t *top_idx,
                                  : reinterpret_cast<uint16_t *>(ws + L.off_lora);
   uint16_t *h = save_h ? static_cast<uint16_t *>(save_h) : reinterpret_cast<uint16_t *>(ws + L.off_h);
   uint16_t *y = save_y ? static_cast<uint16_t *>(save_y) : reinterpret_cast<uint16_t *>(ws + L.off_y);
+  const int y_planes = split ? 2 * f32x3_down_parts(R, num_experts, hidden, ffn) : 1;
   rc = expert_mlp(L.plan, v, num_experts, x, (split ? 3 : 1) * hidden,
                   v.row_token, hidden, ffn, act, w1, w3, w2, l1, l3, l2, lora_buf, lrc, h,
                   static_cast<uint16_t *>(save_gate), static_cast<uint16_t *>(save_up), y,
-                  (split ? 2 : 1) * hidden, v.row_slot, s);
+                  y_planes * hidden, v.row_slot, s);
   if (rc) return rc;
   mark_stage(5, s);
   if (split) {
-    // fp32 layer: combine both y planes in fp32, then add them.
+    // fp32 layer: combine every y plane in fp32, then add them.
     float *sum = reinterpret_cast<float *>(ws + L.off_sum);
     rc = mx_combine(y, top_idx, top_scores, score_dtype, num_tokens, top_k, num_experts,
-                    2 * hidden, sum, MX_DTYPE_F32, stream);
-    if (!rc) rc = sum_halves(sum, num_tokens, hidden, out, out_dtype, s);
+                    y_planes * hidden, sum, MX_DTYPE_F32, stream);
+    if (!rc) rc = sum_planes(sum, num_tokens, hidden, y_planes, out, out_dtype, s);
   } else {
     // The addend (e.g. a shared expert computed on another stream) is needed
     // only here: the routed path above runs concurrently with its producer.

@@ -9,9 +9,10 @@ namespace mx {
 int split_f32(const float *x, int64_t rows, int64_t cols, int pattern, uint16_t *out,
               hipStream_t s);
 
-// out[r, c] = in[r, c] + in[r, cols + c] for fp32 in [rows, 2*cols], written
-// as out_dtype (the fp32 layer's combine of its two output planes).
-int sum_halves(const float *in, int64_t rows, int64_t cols, void *out, int out_dtype,
+// out[r, c] = sum over q < planes of in[r, q*cols + c] for fp32 in
+// [rows, planes*cols], added from the last plane to the first and written as
+// out_dtype (the fp32 layer's combine of its output planes).
+int sum_planes(const float *in, int64_t rows, int64_t cols, int planes, void *out, int out_dtype,
                hipStream_t s);
 
 // mx_combine with an optional addend [T, cols] of out's dtype:

@@ -366,14 +366,20 @@ __global__ __launch_bounds__(256) void split_f32_kernel(const float4 *x, int64_t
   o[2 * chunks] = pattern == MX_SPLIT_ACT ? L : H;
 }
 
+// out[r, c] = sum over planes q of in[r, q cols + c], added from the last
+// plane to the first (the low-order planes first).
 template <int OUT_DTYPE>
-__global__ __launch_bounds__(256) void sum_halves_kernel(const float4 *in, int64_t rows,
-                                                         int64_t chunks, void *out) {
+__global__ __launch_bounds__(256) void sum_planes_kernel(const float4 *in, int64_t rows,
+                                                         int64_t chunks, int planes, void *out) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= rows * chunks) return;
   const int64_t r = i / chunks, c = i - r * chunks;
-  const float4 a = in[r * 2 * chunks + c], b = in[r * 2 * chunks + chunks + c];
-  const float4 v = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+  const float4 *row = in + r * planes * chunks + c;
+  float4 v = row[(planes - 1) * chunks];
+  for (int q = planes - 2; q >= 0; --q) {
+    const float4 a = row[q * chunks];
+    v = make_float4(v.x + a.x, v.y + a.y, v.z + a.z, v.w + a.w);
+  }
   if (OUT_DTYPE == MX_DTYPE_F32) {
     static_cast<float4 *>(out)[i] = v;
   } else {
@@ -383,17 +389,17 @@ __global__ __launch_bounds__(256) void sum_halves_kernel(const float4 *in, int64
 
 }  // namespace
 
-int sum_halves(const float *in, int64_t rows, int64_t cols, void *out, int out_dtype,
+int sum_planes(const float *in, int64_t rows, int64_t cols, int planes, void *out, int out_dtype,
                hipStream_t s) {
   if (rows <= 0) return MX_OK;
   const int64_t chunks = cols / 4;
   const dim3 grid(static_cast<unsigned>(ceil_div(rows * chunks, 256)));
   if (out_dtype == MX_DTYPE_F32)
-    hipLaunchKernelGGL(sum_halves_kernel<MX_DTYPE_F32>, grid, dim3(256), 0, s,
-                       reinterpret_cast<const float4 *>(in), rows, chunks, out);
+    hipLaunchKernelGGL(sum_planes_kernel<MX_DTYPE_F32>, grid, dim3(256), 0, s,
+                       reinterpret_cast<const float4 *>(in), rows, chunks, planes, out);
   else
-    hipLaunchKernelGGL(sum_halves_kernel<MX_DTYPE_BF16>, grid, dim3(256), 0, s,
-                       reinterpret_cast<const float4 *>(in), rows, chunks, out);
+    hipLaunchKernelGGL(sum_planes_kernel<MX_DTYPE_BF16>, grid, dim3(256), 0, s,
+                       reinterpret_cast<const float4 *>(in), rows, chunks, planes, out);
   return check_launch("fp32 layer plane sum");
 }
 

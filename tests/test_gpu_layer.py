@@ -88,6 +88,18 @@ def test_fp32_layer_small(with_lora):
     assert stats["mean_rel"] < 1e-4, stats
 
 
+@pytest.mark.parametrize("d,f", [(192, 640), (320, 1024)])
+def test_fp32_layer_down_projection_in_k_parts(d, f):
+    # 600 routed rows: the down projection's launch has at most 11 (d = 192) or
+    # 22 (d = 320) tiles, so each tile's K (3 f) is split over 3 (f = 640: 30
+    # K steps) or 6 (f = 1024: 48 K steps) workgroups. Each part writes its own
+    # [hi | lo] planes, part 0 with the LoRA delta, and the combine adds the
+    # planes; d = 192 and 320 leave a partial column tile.
+    w = small("fp32", dtype=torch.float32, r=8, alpha=16.0, T=300, E=6, k=2, d=d, f=f)
+    stats = _run_case(w, with_lora=True)
+    assert stats["mean_rel"] < 1e-4, stats
+
+
 @pytest.mark.parametrize("chunk", [0, 128])
 def test_fp32_layer_trains_like_fp64_autograd(chunk):
     # fp32 weights under autograd: the split-precision kernels run the forward,
