@@ -78,6 +78,10 @@ __device__ __forceinline__ float absmax_value(uint32_t raw) {
 // Backward epilogues multiply by W itself rather than W^T; with weights stored
 // [E, in, out] the forward does.
 constexpr bool trans_b(int epi, int fmt) { return (epi == EPI_STORE2) != is_kn(fmt); }
+// Launches whose tiles may run in K parts (Params::k_parts).
+constexpr bool has_k_parts(int fmt, int epi) {
+  return (fmt == MX_FMT_F32X3 && epi == EPI_STORE) || epi == EPI_LORA_A;
+}
 
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 
@@ -145,8 +149,14 @@ struct Params {
   int64_t dq_npe[2];
   // MX_FMT_F32X3 down projection: K parts per tile (1: none) of k_part_len
   // columns each; part q writes its [hi | lo] planes at column 2 N q.
+  // EPI_LORA_A: k_part_len is the canonical part of its K sum (0: one part);
+  // with k_parts > 1 each part runs in its own workgroup and leaves its fp32
+  // sums in part_out [k_parts][part_rows][part_ld].
   int k_parts;
   int64_t k_part_len;
+  float *part_out;
+  int64_t part_rows;
+  int part_ld;
 };
 
 // Per-thread choice among the small kernel-argument arrays by explicit
@@ -363,14 +373,17 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   constexpr bool kSplit = FMT == MX_FMT_F32X3;
   // Its down projection in K parts (launches with too few tiles to fill the
   // GPU): part q multiplies K columns [q k_part_len, (q + 1) k_part_len) and
-  // writes its own planes; the LoRA delta goes with part 0.
-  constexpr bool kKParts = kSplit && EPI == EPI_STORE;
+  // writes its own planes; the LoRA delta goes with part 0. The LoRA
+  // down-projection likewise, its parts leaving fp32 sums (see below).
+  constexpr bool kKParts = has_k_parts(FMT, EPI);
   int64_t k_off = 0;
   if constexpr (kKParts) {
     if (p.k_parts > 1) {
       k_off = static_cast<int64_t>(part) * p.k_part_len;
-      p.out += 2 * p.N * part;
-      if (part != 0) p.lora_r[0] = p.lora_r[1] = 0;
+      if constexpr (EPI == EPI_STORE) {
+        p.out += 2 * p.N * part;
+        if (part != 0) p.lora_r[0] = p.lora_r[1] = 0;
+      }
     }
   }
   const int e = tile.x;
@@ -645,6 +658,41 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
     for (int nb = 0; nb < T::NB; ++nb)
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[mb][nb][j] = 0.0f;
+  // EPI_LORA_A: its K sum runs in canonical parts of p.k_part_len columns, a
+  // function of K alone. Each part's MFMA chain starts from zero and the parts
+  // are added in order, ((0 + s0) + s1) + ..., whether one workgroup runs them
+  // all (folding each finished part into tot) or each part runs in its own
+  // workgroup (k_parts > 1) and a pass adds their fp32 sums in the same order.
+  // So the result does not depend on how many rows a launch has, and a
+  // token-chunked layer stays bit-identical to the whole one. (The 128-column
+  // tile of ranks above 64 sums K in one part: tot would cost it occupancy.)
+  constexpr bool kFold = EPI == EPI_LORA_A && T::BN == 64;
+  f32x16 tot[kFold ? T::MB : 1][kFold ? T::NB : 1];
+  // Steps per part here (the whole K loop when this workgroup runs one part),
+  // counted down to each fold.
+  int fold_steps = 1, fold_left = 1;
+  if constexpr (kFold) {
+#pragma unroll
+    for (int mb = 0; mb < T::MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < T::NB; ++nb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) tot[mb][nb][j] = 0.0f;
+    fold_steps = fold_left = static_cast<int>((p.k_part_len > 0 ? p.k_part_len : p.K) / T::BK);
+  }
+  auto fold = [&]() __attribute__((always_inline)) {
+    if constexpr (kFold) {
+#pragma unroll
+      for (int mb = 0; mb < T::MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < T::NB; ++nb)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            tot[mb][nb][j] += acc[mb][nb][j];
+            acc[mb][nb][j] = 0.0f;
+          }
+    }
+  };
 
   // MFMA operand fragments of one K sub-step, double-buffered so the reads
   // of sub-step kk+1 are in flight while sub-step kk multiplies.
@@ -753,6 +801,10 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
       mfma_frags(cur);
       decode_b(b_next, t, nB, kk);
     }
+    if (kFold && --fold_left == 0) {
+      fold();
+      fold_left = fold_steps;
+    }
     __syncthreads();
     read_frags(f0, nA, nB, 0);
   };
@@ -774,6 +826,12 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
     step(kt + 1, sA1, sB1, sA0, sB0, rb0, rb1);
   }
   if (kt < KT) step(kt, sA0, sB0, sA1, sB1, rb1, rb0);
+  if constexpr (kFold) {
+#pragma unroll
+    for (int mb = 0; mb < T::MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < T::NB; ++nb) acc[mb][nb] = tot[mb][nb];
+  }
 
   // ------------------------------------------- LoRA up-projection (K = 32)
   // Multiplied block by block in the epilogue, into accumulators kept apart
@@ -1083,6 +1141,27 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
             *reinterpret_cast<u32x2 *>(dst) = u32x2{w0, w1};
             *reinterpret_cast<u32x2 *>(dst + p.N) = u32x2{l0, l1};
           }
+        }
+      }
+    }
+  } else if (EPI == EPI_LORA_A && p.k_parts > 1) {
+    // EPI_LORA_A, one K part of the tile: its fp32 sums, rows and columns as
+    // the output's, to part_out (the finishing pass adds the parts and rounds).
+#pragma unroll
+    for (int mb = 0; mb < T::MB; ++mb) {
+      const int r = wm * T::WM + mb * 32 + lrow;
+      if (r >= tile_rows) continue;
+      float *prow = p.part_out + (static_cast<int64_t>(part) * p.part_rows + row0 + r) * p.part_ld;
+#pragma unroll
+      for (int nb = 0; nb < T::NB; ++nb) {
+        const int nblk = wn * T::WN + nb * 32;
+        if (nblk >= p.N) continue;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int jc = 8 * g + lcol;
+          *reinterpret_cast<f32x4 *>(prow + nblk + jc) =
+              f32x4{acc[mb][nb][4 * g], acc[mb][nb][4 * g + 1], acc[mb][nb][4 * g + 2],
+                    acc[mb][nb][4 * g + 3]};
         }
       }
     }
@@ -1420,8 +1499,7 @@ void grouped_gemm_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t sB1[T::STAGE_B];
   __shared__ __attribute__((aligned(16))) uint8_t sLt[lora_tile_bytes<EPI, LORA, T>()];
   __shared__ float sCode[is_dq(FMT) ? 512 : 1];
-  constexpr bool kKParts = FMT == MX_FMT_F32X3 && EPI == EPI_STORE;
-  const int parts = kKParts && p.k_parts > 1 ? p.k_parts : 1;
+  const int parts = has_k_parts(FMT, EPI) && p.k_parts > 1 ? p.k_parts : 1;
   const int total = *p.num_tiles * p.n_tiles_n * parts;
   const int per_xcd = (total + 7) >> 3;
   const int slot = blockIdx.x >> 3;
@@ -1501,8 +1579,7 @@ void grouped_gemm_dual_kernel(Params p) {
 template <int FMT, int EPI, bool LORA, class T>
 int launch(const Params &p, int64_t max_row_tiles, hipStream_t s) {
   const int64_t total =
-      max_row_tiles * p.n_tiles_n *
-      (FMT == MX_FMT_F32X3 && EPI == EPI_STORE && p.k_parts > 1 ? p.k_parts : 1);
+      max_row_tiles * p.n_tiles_n * (has_k_parts(FMT, EPI) && p.k_parts > 1 ? p.k_parts : 1);
   if (total <= 0) return MX_OK;
   const int64_t grid = 8 * ceil_div(total, 8);
   if (grid > 0x7fffffff) {
@@ -1820,14 +1897,86 @@ Params base_params(const PlanView &v) {
   return p;
 }
 
+// The canonical part of a LoRA down-projection's K sum: the split of its K
+// steps into the most equal parts, at most 6, of at least 8 steps each. It
+// depends on K alone, so every launch over the same K sums alike.
+int64_t lora_a_part_len(int64_t K) {
+  const int64_t steps = K / 64;
+  int best = 1;
+  for (int d = 2; d <= 6; ++d)
+    if (steps % d == 0 && steps / d >= 8) best = d;
+  return K / best;
+}
+
+// The finishing pass of a LoRA down-projection run in K parts: the parts'
+// fp32 sums added in part order (the order one workgroup folds them in), then
+// the epilogue of the unsplit tile, per run of 4 columns of a sorted row.
+struct LoraFinish {
+  const float *part;
+  int parts;
+  int64_t rows;
+  int ld;
+  int N;
+  uint16_t *out;
+  int64_t ldo;
+  float scale[4];
+  int split_r[4];
+};
+
+template <bool SPLIT>
+__global__ __launch_bounds__(256) void lora_a_finish_kernel(LoraFinish f) {
+  const int runs = f.N / 4;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= f.rows * runs) return;
+  const int64_t r = i / runs;
+  const int c = static_cast<int>(i - r * runs) * 4;
+  const float *src = f.part + r * f.ld + c;
+  f32x4 a = *reinterpret_cast<const f32x4 *>(src);
+  for (int q = 1; q < f.parts; ++q) {
+    const f32x4 b = *reinterpret_cast<const f32x4 *>(src + q * f.rows * f.ld);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = a[j] + b[j];
+  }
+  float v[4] = {a[0], a[1], a[2], a[3]};
+  const int blk = c >> 5, jc = c & 31;
+  const float sc = pick(f.scale, blk);
+  uint16_t *orow = f.out + r * f.ldo + (c - jc);
+  typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+  if constexpr (SPLIT) {
+    // The fp32 layer's planes [hi | hi | lo] at columns j, r + j, 2r + j.
+    const int rk = pick(f.split_r, blk);
+    const bool own = jc < rk, zero = jc >= 3 * rk;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] *= sc;
+    const uint32_t hi0 = pack_bf16x2(v[0], v[1]), hi1 = pack_bf16x2(v[2], v[3]);
+    if (own) {
+      const uint32_t lo0 = pack_bf16x2(v[0] - bf16_bits_to_f32(hi0 & 0xffffu), v[1] - bf16_bits_to_f32(hi0 >> 16));
+      const uint32_t lo1 = pack_bf16x2(v[2] - bf16_bits_to_f32(hi1 & 0xffffu), v[3] - bf16_bits_to_f32(hi1 >> 16));
+      *reinterpret_cast<u32x2v *>(orow + jc) = u32x2v{hi0, hi1};
+      *reinterpret_cast<u32x2v *>(orow + rk + jc) = u32x2v{hi0, hi1};
+      *reinterpret_cast<u32x2v *>(orow + 2 * rk + jc) = u32x2v{lo0, lo1};
+    } else if (zero) {
+      *reinterpret_cast<u32x2v *>(orow + jc) = u32x2v{0u, 0u};
+    }
+  } else {
+    round2(v[0], v[1]);
+    round2(v[2], v[3]);
+    *reinterpret_cast<u32x2v *>(orow + jc) =
+        u32x2v{pack_bf16x2(v[0] * sc, v[1] * sc), pack_bf16x2(v[2] * sc, v[3] * sc)};
+  }
+}
+
 // LoRA down-projection p = bf16(s * bf16(x a^T)) for adapters that share the
 // same input rows: adapter i lands in columns [i rc, (i + 1) rc) of `out`,
 // zero past its rank. A rank-r adapter runs as ceil(r / 32) sub-adapters of
 // at most 32 factor rows (rows [32c, 32c + 32) of every expert's [r, K]
-// factor), up to four sub-adapters per launch.
+// factor), up to four sub-adapters per launch. With `part_buf` (fp32 scratch
+// of part_bytes, free for the call) and few tiles for the chip, each tile's
+// K parts run in workgroups of their own: a launch of `rows` sorted rows.
 int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t *x, int64_t ldx,
               const int32_t *row_token, int64_t K, const mx_lora *const *adapters, int n_adapt,
-              int rc, uint16_t *out, int64_t ldo, hipStream_t s, bool split = false) {
+              int rc, uint16_t *out, int64_t ldo, hipStream_t s, bool split = false,
+              int64_t rows = 0, float *part_buf = nullptr, size_t part_bytes = 0) {
   struct Sub {
     const uint16_t *a = nullptr;
     int rows = 0, stride = 0;
@@ -1872,6 +2021,21 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
     p.seg_end = v.seg + experts;
     p.out = out + kLoraK * first;
     p.ldo = ldo;
+    // The tile width of the launch below; the 64-column tile sums K in its
+    // canonical parts, and runs them in workgroups of their own when the
+    // launch would not give three workgroups to each CU.
+    const int bn = (split || cnt <= 2) ? 64 : 128;
+    const int64_t part_len = bn == 64 ? lora_a_part_len(K) : K;
+    const int kpc = static_cast<int>(K / part_len);
+    p.k_part_len = kpc > 1 ? part_len : 0;
+    const bool parts = kpc > 1 && part_buf && rows > 0 && max_tiles * kpc <= 3 * kChipCUs &&
+                       static_cast<size_t>(kpc) * rows * bn * sizeof(float) <= part_bytes;
+    if (parts) {
+      p.k_parts = kpc;
+      p.part_out = part_buf;
+      p.part_rows = rows;
+      p.part_ld = bn;
+    }
     // Up to two sub-adapters fill a 64-column tile; the kernel is bound by
     // the activation reads, so the narrower tile (more workgroups, half the
     // MFMA and B traffic) is the faster one (K stages of 32, for more
@@ -1885,6 +2049,26 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
     else
       rc2 = launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 128, 2, 2, 64>>(p, max_tiles, s);
     if (rc2) return rc2;
+    if (parts) {
+      LoraFinish f = {};
+      f.part = part_buf;
+      f.parts = kpc;
+      f.rows = rows;
+      f.ld = bn;
+      f.N = static_cast<int>(p.N);
+      f.out = p.out;
+      f.ldo = ldo;
+      for (int i = 0; i < 4; ++i) {
+        f.scale[i] = p.scale[i];
+        f.split_r[i] = p.split_r[i];
+      }
+      const dim3 grid(static_cast<unsigned>(ceil_div(rows * (p.N / 4), 256)));
+      if (split)
+        hipLaunchKernelGGL(lora_a_finish_kernel<true>, grid, dim3(256), 0, s, f);
+      else
+        hipLaunchKernelGGL(lora_a_finish_kernel<false>, grid, dim3(256), 0, s, f);
+      if ((rc2 = check_launch("LoRA down-projection parts"))) return rc2;
+    }
   }
   return MX_OK;
 }
@@ -1904,10 +2088,14 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
   const int64_t kx = split ? 3 : 1;
   const int rx = split ? 3 : 1;
   int rc;
+  // A LoRA down-projection run in K parts keeps its fp32 sums in the buffer
+  // the next GEMM writes: h before the gate/up GEMM, y before the down GEMM.
+  const int64_t R = PL.rows;
   if (lora13) {
     const mx_lora *ad[2] = {l1, l3};
     rc = lora_down(v, experts, PL.max_tiles, x, ldx, row_token, kx * hidden, ad, 2, lrc,
-                   lora_buf, 3 * lrc, s, split);
+                   lora_buf, 3 * lrc, s, split, R, reinterpret_cast<float *>(h),
+                   sizeof(uint16_t) * R * kx * ffn);
     if (rc) return rc;
   }
   mark_stage(2, s);
@@ -1940,7 +2128,8 @@ int expert_mlp(const PlanLayout &PL, const PlanView &v, int experts, const uint1
   if (lora2) {
     const mx_lora *ad[1] = {l2};
     rc = lora_down(v, experts, PL.max_tiles, h, kx * ffn, nullptr, kx * ffn, ad, 1, lrc,
-                   lora_buf + 2 * lrc, 3 * lrc, s, split);
+                   lora_buf + 2 * lrc, 3 * lrc, s, split, R, reinterpret_cast<float *>(y),
+                   sizeof(uint16_t) * R * ldy);
     if (rc) return rc;
   }
   mark_stage(4, s);
