@@ -88,13 +88,15 @@ def test_fp32_layer_small(with_lora):
     assert stats["mean_rel"] < 1e-4, stats
 
 
-@pytest.mark.parametrize("d,f", [(192, 640), (320, 1024)])
-def test_fp32_layer_down_projection_in_k_parts(d, f):
-    # 600 routed rows: the down projection's launch has at most 11 (d = 192) or
-    # 22 (d = 320) tiles, so each tile's K (3 f) is split over 3 (f = 640: 30
-    # K steps) or 6 (f = 1024: 48 K steps) workgroups. Each part writes its own
-    # [hi | lo] planes, part 0 with the LoRA delta, and the combine adds the
-    # planes; d = 192 and 320 leave a partial column tile.
+@pytest.mark.parametrize("d,f", [(192, 640), (320, 1024), (384, 640), (512, 1024)])
+def test_fp32_layer_in_k_parts(d, f):
+    # 600 routed rows, so few tiles: the down projection splits each tile's K
+    # (3 f) over 3 (f = 640: 30 K steps) or 6 (f = 1024: 48) workgroups, each
+    # writing its own [hi | lo] planes (part 0 with the LoRA delta) that the
+    # combine adds; d = 192 and 320 leave a partial column tile. The LoRA
+    # down-projections run in K parts where K allows (3 d = 1152 and 1536: 2
+    # and 3 parts; 3 f = 1920 and 3072: 3 and 6), summed by their finishing
+    # pass.
     w = small("fp32", dtype=torch.float32, r=8, alpha=16.0, T=300, E=6, k=2, d=d, f=f)
     stats = _run_case(w, with_lora=True)
     assert stats["mean_rel"] < 1e-4, stats
