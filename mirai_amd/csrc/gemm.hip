@@ -241,6 +241,27 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const uint16_t *base
 // NF4 decode in registers. `lo`/`hi` hold the low / high bytes of the 16
 // decoded bf16 values bf16(level[q] * absmax) of the current block, 4 per
 // register; v_perm_b32 looks four codes up at once.
+// Signed byte N of w as fp32 in one VALU instruction: v_cvt_f32_i32 with an
+// SDWA byte select and sign extension. (From the C++ conversion the compiler
+// emits a bit-field extract and then the conversion: two instructions.)
+template <int N>
+__device__ __forceinline__ float sbyte_to_f32(uint32_t w) {
+  float r;
+  if constexpr (N == 0)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0"
+        : "=v"(r) : "v"(w));
+  else if constexpr (N == 1)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1"
+        : "=v"(r) : "v"(w));
+  else if constexpr (N == 2)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2"
+        : "=v"(r) : "v"(w));
+  else
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3"
+        : "=v"(r) : "v"(w));
+  return r;
+}
+
 struct Nf4Table {
   uint32_t lo[4], hi[4];
 };
@@ -629,10 +650,10 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const uint32_t w = ws[h];
-          const float q0 = static_cast<float>(static_cast<int8_t>(w & 0xffu));
-          const float q1 = static_cast<float>(static_cast<int8_t>((w >> 8) & 0xffu));
-          const float q2 = static_cast<float>(static_cast<int8_t>((w >> 16) & 0xffu));
-          const float q3 = static_cast<float>(static_cast<int8_t>(w >> 24));
+          const float q0 = sbyte_to_f32<0>(w);
+          const float q1 = sbyte_to_f32<1>(w);
+          const float q2 = sbyte_to_f32<2>(w);
+          const float q3 = sbyte_to_f32<3>(w);
           d[2 * h] = pack_bf16x2(q0 * sc, q1 * sc);
           d[2 * h + 1] = pack_bf16x2(q2 * sc, q3 * sc);
         }
