@@ -298,20 +298,12 @@ __device__ __forceinline__ void nf4_lookup4(const Nf4Table &t, uint32_t s7, uint
 // element i + 4 in its high nibble) -> four dwords of bf16 pairs in element
 // order. The low nibbles give elements 0..3 and the high nibbles 4..7, so one
 // v_perm_b32 per output dword interleaves the looked-up low and high bytes.
-// (x & m) | k in one VALU instruction, m and k uniform. (The compiler keeps
-// an AND and an OR with literal operands for this pattern.)
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t k) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "s"(k));
-  return r;
-}
-
 __device__ __forceinline__ void nf4_decode8(const Nf4Table &t, uint32_t c, uint32_t *out) {
   uint32_t le, he, lo_, ho;
   // Low nibbles: bit 3 of the code sits at bit 3 of each byte.
-  nf4_lookup4(t, c & 0x07070707u, and_or(c >> 1, 0x04040404u, 0x03020100u), le, he);
+  nf4_lookup4(t, c & 0x07070707u, ((c >> 1) & 0x04040404u) | 0x03020100u, le, he);
   // High nibbles: bit 3 of the code is bit 7 of the byte.
-  nf4_lookup4(t, (c >> 4) & 0x07070707u, and_or(c >> 5, 0x04040404u, 0x03020100u), lo_, ho);
+  nf4_lookup4(t, (c >> 4) & 0x07070707u, ((c >> 5) & 0x04040404u) | 0x03020100u, lo_, ho);
   out[0] = __builtin_amdgcn_perm(he, le, 0x05010400u);   // e0, e1
   out[1] = __builtin_amdgcn_perm(he, le, 0x07030602u);   // e2, e3
   out[2] = __builtin_amdgcn_perm(ho, lo_, 0x05010400u);  // e4, e5
