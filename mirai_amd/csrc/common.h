@@ -35,7 +35,6 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
-__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
 
 // Two fp32 values -> packed bf16 pair (lo in bits 0-15), round to nearest even,
 // as one v_cvt_pk_bf16_f32.
@@ -44,6 +43,10 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
+
+// f rounded to bf16 (nearest even), as an fp32 value: one v_cvt_pk_bf16_f32
+// with 0 in the low half, whose result bits are then the fp32 value itself.
+__device__ __forceinline__ float round_bf16(float f) { return __uint_as_float(pack_bf16x2(0.0f, f)); }
 
 // IEEE correctly rounded fp32 division: the quotient is formed in fp64 and
 // rounded once to fp32. fp64 carries 53 >= 2*24+2 bits, so the double rounding

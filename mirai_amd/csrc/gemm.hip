@@ -216,11 +216,10 @@ __device__ __forceinline__ float swiglu7(float g, float u) {
   return (gc * sig) * (uc + 1.0f);
 }
 
-// Rounds two fp32 values to bf16 precision with one packed conversion.
+// Rounds two fp32 values to bf16 precision, one conversion each.
 __device__ __forceinline__ void round2(float &a, float &b) {
-  const uint32_t t = pack_bf16x2(a, b);
-  a = __uint_as_float(t << 16);
-  b = __uint_as_float(t & 0xffff0000u);
+  a = round_bf16(a);
+  b = round_bf16(b);
 }
 
 // The calling wave's index in its workgroup, as a value the compiler keeps in
