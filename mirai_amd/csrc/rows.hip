@@ -178,18 +178,20 @@ __global__ __launch_bounds__(256) void combine_wave_kernel(const uint16_t *y, co
       }
     }
   };
-  // Four 512-column spans per round: all 4 * KC row loads are in flight
-  // before the first sum.
+  // kSpans 512-column spans per round: all kSpans * KC row loads (at most 16
+  // per lane, so the registers leave room for several waves per SIMD) are in
+  // flight before the first sum.
+  constexpr int kSpans = KC > 4 ? 2 : 4;
   int64_t c0 = static_cast<int64_t>(lane) * 8;
-  for (; c0 + 3 * 512 < cols; c0 += 4 * 512) {
-    uint4 v[4][KC];
+  for (; c0 + (kSpans - 1) * 512 < cols; c0 += kSpans * 512) {
+    uint4 v[kSpans][KC];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < kSpans; ++u)
 #pragma unroll
       for (int q = 0; q < KC; ++q)
         v[u][q] = ok[q] ? nt_load16(row[q] + c0 + 512 * u) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kSpans; ++u) {
       float acc[8];
       span_sum(v[u], acc);
       store_combined(out, out_dtype, addend, t * cols + c0 + 512 * u, acc);
