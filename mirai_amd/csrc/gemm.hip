@@ -931,14 +931,14 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   // (mb, nbp + NB/2)) -> the packed bf16 h run; gv / uv end rounded as the
   // reference's bf16 gate / up (with the bf16 LoRA deltas added).
   auto swiglu_run = [&](float (&gv)[4], float (&uv)[4], const f32x16 &lg, const f32x16 &lu, int g,
-                        uint32_t &h0, uint32_t &h1) __attribute__((always_inline)) {
+                        uint32_t &h0, uint32_t &h1, int act) __attribute__((always_inline)) {
     float a[4], b[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       a[q] = LORA ? lg[4 * g + q] : 0.0f;
       b[q] = LORA ? lu[4 * g + q] : 0.0f;
     }
-    gated_run<LORA>(gv, uv, a, b, p.act, h0, h1);
+    gated_run<LORA>(gv, uv, a, b, act, h0, h1);
   };
   // Down / backward run of 4 columns of block (mb, nb): the bf16 projection
   // plus the bf16 LoRA delta, rounded again (experts.py:3370-3374).
@@ -967,6 +967,8 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
     auto h_stage = [&](int r) -> uint8_t * {
       return (r < T::BM / 2 ? sB0 : sB1) + (r & (T::BM / 2 - 1)) * RSB;
     };
+    // The activation is chosen once per tile, outside the unrolled runs.
+    auto stage_h = [&](auto act_c) __attribute__((always_inline)) {
 #pragma unroll
     for (int mb = 0; mb < T::MB; ++mb) {
       const int r = wm * T::WM + mb * 32 + lrow;
@@ -988,13 +990,18 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
             uv[q] = acc[mb][nbp + T::NB / 2][4 * g + q];
           }
           uint32_t h0, h1;
-          swiglu_run(gv, uv, lg, lu, g, h0, h1);
+          swiglu_run(gv, uv, lg, lu, g, h0, h1, decltype(act_c)::value);
           const int hc = hc0 + 8 * g;
           *reinterpret_cast<u32x2 *>(srow + (((hc >> 3) ^ (r & 15)) << 4) + ((hc & 7) << 1)) =
               u32x2{h0, h1};
         }
       }
     }
+    };
+    if (p.act == MX_ACT_SWIGLU7)
+      stage_h(std::integral_constant<int, MX_ACT_SWIGLU7>{});
+    else
+      stage_h(std::integral_constant<int, MX_ACT_SILU>{});
     __syncthreads();
     constexpr int RPW = T::BM / kWaves;  // rows stored per wave
     const int c = lane & 15;
@@ -1057,7 +1064,7 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
             continue;
           }
           uint32_t h0, h1;
-          swiglu_run(gv, uv, lg, lu, g, h0, h1);
+          swiglu_run(gv, uv, lg, lu, g, h0, h1, p.act);
           st8(rs_h, off_h, h0, h1);
           if (saves) {
             st8(rs_g, off_s, pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3]));
