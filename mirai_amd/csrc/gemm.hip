@@ -1741,9 +1741,11 @@ int launch_fmt(int fmt, Params p, const PlanLayout &PL, const PlanView &v, bool 
   p.num_tiles_r = v.num_tilesr;
   // Half of the 32 CUs of an XCD (gfx950: 256 CUs in 8 XCDs) start on a
   // remainder tile when experts average under 1024 rows, where remainder
-  // tiles are a large share of the work (A/B: C5 -2.6 %, C3 -1.3 %; at about
-  // 2048 rows per expert it gained nothing at the target and cost C4 1.2 %).
-  p.stagger = PL.rows < 1024 * static_cast<int64_t>(PL.experts) ? 16 : 0;
+  // tiles are a large share of the work (A/B: C5 -2.6 %, C3 -1.3 %), and in
+  // the forward down projection, whose epilogue is mostly output stores that
+  // then stop coinciding across the chip (C4 down -1.8 %). At about 2048 rows
+  // per expert the gate/up GEMM gained nothing from it and lost 1.2 % at C4.
+  p.stagger = (EPI == EPI_STORE || PL.rows < 1024 * static_cast<int64_t>(PL.experts)) ? 16 : 0;
   return launch_tile_dual<EPI, LORA, Tall, Short>(fmt, p, PL.max_tiles2, PL.experts, s);
 }
 
