@@ -685,8 +685,9 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   // workgroup (k_parts > 1) and a pass adds their fp32 sums in the same order.
   // So the result does not depend on how many rows a launch has, and a
   // token-chunked layer stays bit-identical to the whole one. (The 128-column
-  // tile of ranks above 64 sums K in one part: tot would cost it occupancy.)
-  constexpr bool kFold = EPI == EPI_LORA_A && T::BN == 64;
+  // tile of ranks above 64 sums K in one part: tot would cost it occupancy;
+  // the 32- and 64-column tiles fold.)
+  constexpr bool kFold = EPI == EPI_LORA_A && T::BN <= 64;
   f32x16 tot[kFold ? T::MB : 1][kFold ? T::NB : 1];
   // Steps per part here (the whole K loop when this workgroup runs one part),
   // counted down to each fold.
@@ -760,7 +761,8 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   constexpr int kPDma = n_adapt * T::BM * 64 / 1024, kLDma = n_lb * T::BN * 64 / 1024;
   static_assert(n_adapt * T::BM * 64 <= T::STAGE_A && (!LORA || n_lb * T::BN * 64 <= kLTile),
                 "LoRA tiles must fit their buffers");
-  static_assert(kPDma % kWaves == 0 && kLDma % kWaves == 0, "LoRA tiles split evenly over waves");
+  static_assert(!LORA || (kPDma % kWaves == 0 && kLDma % kWaves == 0),
+                "LoRA tiles split evenly over waves");
   auto dma16 = [&](const uint16_t *src, uint8_t *dst) __attribute__((always_inline)) {
     __builtin_amdgcn_global_load_lds(
         reinterpret_cast<const void *>(src),
@@ -2050,11 +2052,11 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
     p.seg_end = v.seg + experts;
     p.out = out + kLoraK * first;
     p.ldo = ldo;
-    // The tile width of the launch below; the 64-column tile sums K in its
-    // canonical parts, and runs them in workgroups of their own when the
-    // launch would not give three workgroups to each CU.
-    const int bn = (split || cnt <= 2) ? 64 : 128;
-    const int64_t part_len = bn == 64 ? lora_a_part_len(K) : K;
+    // The tile width of the launch below; the 32- and 64-column tiles sum K
+    // in its canonical parts, and run them in workgroups of their own when
+    // the launch would not give three workgroups to each CU.
+    const int bn = (!split && cnt == 1) ? 32 : (split || cnt <= 2) ? 64 : 128;
+    const int64_t part_len = bn <= 64 ? lora_a_part_len(K) : K;
     const int kpc = static_cast<int>(K / part_len);
     p.k_part_len = kpc > 1 ? part_len : 0;
     const bool parts = kpc > 1 && part_buf && rows > 0 && max_tiles * kpc <= 3 * kChipCUs &&
@@ -2065,14 +2067,18 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
       p.part_rows = rows;
       p.part_ld = bn;
     }
-    // Up to two sub-adapters fill a 64-column tile; the kernel is bound by
-    // the activation reads, so the narrower tile (more workgroups, half the
-    // MFMA and B traffic) is the faster one (K stages of 32, for more
-    // resident workgroups, measured slower: 112 vs 92 us at the target
-    // shape). The fp32 layer (split planes, K = 3 * in) writes split outputs.
+    // Up to two sub-adapters fill a 64-column tile, one a 32-column tile;
+    // the kernel is bound by the activation reads, so the narrowest tile
+    // (more workgroups per CU, less MFMA and factor traffic) is the fastest
+    // (one adapter on 32 columns against 64: C4's h launch 139 -> 136 us, the
+    // C5 backward 1.10 -> 1.09 ms; K stages of 32, for more resident
+    // workgroups, measured slower: 112 vs 92 us at the target shape). The
+    // fp32 layer (split planes, K = 3 * in) writes split outputs.
     int rc2;
     if (split)
       rc2 = launch<MX_FMT_F32X3, EPI_LORA_A, false, Tile<128, 64, 4, 1, 64>>(p, max_tiles, s);
+    else if (cnt == 1)
+      rc2 = launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 32, 4, 1, 64>>(p, max_tiles, s);
     else if (cnt <= 2)
       rc2 = launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 64, 4, 1, 64>>(p, max_tiles, s);
     else
