@@ -874,6 +874,9 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
       if (r == 0) continue;  // absent adapter: its tiles are not staged
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
+        // Ranks up to 16 leave the second K step's activations zero: the
+        // step would add exact zeros to a sum that is not -0.
+        if (kk == 1 && r <= 16) break;
         const int ch = kk * 2 + (lane >> 5);
         const bf16x8 a = *reinterpret_cast<const bf16x8 *>(
             sP + ad * T::BM * 64 + swz64(wm * T::WM + mb * 32 + (lane & 31), ch));
