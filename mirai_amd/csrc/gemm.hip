@@ -2428,15 +2428,17 @@ int backward_core(const BackLayout &L, const PlanView &v, int num_experts, int64
   // is still in the memory-side cache from the SwiGLU backward and the dz
   // passes (nothing here reads what the dx GEMM overwrites).
   {
+    // The dA job (two V blocks per gathered row, the heaviest workgroups)
+    // is dispatched first, so the lighter dB workgroups fill the launch's tail.
     GradPhase ph;
-    for (int i = 0; i < 2; ++i)
-      if (has_lora(l13[i]))
-        ph.add({dgu + i * ffn, 2 * ffn, nullptr, ffn}, lsave + lrc * i, ldz, l13[i]->rank,
-               i ? grad_b3 : grad_b1, false);
     for (int i = 0; i < 2; ++i)
       if (has_lora(l13[i]))
         ph.add({x, hidden, v.row_token, hidden}, dz + lrc * i, ldz, l13[i]->rank,
                i ? grad_a3 : grad_a1, true);
+    for (int i = 0; i < 2; ++i)
+      if (has_lora(l13[i]))
+        ph.add({dgu + i * ffn, 2 * ffn, nullptr, ffn}, lsave + lrc * i, ldz, l13[i]->rank,
+               i ? grad_b3 : grad_b1, false);
     if ((rc = ph.run(v, num_experts, s))) return rc;
   }
   mark_stage(4, s);
