@@ -139,6 +139,10 @@ struct Params {
   uint16_t *save_up;
   float scale[4];
   int split_r[4];            // MX_FMT_F32X3 LoRA down-projection: rank of each adapter
+  // EPI_LORA_A: two adapters of rank <= 16 share one 32-column block, 16
+  // factor rows each (columns [16a, 16a + 16) hold adapter a, written to its
+  // own 32-column output block with zeros above).
+  int lora_pack;
   int act;                   // EPI_SWIGLU: MX_ACT_SILU or MX_ACT_SWIGLU7
   // MX_FMT_NF4_DQ*: per weight group (as w[0], w[1]) the nested scales [E,
   // dq_npe], the offsets [E] and the 256-entry code table; wscale holds the
@@ -187,6 +191,12 @@ __device__ __forceinline__ void b_row(int j, int nt, int &which, int64_t &n) {
     which = j >> 5;
     n = j & 31;
   }
+}
+
+// EPI_LORA_A rows of a packed block: sub-adapter j / 16, factor row j % 16.
+__device__ __forceinline__ void b_row_packed(int j, int &which, int64_t &n) {
+  which = j >> 4;
+  n = j & 15;
 }
 
 // Row key of the 128-byte-row stage swizzle: any 16 consecutive rows at one
@@ -452,6 +462,7 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
   int which = 0;
   int64_t bn = 0;
   if (!TRANS) b_row<EPI, T>(bj, nt, which, bn);
+  if (EPI == EPI_LORA_A && p.lora_pack) b_row_packed(bj, which, bn);
   // Transposed B: lane = k row of the stage, wave = 32-column slice. Columns
   // past N re-read the last full 32-column slice (discarded by the epilogue).
   // SwiGLU with transposed B (weights [E, in, out]): slice tc holds 32 gate
@@ -1216,6 +1227,20 @@ __device__ __forceinline__ void gemm_tile(Params p, int2 tile, int nt, uint8_t *
           float v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) v[q] = acc[mb][nb][4 * g + q];
+          if constexpr (!kSplit) {
+            if (p.lora_pack) {
+              // Packed block (nblk == 0): columns 16a.. hold adapter a, which
+              // leaves at its own block a * 32, zeros in its upper 16 columns.
+              const int a = jc >> 4, c = jc & 15;
+              const float psc = pick(p.scale, a);
+              round2(v[0], v[1]);
+              round2(v[2], v[3]);
+              const uint32_t o = nblk < p.N ? r * ld2 + static_cast<uint32_t>(32 * a + c) * 2u : kDrop;
+              st8(rs_o, o, pack_bf16x2(v[0] * psc, v[1] * psc), pack_bf16x2(v[2] * psc, v[3] * psc));
+              st8(rs_o, o == kDrop ? kDrop : o + 32u, 0u, 0u);
+              continue;
+            }
+          }
           if constexpr (kSplit) {
             // fp32 layer: column j < r of an adapter block leaves as planes
             // [hi | hi | lo] at columns j, r + j, 2r + j (3r <= 32); columns
@@ -1955,6 +1980,7 @@ struct LoraFinish {
   int64_t ldo;
   float scale[4];
   int split_r[4];
+  int pack;  // Params::lora_pack: two 16-column adapters in a 32-column block
 };
 
 template <bool SPLIT>
@@ -1972,10 +1998,22 @@ __global__ __launch_bounds__(256) void lora_a_finish_kernel(LoraFinish f) {
     for (int j = 0; j < 4; ++j) a[j] = a[j] + b[j];
   }
   float v[4] = {a[0], a[1], a[2], a[3]};
+  typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+  if (!SPLIT && f.pack) {
+    // Adapter c / 16 leaves at its own 32-column block, zeros above its 16.
+    const int ad = c >> 4, jp = c & 15;
+    const float psc = pick(f.scale, ad);
+    round2(v[0], v[1]);
+    round2(v[2], v[3]);
+    uint16_t *prow = f.out + r * f.ldo + 32 * ad + jp;
+    *reinterpret_cast<u32x2v *>(prow) =
+        u32x2v{pack_bf16x2(v[0] * psc, v[1] * psc), pack_bf16x2(v[2] * psc, v[3] * psc)};
+    *reinterpret_cast<u32x2v *>(prow + 16) = u32x2v{0u, 0u};
+    return;
+  }
   const int blk = c >> 5, jc = c & 31;
   const float sc = pick(f.scale, blk);
   uint16_t *orow = f.out + r * f.ldo + (c - jc);
-  typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
   if constexpr (SPLIT) {
     // The fp32 layer's planes [hi | hi | lo] at columns j, r + j, 2r + j.
     const int rk = pick(f.split_r, blk);
@@ -2035,9 +2073,13 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
       u.scale = l->scale;
     }
   }
+  // Two adapters of rank <= 16 (one sub-adapter each) share one 32-column
+  // block of 16 factor rows apiece.
+  const bool pack = !split && n_sub == 2 && per == 1 && subs[0].rows <= 16 && subs[1].rows <= 16;
   for (int first = 0; first < n_sub; first += 4) {
     const int cnt = std::min(4, n_sub - first);
     Params p = base_params(v);
+    p.lora_pack = pack ? 1 : 0;
     p.x = x;
     p.ldx = ldx;
     p.row_token = row_token;
@@ -2050,7 +2092,7 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
       p.scale[i] = u.scale;
       p.split_r[i] = u.rows;
     }
-    p.N = kLoraK * cnt;
+    p.N = pack ? kLoraK : kLoraK * cnt;
     p.n_tiles_n = 1;
     p.seg_end = v.seg + experts;
     p.out = out + kLoraK * first;
@@ -2058,7 +2100,7 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
     // The tile width of the launch below; the 32- and 64-column tiles sum K
     // in its canonical parts, and run them in workgroups of their own when
     // the launch would not give three workgroups to each CU.
-    const int bn = (!split && cnt == 1) ? 32 : (split || cnt <= 2) ? 64 : 128;
+    const int bn = (!split && (cnt == 1 || pack)) ? 32 : (split || cnt <= 2) ? 64 : 128;
     const int64_t part_len = bn <= 64 ? lora_a_part_len(K) : K;
     const int kpc = static_cast<int>(K / part_len);
     p.k_part_len = kpc > 1 ? part_len : 0;
@@ -2080,7 +2122,7 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
     int rc2;
     if (split)
       rc2 = launch<MX_FMT_F32X3, EPI_LORA_A, false, Tile<128, 64, 4, 1, 64>>(p, max_tiles, s);
-    else if (cnt == 1)
+    else if (cnt == 1 || pack)
       rc2 = launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 32, 4, 1, 64>>(p, max_tiles, s);
     else if (cnt <= 2)
       rc2 = launch<MX_FMT_BF16, EPI_LORA_A, false, Tile<128, 64, 4, 1, 64>>(p, max_tiles, s);
@@ -2094,6 +2136,7 @@ int lora_down(const PlanView &v, int experts, int64_t max_tiles, const uint16_t 
       f.rows = rows;
       f.ld = bn;
       f.N = static_cast<int>(p.N);
+      f.pack = p.lora_pack;
       f.out = p.out;
       f.ldo = ldo;
       for (int i = 0; i < 4; ++i) {
